@@ -1,0 +1,200 @@
+/* mote_relation.h — C ABI of the MI355X (gfx950) Relation library, libmote_relation.so.
+ *
+ * The library holds the hand-written HIP kernels of Mote's Relation mixer. Every entry point takes
+ * plain device pointers, sizes and element strides, launches on the caller's HIP stream and
+ * returns a status code; it allocates nothing, keeps no reference to its arguments after it
+ * returns and never synchronises the device. `mote_last_error()` explains a non-zero status.
+ * Entry points are reentrant: the only mutable state is the thread-local error text.
+ *
+ * Reference interfaces (noahsabaj/mote, paths relative to its source root) are cited per function.
+ */
+#ifndef MOTE_RELATION_H
+#define MOTE_RELATION_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+enum {
+  MOTE_OK = 0,
+  MOTE_ERR_ARGUMENT = 1,    /* null pointer, bad enum, inconsistent sizes */
+  MOTE_ERR_SHAPE = 2,       /* shape outside what the kernels support (e.g. D > 128, D % 8 != 0) */
+  MOTE_ERR_WORKSPACE = 3,   /* workspace smaller than the matching *_workspace() query */
+  MOTE_ERR_LAUNCH = 4       /* the HIP runtime refused a launch */
+};
+
+/* Element types of the input/output tensors. Statistics are always fp32. */
+enum { MOTE_F32 = 0, MOTE_BF16 = 1 };
+
+/* A [batch, heads, rows, D] tensor view with unit stride along D; strides count elements. */
+typedef struct mote_view {
+  void* data;
+  int64_t stride_b;
+  int64_t stride_h;
+  int64_t stride_r;
+} mote_view;
+
+/* Text of the last error on this thread ("" when none). */
+const char* mote_last_error(void);
+
+/* Library version and the GPU architecture its kernels were built for ("gfx950"). */
+const char* mote_version(void);
+
+/* ------------------------------------------------------------------------------------------------
+ * Fused Relation forward.
+ * Replaces: the Triton `_fwd_kernel` and its launcher `_launch_fwd`
+ * (mote/model/flash_relation.py:76-183, 507-541), behind the custom op `mote::relation_fwd`
+ * (flash_relation.py:620-622). Same outputs: y (dtype of info), ibar fp32, lse fp32 (natural
+ * units, -inf for rows without a past), g fp32.
+ *
+ * Dense mode (cu_seqlens == NULL): p1/y are [B, H, TQ, D]; p2/info are [B, H, TK, D] with
+ * TK == q_start + TQ (flash_relation.py:511); ibar is [B, H, TQ, D] and lse/g are [B, H, TQ],
+ * all contiguous. Any row/head/batch strides are accepted for p1, p2, info and y (the decode
+ * arena's head stride capacity*D included, flash_relation.py:513-525).
+ * Varlen mode (cu_seqlens != NULL, no counterpart in the reference, which pads instead,
+ * mote/model/dc.py:192-218): B sequences packed along the row axis, sequence b owning rows
+ * [cu_seqlens[b], cu_seqlens[b+1]); q_start must be 0, TQ = TK = the longest sequence, total_rows =
+ * cu_seqlens[B]; stride_b is ignored; ibar is [H, total_rows, D], lse/g are [H, total_rows].
+ * ------------------------------------------------------------------------------------------------ */
+typedef struct mote_relation_fwd_args {
+  int dtype;          /* MOTE_F32 or MOTE_BF16, for p1, p2, info and y */
+  int B, H, TQ, TK, D, q_start;
+  float tau_s;        /* Self temperature (RelationCfg.tau_s, mote/config.py:38) */
+  mote_view p1, p2, info, y;
+  float* ibar;
+  float* lse;
+  float* g;
+  const float* lam;   /* device pointer to the fp32 count-calibration scalar */
+  const int32_t* cu_seqlens;
+  int total_rows;
+} mote_relation_fwd_args;
+
+int mote_relation_fwd(const mote_relation_fwd_args* args, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * Fused Relation backward.
+ * Replaces: `_bwd_rows_kernel` + `_bwd_kernel` (one pass, fp32 atomics for dp1) and the
+ * deterministic two-pass `_bwd_kv_kernel` + `_bwd_q_kernel` with their launchers
+ * (mote/model/flash_relation.py:186-460, 544-615), behind `mote::relation_bwd` (:634-637).
+ * `deterministic` != 0 selects the atomic-free path (the reference's MOTE_DETERMINISTIC_RELATION,
+ * flash_relation.py:51): its results are bitwise reproducible run to run.
+ * Inputs are the forward's inputs and saved statistics (ibar, lse, g as produced by
+ * mote_relation_fwd, dense layout) and dy ([B, H, TQ, D], any strides). Outputs dp1 [B,H,TQ,D],
+ * dp2 and dinfo [B,H,TK,D] in `dtype` (any strides) and dlam (one fp32, overwritten).
+ * The workspace is caller-allocated device memory of at least mote_relation_bwd_workspace()
+ * bytes; its contents on entry do not matter.
+ * ------------------------------------------------------------------------------------------------ */
+typedef struct mote_relation_bwd_args {
+  int dtype;
+  int B, H, TQ, TK, D, q_start;
+  float tau_s;
+  int deterministic;
+  mote_view p1, p2, info, dy;
+  const float* ibar;
+  const float* lse;
+  const float* g;
+  mote_view dp1, dp2, dinfo;
+  float* dlam;
+  void* workspace;
+  size_t workspace_bytes;
+} mote_relation_bwd_args;
+
+size_t mote_relation_bwd_workspace(const mote_relation_bwd_args* args);
+int mote_relation_bwd(const mote_relation_bwd_args* args, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * RoPE on p1/p2 and Givens head mixing on I~, fused with the split of the projection output.
+ * Replaces: `_rope_cos_sin` / `rope_tables` / `_apply_rope` and `FullRelation._givens`
+ * (mote/model/relation.py:37-68, 160-174) as called from FullRelation.forward (:204-215).
+ * qkv is the [B, T, 3*H*D] output of the fused projection [w1; w2; wi] (row stride qkv_sr, batch
+ * stride qkv_sb, elements); positions are pos0 .. pos0+T-1. inv_freq is the fp32 [D/2] table
+ * 1/theta^(2k/D) (relation.py:39), or NULL for no RoPE (NoPE Relation, relation.py:141).
+ * theta is the fp32 [H/2] Givens angle vector, or NULL for no Givens; layer_parity picks the
+ * pairing (0: (0,1),(2,3)...; 1: (1,2),...,(H-1,0), relation.py:150-157). The cos/sin factors are
+ * rounded to `dtype` before use, as the reference casts them (relation.py:42, 165-166).
+ * ------------------------------------------------------------------------------------------------ */
+typedef struct mote_rope_givens_args {
+  int dtype;
+  int B, T, H, D, pos0, layer_parity;
+  const float* inv_freq;
+  const float* theta;
+  const void* qkv;
+  int64_t qkv_sb, qkv_sr;
+  mote_view p1, p2, info;   /* outputs, [B, H, T, D] views */
+} mote_rope_givens_args;
+
+int mote_rope_givens_fwd(const mote_rope_givens_args* args, void* stream);
+
+/* Backward of mote_rope_givens_fwd: gradients dp1, dp2, dinfo ([B,H,T,D] views) -> dqkv
+ * ([B, T, 3*H*D], strides dqkv_sb/dqkv_sr) and dtheta (fp32 [H/2], overwritten; deterministic).
+ * qkv is the forward's input (needed for dtheta). Workspace: mote_rope_givens_bwd_workspace(). */
+typedef struct mote_rope_givens_bwd_args {
+  int dtype;
+  int B, T, H, D, pos0, layer_parity;
+  const float* inv_freq;
+  const float* theta;
+  const void* qkv;
+  int64_t qkv_sb, qkv_sr;
+  mote_view dp1, dp2, dinfo;
+  void* dqkv;
+  int64_t dqkv_sb, dqkv_sr;
+  float* dtheta;
+  void* workspace;
+  size_t workspace_bytes;
+} mote_rope_givens_bwd_args;
+
+size_t mote_rope_givens_bwd_workspace(const mote_rope_givens_bwd_args* args);
+int mote_rope_givens_bwd(const mote_rope_givens_bwd_args* args, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * One decode step of one Relation layer over the {P2, I~} cache.
+ * Replaces: GraphDecoder._relation_step between the projections and `_out`
+ * (mote/infer/graph.py:158-186): RoPE at the device position S, Givens, the cast to the cache
+ * dtype, the append of the new P2 / I~ row at S (index_copy_, :173-175), and the masked
+ * softmax read of rows [0, S] (:177-185), for B independent sequences (the reference decodes
+ * B = 1; B > 1 is B independent batch-1 steps). S[b] (int64, device) is read on the device, so the
+ * launch is capturable in a HIP graph with a fixed argument set (graph.py:1-17).
+ * Inputs p1/p2/info are the raw projections of the new chunk, [B, H, D] with batch stride in_sb
+ * and head stride D, in `dtype` (the cache dtype). Outputs: y [B, H, D] (dtype, batch stride y_sb)
+ * and g [B, H] fp32, the exchange mass g = 1 - F_SS (graph.py:186 averages it over heads).
+ * The caches are [B, H, capacity, D] views (mote/model/arena.py:30-51, 141-143); rows past S are
+ * never read. S[b] >= capacity writes NaN into y[b] and skips the append.
+ * flags bit 0 (MOTE_DECODE_ADVANCE): add 1 to every S[b] once the step has read it (graph.py's
+ * S += 1, :189-190), so a captured step needs no separate kernel for it.
+ * The workspace (mote_relation_decode_workspace() bytes) must be zero-filled once before its first
+ * use; every call leaves it ready for the next. Calls that share a workspace must not overlap.
+ * ------------------------------------------------------------------------------------------------ */
+#define MOTE_DECODE_ADVANCE 1
+
+typedef struct mote_relation_decode_args {
+  int dtype;
+  int B, H, D, capacity, layer_parity, flags;
+  float tau_s;
+  const float* lam;
+  const float* inv_freq;   /* [D/2] fp32 or NULL (no RoPE) */
+  const float* theta;      /* [H/2] fp32 or NULL (no Givens) */
+  int64_t* S;              /* [B] positions on the device */
+  const void* p1;
+  const void* p2;
+  const void* info;
+  int64_t in_sb;
+  mote_view cache_p2, cache_info;
+  void* y;
+  int64_t y_sb;
+  float* g;
+  void* workspace;
+  size_t workspace_bytes;
+} mote_relation_decode_args;
+
+size_t mote_relation_decode_workspace(const mote_relation_decode_args* args);
+int mote_relation_decode(const mote_relation_decode_args* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOTE_RELATION_H */

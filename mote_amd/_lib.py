@@ -1,0 +1,149 @@
+"""ctypes binding of libmote_relation.so (include/mote_relation.h).
+
+The structures below mirror the header field by field. `lib()` loads the in-tree library once and
+raises if it is missing: there is no fallback path. Calls pass raw device pointers and the current
+HIP stream of the tensors' device.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+import threading
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libmote_relation.so")
+
+MOTE_OK = 0
+MOTE_F32 = 0
+MOTE_BF16 = 1
+MOTE_DECODE_ADVANCE = 1
+
+_DTYPES = {torch.float32: MOTE_F32, torch.bfloat16: MOTE_BF16}
+
+
+class View(C.Structure):
+    _fields_ = [("data", C.c_void_p), ("stride_b", C.c_int64), ("stride_h", C.c_int64), ("stride_r", C.c_int64)]
+
+
+class FwdArgs(C.Structure):
+    _fields_ = [
+        ("dtype", C.c_int), ("B", C.c_int), ("H", C.c_int), ("TQ", C.c_int), ("TK", C.c_int), ("D", C.c_int),
+        ("q_start", C.c_int), ("tau_s", C.c_float),
+        ("p1", View), ("p2", View), ("info", View), ("y", View),
+        ("ibar", C.c_void_p), ("lse", C.c_void_p), ("g", C.c_void_p), ("lam", C.c_void_p),
+        ("cu_seqlens", C.c_void_p), ("total_rows", C.c_int),
+    ]
+
+
+class BwdArgs(C.Structure):
+    _fields_ = [
+        ("dtype", C.c_int), ("B", C.c_int), ("H", C.c_int), ("TQ", C.c_int), ("TK", C.c_int), ("D", C.c_int),
+        ("q_start", C.c_int), ("tau_s", C.c_float), ("deterministic", C.c_int),
+        ("p1", View), ("p2", View), ("info", View), ("dy", View),
+        ("ibar", C.c_void_p), ("lse", C.c_void_p), ("g", C.c_void_p),
+        ("dp1", View), ("dp2", View), ("dinfo", View),
+        ("dlam", C.c_void_p), ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
+    ]
+
+
+class RopeArgs(C.Structure):
+    _fields_ = [
+        ("dtype", C.c_int), ("B", C.c_int), ("T", C.c_int), ("H", C.c_int), ("D", C.c_int), ("pos0", C.c_int),
+        ("layer_parity", C.c_int), ("inv_freq", C.c_void_p), ("theta", C.c_void_p),
+        ("qkv", C.c_void_p), ("qkv_sb", C.c_int64), ("qkv_sr", C.c_int64),
+        ("p1", View), ("p2", View), ("info", View),
+    ]
+
+
+class RopeBwdArgs(C.Structure):
+    _fields_ = [
+        ("dtype", C.c_int), ("B", C.c_int), ("T", C.c_int), ("H", C.c_int), ("D", C.c_int), ("pos0", C.c_int),
+        ("layer_parity", C.c_int), ("inv_freq", C.c_void_p), ("theta", C.c_void_p),
+        ("qkv", C.c_void_p), ("qkv_sb", C.c_int64), ("qkv_sr", C.c_int64),
+        ("dp1", View), ("dp2", View), ("dinfo", View),
+        ("dqkv", C.c_void_p), ("dqkv_sb", C.c_int64), ("dqkv_sr", C.c_int64),
+        ("dtheta", C.c_void_p), ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
+    ]
+
+
+class DecodeArgs(C.Structure):
+    _fields_ = [
+        ("dtype", C.c_int), ("B", C.c_int), ("H", C.c_int), ("D", C.c_int), ("capacity", C.c_int),
+        ("layer_parity", C.c_int), ("flags", C.c_int), ("tau_s", C.c_float),
+        ("lam", C.c_void_p), ("inv_freq", C.c_void_p), ("theta", C.c_void_p), ("S", C.c_void_p),
+        ("p1", C.c_void_p), ("p2", C.c_void_p), ("info", C.c_void_p), ("in_sb", C.c_int64),
+        ("cache_p2", View), ("cache_info", View),
+        ("y", C.c_void_p), ("y_sb", C.c_int64), ("g", C.c_void_p),
+        ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
+    ]
+
+
+# every symbol the header declares, with its argument types
+EXPORTS = {
+    "mote_last_error": ([], C.c_char_p),
+    "mote_version": ([], C.c_char_p),
+    "mote_relation_fwd": ([C.POINTER(FwdArgs), C.c_void_p], C.c_int),
+    "mote_relation_bwd_workspace": ([C.POINTER(BwdArgs)], C.c_size_t),
+    "mote_relation_bwd": ([C.POINTER(BwdArgs), C.c_void_p], C.c_int),
+    "mote_rope_givens_fwd": ([C.POINTER(RopeArgs), C.c_void_p], C.c_int),
+    "mote_rope_givens_bwd_workspace": ([C.POINTER(RopeBwdArgs)], C.c_size_t),
+    "mote_rope_givens_bwd": ([C.POINTER(RopeBwdArgs), C.c_void_p], C.c_int),
+    "mote_relation_decode_workspace": ([C.POINTER(DecodeArgs)], C.c_size_t),
+    "mote_relation_decode": ([C.POINTER(DecodeArgs), C.c_void_p], C.c_int),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+def lib():
+    """The loaded library; raises RuntimeError when it has not been built."""
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not os.path.exists(LIB_PATH):
+                    raise RuntimeError(
+                        f"libmote_relation.so is not built ({LIB_PATH}); run `python -m mote_amd.build` "
+                        "(the Relation path has no fallback without it)")
+                handle = C.CDLL(LIB_PATH)
+                for name, (argtypes, restype) in EXPORTS.items():
+                    fn = getattr(handle, name)
+                    fn.argtypes = argtypes
+                    fn.restype = restype
+                _lib = handle
+    return _lib
+
+
+def available() -> bool:
+    return os.path.exists(LIB_PATH)
+
+
+def check(rc: int, what: str) -> None:
+    if rc != MOTE_OK:
+        msg = lib().mote_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed (status {rc}): {msg}")
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise TypeError(f"Relation kernels take float32 or bfloat16 tensors, got {t.dtype}") from None
+
+
+def view(t: torch.Tensor) -> View:
+    """A [B, H, rows, D] tensor as a mote_view (unit stride along D required)."""
+    assert t.dim() == 4 and t.stride(3) == 1, "last axis must be contiguous"
+    return View(t.data_ptr(), t.stride(0), t.stride(1), t.stride(2))
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def ptr(t) -> int:
+    return 0 if t is None else t.data_ptr()

@@ -1,0 +1,74 @@
+// extern "C" entry points of libmote_relation.so (declared in include/mote_relation.h).
+//
+// The entry points validate their arguments, translate the argument blocks into kernel parameter
+// blocks and launch on the caller's stream. They allocate nothing and never synchronise; the only
+// mutable state is the thread-local error text.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "params.hpp"
+
+namespace mote {
+
+static thread_local char g_err[512] = "";
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(MOTE_ERR_LAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return MOTE_OK;
+}
+
+}  // namespace mote
+
+extern "C" {
+
+const char* mote_last_error(void) { return mote::g_err; }
+
+const char* mote_version(void) { return "mote_relation 0.1 gfx950"; }
+
+int mote_relation_fwd(const mote_relation_fwd_args* args, void* stream) {
+  mote::g_err[0] = 0;
+  return mote::launch_fwd(args, reinterpret_cast<hipStream_t>(stream));
+}
+
+size_t mote_relation_bwd_workspace(const mote_relation_bwd_args* args) {
+  return args ? mote::bwd_workspace_bytes(args) : 0;
+}
+
+int mote_relation_bwd(const mote_relation_bwd_args* args, void* stream) {
+  mote::g_err[0] = 0;
+  return mote::launch_bwd(args, reinterpret_cast<hipStream_t>(stream));
+}
+
+int mote_rope_givens_fwd(const mote_rope_givens_args* args, void* stream) {
+  mote::g_err[0] = 0;
+  return mote::launch_rope_givens_fwd(args, reinterpret_cast<hipStream_t>(stream));
+}
+
+size_t mote_rope_givens_bwd_workspace(const mote_rope_givens_bwd_args* args) {
+  return args ? mote::rope_givens_bwd_workspace_bytes(args) : 0;
+}
+
+int mote_rope_givens_bwd(const mote_rope_givens_bwd_args* args, void* stream) {
+  mote::g_err[0] = 0;
+  return mote::launch_rope_givens_bwd(args, reinterpret_cast<hipStream_t>(stream));
+}
+
+size_t mote_relation_decode_workspace(const mote_relation_decode_args* args) {
+  return args ? mote::decode_workspace_bytes(args) : 0;
+}
+
+int mote_relation_decode(const mote_relation_decode_args* args, void* stream) {
+  mote::g_err[0] = 0;
+  return mote::launch_decode(args, reinterpret_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

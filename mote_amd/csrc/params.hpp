@@ -1,0 +1,46 @@
+// Kernel parameter blocks (device side) and launcher declarations shared by the .hip files.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/mote_relation.h"
+
+namespace mote {
+
+// Forward: dense [B,H,T,D] batches or cu_seqlens-packed sequences (see mote_relation_fwd_args).
+struct FwdParams {
+  const void* p1;
+  const void* p2;
+  const void* info;
+  void* y;
+  float* ibar;
+  float* lse;
+  float* g;
+  const float* lam;
+  const int32_t* cu;  // null in dense mode
+  int64_t q_sb, q_sh, q_sr;
+  int64_t k_sb, k_sh, k_sr;
+  int64_t v_sb, v_sh, v_sr;
+  int64_t y_sb, y_sh, y_sr;
+  int nseq, H, TQ, TK, D, q_start, total_rows, nqb;
+  float scale, tau_inv;
+};
+
+int launch_fwd(const mote_relation_fwd_args* a, hipStream_t stream);
+int launch_bwd(const mote_relation_bwd_args* a, hipStream_t stream);
+size_t bwd_workspace_bytes(const mote_relation_bwd_args* a);
+int launch_rope_givens_fwd(const mote_rope_givens_args* a, hipStream_t stream);
+int launch_rope_givens_bwd(const mote_rope_givens_bwd_args* a, hipStream_t stream);
+size_t rope_givens_bwd_workspace_bytes(const mote_rope_givens_bwd_args* a);
+int launch_decode(const mote_relation_decode_args* a, hipStream_t stream);
+size_t decode_workspace_bytes(const mote_relation_decode_args* a);
+
+// Error reporting shared by the launchers (thread-local text, see abi.cpp).
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+
+// The padded head dim a kernel instance is compiled for: D rounded up to 32 (D <= 128, D % 8 == 0).
+inline int padded_dim(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <= 96 ? 96 : 128; }
+
+}  // namespace mote

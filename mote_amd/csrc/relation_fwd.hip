@@ -1,0 +1,453 @@
+// Fused Relation forward for gfx950.
+//
+// One workgroup owns BM = 32 * NW query rows of one (sequence, head); wave w owns rows
+// [32w, 32w + 32) as two 16-row tiles. The strictly-past keys are streamed in blocks of BN rows:
+// each block of P2 is staged row-major in LDS (Ks) and the matching I~ block transposed (Vt, head
+// dim major), both from registers prefetched during the previous block's math.
+//
+// Per block and wave:
+//   S^T = K Q^T       A = K rows from Ks, B = the wave's queries (registers, loaded once)
+//   e   = SiLU(S^T / sqrt(D)) in log2 units, masked on the diagonal blocks
+//   online softmax over keys with a running max per query, rescaled only when a block raises it
+//   by more than 2^8 (the reference's RESCALE_THRESH, flash_relation.py:57, 124-134)
+//   O^T += V^T P^T    A = I~ columns from Vt, B = P^T taken straight from the S^T accumulators:
+//                     a lane holds one query and keys 4g + r of each 16-key tile, which is a
+//                     permuted k order of the operand; the Vt fragment uses the same order.
+// Epilogue per query (flash_relation.py:151-183): LSE, I-bar = O / l, the Self score from the
+// query's own key row, g = sigmoid(LSE - lam ln(i+1) - S), Y = (1 - g) I~_i + g I-bar.
+//
+// Block order: the grid is [query block (descending) x sequence x head], head fastest. Long
+// query blocks are dispatched first (longest-processing-time order) and consecutive workgroups
+// of one query block land on different XCDs, so with 8 heads every XCD's L2 holds one head's
+// P2 / I~ rows.
+#include "common.hpp"
+#include "params.hpp"
+
+namespace mote {
+
+template <typename T, int DP, int BN, int NW>
+__global__ void __launch_bounds__(NW * 64) relation_fwd_kernel(const FwdParams p) {
+  using E = Elem<T>;
+  using Frag = typename E::Frag;
+  constexpr int NTH = NW * 64;
+  constexpr int KS = DP / 32;                 // k-steps over the head dim
+  constexpr int DT = DP / 16;                 // 16-row tiles of the head dim (outputs)
+  constexpr int NT = BN / 16;                 // 16-key tiles per block
+  constexpr int BM = NW * 32;
+  constexpr int EPC = 16 / sizeof(T);         // elements per 16-byte chunk
+  constexpr int KLD = DP + EPC;               // Ks row stride (elements): +16 bytes against bank conflicts
+  constexpr int VLD = BN + (sizeof(T) == 2 ? 8 : 4);
+  constexpr int CPR = DP / EPC;               // chunks per row
+  constexpr int KCH = BN * CPR;               // K chunks per block
+  constexpr int KCT = (KCH + NTH - 1) / NTH;
+  constexpr int VIT = (BN / 4) * CPR;         // V items (4 keys x one chunk) per block
+  constexpr int VIT_T = (VIT + NTH - 1) / NTH;
+
+  __shared__ __align__(16) T Ks[BN * KLD];
+  __shared__ __align__(16) T Vt[DP * VLD];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int li = lane & 15;
+  const int lg = lane >> 4;
+
+  // ---- which (query block, sequence, head) ----
+  const int bid = blockIdx.x;
+  const int h = bid % p.H;
+  const int rest = bid / p.H;
+  const int seq = rest % p.nseq;
+  const int qb = p.nqb - 1 - rest / p.nseq;
+
+  int TQs, TKs, qs;
+  int64_t qoff, koff, voff, yoff, soff;  // element offsets of (seq, head) row 0; soff: stats row 0
+  if (p.cu) {
+    const int r0 = p.cu[seq];
+    TQs = p.cu[seq + 1] - r0;
+    TKs = TQs;
+    qs = 0;
+    qoff = int64_t(r0) * p.q_sr;
+    koff = int64_t(r0) * p.k_sr;
+    voff = int64_t(r0) * p.v_sr;
+    yoff = int64_t(r0) * p.y_sr;
+    soff = int64_t(h) * p.total_rows + r0;
+  } else {
+    TQs = p.TQ;
+    TKs = p.TK;
+    qs = p.q_start;
+    qoff = int64_t(seq) * p.q_sb;
+    koff = int64_t(seq) * p.k_sb;
+    voff = int64_t(seq) * p.v_sb;
+    yoff = int64_t(seq) * p.y_sb;
+    soff = (int64_t(seq) * p.H + h) * p.TQ;
+  }
+  if (qb * BM >= TQs) return;  // uniform across the workgroup
+  const T* qbase = reinterpret_cast<const T*>(p.p1) + qoff + int64_t(h) * p.q_sh;
+  const T* kbase = reinterpret_cast<const T*>(p.p2) + koff + int64_t(h) * p.k_sh;
+  const T* vbase = reinterpret_cast<const T*>(p.info) + voff + int64_t(h) * p.v_sh;
+  T* ybase = reinterpret_cast<T*>(p.y) + yoff + int64_t(h) * p.y_sh;
+  const int D = p.D;
+
+  // ---- the wave's queries: B fragments of Q^T, loaded once ----
+  const int q0 = qb * BM + wave * 32;  // local index of the wave's first query
+  const bool wave_active = q0 < TQs;
+  Frag qf[2][KS];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const int qi = q0 + 16 * s + li;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int d0 = 32 * ks + 8 * lg;
+      if (qi < TQs && d0 < D) {
+        qf[s][ks] = E::load8(qbase + int64_t(qi) * p.q_sr + d0);
+      } else {
+        qf[s][ks] = E::zero();
+      }
+    }
+  }
+  const int qlast_wg = min(TQs, (qb + 1) * BM) - 1;
+  const int kend = qs + qlast_wg;  // keys j < kend are somebody's strict past
+  const int nkb = (kend + BN - 1) / BN;
+  const int wave_kend = wave_active ? qs + min(q0 + 32, TQs) - 1 : 0;
+  const int wave_q0abs = qs + q0;
+  int qabs[2];
+  qabs[0] = qs + q0 + li;
+  qabs[1] = qs + q0 + 16 + li;
+
+  const float c2 = p.scale * kLog2e;
+  float m_run[2] = {kNegInf, kNegInf};
+  float l_run[2] = {0.f, 0.f};
+  f32x4 oacc[DT][2];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) oacc[dt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  Chunk kreg[KCT];
+  Chunk vreg[VIT_T][4];
+
+  auto load_block = [&](int kb) {
+    const int j0 = kb * BN;
+#pragma unroll
+    for (int c = 0; c < KCT; ++c) {
+      const int idx = tid + c * NTH;
+      const int row = idx / CPR, cc = idx % CPR;
+      const int j = j0 + row;
+      const bool ok = idx < KCH && j < TKs && cc * EPC < D;
+      kreg[c] = ok ? load_chunk(kbase + int64_t(j) * p.k_sr + cc * EPC) : zero_chunk();
+    }
+#pragma unroll
+    for (int c = 0; c < VIT_T; ++c) {
+      const int it = tid + c * NTH;
+      const int kq = it % (BN / 4), cc = it / (BN / 4);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = j0 + 4 * kq + r;
+        const bool ok = it < VIT && j < TKs && cc * EPC < D;
+        vreg[c][r] = ok ? load_chunk(vbase + int64_t(j) * p.v_sr + cc * EPC) : zero_chunk();
+      }
+    }
+  };
+
+  auto store_block = [&]() {
+#pragma unroll
+    for (int c = 0; c < KCT; ++c) {
+      const int idx = tid + c * NTH;
+      if (idx < KCH) {
+        const int row = idx / CPR, cc = idx % CPR;
+        store_chunk(&Ks[row * KLD + cc * EPC], kreg[c]);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < VIT_T; ++c) {
+      const int it = tid + c * NTH;
+      if (it < VIT) {
+        const int kq = it % (BN / 4), cc = it / (BN / 4);
+        if constexpr (sizeof(T) == 2) {
+          // 8 head-dim rows x 4 keys: rows cc*8 + e, columns 4kq .. 4kq+3
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int w = e >> 1, sh = (e & 1) * 16;
+            const uint32_t a0 = (vreg[c][0].w[w] >> sh) & 0xffffu;
+            const uint32_t a1 = (vreg[c][1].w[w] >> sh) & 0xffffu;
+            const uint32_t a2 = (vreg[c][2].w[w] >> sh) & 0xffffu;
+            const uint32_t a3 = (vreg[c][3].w[w] >> sh) & 0xffffu;
+            uint2 v;
+            v.x = a0 | (a1 << 16);
+            v.y = a2 | (a3 << 16);
+            *reinterpret_cast<uint2*>(&Vt[(cc * 8 + e) * VLD + 4 * kq]) = v;
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            uint4 v;
+            v.x = vreg[c][0].w[e];
+            v.y = vreg[c][1].w[e];
+            v.z = vreg[c][2].w[e];
+            v.w = vreg[c][3].w[e];
+            *reinterpret_cast<uint4*>(&Vt[(cc * 4 + e) * VLD + 4 * kq]) = v;
+          }
+        }
+      }
+    }
+  };
+
+  if (nkb > 0) load_block(0);
+  for (int kb = 0; kb < nkb; ++kb) {
+    __syncthreads();
+    store_block();
+    __syncthreads();
+    if (kb + 1 < nkb) load_block(kb + 1);
+
+    const int j0 = kb * BN;
+    if (!wave_active || j0 >= wave_kend) continue;  // nothing in this block is in the wave's past
+    const bool masked = j0 + BN > wave_q0abs;
+
+    // S^T = K Q^T for NT key tiles x 2 query tiles
+    f32x4 sacc[NT][2];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) sacc[t][s] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const Frag kf = E::load8(&Ks[(16 * t + li) * KLD + 32 * ks + 8 * lg]);
+#pragma unroll
+        for (int s = 0; s < 2; ++s) sacc[t][s] = E::mma(kf, qf[s][ks], sacc[t][s]);
+      }
+    }
+
+    // exchange scores in log2 units and the block max per query
+    float bmax[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      float mx = kNegInf;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float u2 = sacc[t][s][r] * c2;
+          float e = u2 * frcp(1.0f + fexp2(-u2));
+          if (masked) {
+            const int j = j0 + 16 * t + 4 * lg + r;
+            if (j >= qabs[s]) e = kNegInf;
+          }
+          sacc[t][s][r] = e;
+          mx = fmaxf(mx, e);
+        }
+      }
+      mx = fmaxf(mx, wave_xor(mx, 16));
+      mx = fmaxf(mx, wave_xor(mx, 32));
+      bmax[s] = mx;
+    }
+    const bool need = (bmax[0] > m_run[0] + kRescale) || (bmax[1] > m_run[1] + kRescale);
+    if (__ballot(need) != 0ull) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const float mn = bmax[s] > m_run[s] + kRescale ? bmax[s] : m_run[s];
+        const float alpha = fexp2(m_run[s] - (mn == kNegInf ? 0.f : mn));
+        l_run[s] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) oacc[dt][s] *= alpha;
+        m_run[s] = mn;
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const float ms = m_run[s] == kNegInf ? 0.f : m_run[s];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float pr = fexp2(sacc[t][s][r] - ms);
+          l_run[s] += pr;
+          sacc[t][s][r] = pr;
+        }
+      }
+    }
+
+    // O^T += V^T P^T, 32 keys per step
+#pragma unroll
+    for (int kk = 0; kk < NT / 2; ++kk) {
+      Frag pf[2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        float pv[8];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          pv[r] = sacc[2 * kk][s][r];
+          pv[4 + r] = sacc[2 * kk + 1][s][r];
+        }
+        pf[s] = E::from_f32(pv);
+      }
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const T* vrow = &Vt[(16 * dt + li) * VLD + 32 * kk + 4 * lg];
+        const Frag vf = E::load4x2(vrow, vrow + 16);
+#pragma unroll
+        for (int s = 0; s < 2; ++s) oacc[dt][s] = E::mma(vf, pf[s], oacc[dt][s]);
+      }
+    }
+  }
+
+  if (!wave_active) return;
+
+  // ---- epilogue ----
+  const float lam = *p.lam;
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    float lt = l_run[s];
+    lt += wave_xor(lt, 16);
+    lt += wave_xor(lt, 32);
+    const int qi = q0 + 16 * s + li;
+    const bool qv = qi < TQs;
+    const int qa = qs + qi;
+    const bool has = lt > 0.f;
+    const float lse = has ? (m_run[s] + __log2f(lt)) * kLn2 : kNegInf;
+    const float inv_l = has ? 1.0f / lt : 0.f;
+    // Self score U_ii from the query's own key row
+    float ud = 0.f;
+    if (qv) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int d0 = 32 * ks + 8 * lg;
+        if (d0 < D) {
+          const Frag kr = E::load8(kbase + int64_t(qa) * p.k_sr + d0);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            float a, b;
+            if constexpr (sizeof(T) == 2) {
+              a = (float)qf[s][ks].v[j];
+              b = (float)kr.v[j];
+            } else {
+              a = qf[s][ks].v[j];
+              b = kr.v[j];
+            }
+            ud = fmaf(a, b, ud);
+          }
+        }
+      }
+    }
+    ud += wave_xor(ud, 16);
+    ud += wave_xor(ud, 32);
+    const float sself = sigmoid_acc(ud * p.scale * p.tau_inv);
+    const float gate = has ? sigmoid_acc(lse - lam * logf((float)qa + 1.0f) - sself) : 0.f;
+    if (!qv) continue;
+    const T* irow = vbase + int64_t(qa) * p.v_sr;
+    T* yrow = ybase + int64_t(qi) * p.y_sr;
+    float* brow = p.ibar + (soff + qi) * int64_t(D);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const int d0 = 16 * dt + 4 * lg;
+      if (d0 >= D) continue;
+      float ib[4], yv[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        ib[r] = oacc[dt][s][r] * inv_l;
+        yv[r] = (1.0f - gate) * E::to_f(irow[d0 + r]) + gate * ib[r];
+      }
+      if constexpr (sizeof(T) == 2) {
+        uint2 pk;
+        pk.x = uint32_t(f2bf(yv[0])) | (uint32_t(f2bf(yv[1])) << 16);
+        pk.y = uint32_t(f2bf(yv[2])) | (uint32_t(f2bf(yv[3])) << 16);
+        *reinterpret_cast<uint2*>(yrow + d0) = pk;
+      } else {
+        *reinterpret_cast<float4*>(yrow + d0) = make_float4(yv[0], yv[1], yv[2], yv[3]);
+      }
+      *reinterpret_cast<float4*>(brow + d0) = make_float4(ib[0], ib[1], ib[2], ib[3]);
+    }
+    if (lg == 0) {
+      p.lse[soff + qi] = lse;
+      p.g[soff + qi] = gate;
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// host launcher
+// ------------------------------------------------------------------------------------------------
+template <typename T, int DP, int BN, int NW>
+static void launch_fwd_t(const FwdParams& fp, int nblocks, hipStream_t stream) {
+  hipLaunchKernelGGL((relation_fwd_kernel<T, DP, BN, NW>), dim3(nblocks), dim3(NW * 64), 0, stream, fp);
+}
+
+template <typename T, int BN, int NW>
+static void launch_fwd_dp(const FwdParams& fp, int DP, int nblocks, hipStream_t stream) {
+  switch (DP) {
+    case 32: launch_fwd_t<T, 32, BN, NW>(fp, nblocks, stream); break;
+    case 64: launch_fwd_t<T, 64, BN, NW>(fp, nblocks, stream); break;
+    case 96: launch_fwd_t<T, 96, BN, NW>(fp, nblocks, stream); break;
+    default: launch_fwd_t<T, 128, BN, NW>(fp, nblocks, stream); break;
+  }
+}
+
+static bool view_ok(const mote_view& v) { return v.data != nullptr; }
+
+int launch_fwd(const mote_relation_fwd_args* a, hipStream_t stream) {
+  if (!a) return set_error(MOTE_ERR_ARGUMENT, "relation_fwd: null args");
+  if (a->dtype != MOTE_F32 && a->dtype != MOTE_BF16) return set_error(MOTE_ERR_ARGUMENT, "relation_fwd: bad dtype %d", a->dtype);
+  if (a->D <= 0 || a->D > 128 || a->D % 8 != 0)
+    return set_error(MOTE_ERR_SHAPE, "relation_fwd: head dim %d unsupported (need 8 <= D <= 128, D %% 8 == 0)", a->D);
+  if (a->B <= 0 || a->H <= 0 || a->TQ < 0) return set_error(MOTE_ERR_SHAPE, "relation_fwd: bad sizes B=%d H=%d TQ=%d", a->B, a->H, a->TQ);
+  if (a->cu_seqlens) {
+    if (a->q_start != 0) return set_error(MOTE_ERR_SHAPE, "relation_fwd: varlen mode needs q_start == 0");
+    if (a->TK != a->TQ) return set_error(MOTE_ERR_SHAPE, "relation_fwd: varlen mode needs TK == TQ (the longest sequence)");
+  } else if (a->TK != a->q_start + a->TQ) {
+    return set_error(MOTE_ERR_SHAPE, "relation_fwd: keys must cover the cached prefix plus the new rows (TK=%d, q_start=%d, TQ=%d)",
+                     a->TK, a->q_start, a->TQ);
+  }
+  if (a->TQ == 0) return MOTE_OK;  // empty outputs: nothing to launch (their pointers may be null)
+  if (!view_ok(a->p1) || !view_ok(a->p2) || !view_ok(a->info) || !view_ok(a->y) || !a->ibar || !a->lse || !a->g || !a->lam)
+    return set_error(MOTE_ERR_ARGUMENT, "relation_fwd: null tensor pointer");
+  FwdParams fp;
+  fp.p1 = a->p1.data;
+  fp.p2 = a->p2.data;
+  fp.info = a->info.data;
+  fp.y = a->y.data;
+  fp.ibar = a->ibar;
+  fp.lse = a->lse;
+  fp.g = a->g;
+  fp.lam = a->lam;
+  fp.cu = a->cu_seqlens;
+  fp.q_sb = a->p1.stride_b; fp.q_sh = a->p1.stride_h; fp.q_sr = a->p1.stride_r;
+  fp.k_sb = a->p2.stride_b; fp.k_sh = a->p2.stride_h; fp.k_sr = a->p2.stride_r;
+  fp.v_sb = a->info.stride_b; fp.v_sh = a->info.stride_h; fp.v_sr = a->info.stride_r;
+  fp.y_sb = a->y.stride_b; fp.y_sh = a->y.stride_h; fp.y_sr = a->y.stride_r;
+  fp.nseq = a->B;
+  fp.H = a->H;
+  fp.TQ = a->TQ;
+  fp.TK = a->TK;
+  fp.D = a->D;
+  fp.q_start = a->q_start;
+  fp.total_rows = a->total_rows;
+  fp.scale = 1.0f / sqrtf((float)a->D);
+  fp.tau_inv = 1.0f / a->tau_s;
+  const int DP = padded_dim(a->D);
+  // Four waves (128 query rows) per workgroup when that still gives two workgroups per CU;
+  // otherwise two waves (64 rows) to spread short problems over more CUs.
+  const int64_t units = int64_t(a->B) * a->H;
+  const int nqb4 = (a->TQ + 127) / 128;
+  const bool wide = units * nqb4 >= 512;
+  if (a->dtype == MOTE_BF16) {
+    if (wide) {
+      fp.nqb = nqb4;
+      launch_fwd_dp<bf16_t, 64, 4>(fp, DP, int(units * fp.nqb), stream);
+    } else {
+      fp.nqb = (a->TQ + 63) / 64;
+      launch_fwd_dp<bf16_t, 64, 2>(fp, DP, int(units * fp.nqb), stream);
+    }
+  } else {
+    if (wide) {
+      fp.nqb = nqb4;
+      launch_fwd_dp<float, 32, 4>(fp, DP, int(units * fp.nqb), stream);
+    } else {
+      fp.nqb = (a->TQ + 63) / 64;
+      launch_fwd_dp<float, 32, 2>(fp, DP, int(units * fp.nqb), stream);
+    }
+  }
+  return check_launch("relation_fwd");
+}
+
+}  // namespace mote

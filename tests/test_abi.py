@@ -1,0 +1,58 @@
+"""The C ABI: the library loads on a host without a GPU and exports every symbol its header
+declares (no compute calls here)."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "mote_relation.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?(?:int|size_t|char\s*\*|const char\s*\*)\s*\*?\s*(mote_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_entry_points():
+    names = _declared()
+    for n in ["mote_relation_fwd", "mote_relation_bwd", "mote_relation_bwd_workspace", "mote_relation_decode",
+              "mote_relation_decode_workspace", "mote_rope_givens_fwd", "mote_rope_givens_bwd",
+              "mote_rope_givens_bwd_workspace", "mote_last_error", "mote_version"]:
+        assert n in names, n
+
+
+def test_library_exports_every_declared_symbol():
+    from mote_amd import _lib
+
+    if not _lib.available():
+        pytest.skip("libmote_relation.so not built")
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [n for n in _declared() if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(_lib.EXPORTS) == set(_declared())
+    assert b"gfx950" in _lib.lib().mote_version()
+
+
+def test_argument_errors_are_reported_without_a_gpu():
+    """Validation happens before any launch: a bad dtype comes back as a status and a message."""
+    from mote_amd import _lib
+
+    if not _lib.available():
+        pytest.skip("libmote_relation.so not built")
+    a = _lib.FwdArgs()
+    a.dtype = 7
+    rc = _lib.lib().mote_relation_fwd(a, None)
+    assert rc == 1
+    assert b"dtype" in _lib.lib().mote_last_error()
+    a.dtype = _lib.MOTE_BF16
+    a.p1.data = a.p2.data = a.info.data = a.y.data = 16
+    a.ibar = a.lse = a.g = a.lam = 16
+    a.B, a.H, a.TQ, a.TK, a.D = 1, 1, 4, 4, 100
+    assert _lib.lib().mote_relation_fwd(a, None) == 2
+    assert b"head dim" in _lib.lib().mote_last_error()
