@@ -170,6 +170,18 @@ def relation_backward(p1, p2, info, lam, dy, tau_s: float = 2.0, q_start: int = 
     return dp1, dp2, dinfo, lam_dlam
 
 
+def relation_dlam_terms(p1, p2, info, lam, dy, tau_s: float = 2.0, q_start: int = 0, dtype=torch.float64):
+    """The summands of dlam = -sum_i dA_i ln(i+1) (flash_relation.py:12), [B,H,TQ]. Their absolute
+    sum is the natural scale of dlam, which cancels heavily across rows."""
+    TQ = p1.shape[2]
+    q, k, v, dyf = p1.to(dtype), p2.to(dtype), info.to(dtype), dy.to(dtype)
+    _, g, ibar, _ = relation_online(q, k, v, lam, tau_s, q_start, dtype=dtype)
+    qpos = torch.arange(q_start, q_start + TQ)
+    iself = v[:, :, q_start:]
+    da = (dyf * (ibar - iself)).sum(-1) * g * (1.0 - g)
+    return -da * torch.log((qpos + 1).to(dtype))
+
+
 def relation_grads_autograd(p1, p2, info, lam, dy, tau_s: float = 2.0, q_start: int = 0, dtype=torch.float32):
     """Gradients of sum(Y * dy) through `relation_reference` by autograd (the way the reference's
     kernel tests obtain their ground truth, tests/test_flash_relation.py:28-39)."""

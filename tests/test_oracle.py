@@ -323,3 +323,12 @@ def test_planted_core_mistakes_are_caught(plant, pins):
 def test_planted_rope_and_givens_mistakes_are_caught():
     assert not pin_rope_relative(_plant="rope_sign")
     assert not pin_givens(_plant="givens_sign")
+
+
+def test_dlam_terms_sum_to_dlam():
+    p1, p2, info = _inputs(2, 2, 23, 4, 8, seed=13)
+    lam = torch.tensor(0.4, dtype=torch.float64)
+    dy = torch.randn(2, 2, 23, 8, dtype=torch.float64, generator=torch.Generator().manual_seed(14))
+    terms = O.relation_dlam_terms(p1, p2, info, lam, dy, 2.0, 4)
+    dlam = O.relation_grads_autograd(p1, p2, info, lam, dy, 2.0, 4, dtype=torch.float64)[3]
+    assert abs(float(terms.sum()) - float(dlam)) < 1e-12
