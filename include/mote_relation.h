@@ -87,7 +87,15 @@ int mote_relation_fwd(const mote_relation_fwd_args* args, void* stream);
  * dp2 and dinfo [B,H,TK,D] in `dtype` (any strides) and dlam (one fp32, overwritten).
  * The workspace is caller-allocated device memory of at least mote_relation_bwd_workspace()
  * bytes; its contents on entry do not matter.
+ * `stages` selects which of the three launches run (MOTE_BWD_ROWS: per-row terms and operand
+ * copies; MOTE_BWD_KEYS: the key-block kernel(s); MOTE_BWD_FINISH: dp1 and dlam outputs); 0 runs
+ * all three. A caller that splits them (to time or overlap them) issues them in that order on one
+ * stream with one workspace.
  * ------------------------------------------------------------------------------------------------ */
+#define MOTE_BWD_ROWS 1
+#define MOTE_BWD_KEYS 2
+#define MOTE_BWD_FINISH 4
+
 typedef struct mote_relation_bwd_args {
   int dtype;
   int B, H, TQ, TK, D, q_start;
@@ -101,6 +109,7 @@ typedef struct mote_relation_bwd_args {
   float* dlam;
   void* workspace;
   size_t workspace_bytes;
+  int stages;
 } mote_relation_bwd_args;
 
 size_t mote_relation_bwd_workspace(const mote_relation_bwd_args* args);

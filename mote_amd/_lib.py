@@ -20,6 +20,7 @@ MOTE_OK = 0
 MOTE_F32 = 0
 MOTE_BF16 = 1
 MOTE_DECODE_ADVANCE = 1
+MOTE_BWD_ROWS, MOTE_BWD_KEYS, MOTE_BWD_FINISH = 1, 2, 4
 
 _DTYPES = {torch.float32: MOTE_F32, torch.bfloat16: MOTE_BF16}
 
@@ -46,6 +47,7 @@ class BwdArgs(C.Structure):
         ("ibar", C.c_void_p), ("lse", C.c_void_p), ("g", C.c_void_p),
         ("dp1", View), ("dp2", View), ("dinfo", View),
         ("dlam", C.c_void_p), ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
+        ("stages", C.c_int),
     ]
 
 

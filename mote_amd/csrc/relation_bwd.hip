@@ -730,23 +730,30 @@ static WsLayout ws_layout(const mote_relation_bwd_args* a) {
 size_t bwd_workspace_bytes(const mote_relation_bwd_args* a) { return ws_layout(a).total; }
 
 template <typename T, int DP>
-static void launch_bwd_t(const BwdParams& p, bool deterministic, hipStream_t stream) {
+static void launch_bwd_t(const BwdParams& p, bool deterministic, int stages, hipStream_t stream) {
   const int BH = p.B * p.H;
-  hipLaunchKernelGGL((bwd_rows_kernel<T, DP>), dim3(p.TQp / kRowBlock, BH), dim3(256), 0, stream, p);
+  if (stages & MOTE_BWD_ROWS)
+    hipLaunchKernelGGL((bwd_rows_kernel<T, DP>), dim3(p.TQp / kRowBlock, BH), dim3(256), 0, stream, p);
   const int nkb = (p.TK + 63) / 64;
   constexpr int BM = sizeof(T) == 2 ? 64 : 32;
-  if (!deterministic) {
-    hipLaunchKernelGGL((bwd_keys_kernel<T, DP, BM, true>), dim3(nkb * BH), dim3(256), 0, stream, p);
-    const int64_t n = int64_t(BH) * p.TQ * p.D;
-    const int blocks = int((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
-    hipLaunchKernelGGL((bwd_dp1_out_kernel<T>), dim3(blocks), dim3(256), 0, stream, p);
-  } else {
-    hipLaunchKernelGGL((bwd_keys_kernel<T, DP, BM, false>), dim3(nkb * BH), dim3(256), 0, stream, p);
-    constexpr int BNQ = sizeof(T) == 2 ? 64 : 32;
-    const int nqb = (p.TQ + 63) / 64;
-    hipLaunchKernelGGL((bwd_queries_kernel<T, DP, BNQ>), dim3(nqb * BH), dim3(128), 0, stream, p);
+  if (stages & MOTE_BWD_KEYS) {
+    if (!deterministic) {
+      hipLaunchKernelGGL((bwd_keys_kernel<T, DP, BM, true>), dim3(nkb * BH), dim3(256), 0, stream, p);
+    } else {
+      hipLaunchKernelGGL((bwd_keys_kernel<T, DP, BM, false>), dim3(nkb * BH), dim3(256), 0, stream, p);
+      constexpr int BNQ = sizeof(T) == 2 ? 64 : 32;
+      const int nqb = (p.TQ + 63) / 64;
+      hipLaunchKernelGGL((bwd_queries_kernel<T, DP, BNQ>), dim3(nqb * BH), dim3(128), 0, stream, p);
+    }
   }
-  hipLaunchKernelGGL(bwd_dlam_kernel, dim3(1), dim3(256), 0, stream, p.dlam_part, BH * (p.TQp / kRowBlock), p.dlam);
+  if (stages & MOTE_BWD_FINISH) {
+    if (!deterministic) {
+      const int64_t n = int64_t(BH) * p.TQ * p.D;
+      const int blocks = int((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
+      hipLaunchKernelGGL((bwd_dp1_out_kernel<T>), dim3(blocks), dim3(256), 0, stream, p);
+    }
+    hipLaunchKernelGGL(bwd_dlam_kernel, dim3(1), dim3(256), 0, stream, p.dlam_part, BH * (p.TQp / kRowBlock), p.dlam);
+  }
 }
 
 int launch_bwd(const mote_relation_bwd_args* a, hipStream_t stream) {
@@ -797,19 +804,20 @@ int launch_bwd(const mote_relation_bwd_args* a, hipStream_t stream) {
   p.tau_inv = 1.0f / a->tau_s;
   const int DP = padded_dim(a->D);
   const bool det = a->deterministic != 0;
+  const int st = a->stages ? a->stages : (MOTE_BWD_ROWS | MOTE_BWD_KEYS | MOTE_BWD_FINISH);
   if (a->dtype == MOTE_BF16) {
     switch (DP) {
-      case 32: launch_bwd_t<bf16_t, 32>(p, det, stream); break;
-      case 64: launch_bwd_t<bf16_t, 64>(p, det, stream); break;
-      case 96: launch_bwd_t<bf16_t, 96>(p, det, stream); break;
-      default: launch_bwd_t<bf16_t, 128>(p, det, stream); break;
+      case 32: launch_bwd_t<bf16_t, 32>(p, det, st, stream); break;
+      case 64: launch_bwd_t<bf16_t, 64>(p, det, st, stream); break;
+      case 96: launch_bwd_t<bf16_t, 96>(p, det, st, stream); break;
+      default: launch_bwd_t<bf16_t, 128>(p, det, st, stream); break;
     }
   } else {
     switch (DP) {
-      case 32: launch_bwd_t<float, 32>(p, det, stream); break;
-      case 64: launch_bwd_t<float, 64>(p, det, stream); break;
-      case 96: launch_bwd_t<float, 96>(p, det, stream); break;
-      default: launch_bwd_t<float, 128>(p, det, stream); break;
+      case 32: launch_bwd_t<float, 32>(p, det, st, stream); break;
+      case 64: launch_bwd_t<float, 64>(p, det, st, stream); break;
+      case 96: launch_bwd_t<float, 96>(p, det, st, stream); break;
+      default: launch_bwd_t<float, 128>(p, det, st, stream); break;
     }
   }
   return check_launch("relation_bwd");

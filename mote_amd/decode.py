@@ -1,0 +1,118 @@
+"""The one-chunk Relation decode step on MI355X.
+
+`relation_decode` is the core of GraphDecoder._relation_step (mote/infer/graph.py:158-186) as one
+HIP launch: RoPE at the device position S, Givens, the cast to the cache dtype, the append of the
+new P2 / I~ row at S, and the softmax read of rows [0, S]. `RelationDecodeStep` wraps a FullRelation
+layer and its arena rows the way the graph decoder does (projections before, `_out` after) with
+static buffers, so a whole step can be captured in a HIP graph (torch.cuda.CUDAGraph) and replayed:
+S stays on the device and, with `advance=True`, the kernel itself moves it forward.
+
+Batch B > 1 runs B independent sequences in one launch (the reference decodes batch 1).
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib as L
+from .arena import RelationArena
+
+
+def decode_workspace(B: int, H: int, D: int, capacity: int, device, dtype=torch.bfloat16) -> torch.Tensor:
+    """A zero-filled workspace for `relation_decode` (zeroed once; every call leaves it ready for
+    the next). Calls that share one must not overlap."""
+    a = L.DecodeArgs()
+    a.dtype, a.B, a.H, a.D, a.capacity = L.dtype_code(torch.empty(0, dtype=dtype)), B, H, D, capacity
+    n = int(L.lib().mote_relation_decode_workspace(a))
+    return torch.zeros(n, device=device, dtype=torch.uint8)
+
+
+def relation_decode(p1: torch.Tensor, p2: torch.Tensor, info: torch.Tensor, S: torch.Tensor, cache_p2: torch.Tensor,
+                    cache_info: torch.Tensor, lam: torch.Tensor, tau_s: float = 2.0,
+                    inv_freq: Optional[torch.Tensor] = None, theta: Optional[torch.Tensor] = None, layer_idx: int = 0,
+                    advance: bool = False, workspace: Optional[torch.Tensor] = None, y: Optional[torch.Tensor] = None,
+                    g: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """One decode step for B sequences.
+
+    p1, p2, info: raw projections of the new chunk, [B, H, dh] (head stride dh, any batch stride),
+        in the cache dtype; RoPE (inv_freq) and Givens (theta, pairing by layer_idx parity) are
+        applied on the device.
+    S: int64 [B] device positions; row S[b] of the caches receives the new P2 / I~ row.
+    cache_p2, cache_info: [B, H, capacity, dh] views (RelationArena.p2(layer) / .info(layer)).
+    Returns (y [B, H, dh] in the cache dtype, g [B, H] fp32 exchange mass = 1 - F_SS).
+    """
+    B, H, D = p1.shape
+    cap = cache_p2.shape[2]
+    for t in (p1, p2, info):
+        if t.stride(-1) != 1 or t.stride(1) != D or t.stride(0) != p1.stride(0):
+            raise ValueError("p1/p2/info must be [B, H, dh] with head stride dh and one batch stride")
+        if t.dtype != cache_p2.dtype:
+            raise TypeError("decode inputs must be in the cache dtype")
+    if not p1.is_cuda:
+        raise RuntimeError("relation_decode needs the HIP library and an MI355X")
+    if workspace is None:
+        workspace = decode_workspace(B, H, D, cap, p1.device, p1.dtype)
+    if y is None:
+        y = torch.empty(B, H, D, device=p1.device, dtype=p1.dtype)
+    if g is None:
+        g = torch.empty(B, H, device=p1.device, dtype=torch.float32)
+    a = L.DecodeArgs()
+    a.dtype = L.dtype_code(p1)
+    a.B, a.H, a.D, a.capacity = B, H, D, cap
+    a.layer_parity, a.flags, a.tau_s = int(layer_idx) % 2, L.MOTE_DECODE_ADVANCE if advance else 0, float(tau_s)
+    a.lam = lam.data_ptr()
+    a.inv_freq, a.theta = L.ptr(inv_freq), L.ptr(theta)
+    a.S = S.data_ptr()
+    a.p1, a.p2, a.info, a.in_sb = p1.data_ptr(), p2.data_ptr(), info.data_ptr(), p1.stride(0)
+    a.cache_p2, a.cache_info = L.view(cache_p2), L.view(cache_info)
+    a.y, a.y_sb, a.g = y.data_ptr(), y.stride(0), g.data_ptr()
+    a.workspace, a.workspace_bytes = workspace.data_ptr(), workspace.numel()
+    L.check(L.lib().mote_relation_decode(a, L.stream_of(p1)), "mote_relation_decode")
+    return y, g
+
+
+class RelationDecodeStep:
+    """GraphDecoder._relation_step (graph.py:151-187) for one FullRelation layer over its arena rows.
+
+    Holds the static tensors a captured graph needs (fp32 lam/theta/inv_freq copies refreshed by
+    `sync_params()`, the workspace, outputs). `__call__(x [B,1,D], S)` returns (out [B,1,D],
+    xm [B] = mean over heads of the exchange mass, graph.py:186)."""
+
+    def __init__(self, mixer, arena: RelationArena, layer: int):
+        self.mixer, self.arena, self.layer = mixer, arena, layer
+        dev = arena.device
+        B, H, D = arena.batch, mixer.n_heads, mixer.d_head
+        self.B = B
+        self.workspace = decode_workspace(B, H, D, arena.capacity, dev, arena.dtype)
+        self.y = torch.empty(B, H, D, device=dev, dtype=arena.dtype)
+        self.g = torch.empty(B, H, device=dev, dtype=torch.float32)
+        self.lam = torch.empty((), device=dev, dtype=torch.float32)
+        self.theta = torch.empty(max(H // 2, 1), device=dev, dtype=torch.float32) if mixer.use_givens else None
+        self.inv_freq = mixer.inv_freq.to(device=dev, dtype=torch.float32).clone() if mixer.use_rope else None
+        self.sync_params()
+
+    @torch.no_grad()
+    def sync_params(self) -> None:
+        self.lam.copy_(self.mixer.lam.detach().float())
+        if self.theta is not None:
+            self.theta.copy_(self.mixer.theta.detach().float())
+
+    @torch.no_grad()
+    def __call__(self, x: torch.Tensor, S: torch.Tensor, advance: bool = False):
+        m = self.mixer
+        B, T, Dm = x.shape
+        H, dh = m.n_heads, m.d_head
+        w = torch.cat([m.w1.weight, m.w2.weight, m.wi.weight], dim=0)
+        qkv = F.linear(x, w).to(self.arena.dtype).view(B, 3, H, dh)
+        if m.qk_norm:
+            q = m.p1_norm(qkv[:, 0])
+            k = m.p2_norm(qkv[:, 1])
+            qkv = torch.stack([q, k, qkv[:, 2]], dim=1)
+        relation_decode(qkv[:, 0], qkv[:, 1], qkv[:, 2], S, self.arena.p2(self.layer), self.arena.info(self.layer),
+                        self.lam, m.tau_s, self.inv_freq, self.theta, m.layer_idx, advance, self.workspace,
+                        self.y, self.g)
+        y = self.y.to(x.dtype).view(B, H, 1, dh)
+        return m._out(y, x), self.g.mean(-1)

@@ -1,0 +1,259 @@
+"""FullRelation on MI355X — the Relation token mixer behind mote/model/relation.py's interface.
+
+Same constructor, parameter names and construction order (relation.py:97-157), same forward
+signature and return convention (relation.py:184-268). What runs underneath:
+
+    qkv = x [w1; w2; wi]^T                      one GEMM (hipBLASLt) instead of three
+    p1, p2, I~ = mote::rope_givens(qkv)          HIP: RoPE on p1/p2, Givens on I~, head split
+    Y, g = mote::relation_fwd(p1, P2, I~)        HIP: the fused Relation core (any T, decode too)
+    out = wo(Y [* sigmoid(wg x)])                 Y is token-major already, so no transpose copy
+
+There is no materialized path: `USE_FLASH = False` raises, and so does a CPU tensor. The
+materialized restatement lives in the test oracle.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _lib as L
+from .arena import ArenaLayer
+from .flash_relation import HAS_HIP, HAS_TRITON, flash_relation  # noqa: F401  (re-exported names)
+
+RelationCache = Tuple[torch.Tensor, torch.Tensor]  # (P2 [B,H,S,dh], I~ [B,H,S,dh]) or an ArenaLayer
+USE_FLASH = True   # the HIP path; the reference's materialized alternative is not part of this package
+FLASH_MIN_T = 16   # kept for callers that read it; the HIP kernels serve every T, T = 1 included
+
+
+def rope_inv_freq(dim: int, theta: float, device=None) -> torch.Tensor:
+    """fp32 [dim/2] table 1 / theta^(2k/dim), computed with the same fp32 ops as relation.py:39 so
+    the kernels' angles float(pos) * inv_freq[k] round exactly like the reference's tables. Built on
+    the CPU and then moved: a last-ulp difference of the device's pow would grow by the position
+    (one ulp of the angle at pos ~ 1000 is ~6e-5 rad)."""
+    k2 = torch.arange(0, dim, 2, dtype=torch.float32)
+    return (1.0 / (theta ** (k2 / dim))).to(device)
+
+
+# ---- mote::rope_givens ---------------------------------------------------------------------------
+def _heads_out(B, T, H, D, like, dtype):
+    return torch.empty(B, T, H, D, device=like.device, dtype=dtype).transpose(1, 2)
+
+
+@torch.library.custom_op("mote::rope_givens", mutates_args=())
+def _rope_givens(qkv: torch.Tensor, inv_freq: Optional[torch.Tensor], theta: Optional[torch.Tensor], n_heads: int,
+                 parity: int, pos0: int) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    B, T, D3 = qkv.shape
+    H = n_heads
+    D = D3 // (3 * H)
+    if not qkv.is_cuda:
+        raise RuntimeError("mote::rope_givens needs the HIP library and an MI355X")
+    qkv = qkv if qkv.stride(-1) == 1 else qkv.contiguous()
+    p1 = _heads_out(B, T, H, D, qkv, qkv.dtype)
+    p2 = _heads_out(B, T, H, D, qkv, qkv.dtype)
+    info = _heads_out(B, T, H, D, qkv, qkv.dtype)
+    a = L.RopeArgs()
+    a.dtype = L.dtype_code(qkv)
+    a.B, a.T, a.H, a.D, a.pos0, a.layer_parity = B, T, H, D, int(pos0), int(parity)
+    inv = None if inv_freq is None else inv_freq.to(device=qkv.device, dtype=torch.float32).contiguous()
+    th = None if theta is None else theta.detach().to(device=qkv.device, dtype=torch.float32).contiguous()
+    a.inv_freq, a.theta = L.ptr(inv), L.ptr(th)
+    a.qkv, a.qkv_sb, a.qkv_sr = qkv.data_ptr(), qkv.stride(0), qkv.stride(1)
+    a.p1, a.p2, a.info = L.view(p1), L.view(p2), L.view(info)
+    L.check(L.lib().mote_rope_givens_fwd(a, L.stream_of(qkv)), "mote_rope_givens_fwd")
+    return p1, p2, info
+
+
+@_rope_givens.register_fake
+def _rope_givens_fake(qkv, inv_freq, theta, n_heads, parity, pos0):
+    B, T, D3 = qkv.shape
+    H = n_heads
+    D = D3 // (3 * H)
+    mk = lambda: qkv.new_empty((B, T, H, D)).transpose(1, 2)
+    return mk(), mk(), mk()
+
+
+@torch.library.custom_op("mote::rope_givens_bwd", mutates_args=())
+def _rope_givens_bwd(dp1: torch.Tensor, dp2: torch.Tensor, dinfo: torch.Tensor, qkv: torch.Tensor,
+                     inv_freq: Optional[torch.Tensor], theta: Optional[torch.Tensor], n_heads: int, parity: int,
+                     pos0: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    B, T, D3 = qkv.shape
+    H = n_heads
+    D = D3 // (3 * H)
+    qkv = qkv if qkv.stride(-1) == 1 else qkv.contiguous()
+    dp1, dp2, dinfo = (t.to(qkv.dtype) if t.stride(-1) == 1 else t.to(qkv.dtype).contiguous() for t in (dp1, dp2, dinfo))
+    dqkv = torch.empty(B, T, D3, device=qkv.device, dtype=qkv.dtype)
+    dtheta = torch.zeros(max(H // 2, 1), device=qkv.device, dtype=torch.float32)
+    a = L.RopeBwdArgs()
+    a.dtype = L.dtype_code(qkv)
+    a.B, a.T, a.H, a.D, a.pos0, a.layer_parity = B, T, H, D, int(pos0), int(parity)
+    inv = None if inv_freq is None else inv_freq.to(device=qkv.device, dtype=torch.float32).contiguous()
+    th = None if theta is None else theta.detach().to(device=qkv.device, dtype=torch.float32).contiguous()
+    a.inv_freq, a.theta = L.ptr(inv), L.ptr(th)
+    a.qkv, a.qkv_sb, a.qkv_sr = qkv.data_ptr(), qkv.stride(0), qkv.stride(1)
+    a.dp1, a.dp2, a.dinfo = L.view(dp1), L.view(dp2), L.view(dinfo)
+    a.dqkv, a.dqkv_sb, a.dqkv_sr = dqkv.data_ptr(), dqkv.stride(0), dqkv.stride(1)
+    a.dtheta = dtheta.data_ptr()
+    nbytes = L.lib().mote_rope_givens_bwd_workspace(a)
+    ws = torch.empty(max(int(nbytes), 16), device=qkv.device, dtype=torch.uint8)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    L.check(L.lib().mote_rope_givens_bwd(a, L.stream_of(qkv)), "mote_rope_givens_bwd")
+    return dqkv, dtheta
+
+
+@_rope_givens_bwd.register_fake
+def _rope_givens_bwd_fake(dp1, dp2, dinfo, qkv, inv_freq, theta, n_heads, parity, pos0):
+    return qkv.new_empty(qkv.shape), qkv.new_empty((max(n_heads // 2, 1),), dtype=torch.float32)
+
+
+def _rg_setup(ctx, inputs, output):
+    qkv, inv_freq, theta, n_heads, parity, pos0 = inputs
+    ctx.save_for_backward(qkv, inv_freq, theta)
+    ctx.has_theta = theta is not None
+    ctx.n_heads, ctx.parity, ctx.pos0 = n_heads, parity, pos0
+
+
+def _rg_backward(ctx, dp1, dp2, dinfo):
+    qkv, inv_freq, theta = ctx.saved_tensors
+    B, T, D3 = qkv.shape
+    H = ctx.n_heads
+    D = D3 // (3 * H)
+    z = lambda: torch.zeros(B, H, T, D, device=qkv.device, dtype=qkv.dtype)
+    dp1 = z() if dp1 is None else dp1
+    dp2 = z() if dp2 is None else dp2
+    dinfo = z() if dinfo is None else dinfo
+    dqkv, dtheta = _rope_givens_bwd(dp1, dp2, dinfo, qkv, inv_freq, theta, H, ctx.parity, ctx.pos0)
+    return dqkv, None, (dtheta[: H // 2] if ctx.has_theta else None), None, None, None
+
+
+_rope_givens.register_autograd(_rg_backward, setup_context=_rg_setup)
+
+
+def rope_givens(qkv: torch.Tensor, n_heads: int, inv_freq: Optional[torch.Tensor], theta: Optional[torch.Tensor],
+                layer_idx: int, pos0: int = 0):
+    """[B, T, 3*H*dh] projections -> (p1, p2, I~) as [B, H, T, dh] views: RoPE at positions
+    pos0.. on p1/p2 (relation.py:211-214), Givens on I~ (relation.py:215). Differentiable in qkv
+    and theta."""
+    return _rope_givens(qkv, inv_freq, theta, int(n_heads), int(layer_idx) % 2, int(pos0))
+
+
+class HeadRMSNorm(nn.Module):
+    """QK-Norm over the head dim with a learnable gain (relation.py:71-94); fp32 math."""
+
+    def __init__(self, dim: int, eps: float = 1e-5, device=None, dtype=None):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(dim, device=device, dtype=dtype))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        xf = x.float()
+        y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
+        return (y * self.weight.float()).to(x.dtype)
+
+
+class FullRelation(nn.Module):
+    def __init__(self, d_model: int, n_heads: int, layer_idx: int, tau_s: float = 2.0, lambda_init: float = 0.5,
+                 rope_theta: float = 10000.0, givens: bool = True, qk_norm: bool = False, out_gate: bool = False,
+                 rope: bool = True, device=None, dtype=None):
+        super().__init__()
+        assert d_model % n_heads == 0, "d_model must be divisible by n_heads"
+        assert n_heads % 2 == 0, "Givens pairing needs an even number of heads"
+        fk = {"device": device, "dtype": dtype}
+        self.d_model, self.n_heads, self.d_head = d_model, n_heads, d_model // n_heads
+        assert self.d_head % 2 == 0, "head dim must be even for RoPE"
+        self.layer_idx = layer_idx
+        self.tau_s = tau_s
+        self.rope_theta = rope_theta
+        self.use_givens = givens
+        self.telemetry: Optional[dict] = None
+        self.qk_norm = qk_norm
+        if qk_norm:
+            self.p1_norm = HeadRMSNorm(self.d_head, **fk)
+            self.p2_norm = HeadRMSNorm(self.d_head, **fk)
+        self.w1 = nn.Linear(d_model, d_model, bias=False, **fk)
+        self.w2 = nn.Linear(d_model, d_model, bias=False, **fk)
+        self.wi = nn.Linear(d_model, d_model, bias=False, **fk)
+        self.wo = nn.Linear(d_model, d_model, bias=False, **fk)
+        self.out_gate = out_gate
+        if out_gate:
+            self.wg = nn.Linear(d_model, d_model, bias=False, **fk)
+        self.use_rope = rope
+        self.lam = nn.Parameter(torch.tensor(float(lambda_init), dtype=torch.float32, device=device))
+        self.lam._no_weight_decay = True
+        if givens:
+            self.theta = nn.Parameter(torch.zeros(n_heads // 2, dtype=torch.float32, device=device))
+            self.theta._no_weight_decay = True
+            if layer_idx % 2 == 0:
+                a = torch.arange(0, n_heads, 2)
+                b = torch.arange(1, n_heads, 2)
+            else:
+                a = torch.arange(1, n_heads, 2)
+                b = (torch.arange(2, n_heads + 1, 2)) % n_heads
+            self.register_buffer("pair_a", a, persistent=False)
+            self.register_buffer("pair_b", b, persistent=False)
+        self.register_buffer("inv_freq", rope_inv_freq(self.d_head, rope_theta, device), persistent=False)
+
+    # ------------------------------------------------------------------------------------------
+    def heads(self, x: torch.Tensor, S: int):
+        """Projections -> (QK-Norm) -> RoPE / Givens: (p1, p2, I~) as [B, H, T, dh] views."""
+        B, T, D = x.shape
+        H, dh = self.n_heads, self.d_head
+        w = torch.cat([self.w1.weight, self.w2.weight, self.wi.weight], dim=0)
+        qkv = F.linear(x, w)
+        if self.qk_norm:
+            q, k, v = qkv.split(D, dim=-1)
+            q = self.p1_norm(q.reshape(B, T, H, dh)).reshape(B, T, D)
+            k = self.p2_norm(k.reshape(B, T, H, dh)).reshape(B, T, D)
+            qkv = torch.cat([q, k, v], dim=-1)
+        inv = self.inv_freq if self.use_rope else None
+        theta = self.theta if self.use_givens else None
+        return rope_givens(qkv, H, inv, theta, self.layer_idx, S)
+
+    def _out(self, y: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+        """[B, H, T, dh] -> [B, T, D] -> optional output gate -> wo (relation.py:176-182)."""
+        B, H, T, dh = y.shape
+        y = y.transpose(1, 2).reshape(B, T, H * dh)
+        if self.out_gate:
+            y = y * torch.sigmoid(self.wg(x))
+        return self.wo(y)
+
+    def forward(self, x: torch.Tensor, cache: Optional[RelationCache] = None, return_cache: bool = False,
+                return_gates: bool = False):
+        """x: [B, T, D]. With a cache, x holds the new T positions appended after S cached ones.
+        Returns out [B, T, D], then (in this order, when asked) the updated cache and the exchange
+        mass g [B, H, T] (relation.py:184-268)."""
+        if not USE_FLASH:
+            raise RuntimeError("mote_amd.relation has only the HIP path (USE_FLASH = False is not supported)")
+        if not x.is_cuda:
+            raise RuntimeError("FullRelation needs the HIP library and an MI355X (x is on the CPU)")
+        B, T, D = x.shape
+        arena = isinstance(cache, ArenaLayer)
+        S = cache.n if arena else (0 if cache is None else cache[0].shape[2])
+        p1, p2, info = self.heads(x, S)
+        if arena:
+            cache.write(p2, info)
+            p2_all, info_all = cache.views(S + T)
+        elif cache is not None:
+            p2_all = torch.cat([cache[0], p2], dim=2)
+            info_all = torch.cat([cache[1], info], dim=2)
+        else:
+            p2_all, info_all = p2, info
+        new_cache = cache if arena else (p2_all, info_all)
+        if p2_all.dtype != p1.dtype:  # an arena kept in another dtype than the activations
+            p1 = p1.to(p2_all.dtype)
+        y, g = flash_relation(p1, p2_all, info_all, self.lam, self.tau_s, q_start=S)
+        if y.dtype != x.dtype and not torch.is_autocast_enabled():
+            y = y.to(x.dtype)  # an arena in a narrower dtype than an fp32 module
+        out = self._out(y, x)
+        extras = []
+        if return_cache:
+            extras.append(new_cache)
+        if self.telemetry is not None:
+            self.telemetry["exchange_mass"] = float(g[0, :, -1].detach().mean())
+        if return_gates:
+            extras.append(g)
+        return (out, *extras) if extras else out

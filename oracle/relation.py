@@ -404,3 +404,32 @@ def relation_decode_ref(p1, p2buf, infobuf, S, lam, tau_s: float = 2.0, dtype=to
         ys.append(y[0, :, 0])
         gs.append(g[0, :, 0])
     return torch.stack(ys), torch.stack(gs)
+
+
+def decode_rows_ref(p1, p2, info, S, inv_freq, theta, layer_idx: int, dtype):
+    """The new chunk's rows as the graph decoder prepares them (mote/infer/graph.py:158-172):
+    RoPE at position S[b] on p1 and p2 (fp32 angle float(S) * inv_freq, cos/sin cast to the cache
+    dtype), Givens on I~, then the cast to the cache dtype. Inputs [B, H, dh] raw projections;
+    `inv_freq` / `theta` None skip RoPE / Givens. Returns three [B, H, dh] tensors in `dtype`."""
+    B, H, dh = p1.shape
+    outs = []
+    for b in range(B):
+        s = int(S[b])
+        q, k, v = (t[b : b + 1, :, None, :].double() for t in (p1, p2, info))
+        if inv_freq is not None:
+            ang = torch.tensor(float(s), dtype=torch.float32) * inv_freq.float().cpu()
+            full = torch.cat([ang, ang])
+            cos = full.cos().to(dtype).double()[None, None, None]
+            sin = full.sin().to(dtype).double()[None, None, None]
+            q = q * cos + rotate_half(q) * sin
+            k = k * cos + rotate_half(k) * sin
+        if theta is not None:
+            c = torch.cos(theta.float().cpu()).to(dtype).double()
+            sn = torch.sin(theta.float().cpu()).to(dtype).double()
+            a_idx, b_idx = givens_pairs(H, layer_idx)
+            ia, ib = v[:, a_idx].clone(), v[:, b_idx].clone()
+            v = v.clone()
+            v[:, a_idx] = c[None, :, None, None] * ia - sn[None, :, None, None] * ib
+            v[:, b_idx] = sn[None, :, None, None] * ia + c[None, :, None, None] * ib
+        outs.append([t[0, :, 0].to(dtype) for t in (q, k, v)])
+    return tuple(torch.stack([o[i] for o in outs]) for i in range(3))

@@ -1,0 +1,144 @@
+"""The decode step (one HIP launch per layer) against the CPU oracle: the core, the append, the
+device-side position advance, batch 16, edge positions, and replay inside a HIP graph."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from conftest import rel_err
+from oracle import relation as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _setup(B, H, D, cap, S, dtype, seed=0, theta=True, rope=True):
+    g = torch.Generator().manual_seed(seed)
+    kc = (torch.randn(B, H, cap, D, generator=g) * 0.7).to(dtype)
+    vc = (torch.randn(B, H, cap, D, generator=g) * 0.7).to(dtype)
+    raw = [(torch.randn(B, H, D, generator=g) * 0.7).to(dtype) for _ in range(3)]
+    th = (torch.rand(H // 2, generator=g) * 0.6 - 0.3) if theta else None
+    inv = O.rope_inv_freq(D, 10000.0) if rope else None
+    Sv = torch.tensor(S, dtype=torch.int64)
+    return kc, vc, raw, th, inv, Sv
+
+
+def _oracle(kc, vc, raw, th, inv, Sv, layer_idx, lam, dtype):
+    q, k, v = O.decode_rows_ref(*raw, Sv, inv, th, layer_idx, dtype)
+    kc2, vc2 = kc.clone(), vc.clone()
+    for b in range(kc.shape[0]):
+        kc2[b, :, int(Sv[b])] = k[b]
+        vc2[b, :, int(Sv[b])] = v[b]
+    y, gg = O.relation_decode_ref(q, kc2, vc2, Sv, torch.tensor(lam), 2.0, dtype=torch.float64)
+    return y, gg, kc2, vc2
+
+
+def _check_append(kd, vd, kc2, vc2, dtype):
+    if dtype == torch.bfloat16:
+        assert torch.equal(kd.cpu(), kc2) and torch.equal(vd.cpu(), vc2)
+    else:
+        assert rel_err(kd, kc2) < 1e-5 and rel_err(vd, vc2) < 1e-5
+
+
+def _run(kc, vc, raw, th, inv, Sv, layer_idx, lam, advance=False):
+    from mote_amd.decode import relation_decode
+
+    kd, vd = kc.cuda(), vc.cuda()
+    Sd = Sv.cuda()
+    y, gg = relation_decode(*(t.cuda() for t in raw), Sd, kd, vd, torch.tensor(lam, device="cuda"), 2.0,
+                            None if inv is None else inv.cuda(), None if th is None else th.cuda(), layer_idx,
+                            advance=advance)
+    torch.cuda.synchronize()
+    return y, gg, kd, vd, Sd
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+@pytest.mark.parametrize("S", [1, 37, 700, 4096])
+@pytest.mark.parametrize("layer_idx", [0, 1])
+def test_decode_batch1_matches_oracle(cuda, dtype, tol, S, layer_idx):
+    print(f"case decode b1 {dtype} S={S} layer={layer_idx}", flush=True)
+    kc, vc, raw, th, inv, Sv = _setup(1, 8, 96, 4352, [S], dtype, seed=S)
+    y, gg, kd, vd, _ = _run(kc, vc, raw, th, inv, Sv, layer_idx, 0.4)
+    yr, gr, kc2, vc2 = _oracle(kc, vc, raw, th, inv, Sv, layer_idx, 0.4, dtype)
+    assert rel_err(y, yr) < tol, rel_err(y, yr)
+    assert float((gg.cpu().double() - gr).abs().max()) < tol
+    # the append wrote row S and nothing else: bit-exact in bf16 (one rounding of the same value);
+    # in fp32 the kernel's single-precision rotation is within the fp32 bar of the float64 one
+    _check_append(kd, vd, kc2, vc2, dtype)
+
+
+def test_decode_batch16_mixed_positions(cuda):
+    S = [4096, 1, 17, 2049, 300, 4351, 64, 65, 1000, 3000, 5, 4095, 128, 129, 2500, 4000]
+    kc, vc, raw, th, inv, Sv = _setup(16, 8, 96, 4352, S, torch.bfloat16, seed=3)
+    y, gg, kd, vd, _ = _run(kc, vc, raw, th, inv, Sv, 1, 0.5)
+    yr, gr, kc2, vc2 = _oracle(kc, vc, raw, th, inv, Sv, 1, 0.5, torch.bfloat16)
+    assert rel_err(y, yr) < 2e-2
+    assert float((gg.cpu().double() - gr).abs().max()) < 2e-2
+    assert torch.equal(kd.cpu(), kc2) and torch.equal(vd.cpu(), vc2)
+
+
+def test_decode_position_zero_is_pure_self(cuda):
+    kc, vc, raw, th, inv, Sv = _setup(2, 4, 64, 512, [0, 0], torch.float32)
+    y, gg, kd, vd, _ = _run(kc, vc, raw, th, inv, Sv, 0, 0.5)
+    q, k, v = O.decode_rows_ref(*raw, Sv, inv, th, 0, torch.float32)
+    assert torch.allclose(y.cpu(), v, atol=1e-6)
+    assert float(gg.abs().max()) == 0.0
+
+
+def test_decode_advance_and_no_rope_no_givens(cuda):
+    kc, vc, raw, th, inv, Sv = _setup(2, 4, 48, 256, [10, 200], torch.float32, theta=False, rope=False)
+    y, gg, kd, vd, Sd = _run(kc, vc, raw, th, inv, Sv, 0, 0.3, advance=True)
+    yr, gr, _, _ = _oracle(kc, vc, raw, th, inv, Sv, 0, 0.3, torch.float32)
+    assert rel_err(y, yr) < 1e-5
+    assert Sd.cpu().tolist() == [11, 201]
+
+
+def test_decode_out_of_range_position_is_flagged(cuda):
+    kc, vc, raw, th, inv, Sv = _setup(2, 4, 64, 128, [5, 128], torch.float32)
+    y, gg, kd, vd, _ = _run(kc, vc, raw, th, inv, Sv, 0, 0.5)
+    assert torch.isnan(y[1]).all() and torch.isnan(gg[1]).all()
+    assert torch.isfinite(y[0]).all()
+    assert torch.equal(kd[1].cpu(), kc[1])  # nothing appended for the bad sequence
+
+
+def test_decode_replays_in_a_hip_graph(cuda):
+    """A captured step with the device-side advance, replayed with eager work in between, equals
+    the same steps run eagerly (every replay checked)."""
+    from mote_amd.decode import decode_workspace, relation_decode
+
+    B, H, D, cap = 2, 8, 96, 1024
+    kc, vc, raw, th, inv, Sv = _setup(B, H, D, cap, [300, 301], torch.bfloat16, seed=9)
+    steps = 5
+    g = torch.Generator().manual_seed(10)
+    xs = [[(torch.randn(B, H, D, generator=g) * 0.7).to(torch.bfloat16) for _ in range(3)] for _ in range(steps)]
+    # eager
+    ke, ve, Se = kc.cuda(), vc.cuda(), Sv.cuda()
+    lam = torch.tensor(0.4, device="cuda")
+    eager = []
+    for s in range(steps):
+        y, gg = relation_decode(*(t.cuda() for t in xs[s]), Se, ke, ve, lam, 2.0, inv.cuda(), th.cuda(), 1, advance=True)
+        eager.append((y.clone(), gg.clone()))
+    # graph
+    kg, vg, Sg = kc.cuda(), vc.cuda(), Sv.cuda()
+    ins = [torch.empty(B, H, D, device="cuda", dtype=torch.bfloat16) for _ in range(3)]
+    ws = decode_workspace(B, H, D, cap, "cuda", torch.bfloat16)
+    yb = torch.empty(B, H, D, device="cuda", dtype=torch.bfloat16)
+    gb = torch.empty(B, H, device="cuda")
+    invd, thd = inv.cuda(), th.cuda()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            relation_decode(*ins, Sg, kg, vg, lam, 2.0, invd, thd, 1, advance=True, workspace=ws, y=yb, g=gb)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    for s in range(steps):
+        for dst, src in zip(ins, xs[s]):
+            dst.copy_(src.cuda())
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(yb, eager[s][0]), s
+        assert torch.equal(gb, eager[s][1]), s
+        _ = (yb.float() * 2).sum()  # eager work between replays
+    assert torch.equal(kg, ke) and torch.equal(vg, ve) and torch.equal(Sg, Se)
