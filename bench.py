@@ -1,0 +1,358 @@
+#!/usr/bin/env python3
+"""Benchmark of Mote's Relation hot path on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-decode]
+
+Headline (BASELINE.json `metric`, the config it is quoted on): the Mote-96M Relation stack,
+bf16 forward + backward, B = 1, a 16384-byte window with Bernoulli(1/3.3) chunk boundaries
+(seed 2, ~4965 chunks), 12 layers. One step = for every layer: RoPE/Givens prologue, fused
+forward, fused backward (one pass), prologue backward. Inputs (the layer's fused projection
+output and dY) are synthetic, resident in HBM before timing. FLOPs follow the reference's causal
+convention: 7 * H * dh * T^2 per layer (fwd 2x, bwd 5x), projections and RoPE/Givens excluded.
+
+Also reported: the decode step (12 layers, cache prefilled to 4096 chunks, one chunk per step,
+256 steps, batch 1 and 16, HIP-graph replayed; batch 1 rotates 4 independent caches so the
+Infinity Cache cannot hold them), the roofline of the dominant kernel (HIP events around that
+kernel's launches) and the CPU oracle timed on the host cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "Relation fwd+bwd TFLOP/s & decode µs/step at Mote-96M shape; % of roofline"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+D_MODEL, N_HEADS, D_HEAD, N_LAYERS = 768, 8, 96, 12   # Mote-96M main network (mote/config.py)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def rmsnorm(x, eps=1e-5):
+    return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps)
+
+
+def chunk_count(seed: int, nbytes: int, batch: int = 1) -> int:
+    g = torch.Generator().manual_seed(seed)
+    mask = torch.rand(batch, nbytes, generator=g) < (1.0 / 3.3)
+    mask[:, 0] = True
+    return int(mask.sum(-1).max())
+
+
+# ------------------------------------------------------------------------------------------------
+# fwd + bwd (C3)
+# ------------------------------------------------------------------------------------------------
+class StackInputs:
+    def __init__(self, T: int, seed: int, dev):
+        from mote_amd.relation import FullRelation
+
+        torch.manual_seed(seed)
+        x = rmsnorm(torch.randn(1, T, D_MODEL))
+        self.layers = []
+        for li in range(N_LAYERS):
+            m = FullRelation(D_MODEL, N_HEADS, li)
+            with torch.no_grad():
+                m.theta.uniform_(-0.3, 0.3)
+            w = torch.cat([m.w1.weight, m.w2.weight, m.wi.weight], 0).detach()
+            qkv = (x @ w.t()).to(torch.bfloat16).to(dev)
+            dy = torch.randn(1, N_HEADS, T, D_HEAD).to(torch.bfloat16).to(dev)
+            self.layers.append(dict(qkv=qkv, dy=dy, theta=m.theta.detach().to(dev), lam=m.lam.detach().to(dev),
+                                    inv=m.inv_freq.to(dev), parity=li % 2))
+        self.T = T
+
+
+def stack_step(inp: StackInputs, timers=None):
+    """One fwd+bwd pass of the 12-layer stack through the HIP ops."""
+    ops = torch.ops.mote
+    for L in inp.layers:
+        p1, p2, info = ops.rope_givens(L["qkv"], L["inv"], L["theta"], N_HEADS, L["parity"], 0)
+        if timers is not None:
+            timers["fwd"][0].append(torch.cuda.Event(enable_timing=True))
+            timers["fwd"][0][-1].record()
+        y, g, ibar, lse = ops.relation_fwd(p1, p2, info, L["lam"], 2.0, 0)
+        if timers is not None:
+            timers["fwd"][1].append(torch.cuda.Event(enable_timing=True))
+            timers["fwd"][1][-1].record()
+            dp = staged_bwd(p1, p2, info, ibar, lse, g, L["dy"], timers)
+        else:
+            dp = ops.relation_bwd(p1, p2, info, ibar, lse, g, L["dy"], 2.0, 0)
+        ops.rope_givens_bwd(dp[0], dp[1], dp[2], L["qkv"], L["inv"], L["theta"], N_HEADS, L["parity"], 0)
+
+
+def staged_bwd(p1, p2, info, ibar, lse, g, dy, timers):
+    """The one-pass backward with the key-block kernel bracketed by events (its three launches
+    issued separately through the ABI's `stages` field)."""
+    from mote_amd import _lib as Lb
+    from mote_amd.flash_relation import _token_major
+
+    B, H, TQ, D = p1.shape
+    dp1 = _token_major(B, H, TQ, D, p1, p1.dtype)
+    dp2 = _token_major(B, H, TQ, D, p1, p1.dtype)
+    dinfo = _token_major(B, H, TQ, D, p1, p1.dtype)
+    dlam = torch.empty((), device=p1.device, dtype=torch.float32)
+    a = Lb.BwdArgs()
+    a.dtype, a.B, a.H, a.TQ, a.TK, a.D, a.q_start = Lb.dtype_code(p1), B, H, TQ, TQ, D, 0
+    a.tau_s, a.deterministic = 2.0, 0
+    a.p1, a.p2, a.info, a.dy = Lb.view(p1), Lb.view(p2), Lb.view(info), Lb.view(dy)
+    a.ibar, a.lse, a.g = ibar.data_ptr(), lse.data_ptr(), g.data_ptr()
+    a.dp1, a.dp2, a.dinfo, a.dlam = Lb.view(dp1), Lb.view(dp2), Lb.view(dinfo), dlam.data_ptr()
+    ws = torch.empty(int(Lb.lib().mote_relation_bwd_workspace(a)), device=p1.device, dtype=torch.uint8)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    st = Lb.stream_of(p1)
+    a.stages = Lb.MOTE_BWD_ROWS
+    Lb.check(Lb.lib().mote_relation_bwd(a, st), "bwd rows")
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    a.stages = Lb.MOTE_BWD_KEYS
+    Lb.check(Lb.lib().mote_relation_bwd(a, st), "bwd keys")
+    e1.record()
+    timers["bwd_keys"][0].append(e0)
+    timers["bwd_keys"][1].append(e1)
+    a.stages = Lb.MOTE_BWD_FINISH
+    Lb.check(Lb.lib().mote_relation_bwd(a, st), "bwd finish")
+    return dp1, dp2, dinfo, dlam
+
+
+def bench_stack(steps: int, warmup: int, dev):
+    T = chunk_count(2, 16384)
+    log(f"[bench] Mote-96M stack: T = {T} chunks, {N_LAYERS} layers, bf16 fwd+bwd")
+    inp = StackInputs(T, 2, dev)
+    for _ in range(warmup):
+        stack_step(inp)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t_wall = time.perf_counter()
+    t0.record()
+    for _ in range(steps):
+        stack_step(inp)
+    t1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_wall
+    ms = t0.elapsed_time(t1) / steps
+    flops = N_LAYERS * 7.0 * N_HEADS * D_HEAD * T * T
+    # kernel-level timing pass (same work, stages bracketed by events)
+    timers = {"fwd": ([], []), "bwd_keys": ([], [])}
+    for _ in range(max(1, min(steps, 3))):
+        stack_step(inp, timers)
+    torch.cuda.synchronize()
+    avg = {k: sum(a.elapsed_time(b) for a, b in zip(*v)) / len(v[0]) for k, v in timers.items()}
+    keys_flops = 5.0 * N_HEADS * D_HEAD * T * T
+    fwd_flops = 2.0 * N_HEADS * D_HEAD * T * T
+    res = dict(T=T, ms_per_step=ms, wall_s=wall, tflops=flops / (ms * 1e-3) / 1e12, flops_per_step=flops,
+               keys_ms=avg["bwd_keys"], fwd_ms=avg["fwd"],
+               keys_tflops=keys_flops / (avg["bwd_keys"] * 1e-3) / 1e12,
+               fwd_tflops=fwd_flops / (avg["fwd"] * 1e-3) / 1e12)
+    log(f"[bench] stack: {ms:.3f} ms/step = {res['tflops']:.1f} TFLOP/s; fwd kernel {avg['fwd']*1e3:.1f} us "
+        f"({res['fwd_tflops']:.1f} TF/s), bwd key kernel {avg['bwd_keys']*1e3:.1f} us ({res['keys_tflops']:.1f} TF/s)")
+    return res
+
+
+# ------------------------------------------------------------------------------------------------
+# decode (C4)
+# ------------------------------------------------------------------------------------------------
+def bench_decode(batch: int, steps: int, dev, copies: int):
+    from mote_amd.arena import RelationArena
+    from mote_amd.decode import decode_workspace, relation_decode
+    from mote_amd.relation import FullRelation, rope_givens
+
+    S0 = 4096
+    cap = S0 + steps + 256
+    torch.manual_seed(3)
+    mods = []
+    for li in range(N_LAYERS):
+        m = FullRelation(D_MODEL, N_HEADS, li)
+        with torch.no_grad():
+            m.theta.uniform_(-0.3, 0.3)
+        mods.append(m)
+    arenas, Ss = [], []
+    for c in range(copies):
+        ar = RelationArena(N_LAYERS, N_HEADS, cap, D_HEAD, dev, torch.bfloat16, batch=batch)
+        for li, m in enumerate(mods):
+            w = torch.cat([m.w1.weight, m.w2.weight, m.wi.weight], 0).detach().to(dev, torch.bfloat16)
+            for b0 in range(batch):
+                x = rmsnorm(torch.randn(1, S0, D_MODEL, device=dev)).to(torch.bfloat16)
+                qkv = x @ w.t()
+                _, p2, info = rope_givens(qkv, N_HEADS, m.inv_freq.to(dev), m.theta.detach().to(dev), li, 0)
+                ar.p2(li)[b0, :, :S0] = p2[0]
+                ar.info(li)[b0, :, :S0] = info[0]
+        arenas.append(ar)
+        Ss.append(torch.full((batch,), S0, device=dev, dtype=torch.int64))
+    lam = [m.lam.detach().float().to(dev) for m in mods]
+    theta = [m.theta.detach().float().to(dev) for m in mods]
+    inv = [m.inv_freq.to(dev) for m in mods]
+    ins = [torch.randn(batch, 3, N_HEADS, D_HEAD, device=dev).to(torch.bfloat16) for _ in range(N_LAYERS)]
+    ws = [decode_workspace(batch, N_HEADS, D_HEAD, cap, dev) for _ in range(copies)]
+    ys = [torch.empty(batch, N_HEADS, D_HEAD, device=dev, dtype=torch.bfloat16) for _ in range(N_LAYERS)]
+    gs = [torch.empty(batch, N_HEADS, device=dev) for _ in range(N_LAYERS)]
+
+    def step(c):
+        for li in range(N_LAYERS):
+            q = ins[li]
+            relation_decode(q[:, 0], q[:, 1], q[:, 2], Ss[c], arenas[c].p2(li), arenas[c].info(li), lam[li], 2.0,
+                            inv[li], theta[li], li, advance=(li == N_LAYERS - 1), workspace=ws[c], y=ys[li], g=gs[li])
+
+    # eager per-launch timing of the decode kernel (for the roofline), then restore S
+    ev = []
+    for c in range(copies):
+        for li in range(N_LAYERS):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            q = ins[li]
+            relation_decode(q[:, 0], q[:, 1], q[:, 2], Ss[c], arenas[c].p2(li), arenas[c].info(li), lam[li], 2.0,
+                            inv[li], theta[li], li, advance=False, workspace=ws[c], y=ys[li], g=gs[li])
+            e1.record()
+            ev.append((e0, e1))
+    torch.cuda.synchronize()
+    kern_ms = sum(a.elapsed_time(b) for a, b in ev[copies:]) / max(1, len(ev) - copies)
+    # graphs: one per cache copy
+    graphs = []
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for c in range(copies):
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr, stream=side):
+                step(c)
+            graphs.append(gr)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    for c in range(copies):  # capture does not run the kernels; positions are still S0
+        assert int(Ss[c][0]) == S0
+    for i in range(3 * copies):  # warm-up replays
+        graphs[i % copies].replay()
+    torch.cuda.synchronize()
+    s_begin = [int(s[0]) for s in Ss]
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for i in range(steps):
+        graphs[i % copies].replay()
+    t1.record()
+    torch.cuda.synchronize()
+    us = t0.elapsed_time(t1) * 1e3 / steps
+    # algorithmic bytes: rows [0, S] of P2 and I~ per layer and sequence
+    rows = 0
+    for i in range(steps):
+        c = i % copies
+        s = s_begin[c] + i // copies
+        rows += (s + 1)
+    bytes_per_step = rows / steps * 2 * N_HEADS * D_HEAD * 2 * N_LAYERS * batch
+    s_avg = rows / steps - 1
+    kern_bytes = (S0 + 1) * 2 * N_HEADS * D_HEAD * 2 * batch  # the eager launches ran at S = S0
+    res = dict(batch=batch, us_per_step=us, gbs=bytes_per_step / (us * 1e-6) / 1e9, bytes_per_step=bytes_per_step,
+               avg_S=s_avg, kernel_us=kern_ms * 1e3, kernel_gbs=kern_bytes / (kern_ms * 1e-3) / 1e9, copies=copies)
+    log(f"[bench] decode b{batch}: {us:.1f} us/step ({res['gbs']:.0f} GB/s over the step), "
+        f"one launch {res['kernel_us']:.1f} us ({res['kernel_gbs']:.0f} GB/s)")
+    return res
+
+
+# ------------------------------------------------------------------------------------------------
+# CPU baseline: the oracle on the host cores
+# ------------------------------------------------------------------------------------------------
+def bench_cpu(T: int):
+    from oracle import relation as O
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(2)
+    p1, p2, info = (torch.randn(1, N_HEADS, T, D_HEAD, generator=g).requires_grad_(True) for _ in range(3))
+    lam = torch.tensor(0.5, requires_grad=True)
+    dy = torch.randn(1, N_HEADS, T, D_HEAD, generator=g)
+    t0 = time.perf_counter()
+    y, _ = O.relation_reference(p1, p2, info, lam, 2.0, 0)
+    torch.autograd.grad((y * dy).sum(), [p1, p2, info, lam])
+    dt = time.perf_counter() - t0
+    flops = 7.0 * N_HEADS * D_HEAD * T * T
+    cpu = platform.processor() or platform.machine()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    log(f"[bench] CPU oracle: one layer fwd+bwd {dt:.1f} s on {cores} threads ({cpu})")
+    return dict(value=flops / dt / 1e12, unit="TFLOP/s", cores=cores, kind="port",
+                sample=f"one Mote-96M Relation layer fwd+bwd (T={T}, H=8, dh=96, fp32, materialized oracle), "
+                       f"timed once: {dt:.2f} s; the 12-layer step would take {12 * dt:.1f} s",
+                cpu=cpu, seconds_per_layer=dt)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--decode-steps", type=int, default=256)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: the Relation path is built and measured on a single GPU "
+              "(run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+    import mote_amd.flash_relation as fr  # noqa: F401  (registers the ops)
+    import mote_amd.relation  # noqa: F401
+
+    if not fr.HAS_HIP:
+        raise SystemExit("bench.py needs libmote_relation.so and a GPU")
+    dev = torch.device("cuda")
+    st = bench_stack(args.steps, args.warmup, dev)
+    dec = {}
+    if not args.no_decode:
+        dec["b1"] = bench_decode(1, args.decode_steps, dev, copies=4)
+        dec["b16"] = bench_decode(16, args.decode_steps, dev, copies=1)
+    cpu = None if args.no_cpu else bench_cpu(st["T"])
+    out = {
+        "metric": METRIC,
+        "value": round(st["tflops"], 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(st["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (N(0,1) hidden states, random-init weights, Bernoulli(1/3.3) chunk boundaries, seed 2)",
+        "config": {"workload": "Mote-96M Relation stack fwd+bwd (12 layers, B=1, 16384-byte window)",
+                   "T_chunks": st["T"], "heads": N_HEADS, "d_head": D_HEAD, "layers": N_LAYERS,
+                   "flop_convention": "7*H*dh*T^2 per layer (causal; fwd 2x, bwd 5x)"},
+        "roofline": {"kernel": "bwd_keys_kernel (one-pass backward, key blocks)", "bound": "mfma",
+                     "achieved": round(st["keys_tflops"], 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(st["keys_tflops"] / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "avg_launch_ms": round(st["keys_ms"], 4)},
+        "roofline_fwd": {"kernel": "relation_fwd_kernel", "bound": "mfma", "achieved": round(st["fwd_tflops"], 2),
+                         "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(st["fwd_tflops"] / PEAK_BF16_TFLOPS, 4), "avg_launch_ms": round(st["fwd_ms"], 4)},
+        "stack_frac_of_peak": round(st["tflops"] / PEAK_BF16_TFLOPS, 4),
+    }
+    if dec:
+        out["decode"] = {
+            k: {"batch": v["batch"], "us_per_step": round(v["us_per_step"], 2), "layers": N_LAYERS,
+                "avg_S": round(v["avg_S"], 1), "step_GBs": round(v["gbs"], 1),
+                "step_frac_hbm": round(v["gbs"] / PEAK_HBM_GBS, 4), "kernel_us": round(v["kernel_us"], 2),
+                "kernel_GBs": round(v["kernel_gbs"], 1), "kernel_frac_hbm": round(v["kernel_gbs"] / PEAK_HBM_GBS, 4),
+                "cache_copies_rotated": v["copies"]}
+            for k, v in dec.items()}
+    if cpu is not None:
+        out["cpu_baseline"] = {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")}
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()
