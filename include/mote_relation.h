@@ -174,8 +174,9 @@ int mote_rope_givens_bwd(const mote_rope_givens_bwd_args* args, void* stream);
  * never read. S[b] >= capacity writes NaN into y[b] and skips the append.
  * flags bit 0 (MOTE_DECODE_ADVANCE): add 1 to every S[b] once the step has read it (graph.py's
  * S += 1, :189-190), so a captured step needs no separate kernel for it.
- * The workspace (mote_relation_decode_workspace() bytes) must be zero-filled once before its first
- * use; every call leaves it ready for the next. Calls that share a workspace must not overlap.
+ * Two launches on `stream` (a split-S sweep, then a per-sequence merge). The workspace
+ * (mote_relation_decode_workspace() bytes) holds the per-split partials; its contents on entry do
+ * not matter. Calls that share a workspace must not overlap.
  * ------------------------------------------------------------------------------------------------ */
 #define MOTE_DECODE_ADVANCE 1
 

@@ -62,100 +62,135 @@ constexpr int kRowBlock = 64;  // rows per workgroup in the rows stage; also TQp
 template <typename T, int DP>
 __global__ void __launch_bounds__(256) bwd_rows_kernel(const BwdParams p) {
   using E = Elem<T>;
-  constexpr int DQ = DP / 4;         // head-dim elements per lane (4 lanes per row)
-  constexpr int LD = DP + 16 / sizeof(T);
+  constexpr int EPC = 16 / sizeof(T);       // elements per 16-byte chunk
+  constexpr int CPR = DP / EPC;             // chunks per row
+  constexpr int NCH = kRowBlock * CPR;      // chunks per block
+  constexpr int CT = (NCH + 255) / 256;     // chunks per thread
+  constexpr int LD = DP + EPC;              // LDS row stride (elements)
   __shared__ __align__(16) T sq[kRowBlock * LD];
   __shared__ __align__(16) T sd[kRowBlock * LD];
+  __shared__ float part[3][kRowBlock][CPR + 1];
+  __shared__ float sdu[kRowBlock];
   __shared__ float sred[kRowBlock];
 
   const int bh = blockIdx.y;
   const int b = bh / p.H, h = bh % p.H;
   const int i0 = blockIdx.x * kRowBlock;
   const int tid = threadIdx.x;
-  const int row = tid >> 2, qd = tid & 3;
-  const int i = i0 + row;
-  const bool valid = i < p.TQ;
-  const int qa = p.q_start + i;
   const int D = p.D;
-  const int dbeg = qd * DQ;
+  const T* qb = reinterpret_cast<const T*>(p.p1) + b * p.q_sb + h * p.q_sh;
+  const T* kb = reinterpret_cast<const T*>(p.p2) + b * p.k_sb + h * p.k_sh;
+  const T* vb = reinterpret_cast<const T*>(p.info) + b * p.v_sb + h * p.v_sh;
+  const T* yb = reinterpret_cast<const T*>(p.dy) + b * p.y_sb + h * p.y_sh;
+  T* wq = reinterpret_cast<T*>(p.wq) + (int64_t(bh) * p.TQp + i0) * DP;
+  T* wd = reinterpret_cast<T*>(p.wdib) + (int64_t(bh) * p.TQp + i0) * DP;
 
-  const T* q = reinterpret_cast<const T*>(p.p1) + b * p.q_sb + h * p.q_sh + int64_t(i) * p.q_sr;
-  const T* kself = reinterpret_cast<const T*>(p.p2) + b * p.k_sb + h * p.k_sh + int64_t(qa) * p.k_sr;
-  const T* iself = reinterpret_cast<const T*>(p.info) + b * p.v_sb + h * p.v_sh + int64_t(qa) * p.v_sr;
-  const T* dy = reinterpret_cast<const T*>(p.dy) + b * p.y_sb + h * p.y_sh + int64_t(i) * p.y_sr;
-  const int64_t srow = int64_t(bh) * p.TQ + i;
-  const float* ib = p.ibar + srow * D;
-
-  float gi = 0.f, lse = 0.f;
-  if (valid) {
-    gi = p.g[srow];
-    lse = p.lse[srow];
-  }
-  float dgate = 0.f, delta = 0.f, uii = 0.f;
-  float kv[DQ];
+  // pass 1: 16-byte chunks; per-chunk partial dot products, dI-bar and the row-major copies
+  Chunk kreg[CT];
 #pragma unroll
-  for (int e = 0; e < DQ; ++e) {
-    const int d = dbeg + e;
-    float vq = 0.f, vk = 0.f, vy = 0.f, vb = 0.f, vi = 0.f;
-    if (valid && d < D) {
-      vq = E::to_f(q[d]);
-      vk = E::to_f(kself[d]);
-      vy = E::to_f(dy[d]);
-      vb = ib[d];
-      vi = E::to_f(iself[d]);
+  for (int c = 0; c < CT; ++c) {
+    const int idx = tid + 256 * c;
+    if (idx >= NCH) break;
+    const int r = idx / CPR, cc = idx % CPR;
+    const int i = i0 + r;
+    const int d0 = cc * EPC;
+    const bool ok = i < p.TQ && d0 < D;
+    const int qa = p.q_start + i;
+    Chunk cq = zero_chunk(), ck = zero_chunk(), cv = zero_chunk(), cy = zero_chunk();
+    float ibv[EPC];
+    float gi = 0.f;
+    if (ok) {
+      cq = load_chunk(qb + int64_t(i) * p.q_sr + d0);
+      ck = load_chunk(kb + int64_t(qa) * p.k_sr + d0);
+      cv = load_chunk(vb + int64_t(qa) * p.v_sr + d0);
+      cy = load_chunk(yb + int64_t(i) * p.y_sr + d0);
+      const float* ibr = p.ibar + (int64_t(bh) * p.TQ + i) * D + d0;
+#pragma unroll
+      for (int e = 0; e < EPC; e += 4) {
+        const float4 f = *reinterpret_cast<const float4*>(ibr + e);
+        ibv[e] = f.x; ibv[e + 1] = f.y; ibv[e + 2] = f.z; ibv[e + 3] = f.w;
+      }
+      gi = p.g[int64_t(bh) * p.TQ + i];
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) ibv[e] = 0.f;
     }
-    kv[e] = vk;
-    // dI-bar in the operand dtype, as the reference stores it for its dots (flash_relation.py:215-216)
-    const T dib = E::from_f(gi * vy);
-    dgate += vy * (vb - vi);
-    delta += (gi * vy) * vb;
-    uii += vq * vk;
-    sq[row * LD + d] = E::from_f(vq);
-    sd[row * LD + d] = dib;
-  }
+    kreg[c] = ck;
+    const T* eq = reinterpret_cast<const T*>(&cq);
+    const T* ek = reinterpret_cast<const T*>(&ck);
+    const T* ev = reinterpret_cast<const T*>(&cv);
+    const T* ey = reinterpret_cast<const T*>(&cy);
+    float dgate = 0.f, delta = 0.f, uii = 0.f;
+    Chunk cd;
+    T* ed = reinterpret_cast<T*>(&cd);
 #pragma unroll
-  for (int m = 1; m <= 2; m <<= 1) {
-    dgate += __shfl_xor(dgate, m, 64);
-    delta += __shfl_xor(delta, m, 64);
-    uii += __shfl_xor(uii, m, 64);
+    for (int e = 0; e < EPC; ++e) {
+      const float vy = E::to_f(ey[e]);
+      const float dib = gi * vy;
+      dgate += vy * (ibv[e] - E::to_f(ev[e]));
+      delta += dib * ibv[e];
+      uii += E::to_f(eq[e]) * E::to_f(ek[e]);
+      // dI-bar in the operand dtype, as the reference stores it for its dots (flash_relation.py:215-216)
+      ed[e] = E::from_f(dib);
+    }
+    part[0][r][cc] = dgate;
+    part[1][r][cc] = delta;
+    part[2][r][cc] = uii;
+    store_chunk(&sq[r * LD + d0], cq);
+    store_chunk(&sd[r * LD + d0], cd);
+    store_chunk(wq + r * DP + d0, cq);
+    store_chunk(wd + r * DP + d0, cd);
   }
-  const float da = dgate * gi * (1.0f - gi);
-  const float s = sigmoid_acc(uii * p.scale * p.tau_inv);
-  const float du = valid ? (-da) * s * (1.0f - s) * p.tau_inv : 0.f;
-  const bool has = valid && lse > kNegInf;
-  if (qd == 0) {
+  __syncthreads();
+  // per-row terms
+  if (tid < kRowBlock) {
+    const int r = tid, i = i0 + r;
+    const bool valid = i < p.TQ;
+    float dgate = 0.f, delta = 0.f, uii = 0.f;
+#pragma unroll
+    for (int cc = 0; cc < CPR; ++cc) {
+      dgate += part[0][r][cc];
+      delta += part[1][r][cc];
+      uii += part[2][r][cc];
+    }
+    float gi = 0.f, lse = kNegInf;
+    if (valid) {
+      gi = p.g[int64_t(bh) * p.TQ + i];
+      lse = p.lse[int64_t(bh) * p.TQ + i];
+    }
+    const float da = dgate * gi * (1.0f - gi);
+    const float s = sigmoid_acc(uii * p.scale * p.tau_inv);
+    const float du = valid ? (-da) * s * (1.0f - s) * p.tau_inv : 0.f;
+    const bool has = valid && lse > kNegInf;
     const int64_t w = int64_t(bh) * p.TQp + i;
     p.lse2[w] = has ? lse * kLog2e : __builtin_inff();
     p.cvec[w] = valid ? da - delta : 0.f;
     p.duii[w] = du;
-    sred[row] = valid ? -da * logf((float)qa + 1.0f) : 0.f;
-  }
-  if (valid) {
-    float* acc = p.dp1acc + srow * D;
-#pragma unroll
-    for (int e = 0; e < DQ; ++e) {
-      const int d = dbeg + e;
-      if (d < D) acc[d] = du * kv[e] * p.scale;
-    }
+    sdu[r] = du;
+    sred[r] = valid ? -da * logf((float)(p.q_start + i) + 1.0f) : 0.f;
   }
   __syncthreads();
-  // row-major padded copies
-  {
-    T* wq = reinterpret_cast<T*>(p.wq) + (int64_t(bh) * p.TQp + i0) * DP;
-    T* wd = reinterpret_cast<T*>(p.wdib) + (int64_t(bh) * p.TQp + i0) * DP;
-    constexpr int EPC = 16 / sizeof(T);
-    constexpr int CH = kRowBlock * DP / EPC;
-    for (int c = tid; c < CH; c += 256) {
-      const int r = c / (DP / EPC), cc = c % (DP / EPC);
-      store_chunk(wq + r * DP + cc * EPC, *reinterpret_cast<const Chunk*>(&sq[r * LD + cc * EPC]));
-      store_chunk(wd + r * DP + cc * EPC, *reinterpret_cast<const Chunk*>(&sd[r * LD + cc * EPC]));
-    }
+  // pass 2: dP1 accumulator initialised with the Self part dU_ii P2_i / sqrt(D)
+#pragma unroll
+  for (int c = 0; c < CT; ++c) {
+    const int idx = tid + 256 * c;
+    if (idx >= NCH) break;
+    const int r = idx / CPR, cc = idx % CPR;
+    const int i = i0 + r;
+    const int d0 = cc * EPC;
+    if (i >= p.TQ || d0 >= D) continue;
+    const float f = sdu[r] * p.scale;
+    const T* ek = reinterpret_cast<const T*>(&kreg[c]);
+    float* acc = p.dp1acc + (int64_t(bh) * p.TQ + i) * D + d0;
+#pragma unroll
+    for (int e = 0; e < EPC; e += 4)
+      *reinterpret_cast<float4*>(acc + e) =
+          make_float4(f * E::to_f(ek[e]), f * E::to_f(ek[e + 1]), f * E::to_f(ek[e + 2]), f * E::to_f(ek[e + 3]));
   }
   // transposed copies: row d holds the 64 rows of this block
   {
     T* wqT = reinterpret_cast<T*>(p.wqT) + int64_t(bh) * DP * p.TQp + i0;
     T* wdT = reinterpret_cast<T*>(p.wdibT) + int64_t(bh) * DP * p.TQp + i0;
-    constexpr int EPC = 16 / sizeof(T);
     constexpr int CH = DP * kRowBlock / EPC;
     for (int c = tid; c < CH; c += 256) {
       const int d = c / (kRowBlock / EPC), cc = c % (kRowBlock / EPC);

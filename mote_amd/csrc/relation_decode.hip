@@ -1,18 +1,21 @@
-// One decode step of one Relation layer (mote/infer/graph.py:151-187), one launch.
+// One decode step of one Relation layer (mote/infer/graph.py:151-187): two launches.
 //
-// Grid: nsplit x (B*H) workgroups, block id = split * (B*H) + head index, so with B*H a multiple
-// of 8 every split of one (sequence, head) runs on the same XCD (ids go round-robin over the 8 XCDs)
-// and the merge reads partials from its own L2. Every split reads a contiguous range of the past
-// rows [0, S) of its head:
-//   phase 1  U_j = <q, P2_j> / sqrt(D) for its rows (4 lanes per row, 16-byte loads), exchange
-//            score SiLU(U_j) in log2 units kept in LDS;
-//   phase 2  the workgroup max, p_j = 2^(e_j - max), z += p_j I~_j, l += p_j.
-// Each split writes (max, l, z[D]) to the workspace; the last split of a head to arrive (counter in
-// the workspace, device-scope fences) merges them, computes the Self score from the new row,
-// g = sigmoid(LSE - lam ln(S+1) - S_self) and Y = (1-g) I~_S + g z/l, and appends the new P2 / I~
-// row at S. The merge resets the counter, so the workspace is ready for the next call and the
-// launch can sit in a HIP graph. With MOTE_DECODE_ADVANCE the last head to finish adds 1 to every
-// S[b] once all workgroups have read it.
+// Split kernel. Grid: nsplit x (B*H) workgroups, block id = split * (B*H) + head index. Split s owns
+// the past rows [s*R, (s+1)*R) of its head, R = 64 * rows_mult (a host choice that keeps ~2k
+// workgroups in flight); splits that start at or past S leave at once, so the launch shape only
+// depends on the cache capacity and can be captured in a HIP graph. Each workgroup (4 waves; a wave
+// reads 16 rows per step, 4 lanes per row, 16-byte loads of P2 and I~ issued together with a one-step
+// register prefetch) computes U_j = <q, P2_j> / sqrt(D), e_j = SiLU(U_j) in log2 units and an online
+// softmax per row group (running max raised lazily, by more than 2^8 only), merges its row groups and
+// waves, and writes (max, l, z[D]) to the workspace.
+//
+// Merge kernel. One workgroup per sequence: for each head it loads the partials into LDS (parallel,
+// coalesced), merges them in a fixed order, computes the Self score from the new row,
+// g = sigmoid(LSE - lam ln(S+1) - S_self) and Y = (1-g) I~_S + g z/l, and appends the new P2 / I~ row
+// at S; with MOTE_DECODE_ADVANCE it then adds 1 to S[b] (every reader of S[b] in this step has run:
+// the split kernel finished before, and this workgroup is its only other reader).
+// The kernel boundary orders the partials; there is no in-kernel device-scope handshake (on gfx950
+// a device-scope release writes back the XCD's whole L2, which costs ~0.1 us per workgroup).
 //
 // The query is RoPE'd at S and rounded to the cache dtype (graph.py:158-172) by every workgroup; the
 // new P2 row gets the same rotation and I~ the Givens rotation with its partner head's raw row.
@@ -31,20 +34,18 @@ struct DecParams {
   const void* p2;
   const void* info;
   int64_t in_sb;
-  const void* kc; int64_t kc_sb, kc_sh, kc_sr;
-  const void* vc; int64_t vc_sb, vc_sh, vc_sr;
-  void* kc_w;  // writable aliases of the caches (append)
-  void* vc_w;
+  void* kc; int64_t kc_sb, kc_sh, kc_sr;
+  void* vc; int64_t vc_sb, vc_sh, vc_sr;
   void* y;
   int64_t y_sb;
   float* g;
   float* part;        // [BH][nsplit][D + 2]  (max, l, z)
-  unsigned* counter;  // [BH + 1], zero between calls
-  int B, H, D, cap, parity, flags, nsplit;
+  int64_t* S_used;    // [B] the positions the split kernel read (the merge reads these)
+  int B, H, D, cap, parity, flags, nsplit, rps;  // rps: rows per split
   float scale, tau_inv;
 };
 
-constexpr int kDecRowsMax = 2048;  // rows one split may own (LDS scores)
+constexpr int kDecMaxSplits = 120;  // partials one merge holds in LDS (D <= 128: at most 62 KB)
 
 template <typename T>
 __device__ __forceinline__ float round_to(float x) {
@@ -55,11 +56,9 @@ template <typename T, int DP>
 __global__ void __launch_bounds__(256) relation_decode_kernel(const DecParams p) {
   using E = Elem<T>;
   constexpr int EPC = 16 / sizeof(T);
+  constexpr int MAXC = (DP / EPC + 3) / 4;  // 16-byte chunks per lane (lane c owns chunks c, c+4, ...)
   __shared__ float sq[DP];
-  __shared__ float sc[kDecRowsMax];
-  __shared__ float red[4 * DP + 8];
-  __shared__ float sred[8];
-  __shared__ int s_last;
+  __shared__ float red[4 * (DP + 2)];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int BH = p.B * p.H;
@@ -70,6 +69,9 @@ __global__ void __launch_bounds__(256) relation_decode_kernel(const DecParams p)
   const int64_t S64 = p.S[b];
   const bool bad = S64 < 0 || S64 >= p.cap;
   const int S = bad ? 0 : int(S64);
+  const int nact = S > 0 ? (S + p.rps - 1) / p.rps : 1;  // splits with rows (split 0 always takes part)
+  if (split >= nact) return;
+  if (split == 0 && h == 0 && tid == 0) p.S_used[b] = S64;
 
   // query: RoPE at S, rounded to the cache dtype
   const T* q_raw = reinterpret_cast<const T*>(p.p1) + b * p.in_sb + h * D;
@@ -90,82 +92,97 @@ __global__ void __launch_bounds__(256) relation_decode_kernel(const DecParams p)
   for (int d = D + tid; d < DP; d += 256) sq[d] = 0.f;
   __syncthreads();
 
-  // rows of this split
-  const int chunk = (S + p.nsplit - 1) / p.nsplit;
-  const int r0 = min(S, split * chunk);
-  const int r1 = min(S, r0 + chunk);
-  const int nrows = r1 - r0;
+  const int r0 = split * p.rps;
+  const int r1 = min(S, r0 + p.rps);
   const T* kbase = reinterpret_cast<const T*>(p.kc) + b * p.kc_sb + h * p.kc_sh;
   const T* vbase = reinterpret_cast<const T*>(p.vc) + b * p.vc_sb + h * p.vc_sh;
   const int rr = lane >> 2, c = lane & 3;
-  const int nch = D / EPC;  // 16-byte chunks per row
+  const int nch = D / EPC;
   const float c2 = p.scale * kLog2e;
-
-  // phase 1: exchange scores
-  for (int base = 0; base < nrows; base += 64) {
-    const int ri = base + wave * 16 + rr;
-    float dot = 0.f;
-    if (ri < nrows) {
-      const T* row = kbase + int64_t(r0 + ri) * p.kc_sr;
-      for (int k = c; k < nch; k += 4) {
-        const Chunk ch = load_chunk(row + k * EPC);
-        const T* e = reinterpret_cast<const T*>(&ch);
+  float qv[MAXC][EPC];
 #pragma unroll
-        for (int j = 0; j < EPC; ++j) dot = fmaf(E::to_f(e[j]), sq[k * EPC + j], dot);
-      }
-    }
-    dot += __shfl_xor(dot, 1, 64);
-    dot += __shfl_xor(dot, 2, 64);
-    if (ri < nrows && c == 0) {
-      const float u2 = dot * c2;
-      sc[ri] = u2 * frcp(1.0f + fexp2(-u2));
-    }
-  }
-  __syncthreads();
-  // workgroup max
-  float mx = kNegInf;
-  for (int i = tid; i < nrows; i += 256) mx = fmaxf(mx, sc[i]);
+  for (int k = 0; k < MAXC; ++k)
 #pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
-  if (lane == 0) sred[wave] = mx;
-  __syncthreads();
-  mx = fmaxf(fmaxf(sred[0], sred[1]), fmaxf(sred[2], sred[3]));
-  const float msafe = mx == kNegInf ? 0.f : mx;
+    for (int j = 0; j < EPC; ++j) qv[k][j] = (c + 4 * k) < nch ? sq[(c + 4 * k) * EPC + j] : 0.f;
 
-  // phase 2: z = sum p I~, l = sum p   (lane owns chunks c, c+4, ... of its rows)
-  constexpr int MAXC = (DP / EPC + 3) / 4;  // chunks per lane
+  float m = kNegInf, l = 0.f;
   float z[MAXC][EPC];
 #pragma unroll
   for (int k = 0; k < MAXC; ++k)
 #pragma unroll
     for (int j = 0; j < EPC; ++j) z[k][j] = 0.f;
-  float l = 0.f;
-  for (int base = 0; base < nrows; base += 64) {
-    const int ri = base + wave * 16 + rr;
-    if (ri < nrows) {
-      const float pr = fexp2(sc[ri] - msafe);
-      if (c == 0) l += pr;
-      const T* row = vbase + int64_t(r0 + ri) * p.vc_sr;
+
+  Chunk kr[MAXC], vr[MAXC];
+  auto fetch = [&](int row) {
+#pragma unroll
+    for (int k = 0; k < MAXC; ++k) {
+      const int kc = c + 4 * k;
+      if (row < r1 && kc < nch) {
+        kr[k] = load_chunk(kbase + int64_t(row) * p.kc_sr + kc * EPC);
+        vr[k] = load_chunk(vbase + int64_t(row) * p.vc_sr + kc * EPC);
+      } else {
+        kr[k] = zero_chunk();
+        vr[k] = zero_chunk();
+      }
+    }
+  };
+  int row = r0 + wave * 16 + rr;
+  fetch(row);
+  for (int base = r0; base < r1; base += 64) {
+    Chunk kc_[MAXC], vc_[MAXC];
+#pragma unroll
+    for (int k = 0; k < MAXC; ++k) {
+      kc_[k] = kr[k];
+      vc_[k] = vr[k];
+    }
+    const int cur = row;
+    row += 64;
+    if (base + 64 < r1) fetch(row);  // prefetch the next step while this one computes
+    float dot = 0.f;
+#pragma unroll
+    for (int k = 0; k < MAXC; ++k) {
+      const T* e = reinterpret_cast<const T*>(&kc_[k]);
+#pragma unroll
+      for (int j = 0; j < EPC; ++j) dot = fmaf(E::to_f(e[j]), qv[k][j], dot);
+    }
+    dot += __shfl_xor(dot, 1, 64);
+    dot += __shfl_xor(dot, 2, 64);
+    if (cur < r1) {
+      const float u2 = dot * c2;
+      const float ev = u2 * frcp(1.0f + fexp2(-u2));
+      if (ev > m + kRescale) {
+        const float alpha = fexp2(m - ev);  // 0 on the first row
+        l *= alpha;
+#pragma unroll
+        for (int k = 0; k < MAXC; ++k)
+#pragma unroll
+          for (int j = 0; j < EPC; ++j) z[k][j] *= alpha;
+        m = ev;
+      }
+      const float pr = fexp2(ev - m);
+      l += pr;
 #pragma unroll
       for (int k = 0; k < MAXC; ++k) {
-        const int kc = c + 4 * k;
-        if (kc < nch) {
-          const Chunk ch = load_chunk(row + kc * EPC);
-          const T* e = reinterpret_cast<const T*>(&ch);
+        const T* e = reinterpret_cast<const T*>(&vc_[k]);
 #pragma unroll
-          for (int j = 0; j < EPC; ++j) z[k][j] = fmaf(pr, E::to_f(e[j]), z[k][j]);
-        }
+        for (int j = 0; j < EPC; ++j) z[k][j] = fmaf(pr, E::to_f(e[j]), z[k][j]);
       }
     }
   }
-  // reduce over the 16 row groups of the wave (lanes with equal c)
+  // merge the 16 row groups of the wave (lanes with equal c hold the same chunks)
 #pragma unroll
-  for (int m = 4; m <= 32; m <<= 1) {
-    l += __shfl_xor(l, m, 64);
+  for (int msk = 4; msk <= 32; msk <<= 1) {
+    const float mo = __shfl_xor(m, msk, 64);
+    const float lo = __shfl_xor(l, msk, 64);
+    const float mn = fmaxf(m, mo);
+    const float ms = mn == kNegInf ? 0.f : mn;
+    const float a = fexp2(m - ms), ao = fexp2(mo - ms);
+    l = l * a + lo * ao;
 #pragma unroll
     for (int k = 0; k < MAXC; ++k)
 #pragma unroll
-      for (int j = 0; j < EPC; ++j) z[k][j] += __shfl_xor(z[k][j], m, 64);
+      for (int j = 0; j < EPC; ++j) z[k][j] = z[k][j] * a + __shfl_xor(z[k][j], msk, 64) * ao;
+    m = mn;
   }
   if (rr == 0) {
 #pragma unroll
@@ -173,51 +190,84 @@ __global__ void __launch_bounds__(256) relation_decode_kernel(const DecParams p)
       const int kc = c + 4 * k;
       if (kc < nch)
 #pragma unroll
-        for (int j = 0; j < EPC; ++j) red[wave * DP + kc * EPC + j] = z[k][j];
+        for (int j = 0; j < EPC; ++j) red[wave * (DP + 2) + 2 + kc * EPC + j] = z[k][j];
     }
-    if (c == 0) red[4 * DP + wave] = l;
+    if (c == 0) {
+      red[wave * (DP + 2)] = m;
+      red[wave * (DP + 2) + 1] = l;
+    }
   }
   __syncthreads();
-  float* part = p.part + (int64_t(bh) * p.nsplit + split) * (D + 2);
-  for (int d = tid; d < D; d += 256) part[2 + d] = red[d] + red[DP + d] + red[2 * DP + d] + red[3 * DP + d];
-  if (tid == 0) {
-    part[0] = nrows > 0 ? mx : kNegInf;
-    part[1] = red[4 * DP] + red[4 * DP + 1] + red[4 * DP + 2] + red[4 * DP + 3];
+  // merge the 4 waves -> this split's partial
+  {
+    float mw[4];
+    float M = kNegInf;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      mw[w] = red[w * (DP + 2)];
+      M = fmaxf(M, mw[w]);
+    }
+    const float Ms = M == kNegInf ? 0.f : M;
+    float* part = p.part + (int64_t(bh) * p.nsplit + split) * (D + 2);
+    for (int d = tid; d < D; d += 256) {
+      float zs = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) zs += red[w * (DP + 2) + 2 + d] * fexp2(mw[w] - Ms);
+      part[2 + d] = zs;
+    }
+    if (tid == 0) {
+      float L = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) L += red[w * (DP + 2) + 1] * fexp2(mw[w] - Ms);
+      part[0] = M;
+      part[1] = L;
+    }
   }
 
-  // ---- the last split of this head merges ----
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) s_last = atomicAdd(&p.counter[bh], 1u) == unsigned(p.nsplit - 1);
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  const float* pb = p.part + int64_t(bh) * p.nsplit * (D + 2);
-  float M = kNegInf;
-  for (int s = 0; s < p.nsplit; ++s) M = fmaxf(M, pb[s * (D + 2)]);
-  const float Ms = M == kNegInf ? 0.f : M;
-  float L = 0.f;
-  for (int s = 0; s < p.nsplit; ++s) {
-    const float ms = pb[s * (D + 2)];
-    const float ls = pb[s * (D + 2) + 1];
-    if (ls > 0.f) L += ls * fexp2(ms - Ms);
-  }
-  // new rows: RoPE'd P2 (sq-style, into red[0..D)) and Givens'd I~ (red[DP..DP+D))
+}
+
+// ------------------------------------------------------------------------------------------------
+// merge: one workgroup per sequence, heads in turn
+// ------------------------------------------------------------------------------------------------
+template <typename T, int DP>
+__global__ void __launch_bounds__(256) relation_decode_merge_kernel(const DecParams p) {
+  using E = Elem<T>;
+  __shared__ float sq[DP];
+  __shared__ float knew[DP];
+  __shared__ float inew[DP];
+  __shared__ float sred[4];
+  __shared__ float sML[2];
+  extern __shared__ float spart[];  // [nact][D + 2], then the split weights [nact]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int bh = blockIdx.x;
+  const int b = bh / p.H, h = bh % p.H;
+  const int D = p.D, half = D / 2;
+  const int stride = D + 2;
+  const int64_t S64 = p.S_used[b];
+  const bool bad = S64 < 0 || S64 >= p.cap;
+  const int S = bad ? 0 : int(S64);
+  const int nact = S > 0 ? (S + p.rps - 1) / p.rps : 1;
+  float* wsp = spart + nact * stride;
+  const float* pb = p.part + int64_t(bh) * p.nsplit * stride;
+  for (int i = tid; i < nact * stride; i += 256) spart[i] = pb[i];
+  // new rows: query and P2 RoPE'd at S, I~ Givens'd with its partner head's raw row
+  const T* q_raw = reinterpret_cast<const T*>(p.p1) + b * p.in_sb + h * D;
   const T* k_raw = reinterpret_cast<const T*>(p.p2) + b * p.in_sb + h * D;
   const T* i_raw = reinterpret_cast<const T*>(p.info) + b * p.in_sb + h * D;
   if (tid < half) {
-    const float x0 = E::to_f(k_raw[tid]), x1 = E::to_f(k_raw[tid + half]);
-    float o0 = x0, o1 = x1;
+    float cs = 1.f, sn = 0.f;
     if (p.inv_freq) {
-      float sn, cs;
       sincosf((float)S * p.inv_freq[tid], &sn, &cs);
       cs = round_to<T>(cs);
       sn = round_to<T>(sn);
-      o0 = x0 * cs - x1 * sn;
-      o1 = x1 * cs + x0 * sn;
     }
-    red[tid] = round_to<T>(o0);
-    red[tid + half] = round_to<T>(o1);
+    const float q0 = E::to_f(q_raw[tid]), q1 = E::to_f(q_raw[tid + half]);
+    const float k0 = E::to_f(k_raw[tid]), k1 = E::to_f(k_raw[tid + half]);
+    sq[tid] = round_to<T>(q0 * cs - q1 * sn);
+    sq[tid + half] = round_to<T>(q1 * cs + q0 * sn);
+    knew[tid] = round_to<T>(k0 * cs - k1 * sn);
+    knew[tid + half] = round_to<T>(k1 * cs + k0 * sn);
   }
   if (tid < D) {
     const float self = E::to_f(i_raw[tid]);
@@ -245,63 +295,84 @@ __global__ void __launch_bounds__(256) relation_decode_kernel(const DecParams p)
       const float oth = E::to_f(reinterpret_cast<const T*>(p.info)[b * p.in_sb + other * D + tid]);
       out = first ? (cs * self - sn * oth) : (sn * oth + cs * self);
     }
-    red[DP + tid] = round_to<T>(out);
+    inew[tid] = round_to<T>(out);
   }
   __syncthreads();
-  // Self score U_SS = <q, P2_S> / sqrt(D)
-  float u = 0.f;
-  for (int d = tid; d < D; d += 256) u = fmaf(sq[d], red[d], u);
+  // split weights 2^(m_s - M) and L = sum_s l_s 2^(m_s - M): wave 0, lanes over splits (fixed order)
+  if (wave == 0) {
+    float mx = kNegInf;
+    for (int s = lane; s < nact; s += 64) mx = fmaxf(mx, spart[s * stride]);
 #pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) u += __shfl_xor(u, m, 64);
-  if (lane == 0) sred[4 + wave] = u;
+    for (int msk = 32; msk >= 1; msk >>= 1) mx = fmaxf(mx, __shfl_xor(mx, msk, 64));
+    const float Ms = mx == kNegInf ? 0.f : mx;
+    float ls = 0.f;
+    for (int s = lane; s < nact; s += 64) {
+      const float w = fexp2(spart[s * stride] - Ms);
+      wsp[s] = w;
+      ls += spart[s * stride + 1] * w;
+    }
+#pragma unroll
+    for (int msk = 32; msk >= 1; msk >>= 1) ls += __shfl_xor(ls, msk, 64);
+    if (lane == 0) {
+      sML[0] = Ms;
+      sML[1] = ls;
+    }
+  } else if (wave == 1) {
+    // Self score U_SS = <q, P2_S> / sqrt(D)
+    float u = 0.f;
+    for (int d = lane; d < D; d += 64) u = fmaf(sq[d], knew[d], u);
+#pragma unroll
+    for (int msk = 32; msk >= 1; msk >>= 1) u += __shfl_xor(u, msk, 64);
+    if (lane == 0) sred[0] = u;
+  }
   __syncthreads();
-  u = (sred[4] + sred[5] + sred[6] + sred[7]) * p.scale;
-  const float sself = sigmoid_acc(u * p.tau_inv);
+  const float Ms = sML[0], L = sML[1];
+  const float sself = sigmoid_acc(sred[0] * p.scale * p.tau_inv);
   const bool has = L > 0.f;
   const float lse = has ? (Ms + __log2f(L)) * kLn2 : kNegInf;
   const float gate = has ? sigmoid_acc(lse - (*p.lam) * logf((float)S + 1.0f) - sself) : 0.f;
   const float invL = has ? 1.0f / L : 0.f;
   T* y = reinterpret_cast<T*>(p.y) + b * p.y_sb + h * D;
+  T* kw = reinterpret_cast<T*>(p.kc) + b * p.kc_sb + h * p.kc_sh + int64_t(S) * p.kc_sr;
+  T* vw = reinterpret_cast<T*>(p.vc) + b * p.vc_sb + h * p.vc_sh + int64_t(S) * p.vc_sr;
   for (int d = tid; d < D; d += 256) {
     float zsum = 0.f;
-    for (int s = 0; s < p.nsplit; ++s) {
-      const float ls = pb[s * (D + 2) + 1];
-      if (ls > 0.f) zsum += pb[s * (D + 2) + 2 + d] *
-                            fexp2(pb[s * (D + 2)] - Ms);
-    }
-    const float yv = (1.0f - gate) * red[DP + d] + gate * zsum * invL;
+#pragma unroll 8
+    for (int s = 0; s < nact; ++s) zsum = fmaf(spart[s * stride + 2 + d], wsp[s], zsum);
+    const float yv = (1.0f - gate) * inew[d] + gate * zsum * invL;
     y[d] = E::from_f(bad ? __builtin_nanf("") : yv);
     if (!bad) {
-      reinterpret_cast<T*>(p.kc_w)[b * p.kc_sb + h * p.kc_sh + int64_t(S) * p.kc_sr + d] = E::from_f(red[d]);
-      reinterpret_cast<T*>(p.vc_w)[b * p.vc_sb + h * p.vc_sh + int64_t(S) * p.vc_sr + d] = E::from_f(red[DP + d]);
+      kw[d] = E::from_f(knew[d]);
+      vw[d] = E::from_f(inew[d]);
     }
   }
   if (tid == 0) {
     p.g[bh] = bad ? __builtin_nanf("") : gate;
-    atomicExch(&p.counter[bh], 0u);
-    if (p.flags & MOTE_DECODE_ADVANCE) {
-      __threadfence();
-      if (atomicAdd(&p.counter[BH], 1u) == unsigned(BH - 1)) {
-        for (int bb = 0; bb < p.B; ++bb) atomicAdd(reinterpret_cast<unsigned long long*>(&p.S[bb]), 1ull);
-        atomicExch(&p.counter[BH], 0u);
-      }
-    }
+    // every reader of S[b] in this step is done: the split kernel ran before this one, and the
+    // merge workgroups read the copy in S_used
+    if (h == 0 && (p.flags & MOTE_DECODE_ADVANCE)) p.S[b] = S64 + 1;
   }
 }
 
-static int decode_nsplit(const mote_relation_decode_args* a) {
-  const int BH = a->B * a->H;
-  int ns = (512 + BH - 1) / BH;
-  ns = ns < 1 ? 1 : (ns > 64 ? 64 : ns);
-  const int need = (a->capacity + kDecRowsMax - 1) / kDecRowsMax;
-  return ns < need ? need : ns;
+// rows per split: a multiple of 64 chosen so that about 2048 workgroups cover a full cache
+static void decode_shape(const mote_relation_decode_args* a, int& rps, int& nsplit) {
+  const int64_t BH = int64_t(a->B) * a->H;
+  int64_t mult = (BH * ((a->capacity + 63) / 64) + 2047) / 2048;
+  if (mult < 1) mult = 1;
+  rps = int(64 * mult);
+  nsplit = (a->capacity + rps - 1) / rps;
+  while (nsplit > kDecMaxSplits) {
+    rps += 64;
+    nsplit = (a->capacity + rps - 1) / rps;
+  }
 }
 
 size_t decode_workspace_bytes(const mote_relation_decode_args* a) {
+  int rps, nsplit;
+  decode_shape(a, rps, nsplit);
   const size_t BH = size_t(a->B) * a->H;
-  const size_t counters = (BH + 1) * sizeof(unsigned);
-  const size_t coff = (counters + 255) & ~size_t(255);
-  return coff + BH * size_t(decode_nsplit(a)) * size_t(a->D + 2) * sizeof(float);
+  const size_t parts = (BH * size_t(nsplit) * size_t(a->D + 2) * sizeof(float) + 255) & ~size_t(255);
+  return parts + size_t(a->B) * sizeof(int64_t);
 }
 
 int launch_decode(const mote_relation_decode_args* a, hipStream_t stream) {
@@ -320,33 +391,39 @@ int launch_decode(const mote_relation_decode_args* a, hipStream_t stream) {
   p.p1 = a->p1; p.p2 = a->p2; p.info = a->info; p.in_sb = a->in_sb;
   p.kc = a->cache_p2.data; p.kc_sb = a->cache_p2.stride_b; p.kc_sh = a->cache_p2.stride_h; p.kc_sr = a->cache_p2.stride_r;
   p.vc = a->cache_info.data; p.vc_sb = a->cache_info.stride_b; p.vc_sh = a->cache_info.stride_h; p.vc_sr = a->cache_info.stride_r;
-  p.kc_w = a->cache_p2.data; p.vc_w = a->cache_info.data;
   p.y = a->y; p.y_sb = a->y_sb; p.g = a->g;
   const size_t BH = size_t(a->B) * a->H;
-  const size_t coff = ((BH + 1) * sizeof(unsigned) + 255) & ~size_t(255);
-  p.counter = reinterpret_cast<unsigned*>(a->workspace);
-  p.part = reinterpret_cast<float*>(reinterpret_cast<char*>(a->workspace) + coff);
+  decode_shape(a, p.rps, p.nsplit);
+  p.part = reinterpret_cast<float*>(a->workspace);
+  const size_t parts = (BH * size_t(p.nsplit) * size_t(a->D + 2) * sizeof(float) + 255) & ~size_t(255);
+  p.S_used = reinterpret_cast<int64_t*>(reinterpret_cast<char*>(a->workspace) + parts);
   p.B = a->B; p.H = a->H; p.D = a->D; p.cap = a->capacity; p.parity = a->layer_parity & 1; p.flags = a->flags;
-  p.nsplit = decode_nsplit(a);
   p.scale = 1.0f / sqrtf((float)a->D);
   p.tau_inv = 1.0f / a->tau_s;
   const int grid = int(BH) * p.nsplit;
+  const size_t shmem = size_t(p.nsplit) * (a->D + 3) * sizeof(float);
   const int DP = padded_dim(a->D);
+#define MOTE_DEC_LAUNCH(T_, DP_)                                                                               \
+  do {                                                                                                       \
+    hipLaunchKernelGGL((relation_decode_kernel<T_, DP_>), dim3(grid), dim3(256), 0, stream, p);              \
+    hipLaunchKernelGGL((relation_decode_merge_kernel<T_, DP_>), dim3(BH), dim3(256), shmem, stream, p);      \
+  } while (0)
   if (a->dtype == MOTE_BF16) {
     switch (DP) {
-      case 32: hipLaunchKernelGGL((relation_decode_kernel<bf16_t, 32>), dim3(grid), dim3(256), 0, stream, p); break;
-      case 64: hipLaunchKernelGGL((relation_decode_kernel<bf16_t, 64>), dim3(grid), dim3(256), 0, stream, p); break;
-      case 96: hipLaunchKernelGGL((relation_decode_kernel<bf16_t, 96>), dim3(grid), dim3(256), 0, stream, p); break;
-      default: hipLaunchKernelGGL((relation_decode_kernel<bf16_t, 128>), dim3(grid), dim3(256), 0, stream, p); break;
+      case 32: MOTE_DEC_LAUNCH(bf16_t, 32); break;
+      case 64: MOTE_DEC_LAUNCH(bf16_t, 64); break;
+      case 96: MOTE_DEC_LAUNCH(bf16_t, 96); break;
+      default: MOTE_DEC_LAUNCH(bf16_t, 128); break;
     }
   } else {
     switch (DP) {
-      case 32: hipLaunchKernelGGL((relation_decode_kernel<float, 32>), dim3(grid), dim3(256), 0, stream, p); break;
-      case 64: hipLaunchKernelGGL((relation_decode_kernel<float, 64>), dim3(grid), dim3(256), 0, stream, p); break;
-      case 96: hipLaunchKernelGGL((relation_decode_kernel<float, 96>), dim3(grid), dim3(256), 0, stream, p); break;
-      default: hipLaunchKernelGGL((relation_decode_kernel<float, 128>), dim3(grid), dim3(256), 0, stream, p); break;
+      case 32: MOTE_DEC_LAUNCH(float, 32); break;
+      case 64: MOTE_DEC_LAUNCH(float, 64); break;
+      case 96: MOTE_DEC_LAUNCH(float, 96); break;
+      default: MOTE_DEC_LAUNCH(float, 128); break;
     }
   }
+#undef MOTE_DEC_LAUNCH
   return check_launch("relation_decode");
 }
 

@@ -209,6 +209,221 @@ __global__ void __launch_bounds__(256) sum_partials_kernel(const float* partial,
   if (threadIdx.x == 0) out[pr] = red[0];
 }
 
+// ------------------------------------------------------------------------------------------------
+// Vectorised kernels (16-byte chunks), used when D/2 is a multiple of the chunk. A block handles
+// kRopeRows rows; each thread loops over (row, unit) pairs: a RoPE unit is one chunk k..k+EPC of
+// the first half of one head, for p1 and p2 together (the angles are shared); a Givens unit is one
+// chunk of both heads of one pair.
+// ------------------------------------------------------------------------------------------------
+constexpr int kRopeRows = 8;
+
+template <typename T>
+__device__ __forceinline__ void rope_chunk_fwd(const T* x, T* o, int half, int k0, const float* ang_c, const float* ang_s) {
+  using E = Elem<T>;
+  constexpr int EPC = 16 / sizeof(T);
+  const Chunk a = load_chunk(x + k0), b = load_chunk(x + half + k0);
+  const T* ea = reinterpret_cast<const T*>(&a);
+  const T* eb = reinterpret_cast<const T*>(&b);
+  Chunk ra, rb;
+  T* oa = reinterpret_cast<T*>(&ra);
+  T* ob = reinterpret_cast<T*>(&rb);
+#pragma unroll
+  for (int e = 0; e < EPC; ++e) {
+    const float x0 = E::to_f(ea[e]), x1 = E::to_f(eb[e]);
+    oa[e] = E::from_f(x0 * ang_c[e] - x1 * ang_s[e]);
+    ob[e] = E::from_f(x1 * ang_c[e] + x0 * ang_s[e]);
+  }
+  store_chunk(o + k0, ra);
+  store_chunk(o + half + k0, rb);
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) rope_givens_fwd_vec_kernel(const RopeParams p) {
+  using E = Elem<T>;
+  constexpr int EPC = 16 / sizeof(T);
+  const int HD = p.H * p.D, half = p.D / 2;
+  const int ur = p.H * (half / EPC);          // RoPE units per row
+  const int ug = (p.H / 2) * (p.D / EPC);     // Givens units per row
+  const int upr = ur + ug;
+  const int rows = p.B * p.T;
+  const int row0 = blockIdx.x * kRopeRows;
+  for (int u = threadIdx.x; u < kRopeRows * upr; u += blockDim.x) {
+    const int row = row0 + u / upr, k = u % upr;
+    if (row >= rows) break;
+    const int b = row / p.T, t = row % p.T;
+    const T* x = reinterpret_cast<const T*>(p.qkv) + int64_t(b) * p.qkv_sb + int64_t(t) * p.qkv_sr;
+    if (k < ur) {
+      const int hd = k / (half / EPC), k0 = (k % (half / EPC)) * EPC;
+      float cs[EPC], sn[EPC];
+      const float pos = (float)(p.pos0 + t);
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) {
+        if (p.inv_freq) {
+          sincosf(pos * p.inv_freq[k0 + e], &sn[e], &cs[e]);
+          cs[e] = rnd<T>(cs[e]);
+          sn[e] = rnd<T>(sn[e]);
+        } else {
+          cs[e] = 1.f;
+          sn[e] = 0.f;
+        }
+      }
+      T* o1 = reinterpret_cast<T*>(p.o1) + int64_t(b) * p.o1_sb + int64_t(hd) * p.o1_sh + int64_t(t) * p.o1_sr;
+      T* o2 = reinterpret_cast<T*>(p.o2) + int64_t(b) * p.o2_sb + int64_t(hd) * p.o2_sh + int64_t(t) * p.o2_sr;
+      rope_chunk_fwd<T>(x + hd * p.D, o1, half, k0, cs, sn);
+      rope_chunk_fwd<T>(x + HD + hd * p.D, o2, half, k0, cs, sn);
+    } else {
+      const int kg = k - ur;
+      const int pr = kg / (p.D / EPC), d0 = (kg % (p.D / EPC)) * EPC;
+      int ha, hb;
+      if (p.parity == 0) {
+        ha = 2 * pr;
+        hb = 2 * pr + 1;
+      } else {
+        ha = 2 * pr + 1;
+        hb = (2 * pr + 2) % p.H;
+      }
+      const T* xi = x + 2 * HD;
+      const Chunk ca = load_chunk(xi + ha * p.D + d0), cb = load_chunk(xi + hb * p.D + d0);
+      Chunk ra = ca, rb = cb;
+      if (p.theta) {
+        float sn, c;
+        sincosf(p.theta[pr], &sn, &c);
+        c = rnd<T>(c);
+        sn = rnd<T>(sn);
+        const T* ea = reinterpret_cast<const T*>(&ca);
+        const T* eb = reinterpret_cast<const T*>(&cb);
+        T* oa = reinterpret_cast<T*>(&ra);
+        T* ob = reinterpret_cast<T*>(&rb);
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) {
+          const float a = E::to_f(ea[e]), bb = E::to_f(eb[e]);
+          oa[e] = E::from_f(c * a - sn * bb);
+          ob[e] = E::from_f(sn * a + c * bb);
+        }
+      }
+      T* o3 = reinterpret_cast<T*>(p.o3) + int64_t(b) * p.o3_sb + int64_t(t) * p.o3_sr;
+      store_chunk(o3 + int64_t(ha) * p.o3_sh + d0, ra);
+      store_chunk(o3 + int64_t(hb) * p.o3_sh + d0, rb);
+    }
+  }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) rope_givens_bwd_vec_kernel(const RopeBwdParams p) {
+  using E = Elem<T>;
+  constexpr int EPC = 16 / sizeof(T);
+  constexpr int kMaxPairChunks = 2048;  // LDS slots for d theta partials (kRopeRows * H/2 * D/EPC)
+  __shared__ float dth[kMaxPairChunks];
+  const int HD = p.H * p.D, half = p.D / 2;
+  const int npair = p.H / 2, cpg = p.D / EPC;   // chunks per head
+  const int ur = p.H * (half / EPC);
+  const int ug = npair * cpg;
+  const int upr = ur + ug;
+  const int rows = p.B * p.T;
+  const int row0 = blockIdx.x * kRopeRows;
+  for (int u = threadIdx.x; u < kRopeRows * upr; u += blockDim.x) {
+    const int rl = u / upr, k = u % upr;
+    const int row = row0 + rl;
+    if (row >= rows) break;
+    const int b = row / p.T, t = row % p.T;
+    T* dx = reinterpret_cast<T*>(p.dqkv) + int64_t(b) * p.dq_sb + int64_t(t) * p.dq_sr;
+    if (k < ur) {
+      const int hd = k / (half / EPC), k0 = (k % (half / EPC)) * EPC;
+      float cs[EPC], sn[EPC];
+      const float pos = (float)(p.pos0 + t);
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) {
+        if (p.inv_freq) {
+          sincosf(pos * p.inv_freq[k0 + e], &sn[e], &cs[e]);
+          cs[e] = rnd<T>(cs[e]);
+          sn[e] = rnd<T>(sn[e]);
+        } else {
+          cs[e] = 1.f;
+          sn[e] = 0.f;
+        }
+      }
+      // transposed rotation: dx_k = d_k c + d_{k+h} s, dx_{k+h} = d_{k+h} c - d_k s
+      float msn[EPC];
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) msn[e] = -sn[e];
+      const T* g1 = reinterpret_cast<const T*>(p.g1) + int64_t(b) * p.g1_sb + int64_t(hd) * p.g1_sh + int64_t(t) * p.g1_sr;
+      const T* g2 = reinterpret_cast<const T*>(p.g2) + int64_t(b) * p.g2_sb + int64_t(hd) * p.g2_sh + int64_t(t) * p.g2_sr;
+      rope_chunk_fwd<T>(g1, dx + hd * p.D, half, k0, cs, msn);
+      rope_chunk_fwd<T>(g2, dx + HD + hd * p.D, half, k0, cs, msn);
+    } else {
+      const int kg = k - ur;
+      const int pr = kg / cpg, d0 = (kg % cpg) * EPC;
+      int ha, hb;
+      if (p.parity == 0) {
+        ha = 2 * pr;
+        hb = 2 * pr + 1;
+      } else {
+        ha = 2 * pr + 1;
+        hb = (2 * pr + 2) % p.H;
+      }
+      const T* g3 = reinterpret_cast<const T*>(p.g3) + int64_t(b) * p.g3_sb + int64_t(t) * p.g3_sr;
+      const Chunk ga = load_chunk(g3 + int64_t(ha) * p.g3_sh + d0), gb = load_chunk(g3 + int64_t(hb) * p.g3_sh + d0);
+      Chunk ra = ga, rb = gb;
+      if (p.theta) {
+        float sn, c;
+        sincosf(p.theta[pr], &sn, &c);
+        const float cr = rnd<T>(c), sr = rnd<T>(sn);
+        const T* xi = reinterpret_cast<const T*>(p.qkv) + int64_t(b) * p.qkv_sb + int64_t(t) * p.qkv_sr + 2 * HD;
+        const Chunk xa = load_chunk(xi + ha * p.D + d0), xb = load_chunk(xi + hb * p.D + d0);
+        const T* ega = reinterpret_cast<const T*>(&ga);
+        const T* egb = reinterpret_cast<const T*>(&gb);
+        const T* exa = reinterpret_cast<const T*>(&xa);
+        const T* exb = reinterpret_cast<const T*>(&xb);
+        T* oa = reinterpret_cast<T*>(&ra);
+        T* ob = reinterpret_cast<T*>(&rb);
+        float acc = 0.f;
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) {
+          const float a = E::to_f(exa[e]), bb = E::to_f(exb[e]);
+          const float da = E::to_f(ega[e]), db = E::to_f(egb[e]);
+          oa[e] = E::from_f(cr * da + sr * db);
+          ob[e] = E::from_f(cr * db - sr * da);
+          acc += da * (-sn * a - c * bb) + db * (c * a - sn * bb);
+        }
+        dth[(rl * npair + pr) * cpg + kg % cpg] = acc;
+      }
+      store_chunk(dx + 2 * HD + ha * p.D + d0, ra);
+      store_chunk(dx + 2 * HD + hb * p.D + d0, rb);
+    }
+  }
+  if (!p.theta) return;
+  __syncthreads();
+  // per (row, pair): fixed-order sum over the head's chunks
+  for (int q = threadIdx.x; q < kRopeRows * npair; q += blockDim.x) {
+    const int rl = q / npair, pr = q % npair;
+    const int row = row0 + rl;
+    if (row >= rows) continue;
+    float acc = 0.f;
+    for (int c = 0; c < cpg; ++c) acc += dth[(rl * npair + pr) * cpg + c];
+    p.partial[int64_t(row) * npair + pr] = acc;
+  }
+}
+
+static bool al16(const void* ptr, int64_t s0, int64_t s1, int64_t s2, int es) {
+  const int64_t m = 16 / es;
+  return (reinterpret_cast<uintptr_t>(ptr) % 16 == 0) && s0 % m == 0 && s1 % m == 0 && s2 % m == 0;
+}
+
+static bool aligned16(const mote_rope_givens_args* a) {
+  const int es = a->dtype == MOTE_BF16 ? 2 : 4;
+  return al16(a->qkv, a->qkv_sb, a->qkv_sr, 0, es) && al16(a->p1.data, a->p1.stride_b, a->p1.stride_h, a->p1.stride_r, es) &&
+         al16(a->p2.data, a->p2.stride_b, a->p2.stride_h, a->p2.stride_r, es) &&
+         al16(a->info.data, a->info.stride_b, a->info.stride_h, a->info.stride_r, es);
+}
+
+static bool aligned16_bwd(const mote_rope_givens_bwd_args* a) {
+  const int es = a->dtype == MOTE_BF16 ? 2 : 4;
+  return al16(a->qkv, a->qkv_sb, a->qkv_sr, 0, es) && al16(a->dqkv, a->dqkv_sb, a->dqkv_sr, 0, es) &&
+         al16(a->dp1.data, a->dp1.stride_b, a->dp1.stride_h, a->dp1.stride_r, es) &&
+         al16(a->dp2.data, a->dp2.stride_b, a->dp2.stride_h, a->dp2.stride_r, es) &&
+         al16(a->dinfo.data, a->dinfo.stride_b, a->dinfo.stride_h, a->dinfo.stride_r, es);
+}
+
 static int check_rope_common(int dtype, int B, int T, int H, int D, const void* qkv) {
   if (dtype != MOTE_F32 && dtype != MOTE_BF16) return set_error(MOTE_ERR_ARGUMENT, "rope_givens: bad dtype %d", dtype);
   if (!qkv) return set_error(MOTE_ERR_ARGUMENT, "rope_givens: null qkv");
@@ -230,10 +445,16 @@ int launch_rope_givens_fwd(const mote_rope_givens_args* a, hipStream_t stream) {
   p.inv_freq = a->inv_freq; p.theta = a->theta;
   p.B = a->B; p.T = a->T; p.H = a->H; p.D = a->D; p.pos0 = a->pos0; p.parity = a->layer_parity & 1;
   const int rows = a->B * a->T;
-  if (a->dtype == MOTE_BF16)
-    hipLaunchKernelGGL(rope_givens_fwd_kernel<bf16_t>, dim3(rows), dim3(256), 0, stream, p);
-  else
-    hipLaunchKernelGGL(rope_givens_fwd_kernel<float>, dim3(rows), dim3(256), 0, stream, p);
+  const int epc = a->dtype == MOTE_BF16 ? 8 : 4;
+  const bool vec = (a->D / 2) % epc == 0 && aligned16(a);
+  const int vblocks = (rows + kRopeRows - 1) / kRopeRows;
+  if (a->dtype == MOTE_BF16) {
+    if (vec) hipLaunchKernelGGL(rope_givens_fwd_vec_kernel<bf16_t>, dim3(vblocks), dim3(256), 0, stream, p);
+    else hipLaunchKernelGGL(rope_givens_fwd_kernel<bf16_t>, dim3(rows), dim3(256), 0, stream, p);
+  } else {
+    if (vec) hipLaunchKernelGGL(rope_givens_fwd_vec_kernel<float>, dim3(vblocks), dim3(256), 0, stream, p);
+    else hipLaunchKernelGGL(rope_givens_fwd_kernel<float>, dim3(rows), dim3(256), 0, stream, p);
+  }
   return check_launch("rope_givens_fwd");
 }
 
@@ -260,10 +481,16 @@ int launch_rope_givens_bwd(const mote_rope_givens_bwd_args* a, hipStream_t strea
   p.partial = reinterpret_cast<float*>(a->workspace);
   p.B = a->B; p.T = a->T; p.H = a->H; p.D = a->D; p.pos0 = a->pos0; p.parity = a->layer_parity & 1;
   const int rows = a->B * a->T;
-  if (a->dtype == MOTE_BF16)
-    hipLaunchKernelGGL(rope_givens_bwd_kernel<bf16_t>, dim3(rows), dim3(256), 0, stream, p);
-  else
-    hipLaunchKernelGGL(rope_givens_bwd_kernel<float>, dim3(rows), dim3(256), 0, stream, p);
+  const int epc = a->dtype == MOTE_BF16 ? 8 : 4;
+  const bool vec = (a->D / 2) % epc == 0 && aligned16_bwd(a) && kRopeRows * (a->H / 2) * (a->D / epc) <= 2048;
+  const int vblocks = (rows + kRopeRows - 1) / kRopeRows;
+  if (a->dtype == MOTE_BF16) {
+    if (vec) hipLaunchKernelGGL(rope_givens_bwd_vec_kernel<bf16_t>, dim3(vblocks), dim3(256), 0, stream, p);
+    else hipLaunchKernelGGL(rope_givens_bwd_kernel<bf16_t>, dim3(rows), dim3(256), 0, stream, p);
+  } else {
+    if (vec) hipLaunchKernelGGL(rope_givens_bwd_vec_kernel<float>, dim3(vblocks), dim3(256), 0, stream, p);
+    else hipLaunchKernelGGL(rope_givens_bwd_kernel<float>, dim3(rows), dim3(256), 0, stream, p);
+  }
   rc = check_launch("rope_givens_bwd");
   if (rc || !a->theta) return rc;
   hipLaunchKernelGGL(sum_partials_kernel, dim3(a->H / 2), dim3(256), 0, stream, p.partial, rows, a->H / 2, a->dtheta);
