@@ -366,6 +366,305 @@ __global__ void __launch_bounds__(NW * 64) relation_fwd_kernel(const FwdParams p
 }
 
 // ------------------------------------------------------------------------------------------------
+// bf16 kernel for D in {32, 64, 96, 128}: direct-to-LDS staging
+//
+// P2 and I~ blocks of 64 rows go global -> LDS with global_load_lds_dwordx4 (lane l of a wave's
+// instruction lands at M0 + 16 l), double-buffered, so no registers carry the staging. Both tiles
+// are row-major with the 16-byte chunks of a row XOR-swizzled (tile_swz) against bank conflicts; for
+// every read pattern below the swizzle value is a per-lane constant. K fragments are ds_read_b128;
+// V^T fragments are ds_read_b64_tr_b16: within a 16-lane group, lane 4k+m pointing at row kb+k,
+// columns [d0+4m, d0+4m+4) hands lane i the column d0+i of rows kb..kb+3 -- the permuted-k order
+// of the P^T fragments. The block math is compiled twice, for diagonal (masked) blocks and for the
+// bulk of the rows.
+// ------------------------------------------------------------------------------------------------
+template <int DP>
+__device__ __forceinline__ int tile_swz(int row) {
+  if constexpr (DP == 64) return (row >> 1) & 7;
+  else if constexpr (DP == 128) return row & 7;
+  else return (row >> 2) & 3;
+}
+
+typedef __attribute__((ext_vector_type(4))) short s16x4;
+
+__device__ __forceinline__ bf16x4 lds_tr4(const bf16_t* p) {
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((s16x4 __attribute__((address_space(3)))*)(p));
+  return __builtin_bit_cast(bf16x4, v);
+}
+
+template <int DP, bool MASKED>
+__device__ __forceinline__ void fwd_block(const bf16_t* Ks, const bf16_t* Vs, const typename Elem<bf16_t>::Frag (&qf)[2][DP / 32],
+                                          f32x4 (&oacc)[DP / 16][2], float (&m_run)[2], float (&l_run)[2], int j0,
+                                          const int (&qabs)[2], float c2, int li, int lg) {
+  using E = Elem<bf16_t>;
+  using Frag = E::Frag;
+  constexpr int KS = DP / 32, DT = DP / 16, NT = 4, CPR = DP / 8;
+  const int kswz = tile_swz<DP>(li);  // rows 16t + li
+  f32x4 sacc[NT][2];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) sacc[t][s] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int row = 16 * t + li;
+      const int ch = (4 * ks + lg) ^ (DP == 128 ? tile_swz<DP>(row) : kswz);
+      const Frag kf = E::load8(Ks + row * DP + ch * 8);
+#pragma unroll
+      for (int s = 0; s < 2; ++s) sacc[t][s] = E::mma(kf, qf[s][ks], sacc[t][s]);
+    }
+  }
+  float bmax[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    float mx = kNegInf;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float u2 = sacc[t][s][r] * c2;
+        float e = u2 * frcp(1.0f + fexp2(-u2));
+        if constexpr (MASKED) {
+          if (j0 + 16 * t + 4 * lg + r >= qabs[s]) e = kNegInf;
+        }
+        sacc[t][s][r] = e;
+        mx = fmaxf(mx, e);
+      }
+    }
+    mx = fmaxf(mx, wave_xor(mx, 16));
+    mx = fmaxf(mx, wave_xor(mx, 32));
+    bmax[s] = mx;
+  }
+  const bool need = (bmax[0] > m_run[0] + kRescale) || (bmax[1] > m_run[1] + kRescale);
+  if (__ballot(need) != 0ull) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const float mn = bmax[s] > m_run[s] + kRescale ? bmax[s] : m_run[s];
+      const float alpha = fexp2(m_run[s] - (mn == kNegInf ? 0.f : mn));
+      l_run[s] *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) oacc[dt][s] *= alpha;
+      m_run[s] = mn;
+    }
+  }
+  Frag pf[2][2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const float ms = m_run[s] == kNegInf ? 0.f : m_run[s];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      float pv[8];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float pr = fexp2(sacc[2 * kk + h][s][r] - ms);
+          l_run[s] += pr;
+          pv[4 * h + r] = pr;
+        }
+      pf[kk][s] = E::from_f32(pv);
+    }
+  }
+  // V^T fragments: lane (k = li / 4, m = li % 4) of group lg reads row 32kk + 4lg + k (+16 for
+  // slots 4..7), columns 16dt + 4m .. +3
+  const int k4 = li >> 2, m4 = li & 3;
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const int c = 2 * dt + (m4 >> 1);
+      const int r0 = 32 * kk + 4 * lg + k4;
+      const bf16_t* a0 = Vs + r0 * DP + (c ^ tile_swz<DP>(r0)) * 8 + (m4 & 1) * 4;
+      const bf16_t* a1 = Vs + (r0 + 16) * DP + (c ^ tile_swz<DP>(r0 + 16)) * 8 + (m4 & 1) * 4;
+      const bf16x4 lo = lds_tr4(a0), hi = lds_tr4(a1);
+      Frag vf;
+      vf.v = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+      for (int s = 0; s < 2; ++s) oacc[dt][s] = E::mma(vf, pf[kk][s], oacc[dt][s]);
+    }
+  }
+  (void)CPR;
+}
+
+template <int DP, int NW>
+__global__ void __launch_bounds__(NW * 64) relation_fwd_lds_kernel(const FwdParams p) {
+  using E = Elem<bf16_t>;
+  using Frag = E::Frag;
+  constexpr int KS = DP / 32, DT = DP / 16, BN = 64, BM = NW * 32;
+  constexpr int CPR = DP / 8;                 // 16-byte chunks per row
+  constexpr int TILE = BN * DP;               // elements per tile
+  constexpr int NINS = BN * CPR / 64;         // wave instructions per tile
+  constexpr int NINS_W = (2 * NINS + NW - 1) / NW;  // per wave, K and V tiles together
+  __shared__ __align__(16) bf16_t smem[2 * 2 * TILE];  // [stage][K | V][BN][DP]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const int bid = blockIdx.x;
+  const int h = bid % p.H;
+  const int rest = bid / p.H;
+  const int seq = rest % p.nseq;
+  const int qb = p.nqb - 1 - rest / p.nseq;
+
+  int TQs, TKs, qs;
+  int64_t qoff, koff, voff, yoff, soff;
+  if (p.cu) {
+    const int r0 = p.cu[seq];
+    TQs = p.cu[seq + 1] - r0;
+    TKs = TQs;
+    qs = 0;
+    qoff = int64_t(r0) * p.q_sr;
+    koff = int64_t(r0) * p.k_sr;
+    voff = int64_t(r0) * p.v_sr;
+    yoff = int64_t(r0) * p.y_sr;
+    soff = int64_t(h) * p.total_rows + r0;
+  } else {
+    TQs = p.TQ;
+    TKs = p.TK;
+    qs = p.q_start;
+    qoff = int64_t(seq) * p.q_sb;
+    koff = int64_t(seq) * p.k_sb;
+    voff = int64_t(seq) * p.v_sb;
+    yoff = int64_t(seq) * p.y_sb;
+    soff = (int64_t(seq) * p.H + h) * p.TQ;
+  }
+  if (qb * BM >= TQs) return;
+  const bf16_t* qbase = reinterpret_cast<const bf16_t*>(p.p1) + qoff + int64_t(h) * p.q_sh;
+  const bf16_t* kbase = reinterpret_cast<const bf16_t*>(p.p2) + koff + int64_t(h) * p.k_sh;
+  const bf16_t* vbase = reinterpret_cast<const bf16_t*>(p.info) + voff + int64_t(h) * p.v_sh;
+  bf16_t* ybase = reinterpret_cast<bf16_t*>(p.y) + yoff + int64_t(h) * p.y_sh;
+
+  const int q0 = qb * BM + wave * 32;
+  const bool wave_active = q0 < TQs;
+  Frag qf[2][KS];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const int qi = q0 + 16 * s + li;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      qf[s][ks] = qi < TQs ? E::load8(qbase + int64_t(qi) * p.q_sr + 32 * ks + 8 * lg) : E::zero();
+  }
+  const int qlast_wg = min(TQs, (qb + 1) * BM) - 1;
+  const int kend = qs + qlast_wg;
+  const int nkb = (kend + BN - 1) / BN;
+  const int wave_kend = wave_active ? qs + min(q0 + 32, TQs) - 1 : 0;
+  const int wave_q0abs = qs + q0;
+  int qabs[2];
+  qabs[0] = qs + q0 + li;
+  qabs[1] = qs + q0 + 16 + li;
+
+  // this lane's share of the staging: instruction n of tile X covers LDS chunks 64n .. 64n+63
+  int st_row[NINS_W], st_col[NINS_W];
+#pragma unroll
+  for (int i = 0; i < NINS_W; ++i) {
+    const int n = (wave + NW * i) % NINS;  // instruction within its tile
+    const int q = 64 * n + lane;
+    const int row = q / CPR, phys = q % CPR;
+    st_row[i] = row;
+    st_col[i] = (phys ^ tile_swz<DP>(row)) * 8;
+  }
+  auto issue = [&](int kb, int stage) {
+    const int j0 = kb * BN;
+#pragma unroll
+    for (int i = 0; i < NINS_W; ++i) {
+      const int ins = wave + NW * i;  // 0 .. 2*NINS-1: K tile first, then V
+      if (ins < 2 * NINS) {
+        const bool isv = ins >= NINS;
+        const int n = ins % NINS;
+        const int j = min(j0 + st_row[i], TKs - 1);  // rows past the keys: any finite row (masked)
+        const bf16_t* src = (isv ? vbase + int64_t(j) * p.v_sr : kbase + int64_t(j) * p.k_sr) + st_col[i];
+        bf16_t* dst = smem + (2 * stage + (isv ? 1 : 0)) * TILE + n * 512;
+        __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)src,
+                                         (void __attribute__((address_space(3)))*)dst, 16, 0, 0);
+      }
+    }
+  };
+
+  const float c2 = p.scale * kLog2e;
+  float m_run[2] = {kNegInf, kNegInf};
+  float l_run[2] = {0.f, 0.f};
+  f32x4 oacc[DT][2];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) oacc[dt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  if (nkb > 0) {
+    issue(0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int stage = kb & 1;
+    if (kb + 1 < nkb) issue(kb + 1, stage ^ 1);
+    const int j0 = kb * BN;
+    if (wave_active && j0 < wave_kend) {
+      const bf16_t* Ks = smem + (2 * stage) * TILE;
+      const bf16_t* Vs = Ks + TILE;
+      if (j0 + BN > wave_q0abs)
+        fwd_block<DP, true>(Ks, Vs, qf, oacc, m_run, l_run, j0, qabs, c2, li, lg);
+      else
+        fwd_block<DP, false>(Ks, Vs, qf, oacc, m_run, l_run, j0, qabs, c2, li, lg);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+  if (!wave_active) return;
+
+  const float lam = *p.lam;
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    float lt = l_run[s];
+    lt += wave_xor(lt, 16);
+    lt += wave_xor(lt, 32);
+    const int qi = q0 + 16 * s + li;
+    const bool qv = qi < TQs;
+    const int qa = qs + qi;
+    const bool has = lt > 0.f;
+    const float lse = has ? (m_run[s] + __log2f(lt)) * kLn2 : kNegInf;
+    const float inv_l = has ? 1.0f / lt : 0.f;
+    float ud = 0.f;
+    if (qv) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const Frag kr = E::load8(kbase + int64_t(qa) * p.k_sr + 32 * ks + 8 * lg);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ud = fmaf((float)qf[s][ks].v[j], (float)kr.v[j], ud);
+      }
+    }
+    ud += wave_xor(ud, 16);
+    ud += wave_xor(ud, 32);
+    const float sself = sigmoid_acc(ud * p.scale * p.tau_inv);
+    const float gate = has ? sigmoid_acc(lse - lam * logf((float)qa + 1.0f) - sself) : 0.f;
+    if (!qv) continue;
+    const bf16_t* irow = vbase + int64_t(qa) * p.v_sr;
+    bf16_t* yrow = ybase + int64_t(qi) * p.y_sr;
+    float* brow = p.ibar + (soff + qi) * int64_t(DP);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const int d0 = 16 * dt + 4 * lg;
+      const uint2 iv = *reinterpret_cast<const uint2*>(irow + d0);
+      const float ivf[4] = {bf2f(iv.x & 0xffffu), bf2f(iv.x >> 16), bf2f(iv.y & 0xffffu), bf2f(iv.y >> 16)};
+      float ib[4], yv[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        ib[r] = oacc[dt][s][r] * inv_l;
+        yv[r] = (1.0f - gate) * ivf[r] + gate * ib[r];
+      }
+      uint2 pk;
+      pk.x = uint32_t(f2bf(yv[0])) | (uint32_t(f2bf(yv[1])) << 16);
+      pk.y = uint32_t(f2bf(yv[2])) | (uint32_t(f2bf(yv[3])) << 16);
+      *reinterpret_cast<uint2*>(yrow + d0) = pk;
+      *reinterpret_cast<float4*>(brow + d0) = make_float4(ib[0], ib[1], ib[2], ib[3]);
+    }
+    if (lg == 0) {
+      p.lse[soff + qi] = lse;
+      p.g[soff + qi] = gate;
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
 // host launcher
 // ------------------------------------------------------------------------------------------------
 template <typename T, int DP, int BN, int NW>
@@ -430,7 +729,16 @@ int launch_fwd(const mote_relation_fwd_args* a, hipStream_t stream) {
   const int64_t units = int64_t(a->B) * a->H;
   const int nqb4 = (a->TQ + 127) / 128;
   const bool wide = units * nqb4 >= 512;
-  if (a->dtype == MOTE_BF16) {
+  if (a->dtype == MOTE_BF16 && DP == a->D) {
+    fp.nqb = (a->TQ + 63) / 64;
+    const int nb = int(units * fp.nqb);
+    switch (DP) {
+      case 32: hipLaunchKernelGGL((relation_fwd_lds_kernel<32, 2>), dim3(nb), dim3(128), 0, stream, fp); break;
+      case 64: hipLaunchKernelGGL((relation_fwd_lds_kernel<64, 2>), dim3(nb), dim3(128), 0, stream, fp); break;
+      case 96: hipLaunchKernelGGL((relation_fwd_lds_kernel<96, 2>), dim3(nb), dim3(128), 0, stream, fp); break;
+      default: hipLaunchKernelGGL((relation_fwd_lds_kernel<128, 2>), dim3(nb), dim3(128), 0, stream, fp); break;
+    }
+  } else if (a->dtype == MOTE_BF16) {
     if (wide) {
       fp.nqb = nqb4;
       launch_fwd_dp<bf16_t, 64, 4>(fp, DP, int(units * fp.nqb), stream);
