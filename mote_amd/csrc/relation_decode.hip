@@ -9,11 +9,11 @@
 // softmax per row group (running max raised lazily, by more than 2^8 only), merges its row groups and
 // waves, and writes (max, l, z[D]) to the workspace.
 //
-// Merge kernel. One workgroup per sequence: for each head it loads the partials into LDS (parallel,
+// Merge kernel. One workgroup per (sequence, head): it loads the head's partials into LDS (parallel,
 // coalesced), merges them in a fixed order, computes the Self score from the new row,
 // g = sigmoid(LSE - lam ln(S+1) - S_self) and Y = (1-g) I~_S + g z/l, and appends the new P2 / I~ row
-// at S; with MOTE_DECODE_ADVANCE it then adds 1 to S[b] (every reader of S[b] in this step has run:
-// the split kernel finished before, and this workgroup is its only other reader).
+// at S. The split kernel copies S[b] to S_used[b] and the merge reads only that copy, so with
+// MOTE_DECODE_ADVANCE the head-0 workgroup can add 1 to S[b] without racing the other heads.
 // The kernel boundary orders the partials; there is no in-kernel device-scope handshake (on gfx950
 // a device-scope release writes back the XCD's whole L2, which costs ~0.1 us per workgroup).
 //
@@ -227,7 +227,7 @@ __global__ void __launch_bounds__(256) relation_decode_kernel(const DecParams p)
 }
 
 // ------------------------------------------------------------------------------------------------
-// merge: one workgroup per sequence, heads in turn
+// merge: one workgroup per (sequence, head)
 // ------------------------------------------------------------------------------------------------
 template <typename T, int DP>
 __global__ void __launch_bounds__(256) relation_decode_merge_kernel(const DecParams p) {
