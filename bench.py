@@ -114,13 +114,18 @@ def staged_bwd(p1, p2, info, ibar, lse, g, dy, timers):
     st = Lb.stream_of(p1)
     a.stages = Lb.MOTE_BWD_ROWS
     Lb.check(Lb.lib().mote_relation_bwd(a, st), "bwd rows")
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    ev[0].record()
     a.stages = Lb.MOTE_BWD_KEYS
     Lb.check(Lb.lib().mote_relation_bwd(a, st), "bwd keys")
-    e1.record()
-    timers["bwd_keys"][0].append(e0)
-    timers["bwd_keys"][1].append(e1)
+    ev[1].record()
+    a.stages = Lb.MOTE_BWD_QUERIES
+    Lb.check(Lb.lib().mote_relation_bwd(a, st), "bwd queries")
+    ev[2].record()
+    timers["bwd_keys"][0].append(ev[0])
+    timers["bwd_keys"][1].append(ev[1])
+    timers["bwd_queries"][0].append(ev[1])
+    timers["bwd_queries"][1].append(ev[2])
     a.stages = Lb.MOTE_BWD_FINISH
     Lb.check(Lb.lib().mote_relation_bwd(a, st), "bwd finish")
     return dp1, dp2, dinfo, dlam
@@ -144,19 +149,22 @@ def bench_stack(steps: int, warmup: int, dev):
     ms = t0.elapsed_time(t1) / steps
     flops = N_LAYERS * 7.0 * N_HEADS * D_HEAD * T * T
     # kernel-level timing pass (same work, stages bracketed by events)
-    timers = {"fwd": ([], []), "bwd_keys": ([], [])}
+    timers = {"fwd": ([], []), "bwd_keys": ([], []), "bwd_queries": ([], [])}
     for _ in range(max(1, min(steps, 3))):
         stack_step(inp, timers)
     torch.cuda.synchronize()
     avg = {k: sum(a.elapsed_time(b) for a, b in zip(*v)) / len(v[0]) for k, v in timers.items()}
-    keys_flops = 5.0 * N_HEADS * D_HEAD * T * T
-    fwd_flops = 2.0 * N_HEADS * D_HEAD * T * T
+    # per-kernel work (units of H*dh*T^2, one per causal product): forward U and P I~ (2); key kernel
+    # U, dW, dV, dK (4); query kernel dQ plus the recomputed U and dW (3, of which 1 is not done elsewhere)
+    unit = N_HEADS * D_HEAD * T * T
     res = dict(T=T, ms_per_step=ms, wall_s=wall, tflops=flops / (ms * 1e-3) / 1e12, flops_per_step=flops,
-               keys_ms=avg["bwd_keys"], fwd_ms=avg["fwd"],
-               keys_tflops=keys_flops / (avg["bwd_keys"] * 1e-3) / 1e12,
-               fwd_tflops=fwd_flops / (avg["fwd"] * 1e-3) / 1e12)
+               keys_ms=avg["bwd_keys"], queries_ms=avg["bwd_queries"], fwd_ms=avg["fwd"],
+               keys_tflops=4.0 * unit / (avg["bwd_keys"] * 1e-3) / 1e12,
+               queries_tflops=3.0 * unit / (avg["bwd_queries"] * 1e-3) / 1e12,
+               fwd_tflops=2.0 * unit / (avg["fwd"] * 1e-3) / 1e12)
     log(f"[bench] stack: {ms:.3f} ms/step = {res['tflops']:.1f} TFLOP/s; fwd kernel {avg['fwd']*1e3:.1f} us "
-        f"({res['fwd_tflops']:.1f} TF/s), bwd key kernel {avg['bwd_keys']*1e3:.1f} us ({res['keys_tflops']:.1f} TF/s)")
+        f"({res['fwd_tflops']:.1f} TF/s), bwd key kernel {avg['bwd_keys']*1e3:.1f} us ({res['keys_tflops']:.1f} TF/s), "
+        f"bwd query kernel {avg['bwd_queries']*1e3:.1f} us ({res['queries_tflops']:.1f} TF/s executed)")
     return res
 
 
@@ -359,14 +367,21 @@ def main():
         "config": {"workload": "Mote-96M Relation stack fwd+bwd (12 layers, B=1, 16384-byte window)",
                    "T_chunks": st["T"], "heads": N_HEADS, "d_head": D_HEAD, "layers": N_LAYERS,
                    "flop_convention": "7*H*dh*T^2 per layer (causal; fwd 2x, bwd 5x)"},
-        "roofline": {"kernel": "bwd_keys_kernel (one-pass backward, key blocks)", "bound": "mfma",
+        "roofline": {"kernel": "bwd_kv_kernel (key-stationary backward: U, dW, dV, dK)", "bound": "mfma",
                      "achieved": round(st["keys_tflops"], 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(st["keys_tflops"] / PEAK_BF16_TFLOPS, 4), "traffic": measured_traffic("bwd_keys_kernel"),
-                     "avg_launch_ms": round(st["keys_ms"], 4)},
+                     "frac": round(st["keys_tflops"] / PEAK_BF16_TFLOPS, 4), "traffic": measured_traffic("bwd_kv_kernel"),
+                     "flop_per_launch": 4.0 * N_HEADS * D_HEAD * st["T"] ** 2, "avg_launch_ms": round(st["keys_ms"], 4)},
+        "roofline_bwd_q": {"kernel": "bwd_q_kernel (query-stationary dQ; recomputes U and dW)", "bound": "mfma",
+                           "achieved": round(st["queries_tflops"], 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                           "frac": round(st["queries_tflops"] / PEAK_BF16_TFLOPS, 4),
+                           "traffic": measured_traffic("bwd_q_kernel"),
+                           "flop_per_launch": 3.0 * N_HEADS * D_HEAD * st["T"] ** 2,
+                           "avg_launch_ms": round(st["queries_ms"], 4)},
         "roofline_fwd": {"kernel": "relation_fwd_lds_kernel", "bound": "mfma", "achieved": round(st["fwd_tflops"], 2),
                          "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(st["fwd_tflops"] / PEAK_BF16_TFLOPS, 4),
-                         "traffic": measured_traffic("relation_fwd_lds_kernel"), "avg_launch_ms": round(st["fwd_ms"], 4)},
+                         "traffic": measured_traffic("relation_fwd_lds_kernel"),
+                         "flop_per_launch": 2.0 * N_HEADS * D_HEAD * st["T"] ** 2, "avg_launch_ms": round(st["fwd_ms"], 4)},
         "stack_frac_of_peak": round(st["tflops"] / PEAK_BF16_TFLOPS, 4),
     }
     if dec:

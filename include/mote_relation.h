@@ -80,21 +80,25 @@ int mote_relation_fwd(const mote_relation_fwd_args* args, void* stream);
  * Replaces: `_bwd_rows_kernel` + `_bwd_kernel` (one pass, fp32 atomics for dp1) and the
  * deterministic two-pass `_bwd_kv_kernel` + `_bwd_q_kernel` with their launchers
  * (mote/model/flash_relation.py:186-460, 544-615), behind `mote::relation_bwd` (:634-637).
- * `deterministic` != 0 selects the atomic-free path (the reference's MOTE_DETERMINISTIC_RELATION,
- * flash_relation.py:51): its results are bitwise reproducible run to run.
  * Inputs are the forward's inputs and saved statistics (ibar, lse, g as produced by
  * mote_relation_fwd, dense layout) and dy ([B, H, TQ, D], any strides). Outputs dp1 [B,H,TQ,D],
  * dp2 and dinfo [B,H,TK,D] in `dtype` (any strides) and dlam (one fp32, overwritten).
+ * bf16 with D in {32, 64, 96, 128} runs atomic-free kernels (key-stationary dp2/dinfo, then
+ * query-stationary dp1): every result is bitwise reproducible whatever `deterministic` says.
+ * Other shapes (fp32, padded head dims): `deterministic` != 0 selects the atomic-free pair of
+ * kernels (the reference's MOTE_DETERMINISTIC_RELATION, flash_relation.py:51), 0 the one-pass
+ * kernel with fp32 atomics for dp1.
  * The workspace is caller-allocated device memory of at least mote_relation_bwd_workspace()
  * bytes; its contents on entry do not matter.
- * `stages` selects which of the three launches run (MOTE_BWD_ROWS: per-row terms and operand
- * copies; MOTE_BWD_KEYS: the key-block kernel(s); MOTE_BWD_FINISH: dp1 and dlam outputs); 0 runs
- * all three. A caller that splits them (to time or overlap them) issues them in that order on one
- * stream with one workspace.
+ * `stages` selects which launches run (MOTE_BWD_ROWS: per-row terms and operand copies;
+ * MOTE_BWD_KEYS: the key-stationary kernel; MOTE_BWD_QUERIES: the query-stationary dp1 kernel,
+ * where the path has one; MOTE_BWD_FINISH: dp1 cast and dlam); 0 runs all of them. A caller that
+ * splits them (to time or overlap them) issues them in that order on one stream with one workspace.
  * ------------------------------------------------------------------------------------------------ */
 #define MOTE_BWD_ROWS 1
 #define MOTE_BWD_KEYS 2
 #define MOTE_BWD_FINISH 4
+#define MOTE_BWD_QUERIES 8
 
 typedef struct mote_relation_bwd_args {
   int dtype;

@@ -20,7 +20,7 @@ MOTE_OK = 0
 MOTE_F32 = 0
 MOTE_BF16 = 1
 MOTE_DECODE_ADVANCE = 1
-MOTE_BWD_ROWS, MOTE_BWD_KEYS, MOTE_BWD_FINISH = 1, 2, 4
+MOTE_BWD_ROWS, MOTE_BWD_KEYS, MOTE_BWD_FINISH, MOTE_BWD_QUERIES = 1, 2, 4, 8
 
 _DTYPES = {torch.float32: MOTE_F32, torch.bfloat16: MOTE_BF16}
 

@@ -24,42 +24,17 @@
 //    atomics (the reference's two-pass `_bwd_q_kernel`, flash_relation.py:419-460), so every
 //    result is bitwise reproducible. dlam: a fixed-order sum of the row partials.
 #include "common.hpp"
-#include "params.hpp"
+#include "bwd.hpp"
 
 namespace mote {
 
-struct BwdParams {
-  const void* p1; int64_t q_sb, q_sh, q_sr;
-  const void* p2; int64_t k_sb, k_sh, k_sr;
-  const void* info; int64_t v_sb, v_sh, v_sr;
-  const void* dy; int64_t y_sb, y_sh, y_sr;
-  const float* ibar;
-  const float* lse;
-  const float* g;
-  void* dp1; int64_t dq_sb, dq_sh, dq_sr;
-  void* dp2; int64_t dk_sb, dk_sh, dk_sr;
-  void* dinfo; int64_t dv_sb, dv_sh, dv_sr;
-  float* dlam;
-  // workspace
-  void* wq;      // [BH][TQp][DP]  P1 rows
-  void* wdib;    // [BH][TQp][DP]  dI-bar rows
-  void* wqT;     // [BH][DP][TQp]  P1 transposed
-  void* wdibT;   // [BH][DP][TQp]  dI-bar transposed
-  float* lse2;   // [BH][TQp]
-  float* cvec;   // [BH][TQp]      dA - Delta
-  float* duii;   // [BH][TQp]
-  float* dp1acc; // [BH][TQ][D]
-  float* dlam_part;  // [BH][TQp / 64]
-  int B, H, TQ, TK, D, q_start, TQp;
-  float scale, tau_inv;
-};
-
-constexpr int kRowBlock = 64;  // rows per workgroup in the rows stage; also TQp's granularity
 
 // ------------------------------------------------------------------------------------------------
 // 1. rows
 // ------------------------------------------------------------------------------------------------
-template <typename T, int DP>
+// LEAN (tile kernels): only dI-bar rows, the per-block stats, dU_ii and the dlam partials; the
+// register-staged kernels also need the P1 copies, both transposes and the dP1 accumulator.
+template <typename T, int DP, bool LEAN>
 __global__ void __launch_bounds__(256) bwd_rows_kernel(const BwdParams p) {
   using E = Elem<T>;
   constexpr int EPC = 16 / sizeof(T);       // elements per 16-byte chunk
@@ -67,8 +42,8 @@ __global__ void __launch_bounds__(256) bwd_rows_kernel(const BwdParams p) {
   constexpr int NCH = kRowBlock * CPR;      // chunks per block
   constexpr int CT = (NCH + 255) / 256;     // chunks per thread
   constexpr int LD = DP + EPC;              // LDS row stride (elements)
-  __shared__ __align__(16) T sq[kRowBlock * LD];
-  __shared__ __align__(16) T sd[kRowBlock * LD];
+  __shared__ __align__(16) T sq[LEAN ? 1 : kRowBlock * LD];
+  __shared__ __align__(16) T sd[LEAN ? 1 : kRowBlock * LD];
   __shared__ float part[3][kRowBlock][CPR + 1];
   __shared__ float sdu[kRowBlock];
   __shared__ float sred[kRowBlock];
@@ -82,7 +57,7 @@ __global__ void __launch_bounds__(256) bwd_rows_kernel(const BwdParams p) {
   const T* kb = reinterpret_cast<const T*>(p.p2) + b * p.k_sb + h * p.k_sh;
   const T* vb = reinterpret_cast<const T*>(p.info) + b * p.v_sb + h * p.v_sh;
   const T* yb = reinterpret_cast<const T*>(p.dy) + b * p.y_sb + h * p.y_sh;
-  T* wq = reinterpret_cast<T*>(p.wq) + (int64_t(bh) * p.TQp + i0) * DP;
+  T* wq = LEAN ? nullptr : reinterpret_cast<T*>(p.wq) + (int64_t(bh) * p.TQp + i0) * DP;
   T* wd = reinterpret_cast<T*>(p.wdib) + (int64_t(bh) * p.TQp + i0) * DP;
 
   // pass 1: 16-byte chunks; per-chunk partial dot products, dI-bar and the row-major copies
@@ -115,7 +90,7 @@ __global__ void __launch_bounds__(256) bwd_rows_kernel(const BwdParams p) {
 #pragma unroll
       for (int e = 0; e < EPC; ++e) ibv[e] = 0.f;
     }
-    kreg[c] = ck;
+    if constexpr (!LEAN) kreg[c] = ck;
     const T* eq = reinterpret_cast<const T*>(&cq);
     const T* ek = reinterpret_cast<const T*>(&ck);
     const T* ev = reinterpret_cast<const T*>(&cv);
@@ -136,9 +111,11 @@ __global__ void __launch_bounds__(256) bwd_rows_kernel(const BwdParams p) {
     part[0][r][cc] = dgate;
     part[1][r][cc] = delta;
     part[2][r][cc] = uii;
-    store_chunk(&sq[r * LD + d0], cq);
-    store_chunk(&sd[r * LD + d0], cd);
-    store_chunk(wq + r * DP + d0, cq);
+    if constexpr (!LEAN) {
+      store_chunk(&sq[r * LD + d0], cq);
+      store_chunk(&sd[r * LD + d0], cd);
+      store_chunk(wq + r * DP + d0, cq);
+    }
     store_chunk(wd + r * DP + d0, cd);
   }
   __syncthreads();
@@ -163,8 +140,16 @@ __global__ void __launch_bounds__(256) bwd_rows_kernel(const BwdParams p) {
     const float du = valid ? (-da) * s * (1.0f - s) * p.tau_inv : 0.f;
     const bool has = valid && lse > kNegInf;
     const int64_t w = int64_t(bh) * p.TQp + i;
-    p.lse2[w] = has ? lse * kLog2e : __builtin_inff();
-    p.cvec[w] = valid ? da - delta : 0.f;
+    const float l2 = has ? lse * kLog2e : __builtin_inff();
+    const float cv = valid ? da - delta : 0.f;
+    if constexpr (LEAN) {
+      float* st = p.stat + (int64_t(bh) * (p.TQp / kRowBlock) + blockIdx.x) * 128;
+      st[r] = l2;
+      st[64 + r] = cv;
+    } else {
+      p.lse2[w] = l2;
+      p.cvec[w] = cv;
+    }
     p.duii[w] = du;
     sdu[r] = du;
     sred[r] = valid ? -da * logf((float)(p.q_start + i) + 1.0f) : 0.f;
@@ -172,7 +157,7 @@ __global__ void __launch_bounds__(256) bwd_rows_kernel(const BwdParams p) {
   __syncthreads();
   // pass 2: dP1 accumulator initialised with the Self part dU_ii P2_i / sqrt(D)
 #pragma unroll
-  for (int c = 0; c < CT; ++c) {
+  for (int c = 0; c < (LEAN ? 0 : CT); ++c) {
     const int idx = tid + 256 * c;
     if (idx >= NCH) break;
     const int r = idx / CPR, cc = idx % CPR;
@@ -188,7 +173,7 @@ __global__ void __launch_bounds__(256) bwd_rows_kernel(const BwdParams p) {
           make_float4(f * E::to_f(ek[e]), f * E::to_f(ek[e + 1]), f * E::to_f(ek[e + 2]), f * E::to_f(ek[e + 3]));
   }
   // transposed copies: row d holds the 64 rows of this block
-  {
+  if constexpr (!LEAN) {
     T* wqT = reinterpret_cast<T*>(p.wqT) + int64_t(bh) * DP * p.TQp + i0;
     T* wdT = reinterpret_cast<T*>(p.wdibT) + int64_t(bh) * DP * p.TQp + i0;
     constexpr int CH = DP * kRowBlock / EPC;
@@ -737,26 +722,34 @@ __global__ void __launch_bounds__(256) bwd_dlam_kernel(const float* part, int n,
 // host side
 // ------------------------------------------------------------------------------------------------
 struct WsLayout {
-  size_t wq, wdib, wqT, wdibT, lse2, cvec, duii, dp1acc, dlam_part, total;
+  size_t wq, wdib, wqT, wdibT, lse2, cvec, stat, duii, dp1acc, dlam_part, total;
 };
 
 static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// bf16 with a head dim the tile kernels are compiled for: the atomic-free tile path.
+static bool use_tiles(const mote_relation_bwd_args* a) { return a->dtype == MOTE_BF16 && padded_dim(a->D) == a->D; }
 
 static WsLayout ws_layout(const mote_relation_bwd_args* a) {
   const size_t es = a->dtype == MOTE_BF16 ? 2 : 4;
   const size_t BH = size_t(a->B) * a->H;
   const size_t TQp = size_t((a->TQ + kRowBlock - 1) / kRowBlock) * kRowBlock;
   const size_t DP = padded_dim(a->D);
-  WsLayout w;
+  const bool tiles = use_tiles(a);
+  WsLayout w{};
   size_t o = 0;
-  w.wq = o; o = align256(o + BH * TQp * DP * es);
   w.wdib = o; o = align256(o + BH * TQp * DP * es);
-  w.wqT = o; o = align256(o + BH * TQp * DP * es);
-  w.wdibT = o; o = align256(o + BH * TQp * DP * es);
-  w.lse2 = o; o = align256(o + BH * TQp * 4);
-  w.cvec = o; o = align256(o + BH * TQp * 4);
+  if (tiles) {
+    w.stat = o; o = align256(o + BH * (TQp / kRowBlock) * 128 * 4);
+  } else {
+    w.wq = o; o = align256(o + BH * TQp * DP * es);
+    w.wqT = o; o = align256(o + BH * TQp * DP * es);
+    w.wdibT = o; o = align256(o + BH * TQp * DP * es);
+    w.lse2 = o; o = align256(o + BH * TQp * 4);
+    w.cvec = o; o = align256(o + BH * TQp * 4);
+    w.dp1acc = o; o = align256(o + BH * size_t(a->TQ) * a->D * 4);
+  }
   w.duii = o; o = align256(o + BH * TQp * 4);
-  w.dp1acc = o; o = align256(o + BH * size_t(a->TQ) * a->D * 4);
   w.dlam_part = o; o = align256(o + BH * (TQp / kRowBlock) * 4);
   w.total = o;
   return w;
@@ -764,22 +757,24 @@ static WsLayout ws_layout(const mote_relation_bwd_args* a) {
 
 size_t bwd_workspace_bytes(const mote_relation_bwd_args* a) { return ws_layout(a).total; }
 
+// Register-staged kernels (fp32, and bf16 head dims that need padding).
 template <typename T, int DP>
 static void launch_bwd_t(const BwdParams& p, bool deterministic, int stages, hipStream_t stream) {
   const int BH = p.B * p.H;
   if (stages & MOTE_BWD_ROWS)
-    hipLaunchKernelGGL((bwd_rows_kernel<T, DP>), dim3(p.TQp / kRowBlock, BH), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((bwd_rows_kernel<T, DP, false>), dim3(p.TQp / kRowBlock, BH), dim3(256), 0, stream, p);
   const int nkb = (p.TK + 63) / 64;
   constexpr int BM = sizeof(T) == 2 ? 64 : 32;
   if (stages & MOTE_BWD_KEYS) {
-    if (!deterministic) {
+    if (!deterministic)
       hipLaunchKernelGGL((bwd_keys_kernel<T, DP, BM, true>), dim3(nkb * BH), dim3(256), 0, stream, p);
-    } else {
+    else
       hipLaunchKernelGGL((bwd_keys_kernel<T, DP, BM, false>), dim3(nkb * BH), dim3(256), 0, stream, p);
-      constexpr int BNQ = sizeof(T) == 2 ? 64 : 32;
-      const int nqb = (p.TQ + 63) / 64;
-      hipLaunchKernelGGL((bwd_queries_kernel<T, DP, BNQ>), dim3(nqb * BH), dim3(128), 0, stream, p);
-    }
+  }
+  if ((stages & MOTE_BWD_QUERIES) && deterministic) {
+    constexpr int BNQ = sizeof(T) == 2 ? 64 : 32;
+    const int nqb = (p.TQ + 63) / 64;
+    hipLaunchKernelGGL((bwd_queries_kernel<T, DP, BNQ>), dim3(nqb * BH), dim3(128), 0, stream, p);
   }
   if (stages & MOTE_BWD_FINISH) {
     if (!deterministic) {
@@ -789,6 +784,16 @@ static void launch_bwd_t(const BwdParams& p, bool deterministic, int stages, hip
     }
     hipLaunchKernelGGL(bwd_dlam_kernel, dim3(1), dim3(256), 0, stream, p.dlam_part, BH * (p.TQp / kRowBlock), p.dlam);
   }
+}
+
+template <int DP>
+static void launch_bwd_tile_path(const BwdParams& p, int stages, hipStream_t stream) {
+  const int BH = p.B * p.H;
+  if (stages & MOTE_BWD_ROWS)
+    hipLaunchKernelGGL((bwd_rows_kernel<bf16_t, DP, true>), dim3(p.TQp / kRowBlock, BH), dim3(256), 0, stream, p);
+  launch_bwd_tiles(p, stages, stream);
+  if (stages & MOTE_BWD_FINISH)
+    hipLaunchKernelGGL(bwd_dlam_kernel, dim3(1), dim3(256), 0, stream, p.dlam_part, BH * (p.TQp / kRowBlock), p.dlam);
 }
 
 int launch_bwd(const mote_relation_bwd_args* a, hipStream_t stream) {
@@ -816,7 +821,7 @@ int launch_bwd(const mote_relation_bwd_args* a, hipStream_t stream) {
     return set_error(MOTE_ERR_ARGUMENT, "relation_bwd: null tensor pointer");
   if (!a->workspace || a->workspace_bytes < w.total)
     return set_error(MOTE_ERR_WORKSPACE, "relation_bwd: workspace of %zu bytes, %zu needed", a->workspace_bytes, w.total);
-  BwdParams p;
+  BwdParams p{};
   p.p1 = a->p1.data; p.q_sb = a->p1.stride_b; p.q_sh = a->p1.stride_h; p.q_sr = a->p1.stride_r;
   p.p2 = a->p2.data; p.k_sb = a->p2.stride_b; p.k_sh = a->p2.stride_h; p.k_sr = a->p2.stride_r;
   p.info = a->info.data; p.v_sb = a->info.stride_b; p.v_sh = a->info.stride_h; p.v_sr = a->info.stride_r;
@@ -826,21 +831,34 @@ int launch_bwd(const mote_relation_bwd_args* a, hipStream_t stream) {
   p.dp2 = a->dp2.data; p.dk_sb = a->dp2.stride_b; p.dk_sh = a->dp2.stride_h; p.dk_sr = a->dp2.stride_r;
   p.dinfo = a->dinfo.data; p.dv_sb = a->dinfo.stride_b; p.dv_sh = a->dinfo.stride_h; p.dv_sr = a->dinfo.stride_r;
   p.dlam = a->dlam;
+  const bool tiles = use_tiles(a);
   char* ws = reinterpret_cast<char*>(a->workspace);
-  p.wq = ws + w.wq; p.wdib = ws + w.wdib; p.wqT = ws + w.wqT; p.wdibT = ws + w.wdibT;
-  p.lse2 = reinterpret_cast<float*>(ws + w.lse2);
-  p.cvec = reinterpret_cast<float*>(ws + w.cvec);
+  p.wdib = ws + w.wdib;
   p.duii = reinterpret_cast<float*>(ws + w.duii);
-  p.dp1acc = reinterpret_cast<float*>(ws + w.dp1acc);
   p.dlam_part = reinterpret_cast<float*>(ws + w.dlam_part);
+  if (tiles) {
+    p.stat = reinterpret_cast<float*>(ws + w.stat);
+  } else {
+    p.wq = ws + w.wq; p.wqT = ws + w.wqT; p.wdibT = ws + w.wdibT;
+    p.lse2 = reinterpret_cast<float*>(ws + w.lse2);
+    p.cvec = reinterpret_cast<float*>(ws + w.cvec);
+    p.dp1acc = reinterpret_cast<float*>(ws + w.dp1acc);
+  }
   p.B = a->B; p.H = a->H; p.TQ = a->TQ; p.TK = a->TK; p.D = a->D; p.q_start = a->q_start;
   p.TQp = (a->TQ + kRowBlock - 1) / kRowBlock * kRowBlock;
   p.scale = 1.0f / sqrtf((float)a->D);
   p.tau_inv = 1.0f / a->tau_s;
   const int DP = padded_dim(a->D);
   const bool det = a->deterministic != 0;
-  const int st = a->stages ? a->stages : (MOTE_BWD_ROWS | MOTE_BWD_KEYS | MOTE_BWD_FINISH);
-  if (a->dtype == MOTE_BF16) {
+  const int st = a->stages ? a->stages : (MOTE_BWD_ROWS | MOTE_BWD_KEYS | MOTE_BWD_QUERIES | MOTE_BWD_FINISH);
+  if (tiles) {
+    switch (DP) {
+      case 32: launch_bwd_tile_path<32>(p, st, stream); break;
+      case 64: launch_bwd_tile_path<64>(p, st, stream); break;
+      case 96: launch_bwd_tile_path<96>(p, st, stream); break;
+      default: launch_bwd_tile_path<128>(p, st, stream); break;
+    }
+  } else if (a->dtype == MOTE_BF16) {
     switch (DP) {
       case 32: launch_bwd_t<bf16_t, 32>(p, det, st, stream); break;
       case 64: launch_bwd_t<bf16_t, 64>(p, det, st, stream); break;

@@ -1,0 +1,482 @@
+// Atomic-free Relation backward for bf16, D in {32, 64, 96, 128} (mote/model/flash_relation.py:10-15
+// for the algebra; the reference's two-pass `_bwd_kv_kernel` / `_bwd_q_kernel`, :370-460, has the
+// same split of the work).
+//
+// Both kernels walk 64 x 64 blocks of the (query, key) plane with four waves per workgroup; wave w
+// owns the 32 x 32 quadrant (query half qh = w / 2, key half kh = w % 2) of every block, so a block
+// costs a quarter of the latency it would on one wave and fully masked quadrants of the diagonal
+// blocks are skipped. Operand tiles of 64 rows are staged global -> LDS with global_load_lds
+// (tiles.hpp), double-buffered.
+//
+// Per element (query i, key j < i) with U = <P1_i, P2_j> / sqrt(D), sg = sigmoid(U), L = LSE_i:
+//   w = exp(SiLU(U) - L)  (computed as exp2(U log2e sg - L log2e)),
+//   dE = w (dW + c_i) with dW = <dI-bar_i, I~_j> and c_i = dA_i - Delta_i,
+//   dU = dE SiLU'(U),     SiLU'(U) = sg + U sg (1 - sg).
+//
+// Key kernel (one workgroup per 64 keys of one (batch, head), longest first): per query block
+// U = Q K^T and dW = dI-bar V^T with queries in the accumulator rows and the wave's keys in the
+// columns, so w and dU feed dV += W^T dI-bar and dK += dU^T Q as permuted-k A operands; the B
+// operands (dI-bar and Q with queries along k) are ds_read_b64_tr_b16 reads of the same tiles.
+// dV, dK stay in registers across query blocks; the two query-half waves of a key half add through
+// LDS at the end, then the Self terms of keys that are also queries ((1 - g) dY into dI~ and
+// dU_ii P1 into dP2) and 16-byte stores.
+//
+// Query kernel (one workgroup per 64 queries, longest first): per key block S^T = K Q^T and
+// dW^T = V dI-bar^T (keys in the accumulator rows), dU^T in the accumulator layout is the permuted-k
+// B operand of dQ^T += K^T dU^T, and K^T comes from transposed reads of the K tile. The key-half
+// waves add through LDS; the Self part dU_ii P2_i joins before the store.
+#include "common.hpp"
+#include "bwd.hpp"
+#include "tiles.hpp"
+
+namespace mote {
+
+// Elementwise core shared by both kernels: raw dot u, raw dW, row terms (lse2 = L log2e,
+// c = dA - Delta). Returns dU; w through the reference.
+__device__ __forceinline__ float bwd_elem(float u, float dw, float lse2, float c, float nc2, float scale, bool keep,
+                                          float& w) {
+  const float t = u * nc2;                 // -U log2e
+  const float sg = frcp(1.0f + fexp2(t));  // sigmoid(U)
+  float wv = fexp2(-fmaf(t, sg, lse2));    // exp2(U log2e sg - lse2)
+  wv = keep ? wv : 0.f;
+  const float de = wv * (dw + c);
+  const float e = (u * scale) * sg;        // SiLU(U)
+  const float sp = fmaf(e, 1.0f - sg, sg); // SiLU'(U)
+  w = wv;
+  return de * sp;
+}
+
+// ------------------------------------------------------------------------------------------------
+// key-stationary kernel: dP2 and dI~
+// ------------------------------------------------------------------------------------------------
+template <int DP, bool MASKED>
+__device__ __forceinline__ void kv_block(const bf16_t* Qs, const bf16_t* Ds, const float* Ss,
+                                         const Elem<bf16_t>::Frag (&kf)[2][DP / 32],
+                                         const Elem<bf16_t>::Frag (&vf)[2][DP / 32], f32x4 (&dvacc)[2][DP / 16],
+                                         f32x4 (&dkacc)[2][DP / 16], int qh, int li, int lg, int key0, int qa0,
+                                         float nc2, float scale) {
+  using E = Elem<bf16_t>;
+  using Frag = E::Frag;
+  constexpr int KS = DP / 32, DT = DP / 16;
+  f32x4 sacc[2][2], wacc[2][2];  // [query tile][key tile]
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      sacc[qt][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      wacc[qt][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      const int row = 32 * qh + 16 * qt + li;
+      const Frag aq = tile_row_frag<DP>(Qs, row, 4 * ks + lg);
+      const Frag ad = tile_row_frag<DP>(Ds, row, 4 * ks + lg);
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        sacc[qt][kt] = E::mma(aq, kf[kt][ks], sacc[qt][kt]);
+        wacc[qt][kt] = E::mma(ad, vf[kt][ks], wacc[qt][kt]);
+      }
+    }
+  }
+  // rows 32 qh + 16 qt + 4 lg + r; key 16 kt + li of the wave's half
+  Frag aw[2], au[2];
+  float wv[2][8], uv[2][8];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const float4 l4 = *reinterpret_cast<const float4*>(Ss + 32 * qh + 16 * qt + 4 * lg);
+    const float4 c4 = *reinterpret_cast<const float4*>(Ss + 64 + 32 * qh + 16 * qt + 4 * lg);
+    const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+    const float cv[4] = {c4.x, c4.y, c4.z, c4.w};
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        bool keep = true;
+        if constexpr (MASKED) keep = key0 + 16 * kt + li < qa0 + 16 * qt + 4 * lg + r;
+        float w;
+        const float du = bwd_elem(sacc[qt][kt][r], wacc[qt][kt][r], lv[r], cv[r], nc2, scale, keep, w);
+        wv[kt][4 * qt + r] = w;
+        uv[kt][4 * qt + r] = du;
+      }
+  }
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt) {
+    aw[kt] = E::from_f32(wv[kt]);
+    au[kt] = E::from_f32(uv[kt]);
+  }
+  // dV += W^T dI-bar, dK += dU^T Q over the wave's 32 queries (k in permuted order)
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    const Frag bd = tile_tr_frag<DP>(Ds, 32 * qh, dt, li, lg);
+    const Frag bq = tile_tr_frag<DP>(Qs, 32 * qh, dt, li, lg);
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      dvacc[kt][dt] = E::mma(aw[kt], bd, dvacc[kt][dt]);
+      dkacc[kt][dt] = E::mma(au[kt], bq, dkacc[kt][dt]);
+    }
+  }
+}
+
+template <int DP>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP <= 96 ? 2 : 1)))
+bwd_kv_kernel(const BwdParams p) {
+  using E = Elem<bf16_t>;
+  using Frag = E::Frag;
+  constexpr int KS = DP / 32, DT = DP / 16, CPR = DP / 8, TILE = 64 * DP;
+  constexpr int STAGE = 2 * TILE + 256;  // bf16 slots per stage: Q tile, dI-bar tile, 128 fp32 stats
+  __shared__ __align__(16) bf16_t smem[2 * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const int kh = wave & 1, qh = wave >> 1;
+  const int BH = p.B * p.H;
+  const int bh = blockIdx.x % BH;
+  const int kb = blockIdx.x / BH;  // key block 0 sees the most queries: longest first
+  const int b = bh / p.H, h = bh % p.H;
+  const int k0 = kb * 64;
+  const int nqb = p.TQp / 64;
+  const bf16_t* qbase = reinterpret_cast<const bf16_t*>(p.p1) + b * p.q_sb + h * p.q_sh;
+  const bf16_t* kbase = reinterpret_cast<const bf16_t*>(p.p2) + b * p.k_sb + h * p.k_sh;
+  const bf16_t* vbase = reinterpret_cast<const bf16_t*>(p.info) + b * p.v_sb + h * p.v_sh;
+  const bf16_t* dbase = reinterpret_cast<const bf16_t*>(p.wdib) + int64_t(bh) * p.TQp * DP;
+  const float* sbase = p.stat + int64_t(bh) * nqb * 128;
+
+  // the wave's 32 keys as B fragments (k = head dim, column = key)
+  const int key0 = k0 + 32 * kh;
+  Frag kf[2][KS], vf[2][KS];
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt) {
+    const int j = key0 + 16 * kt + li;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int d0 = 32 * ks + 8 * lg;
+      kf[kt][ks] = j < p.TK ? E::load8(kbase + int64_t(j) * p.k_sr + d0) : E::zero();
+      vf[kt][ks] = j < p.TK ? E::load8(vbase + int64_t(j) * p.v_sr + d0) : E::zero();
+    }
+  }
+  f32x4 dvacc[2][DT], dkacc[2][DT];
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      dvacc[kt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      dkacc[kt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+  TileStager<DP, 4, 2> st;
+  st.init(wave, lane);
+  const bf16_t* srcs[2] = {qbase, dbase};
+  const int64_t strides[2] = {p.q_sr, DP};
+  auto issue = [&](int qb, int stage) {
+    bf16_t* dst = smem + stage * STAGE;
+    st.issue(dst, srcs, strides, qb * 64, p.TQ - 1, wave);
+    if (wave == 3 && lane < 32) {
+      const float* src = sbase + int64_t(qb) * 128 + 4 * lane;
+      __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)src,
+                                       (void __attribute__((address_space(3)))*)(dst + 2 * TILE), 16, 0, 0);
+    }
+  };
+
+  const float nc2 = -p.scale * kLog2e;
+  const int qb_lo = max(0, k0 + 1 - p.q_start) / 64;
+  if (qb_lo < nqb) {
+    issue(qb_lo, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+  for (int qb = qb_lo; qb < nqb; ++qb) {
+    const int stage = (qb - qb_lo) & 1;
+    if (qb + 1 < nqb) issue(qb + 1, stage ^ 1);
+    const bf16_t* Qs = smem + stage * STAGE;
+    const bf16_t* Ds = Qs + TILE;
+    const float* Ss = reinterpret_cast<const float*>(Qs + 2 * TILE);
+    const int i0 = qb * 64 + 32 * qh;   // the wave's first query row
+    const int qa0 = p.q_start + i0;     // its position
+    // quadrant visible at all (some key < some query position), and not wholly padding rows
+    if (i0 < p.TQ && key0 < qa0 + 31) {
+      if (key0 + 31 >= qa0)
+        kv_block<DP, true>(Qs, Ds, Ss, kf, vf, dvacc, dkacc, qh, li, lg, key0, qa0, nc2, p.scale);
+      else
+        kv_block<DP, false>(Qs, Ds, Ss, kf, vf, dvacc, dkacc, qh, li, lg, key0, qa0, nc2, p.scale);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+
+  // add the two query halves through LDS: R[0] = dV, R[1] = dK, [64 keys][DP] fp32
+  float* R = reinterpret_cast<float*>(smem);
+  __syncthreads();
+  if (qh == 1) {
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = 32 * kh + 16 * kt + 4 * lg + r, col = 16 * dt + li;
+          R[row * DP + col] = dvacc[kt][dt][r];
+          R[64 * DP + row * DP + col] = dkacc[kt][dt][r];
+        }
+  }
+  __syncthreads();
+  if (qh == 0) {
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = 32 * kh + 16 * kt + 4 * lg + r, col = 16 * dt + li;
+          R[row * DP + col] += dvacc[kt][dt][r];
+          R[64 * DP + row * DP + col] += dkacc[kt][dt][r];
+        }
+  }
+  __syncthreads();
+  // Self terms and 16-byte stores: one chunk of 8 head-dim elements of one key row per item
+  const bf16_t* dybase = reinterpret_cast<const bf16_t*>(p.dy) + b * p.y_sb + h * p.y_sh;
+  bf16_t* dkout = reinterpret_cast<bf16_t*>(p.dp2) + b * p.dk_sb + h * p.dk_sh;
+  bf16_t* dvout = reinterpret_cast<bf16_t*>(p.dinfo) + b * p.dv_sb + h * p.dv_sh;
+  for (int item = tid; item < 64 * CPR; item += 256) {
+    const int row = item / CPR, d0 = (item % CPR) * 8;
+    const int j = k0 + row;
+    if (j >= p.TK) continue;
+    float dv[8], dk[8];
+#pragma unroll
+    for (int e = 0; e < 8; e += 4) {
+      const float4 a = *reinterpret_cast<const float4*>(&R[row * DP + d0 + e]);
+      const float4 c = *reinterpret_cast<const float4*>(&R[64 * DP + row * DP + d0 + e]);
+      dv[e] = a.x; dv[e + 1] = a.y; dv[e + 2] = a.z; dv[e + 3] = a.w;
+      dk[e] = c.x; dk[e + 1] = c.y; dk[e + 2] = c.z; dk[e + 3] = c.w;
+    }
+    const int i = j - p.q_start;
+    if (i >= 0) {
+      const float gs = p.g[int64_t(bh) * p.TQ + i];
+      const float us = p.duii[int64_t(bh) * p.TQp + i];
+      const Frag y8 = E::load8(dybase + int64_t(i) * p.y_sr + d0);
+      const Frag q8 = E::load8(qbase + int64_t(i) * p.q_sr + d0);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        dv[e] = fmaf(1.0f - gs, (float)y8.v[e], dv[e]);
+        dk[e] = fmaf(us, (float)q8.v[e], dk[e]);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dk[e] *= p.scale;
+    Frag ov = E::from_f32(dv), ok = E::from_f32(dk);
+    *reinterpret_cast<bf16x8*>(dvout + int64_t(j) * p.dv_sr + d0) = ov.v;
+    *reinterpret_cast<bf16x8*>(dkout + int64_t(j) * p.dk_sr + d0) = ok.v;
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// query-stationary kernel: dP1
+// ------------------------------------------------------------------------------------------------
+template <int DP, bool MASKED>
+__device__ __forceinline__ void q_block(const bf16_t* Ks, const bf16_t* Vs, const Elem<bf16_t>::Frag (&qf)[2][DP / 32],
+                                        const Elem<bf16_t>::Frag (&df)[2][DP / 32], f32x4 (&dqacc)[DP / 16][2],
+                                        const float (&lse2)[2], const float (&cv)[2], const int (&qabs)[2], int kh,
+                                        int li, int lg, int key0, float nc2, float scale) {
+  using E = Elem<bf16_t>;
+  using Frag = E::Frag;
+  constexpr int KS = DP / 32, DT = DP / 16;
+  f32x4 sacc[2][2], wacc[2][2];  // [key tile][query tile]
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      sacc[kt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
+      wacc[kt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      const int row = 32 * kh + 16 * kt + li;
+      const Frag ak = tile_row_frag<DP>(Ks, row, 4 * ks + lg);
+      const Frag av = tile_row_frag<DP>(Vs, row, 4 * ks + lg);
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        sacc[kt][s] = E::mma(ak, qf[s][ks], sacc[kt][s]);
+        wacc[kt][s] = E::mma(av, df[s][ks], wacc[kt][s]);
+      }
+    }
+  }
+  // keys 16 kt + 4 lg + r of the wave's half (rows), query 16 s + li (column)
+  Frag bu[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    float uv[8];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        bool keep = true;
+        if constexpr (MASKED) keep = key0 + 16 * kt + 4 * lg + r < qabs[s];
+        float w;
+        uv[4 * kt + r] = bwd_elem(sacc[kt][s][r], wacc[kt][s][r], lse2[s], cv[s], nc2, scale, keep, w);
+      }
+    bu[s] = E::from_f32(uv);
+  }
+  // dQ^T += K^T dU^T over the wave's 32 keys (k in permuted order)
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    const Frag ak = tile_tr_frag<DP>(Ks, 32 * kh, dt, li, lg);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) dqacc[dt][s] = E::mma(ak, bu[s], dqacc[dt][s]);
+  }
+}
+
+template <int DP>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+bwd_q_kernel(const BwdParams p) {
+  using E = Elem<bf16_t>;
+  using Frag = E::Frag;
+  constexpr int KS = DP / 32, DT = DP / 16, CPR = DP / 8, TILE = 64 * DP;
+  constexpr int STAGE = 2 * TILE;  // K tile, V tile
+  constexpr int RLD = DP + 4;      // fp32 row stride of the reduction buffer
+  __shared__ __align__(16) bf16_t smem[2 * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const int kh = wave & 1, qh = wave >> 1;
+  const int BH = p.B * p.H;
+  const int bh = blockIdx.x % BH;
+  const int nqb = p.TQp / 64;
+  const int qb = nqb - 1 - blockIdx.x / BH;  // the last query block sees the most keys: longest first
+  const int b = bh / p.H, h = bh % p.H;
+  const int i0 = qb * 64;
+  const bf16_t* qbase = reinterpret_cast<const bf16_t*>(p.p1) + b * p.q_sb + h * p.q_sh;
+  const bf16_t* kbase = reinterpret_cast<const bf16_t*>(p.p2) + b * p.k_sb + h * p.k_sh;
+  const bf16_t* vbase = reinterpret_cast<const bf16_t*>(p.info) + b * p.v_sb + h * p.v_sh;
+  const bf16_t* dbase = reinterpret_cast<const bf16_t*>(p.wdib) + int64_t(bh) * p.TQp * DP;
+  const float* sblk = p.stat + (int64_t(bh) * nqb + qb) * 128;
+
+  // the wave's 32 queries as B fragments (k = head dim, column = query), with their row terms
+  const int q0 = i0 + 32 * qh;
+  Frag qf[2][KS], df[2][KS];
+  float lse2[2], cv[2];
+  int qabs[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const int qi = q0 + 16 * s + li;
+    const bool ok = qi < p.TQ;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int d0 = 32 * ks + 8 * lg;
+      qf[s][ks] = ok ? E::load8(qbase + int64_t(qi) * p.q_sr + d0) : E::zero();
+      df[s][ks] = E::load8(dbase + int64_t(qi) * DP + d0);  // rows up to TQp exist (zero padding)
+    }
+    lse2[s] = sblk[32 * qh + 16 * s + li];      // +inf for padding rows and rows without a past
+    cv[s] = sblk[64 + 32 * qh + 16 * s + li];
+    qabs[s] = p.q_start + qi;
+  }
+  f32x4 dqacc[DT][2];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) dqacc[dt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  TileStager<DP, 4, 2> st;
+  st.init(wave, lane);
+  const bf16_t* srcs[2] = {kbase, vbase};
+  const int64_t strides[2] = {p.k_sr, p.v_sr};
+  const int qlast = min(p.TQ, i0 + 64) - 1;
+  const int nkb = (p.q_start + qlast + 63) / 64;  // keys j < q_start + qlast
+  const int wq_last = min(q0 + 31, p.TQ - 1);     // the wave's last query row
+  const float nc2 = -p.scale * kLog2e;
+
+  if (nkb > 0) {
+    st.issue(smem, srcs, strides, 0, p.TK - 1, wave);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int stage = kb & 1;
+    if (kb + 1 < nkb) st.issue(smem + (stage ^ 1) * STAGE, srcs, strides, (kb + 1) * 64, p.TK - 1, wave);
+    const bf16_t* Ks = smem + stage * STAGE;
+    const bf16_t* Vs = Ks + TILE;
+    const int key0 = kb * 64 + 32 * kh;
+    // the quadrant has a visible pair: some key below the wave's last query position
+    if (q0 < p.TQ && key0 < p.q_start + wq_last) {
+      if (key0 + 31 >= p.q_start + q0)
+        q_block<DP, true>(Ks, Vs, qf, df, dqacc, lse2, cv, qabs, kh, li, lg, key0, nc2, p.scale);
+      else
+        q_block<DP, false>(Ks, Vs, qf, df, dqacc, lse2, cv, qabs, kh, li, lg, key0, nc2, p.scale);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+
+  // add the two key halves through LDS: R[64 queries][RLD] fp32
+  float* R = reinterpret_cast<float*>(smem);
+  __syncthreads();
+  if (kh == 1) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const int row = 32 * qh + 16 * s + li;
+        *reinterpret_cast<f32x4*>(&R[row * RLD + 16 * dt + 4 * lg]) = dqacc[dt][s];
+      }
+  }
+  __syncthreads();
+  if (kh == 0) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const int row = 32 * qh + 16 * s + li;
+        f32x4* q = reinterpret_cast<f32x4*>(&R[row * RLD + 16 * dt + 4 * lg]);
+        *q = *q + dqacc[dt][s];
+      }
+  }
+  __syncthreads();
+  // Self part dU_ii P2_i, scale, 16-byte stores
+  bf16_t* dqout = reinterpret_cast<bf16_t*>(p.dp1) + b * p.dq_sb + h * p.dq_sh;
+  for (int item = tid; item < 64 * CPR; item += 256) {
+    const int row = item / CPR, d0 = (item % CPR) * 8;
+    const int i = i0 + row;
+    if (i >= p.TQ) continue;
+    const float us = p.duii[int64_t(bh) * p.TQp + i];
+    const Frag k8 = E::load8(kbase + int64_t(p.q_start + i) * p.k_sr + d0);
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; e += 4) {
+      const float4 a = *reinterpret_cast<const float4*>(&R[row * RLD + d0 + e]);
+      o[e] = a.x; o[e + 1] = a.y; o[e + 2] = a.z; o[e + 3] = a.w;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = fmaf(us, (float)k8.v[e], o[e]) * p.scale;
+    const Frag ov = E::from_f32(o);
+    *reinterpret_cast<bf16x8*>(dqout + int64_t(i) * p.dq_sr + d0) = ov.v;
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// host side
+// ------------------------------------------------------------------------------------------------
+template <int DP>
+static void launch_tiles_dp(const BwdParams& p, int stages, hipStream_t stream) {
+  const int BH = p.B * p.H;
+  if (stages & MOTE_BWD_KEYS) {
+    const int nkb = (p.TK + 63) / 64;
+    hipLaunchKernelGGL((bwd_kv_kernel<DP>), dim3(nkb * BH), dim3(256), 0, stream, p);
+  }
+  if (stages & MOTE_BWD_QUERIES) {
+    const int nqb = p.TQp / 64;
+    hipLaunchKernelGGL((bwd_q_kernel<DP>), dim3(nqb * BH), dim3(256), 0, stream, p);
+  }
+}
+
+void launch_bwd_tiles(const BwdParams& p, int stages, hipStream_t stream) {
+  switch (p.D) {
+    case 32: launch_tiles_dp<32>(p, stages, stream); break;
+    case 64: launch_tiles_dp<64>(p, stages, stream); break;
+    case 96: launch_tiles_dp<96>(p, stages, stream); break;
+    default: launch_tiles_dp<128>(p, stages, stream); break;
+  }
+}
+
+}  // namespace mote

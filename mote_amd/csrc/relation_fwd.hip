@@ -22,6 +22,7 @@
 // P2 / I~ rows.
 #include "common.hpp"
 #include "params.hpp"
+#include "tiles.hpp"
 
 namespace mote {
 
@@ -377,20 +378,6 @@ __global__ void __launch_bounds__(NW * 64) relation_fwd_kernel(const FwdParams p
 // of the P^T fragments. The block math is compiled twice, for diagonal (masked) blocks and for the
 // bulk of the rows.
 // ------------------------------------------------------------------------------------------------
-template <int DP>
-__device__ __forceinline__ int tile_swz(int row) {
-  if constexpr (DP == 64) return (row >> 1) & 7;
-  else if constexpr (DP == 128) return row & 7;
-  else return (row >> 2) & 3;
-}
-
-typedef __attribute__((ext_vector_type(4))) short s16x4;
-
-__device__ __forceinline__ bf16x4 lds_tr4(const bf16_t* p) {
-  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((s16x4 __attribute__((address_space(3)))*)(p));
-  return __builtin_bit_cast(bf16x4, v);
-}
-
 template <int DP, bool MASKED>
 __device__ __forceinline__ void fwd_block(const bf16_t* Ks, const bf16_t* Vs, const typename Elem<bf16_t>::Frag (&qf)[2][DP / 32],
                                           f32x4 (&oacc)[DP / 16][2], float (&m_run)[2], float (&l_run)[2], int j0,

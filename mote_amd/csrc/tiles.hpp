@@ -1,0 +1,95 @@
+// LDS tiles of 64 rows x DP bf16 for the gfx950 kernels: layout, staging and transposed reads.
+//
+// A tile is row-major (DP elements per row, no padding) with the 16-byte chunks of each row
+// XOR-swizzled against bank conflicts: logical chunk c of row r sits at physical chunk
+// c ^ tile_swz<DP>(r). For every read pattern of the kernels the swizzle value is a per-lane
+// constant.
+//
+// Staging goes global -> LDS with global_load_lds_dwordx4: lane l of one wave instruction writes its
+// 16 bytes at M0 + 16 l, so instruction n of a tile fills physical chunks 64 n .. 64 n + 63 and no
+// registers carry the data.
+//
+// Transposed fragments come from ds_read_b64_tr_b16: within a 16-lane group, lane 4k+m pointing at
+// row r0+k, columns [d0+4m, d0+4m+4) hands lane i the column d0+i of rows r0..r0+3.
+#pragma once
+
+#include "common.hpp"
+
+namespace mote {
+
+template <int DP>
+__device__ __forceinline__ int tile_swz(int row) {
+  if constexpr (DP == 64) return (row >> 1) & 7;
+  else if constexpr (DP == 128) return row & 7;
+  else return (row >> 2) & 3;  // DP 32 (4 chunks) and 96 (12 chunks): stays inside aligned groups of 4
+}
+
+typedef __attribute__((ext_vector_type(4))) short s16x4;
+
+__device__ __forceinline__ bf16x4 lds_tr4(const bf16_t* p) {
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((s16x4 __attribute__((address_space(3)))*)(p));
+  return __builtin_bit_cast(bf16x4, v);
+}
+
+// Fragment (8 k-slots) of a transposed operand: lane (k4 = li / 4, m4 = li % 4) of group lg reads
+// rows rb + 4 lg + k4 (slots 0..3) and rb + 16 + 4 lg + k4 (slots 4..7), columns 16 dt + 4 m4 ..
+// +3, so lane li receives column 16 dt + li of rows rb + 4 lg .. +3 and rb + 16 + 4 lg .. +3 -- the
+// permuted-k order {4g + r | 16 + 4g + r} of an accumulator pair.
+template <int DP>
+__device__ __forceinline__ typename Elem<bf16_t>::Frag tile_tr_frag(const bf16_t* tile, int rb, int dt, int li, int lg) {
+  const int k4 = li >> 2, m4 = li & 3;
+  const int c = 2 * dt + (m4 >> 1);
+  const int r0 = rb + 4 * lg + k4, r1 = r0 + 16;
+  const bf16x4 lo = lds_tr4(tile + r0 * DP + (c ^ tile_swz<DP>(r0)) * 8 + (m4 & 1) * 4);
+  const bf16x4 hi = lds_tr4(tile + r1 * DP + (c ^ tile_swz<DP>(r1)) * 8 + (m4 & 1) * 4);
+  typename Elem<bf16_t>::Frag f;
+  f.v = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return f;
+}
+
+// Row fragment: row `row`, logical chunk `ch` (8 consecutive elements).
+template <int DP>
+__device__ __forceinline__ typename Elem<bf16_t>::Frag tile_row_frag(const bf16_t* tile, int row, int ch) {
+  return Elem<bf16_t>::load8(tile + row * DP + (ch ^ tile_swz<DP>(row)) * 8);
+}
+
+// Staging of NT tiles per stage by the NW waves of a workgroup: the NT * CPR wave instructions are
+// dealt round-robin over the waves; each lane precomputes its row and source column per instruction.
+template <int DP, int NW, int NT>
+struct TileStager {
+  static constexpr int CPR = DP / 8;
+  static constexpr int NINS = NT * CPR;
+  static constexpr int PER = (NINS + NW - 1) / NW;
+  int row[PER];
+  int col[PER];
+
+  __device__ __forceinline__ void init(int wave, int lane) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int n = (wave + NW * i) % CPR;
+      const int q = 64 * n + lane;
+      row[i] = q / CPR;
+      col[i] = ((q % CPR) ^ tile_swz<DP>(row[i])) * 8;
+    }
+  }
+
+  // Rows r0 .. r0+63 of every source (row index clamped to rlast: rows past the end load a finite
+  // copy of the last row, which the kernels mask) into dst, tiles back to back.
+  __device__ __forceinline__ void issue(bf16_t* dst, const bf16_t* const (&src)[NT], const int64_t (&stride)[NT], int r0,
+                                        int rlast, int wave) const {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int ins = wave + NW * i;
+      if (ins < NINS) {
+        const int t = ins / CPR, n = ins % CPR;
+        const int j = min(r0 + row[i], rlast);
+        const bf16_t* g = src[t] + int64_t(j) * stride[t] + col[i];
+        bf16_t* l = dst + t * 64 * DP + n * 512;
+        __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)g,
+                                         (void __attribute__((address_space(3)))*)l, 16, 0, 0);
+      }
+    }
+  }
+};
+
+}  // namespace mote

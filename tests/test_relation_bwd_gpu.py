@@ -89,7 +89,7 @@ def test_rescale_branch_grads(cuda):
 
 
 @pytest.mark.parametrize("det", [False, True])
-@pytest.mark.parametrize("D", [48, 64, 96])
+@pytest.mark.parametrize("D", [32, 48, 64, 96, 128])
 @pytest.mark.parametrize("TQ", [33, 257])
 def test_bf16_grads(cuda, D, TQ, det):
     print(f"case bf16 grads D={D} TQ={TQ} det={det}", flush=True)
@@ -106,6 +106,26 @@ def test_bf16_flagship_prefix_grads(cuda):
     got = _grads(p1, p2, info, lam, dy, 64)
     ref = _oracle_grads(p1, p2, info, lam, dy, 64)
     _check(got, ref, 2e-2, p1, p2, info, lam, dy, 64)
+
+
+@pytest.mark.parametrize("D,TQ,S", [(64, 100, 37), (96, 129, 200), (128, 65, 63), (32, 1, 5)])
+def test_bf16_prefix_grads(cuda, D, TQ, S):
+    """Cached prefixes that do not align with the 64-row blocks of the tile kernels."""
+    print(f"case bf16 prefix grads D={D} TQ={TQ} S={S}", flush=True)
+    p1, p2, info, lam, dy = _inputs(2, 2, TQ, S, D, torch.bfloat16, seed=7)
+    got = _grads(p1, p2, info, lam, dy, S)
+    ref = _oracle_grads(p1, p2, info, lam, dy, S)
+    _check(got, ref, 2e-2, p1, p2, info, lam, dy, S)
+
+
+def test_bf16_tile_path_is_bitwise_reproducible(cuda):
+    """The bf16 kernels use no atomics: both settings of the switch give identical bits."""
+    p1, p2, info, lam, dy = _inputs(1, 8, 777, 0, 64, torch.bfloat16, seed=6)
+    a = _grads(p1, p2, info, lam, dy, 0, False)
+    b = _grads(p1, p2, info, lam, dy, 0, False)
+    c = _grads(p1, p2, info, lam, dy, 0, True)
+    for x, y, z, n in zip(a, b, c, NAMES):
+        assert torch.equal(x, y) and torch.equal(x, z), n
 
 
 def test_one_pass_and_two_pass_agree(cuda):
