@@ -377,10 +377,10 @@ def main():
                            "traffic": measured_traffic("bwd_q_kernel"),
                            "flop_per_launch": 3.0 * N_HEADS * D_HEAD * st["T"] ** 2,
                            "avg_launch_ms": round(st["queries_ms"], 4)},
-        "roofline_fwd": {"kernel": "relation_fwd_lds_kernel", "bound": "mfma", "achieved": round(st["fwd_tflops"], 2),
+        "roofline_fwd": {"kernel": "relation_fwd_tile_kernel", "bound": "mfma", "achieved": round(st["fwd_tflops"], 2),
                          "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(st["fwd_tflops"] / PEAK_BF16_TFLOPS, 4),
-                         "traffic": measured_traffic("relation_fwd_lds_kernel"),
+                         "traffic": measured_traffic("relation_fwd_tile_kernel"),
                          "flop_per_launch": 2.0 * N_HEADS * D_HEAD * st["T"] ** 2, "avg_launch_ms": round(st["fwd_ms"], 4)},
         "stack_frac_of_peak": round(st["tflops"] / PEAK_BF16_TFLOPS, 4),
     }

@@ -367,58 +367,58 @@ __global__ void __launch_bounds__(NW * 64) relation_fwd_kernel(const FwdParams p
 }
 
 // ------------------------------------------------------------------------------------------------
-// bf16 kernel for D in {32, 64, 96, 128}: direct-to-LDS staging
+// bf16 tile kernel for D in {32, 64, 96, 128}
 //
-// P2 and I~ blocks of 64 rows go global -> LDS with global_load_lds_dwordx4 (lane l of a wave's
-// instruction lands at M0 + 16 l), double-buffered, so no registers carry the staging. Both tiles
-// are row-major with the 16-byte chunks of a row XOR-swizzled (tile_swz) against bank conflicts; for
-// every read pattern below the swizzle value is a per-lane constant. K fragments are ds_read_b128;
-// V^T fragments are ds_read_b64_tr_b16: within a 16-lane group, lane 4k+m pointing at row kb+k,
-// columns [d0+4m, d0+4m+4) hands lane i the column d0+i of rows kb..kb+3 -- the permuted-k order
-// of the P^T fragments. The block math is compiled twice, for diagonal (masked) blocks and for the
-// bulk of the rows.
+// One workgroup of four waves per 64 query rows of one (sequence, head). P2 and I~ blocks of 64 rows
+// are staged global -> LDS (tiles.hpp), double-buffered. Wave w owns the 32 x 32 quadrant (query
+// half qh = w / 2, key half kh = w % 2) of every 64 x 64 block, so each query row is covered by two
+// waves with separate online-softmax states (m, l, O) that merge through LDS at the end; quadrants
+// with no visible (key < query) pair are skipped. Per block and wave:
+//   S^T = K Q^T       A = K rows (ds_read_b128), B = the wave's queries (registers, loaded once)
+//   e   = SiLU(S^T / sqrt(D)) in log2 units, masked on the diagonal blocks
+//   online softmax per query column, rescaled only when a block raises the max by more than 2^8
+//   O^T += V^T P^T    A = I~ columns by ds_read_b64_tr_b16, B = P^T from the S^T accumulators
+//                     (a lane holds one query and keys 4g + r of each 16-key tile: the permuted k
+//                     order both fragments share)
 // ------------------------------------------------------------------------------------------------
 template <int DP, bool MASKED>
-__device__ __forceinline__ void fwd_block(const bf16_t* Ks, const bf16_t* Vs, const typename Elem<bf16_t>::Frag (&qf)[2][DP / 32],
-                                          f32x4 (&oacc)[DP / 16][2], float (&m_run)[2], float (&l_run)[2], int j0,
-                                          const int (&qabs)[2], float c2, int li, int lg) {
+__device__ __forceinline__ void fwd_quad(const bf16_t* Ks, const bf16_t* Vs, const typename Elem<bf16_t>::Frag (&qf)[2][DP / 32],
+                                         f32x4 (&oacc)[DP / 16][2], float (&m_run)[2], float (&l_run)[2], int key0,
+                                         const int (&qabs)[2], float c2, int kh, int li, int lg) {
   using E = Elem<bf16_t>;
   using Frag = E::Frag;
-  constexpr int KS = DP / 32, DT = DP / 16, NT = 4, CPR = DP / 8;
-  const int kswz = tile_swz<DP>(li);  // rows 16t + li
-  f32x4 sacc[NT][2];
+  constexpr int KS = DP / 32, DT = DP / 16;
+  f32x4 sacc[2][2];  // [key tile][query tile]
 #pragma unroll
-  for (int t = 0; t < NT; ++t)
+  for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-    for (int s = 0; s < 2; ++s) sacc[t][s] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < 2; ++s) sacc[kt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const int row = 16 * t + li;
-      const int ch = (4 * ks + lg) ^ (DP == 128 ? tile_swz<DP>(row) : kswz);
-      const Frag kf = E::load8(Ks + row * DP + ch * 8);
+    for (int kt = 0; kt < 2; ++kt) {
+      const Frag kf = tile_row_frag<DP>(Ks, 32 * kh + 16 * kt + li, 4 * ks + lg);
 #pragma unroll
-      for (int s = 0; s < 2; ++s) sacc[t][s] = E::mma(kf, qf[s][ks], sacc[t][s]);
+      for (int s = 0; s < 2; ++s) sacc[kt][s] = E::mma(kf, qf[s][ks], sacc[kt][s]);
     }
   }
+  // keys key0 + 16 kt + 4 lg + r (rows), query 16 s + li (column)
   float bmax[2];
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
     float mx = kNegInf;
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float u2 = sacc[t][s][r] * c2;
+        const float u2 = sacc[kt][s][r] * c2;
         float e = u2 * frcp(1.0f + fexp2(-u2));
         if constexpr (MASKED) {
-          if (j0 + 16 * t + 4 * lg + r >= qabs[s]) e = kNegInf;
+          if (key0 + 16 * kt + 4 * lg + r >= qabs[s]) e = kNegInf;
         }
-        sacc[t][s][r] = e;
+        sacc[kt][s][r] = e;
         mx = fmaxf(mx, e);
       }
-    }
     mx = fmaxf(mx, wave_xor(mx, 16));
     mx = fmaxf(mx, wave_xor(mx, 32));
     bmax[s] = mx;
@@ -435,58 +435,42 @@ __device__ __forceinline__ void fwd_block(const bf16_t* Ks, const bf16_t* Vs, co
       m_run[s] = mn;
     }
   }
-  Frag pf[2][2];
+  Frag pf[2];
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
     const float ms = m_run[s] == kNegInf ? 0.f : m_run[s];
+    float pv[8];
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      float pv[8];
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float pr = fexp2(sacc[2 * kk + h][s][r] - ms);
-          l_run[s] += pr;
-          pv[4 * h + r] = pr;
-        }
-      pf[kk][s] = E::from_f32(pv);
-    }
+      for (int r = 0; r < 4; ++r) {
+        const float pr = fexp2(sacc[kt][s][r] - ms);
+        l_run[s] += pr;
+        pv[4 * kt + r] = pr;
+      }
+    pf[s] = E::from_f32(pv);
   }
-  // V^T fragments: lane (k = li / 4, m = li % 4) of group lg reads row 32kk + 4lg + k (+16 for
-  // slots 4..7), columns 16dt + 4m .. +3
-  const int k4 = li >> 2, m4 = li & 3;
 #pragma unroll
-  for (int kk = 0; kk < 2; ++kk) {
+  for (int dt = 0; dt < DT; ++dt) {
+    const Frag vf = tile_tr_frag<DP>(Vs, 32 * kh, dt, li, lg);
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      const int c = 2 * dt + (m4 >> 1);
-      const int r0 = 32 * kk + 4 * lg + k4;
-      const bf16_t* a0 = Vs + r0 * DP + (c ^ tile_swz<DP>(r0)) * 8 + (m4 & 1) * 4;
-      const bf16_t* a1 = Vs + (r0 + 16) * DP + (c ^ tile_swz<DP>(r0 + 16)) * 8 + (m4 & 1) * 4;
-      const bf16x4 lo = lds_tr4(a0), hi = lds_tr4(a1);
-      Frag vf;
-      vf.v = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-#pragma unroll
-      for (int s = 0; s < 2; ++s) oacc[dt][s] = E::mma(vf, pf[kk][s], oacc[dt][s]);
-    }
+    for (int s = 0; s < 2; ++s) oacc[dt][s] = E::mma(vf, pf[s], oacc[dt][s]);
   }
-  (void)CPR;
 }
 
-template <int DP, int NW>
-__global__ void __launch_bounds__(NW * 64) relation_fwd_lds_kernel(const FwdParams p) {
+template <int DP>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+relation_fwd_tile_kernel(const FwdParams p) {
   using E = Elem<bf16_t>;
   using Frag = E::Frag;
-  constexpr int KS = DP / 32, DT = DP / 16, BN = 64, BM = NW * 32;
-  constexpr int CPR = DP / 8;                 // 16-byte chunks per row
-  constexpr int TILE = BN * DP;               // elements per tile
-  constexpr int NINS = BN * CPR / 64;         // wave instructions per tile
-  constexpr int NINS_W = (2 * NINS + NW - 1) / NW;  // per wave, K and V tiles together
-  __shared__ __align__(16) bf16_t smem[2 * 2 * TILE];  // [stage][K | V][BN][DP]
+  constexpr int KS = DP / 32, DT = DP / 16, TILE = 64 * DP;
+  constexpr int STAGE = 2 * TILE;  // P2 tile, I~ tile
+  constexpr int RLD = DP + 4;      // fp32 row stride of the merge buffer
+  __shared__ __align__(16) bf16_t smem[2 * STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, lg = lane >> 4;
+  const int kh = wave & 1, qh = wave >> 1;
   const int bid = blockIdx.x;
   const int h = bid % p.H;
   const int rest = bid / p.H;
@@ -515,58 +499,31 @@ __global__ void __launch_bounds__(NW * 64) relation_fwd_lds_kernel(const FwdPara
     yoff = int64_t(seq) * p.y_sb;
     soff = (int64_t(seq) * p.H + h) * p.TQ;
   }
-  if (qb * BM >= TQs) return;
+  if (qb * 64 >= TQs) return;
   const bf16_t* qbase = reinterpret_cast<const bf16_t*>(p.p1) + qoff + int64_t(h) * p.q_sh;
   const bf16_t* kbase = reinterpret_cast<const bf16_t*>(p.p2) + koff + int64_t(h) * p.k_sh;
   const bf16_t* vbase = reinterpret_cast<const bf16_t*>(p.info) + voff + int64_t(h) * p.v_sh;
   bf16_t* ybase = reinterpret_cast<bf16_t*>(p.y) + yoff + int64_t(h) * p.y_sh;
 
-  const int q0 = qb * BM + wave * 32;
-  const bool wave_active = q0 < TQs;
+  const int q0 = qb * 64 + 32 * qh;  // the wave's first query row
   Frag qf[2][KS];
+  int qabs[2];
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
     const int qi = q0 + 16 * s + li;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
       qf[s][ks] = qi < TQs ? E::load8(qbase + int64_t(qi) * p.q_sr + 32 * ks + 8 * lg) : E::zero();
+    qabs[s] = qs + qi;
   }
-  const int qlast_wg = min(TQs, (qb + 1) * BM) - 1;
-  const int kend = qs + qlast_wg;
-  const int nkb = (kend + BN - 1) / BN;
-  const int wave_kend = wave_active ? qs + min(q0 + 32, TQs) - 1 : 0;
-  const int wave_q0abs = qs + q0;
-  int qabs[2];
-  qabs[0] = qs + q0 + li;
-  qabs[1] = qs + q0 + 16 + li;
+  const int qlast = min(TQs, qb * 64 + 64) - 1;
+  const int nkb = (qs + qlast + 63) / 64;       // keys j < qs + qlast
+  const int wq_last = min(q0 + 31, TQs - 1);    // the wave's last query row
 
-  // this lane's share of the staging: instruction n of tile X covers LDS chunks 64n .. 64n+63
-  int st_row[NINS_W], st_col[NINS_W];
-#pragma unroll
-  for (int i = 0; i < NINS_W; ++i) {
-    const int n = (wave + NW * i) % NINS;  // instruction within its tile
-    const int q = 64 * n + lane;
-    const int row = q / CPR, phys = q % CPR;
-    st_row[i] = row;
-    st_col[i] = (phys ^ tile_swz<DP>(row)) * 8;
-  }
-  auto issue = [&](int kb, int stage) {
-    const int j0 = kb * BN;
-#pragma unroll
-    for (int i = 0; i < NINS_W; ++i) {
-      const int ins = wave + NW * i;  // 0 .. 2*NINS-1: K tile first, then V
-      if (ins < 2 * NINS) {
-        const bool isv = ins >= NINS;
-        const int n = ins % NINS;
-        const int j = min(j0 + st_row[i], TKs - 1);  // rows past the keys: any finite row (masked)
-        const bf16_t* src = (isv ? vbase + int64_t(j) * p.v_sr : kbase + int64_t(j) * p.k_sr) + st_col[i];
-        bf16_t* dst = smem + (2 * stage + (isv ? 1 : 0)) * TILE + n * 512;
-        __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)src,
-                                         (void __attribute__((address_space(3)))*)dst, 16, 0, 0);
-      }
-    }
-  };
-
+  TileStager<DP, 4, 2> st;
+  st.init(wave, lane);
+  const bf16_t* srcs[2] = {kbase, vbase};
+  const int64_t strides[2] = {p.k_sr, p.v_sr};
   const float c2 = p.scale * kLog2e;
   float m_run[2] = {kNegInf, kNegInf};
   float l_run[2] = {0.f, 0.f};
@@ -577,33 +534,68 @@ __global__ void __launch_bounds__(NW * 64) relation_fwd_lds_kernel(const FwdPara
     for (int s = 0; s < 2; ++s) oacc[dt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   if (nkb > 0) {
-    issue(0, 0);
+    st.issue(smem, srcs, strides, 0, TKs - 1, wave);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
   for (int kb = 0; kb < nkb; ++kb) {
     const int stage = kb & 1;
-    if (kb + 1 < nkb) issue(kb + 1, stage ^ 1);
-    const int j0 = kb * BN;
-    if (wave_active && j0 < wave_kend) {
-      const bf16_t* Ks = smem + (2 * stage) * TILE;
-      const bf16_t* Vs = Ks + TILE;
-      if (j0 + BN > wave_q0abs)
-        fwd_block<DP, true>(Ks, Vs, qf, oacc, m_run, l_run, j0, qabs, c2, li, lg);
+    if (kb + 1 < nkb) st.issue(smem + (stage ^ 1) * STAGE, srcs, strides, (kb + 1) * 64, TKs - 1, wave);
+    const bf16_t* Ks = smem + stage * STAGE;
+    const bf16_t* Vs = Ks + TILE;
+    const int key0 = kb * 64 + 32 * kh;
+    if (q0 < TQs && key0 < qs + wq_last) {
+      if (key0 + 31 >= qs + q0)
+        fwd_quad<DP, true>(Ks, Vs, qf, oacc, m_run, l_run, key0, qabs, c2, kh, li, lg);
       else
-        fwd_block<DP, false>(Ks, Vs, qf, oacc, m_run, l_run, j0, qabs, c2, li, lg);
+        fwd_quad<DP, false>(Ks, Vs, qf, oacc, m_run, l_run, key0, qabs, c2, kh, li, lg);
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
-  if (!wave_active) return;
+
+  // per-lane row sums over the four lane groups
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    l_run[s] += wave_xor(l_run[s], 16);
+    l_run[s] += wave_xor(l_run[s], 32);
+  }
+  // merge the key halves: kh = 1 hands (m, l, O) to kh = 0 through LDS
+  float* R = reinterpret_cast<float*>(smem);     // [64 queries][RLD]
+  float* RM = R + 64 * RLD;                      // [64] m, then [64] l
+  __syncthreads();
+  if (kh == 1) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int row = 32 * qh + 16 * s + li;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4*>(&R[row * RLD + 16 * dt + 4 * lg]) = oacc[dt][s];
+      if (lg == 0) {
+        RM[row] = m_run[s];
+        RM[64 + row] = l_run[s];
+      }
+    }
+  }
+  __syncthreads();
+  if (kh == 1) return;
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const int row = 32 * qh + 16 * s + li;
+    const float m1 = RM[row], l1 = RM[64 + row];
+    const float mm = fmaxf(m_run[s], m1);
+    const float ref = mm == kNegInf ? 0.f : mm;
+    const float a0 = fexp2(m_run[s] - ref), a1 = fexp2(m1 - ref);
+    l_run[s] = l_run[s] * a0 + l1 * a1;
+    m_run[s] = mm;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+      oacc[dt][s] = oacc[dt][s] * a0 + *reinterpret_cast<const f32x4*>(&R[row * RLD + 16 * dt + 4 * lg]) * a1;
+  }
 
   const float lam = *p.lam;
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
-    float lt = l_run[s];
-    lt += wave_xor(lt, 16);
-    lt += wave_xor(lt, 32);
+    const float lt = l_run[s];
     const int qi = q0 + 16 * s + li;
     const bool qv = qi < TQs;
     const int qa = qs + qi;
@@ -720,10 +712,10 @@ int launch_fwd(const mote_relation_fwd_args* a, hipStream_t stream) {
     fp.nqb = (a->TQ + 63) / 64;
     const int nb = int(units * fp.nqb);
     switch (DP) {
-      case 32: hipLaunchKernelGGL((relation_fwd_lds_kernel<32, 2>), dim3(nb), dim3(128), 0, stream, fp); break;
-      case 64: hipLaunchKernelGGL((relation_fwd_lds_kernel<64, 2>), dim3(nb), dim3(128), 0, stream, fp); break;
-      case 96: hipLaunchKernelGGL((relation_fwd_lds_kernel<96, 2>), dim3(nb), dim3(128), 0, stream, fp); break;
-      default: hipLaunchKernelGGL((relation_fwd_lds_kernel<128, 2>), dim3(nb), dim3(128), 0, stream, fp); break;
+      case 32: hipLaunchKernelGGL((relation_fwd_tile_kernel<32>), dim3(nb), dim3(256), 0, stream, fp); break;
+      case 64: hipLaunchKernelGGL((relation_fwd_tile_kernel<64>), dim3(nb), dim3(256), 0, stream, fp); break;
+      case 96: hipLaunchKernelGGL((relation_fwd_tile_kernel<96>), dim3(nb), dim3(256), 0, stream, fp); break;
+      default: hipLaunchKernelGGL((relation_fwd_tile_kernel<128>), dim3(nb), dim3(256), 0, stream, fp); break;
     }
   } else if (a->dtype == MOTE_BF16) {
     if (wide) {
