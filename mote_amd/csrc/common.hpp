@@ -14,6 +14,14 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+// Timestamp hook of the tile kernels' block loops: MOTE_STAMP(slot, iteration) marks the points
+// (0 loop top, 1 after the prefetch issue, 2 after the block math, 3 after the load wait, 4 after the
+// barrier). It compiles to nothing unless a profiling translation unit defines it before including a
+// kernel source.
+#ifndef MOTE_STAMP
+#define MOTE_STAMP(slot, it) ((void)0)
+#endif
+
 namespace mote {
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;

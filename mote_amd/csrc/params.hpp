@@ -40,6 +40,13 @@ size_t decode_workspace_bytes(const mote_relation_decode_args* a);
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
 
+// The tile kernels address staged rows with 32-bit offsets from the block's first row.
+inline bool tile_strides_ok(const mote_view& a, const mote_view& b, const mote_view& c) {
+  const int64_t lim = int64_t(1) << 24;
+  return a.stride_r >= 0 && a.stride_r < lim && b.stride_r >= 0 && b.stride_r < lim && c.stride_r >= 0 &&
+         c.stride_r < lim;
+}
+
 // The padded head dim a kernel instance is compiled for: D rounded up to 32 (D <= 128, D % 8 == 0).
 inline int padded_dim(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <= 96 ? 96 : 128; }
 

@@ -728,7 +728,9 @@ struct WsLayout {
 static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 // bf16 with a head dim the tile kernels are compiled for: the atomic-free tile path.
-static bool use_tiles(const mote_relation_bwd_args* a) { return a->dtype == MOTE_BF16 && padded_dim(a->D) == a->D; }
+static bool use_tiles(const mote_relation_bwd_args* a) {
+  return a->dtype == MOTE_BF16 && padded_dim(a->D) == a->D && tile_strides_ok(a->p1, a->p2, a->info);
+}
 
 static WsLayout ws_layout(const mote_relation_bwd_args* a) {
   const size_t es = a->dtype == MOTE_BF16 ? 2 : 4;

@@ -25,6 +25,8 @@
 // dW^T = V dI-bar^T (keys in the accumulator rows), dU^T in the accumulator layout is the permuted-k
 // B operand of dQ^T += K^T dU^T, and K^T comes from transposed reads of the K tile. The key-half
 // waves add through LDS; the Self part dU_ii P2_i joins before the store.
+#include <type_traits>
+
 #include "common.hpp"
 #include "bwd.hpp"
 #include "tiles.hpp"
@@ -50,11 +52,9 @@ __device__ __forceinline__ float bwd_elem(float u, float dw, float lse2, float c
 // key-stationary kernel: dP2 and dI~
 // ------------------------------------------------------------------------------------------------
 template <int DP, bool MASKED>
-__device__ __forceinline__ void kv_block(const bf16_t* Qs, const bf16_t* Ds, const float* Ss,
-                                         const Elem<bf16_t>::Frag (&kf)[2][DP / 32],
-                                         const Elem<bf16_t>::Frag (&vf)[2][DP / 32], f32x4 (&dvacc)[2][DP / 16],
-                                         f32x4 (&dkacc)[2][DP / 16], int qh, int li, int lg, int key0, int qa0,
-                                         float nc2, float scale) {
+__device__ __forceinline__ void kv_block(const bf16_t* Qs, const bf16_t* Ds, const float* Ss, const bf16_t* Ks,
+                                         const bf16_t* Vs, f32x4 (&dvacc)[2][DP / 16], f32x4 (&dkacc)[2][DP / 16],
+                                         int qh, int kh, int li, int lg, int key0, int qa0, float nc2, float scale) {
   using E = Elem<bf16_t>;
   using Frag = E::Frag;
   constexpr int KS = DP / 32, DT = DP / 16;
@@ -68,6 +68,12 @@ __device__ __forceinline__ void kv_block(const bf16_t* Qs, const bf16_t* Ds, con
     }
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
+    Frag kf[2], vf[2];  // the wave's keys as B fragments (k = head dim, column = key)
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      kf[kt] = tile_row_frag<DP>(Ks, 32 * kh + 16 * kt + li, 4 * ks + lg);
+      vf[kt] = tile_row_frag<DP>(Vs, 32 * kh + 16 * kt + li, 4 * ks + lg);
+    }
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
       const int row = 32 * qh + 16 * qt + li;
@@ -75,8 +81,8 @@ __device__ __forceinline__ void kv_block(const bf16_t* Qs, const bf16_t* Ds, con
       const Frag ad = tile_row_frag<DP>(Ds, row, 4 * ks + lg);
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) {
-        sacc[qt][kt] = E::mma(aq, kf[kt][ks], sacc[qt][kt]);
-        wacc[qt][kt] = E::mma(ad, vf[kt][ks], wacc[qt][kt]);
+        sacc[qt][kt] = E::mma(aq, kf[kt], sacc[qt][kt]);
+        wacc[qt][kt] = E::mma(ad, vf[kt], wacc[qt][kt]);
       }
     }
   }
@@ -127,8 +133,10 @@ bwd_kv_kernel(const BwdParams p) {
   constexpr int KS = DP / 32, DT = DP / 16, CPR = DP / 8, TILE = 64 * DP;
   constexpr int STAGE = 2 * TILE + 256;  // bf16 slots per stage: Q tile, dI-bar tile, 128 fp32 stats
   __shared__ __align__(16) bf16_t smem[2 * STAGE];
+  __shared__ __align__(16) bf16_t kvs[2 * TILE];  // the workgroup's 64 P2 rows, then its 64 I~ rows
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: staging in scalar registers
   const int li = lane & 15, lg = lane >> 4;
   const int kh = wave & 1, qh = wave >> 1;
   const int BH = p.B * p.H;
@@ -143,19 +151,7 @@ bwd_kv_kernel(const BwdParams p) {
   const bf16_t* dbase = reinterpret_cast<const bf16_t*>(p.wdib) + int64_t(bh) * p.TQp * DP;
   const float* sbase = p.stat + int64_t(bh) * nqb * 128;
 
-  // the wave's 32 keys as B fragments (k = head dim, column = key)
   const int key0 = k0 + 32 * kh;
-  Frag kf[2][KS], vf[2][KS];
-#pragma unroll
-  for (int kt = 0; kt < 2; ++kt) {
-    const int j = key0 + 16 * kt + li;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int d0 = 32 * ks + 8 * lg;
-      kf[kt][ks] = j < p.TK ? E::load8(kbase + int64_t(j) * p.k_sr + d0) : E::zero();
-      vf[kt][ks] = j < p.TK ? E::load8(vbase + int64_t(j) * p.v_sr + d0) : E::zero();
-    }
-  }
   f32x4 dvacc[2][DT], dkacc[2][DT];
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt)
@@ -165,13 +161,13 @@ bwd_kv_kernel(const BwdParams p) {
       dkacc[kt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-  TileStager<DP, 4, 2> st;
-  st.init(wave, lane);
   const bf16_t* srcs[2] = {qbase, dbase};
   const int64_t strides[2] = {p.q_sr, DP};
+  TileStager<DP, 4, 2> st;
+  st.init(wave, lane, strides);
   auto issue = [&](int qb, int stage) {
     bf16_t* dst = smem + stage * STAGE;
-    st.issue(dst, srcs, strides, qb * 64, p.TQ - 1, wave);
+    st.issue(dst, srcs, strides, qb * 64, p.TQ - 1, wave, lane);
     if (wave == 3 && lane < 32) {
       const float* src = sbase + int64_t(qb) * 128 + 4 * lane;
       __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)src,
@@ -181,29 +177,45 @@ bwd_kv_kernel(const BwdParams p) {
 
   const float nc2 = -p.scale * kLog2e;
   const int qb_lo = max(0, k0 + 1 - p.q_start) / 64;
-  if (qb_lo < nqb) {
-    issue(qb_lo, 0);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+  {
+    // the key rows once (rows past the keys: finite copies whose results are never stored)
+    const bf16_t* ksrc[2] = {kbase, vbase};
+    const int64_t kstr[2] = {p.k_sr, p.v_sr};
+    TileStager<DP, 4, 2> kst;
+    kst.init(wave, lane, kstr);
+    kst.issue(kvs, ksrc, kstr, k0, p.TK - 1, wave, lane);
   }
-  for (int qb = qb_lo; qb < nqb; ++qb) {
+  if (qb_lo < nqb) issue(qb_lo, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  // Diagonal query blocks (some key not before some query) first, with the masked block math, then
+  // the rest with the unmasked math: two loops instead of a branch keeps one register assignment
+  // of the accumulators per loop.
+  auto step = [&](int qb, auto masked) {
+    MOTE_STAMP(0, qb - qb_lo);
     const int stage = (qb - qb_lo) & 1;
     if (qb + 1 < nqb) issue(qb + 1, stage ^ 1);
+    MOTE_STAMP(1, qb - qb_lo);
     const bf16_t* Qs = smem + stage * STAGE;
     const bf16_t* Ds = Qs + TILE;
     const float* Ss = reinterpret_cast<const float*>(Qs + 2 * TILE);
     const int i0 = qb * 64 + 32 * qh;   // the wave's first query row
     const int qa0 = p.q_start + i0;     // its position
     // quadrant visible at all (some key < some query position), and not wholly padding rows
-    if (i0 < p.TQ && key0 < qa0 + 31) {
-      if (key0 + 31 >= qa0)
-        kv_block<DP, true>(Qs, Ds, Ss, kf, vf, dvacc, dkacc, qh, li, lg, key0, qa0, nc2, p.scale);
-      else
-        kv_block<DP, false>(Qs, Ds, Ss, kf, vf, dvacc, dkacc, qh, li, lg, key0, qa0, nc2, p.scale);
-    }
+    if (i0 < p.TQ && key0 < qa0 + 31)
+      kv_block<DP, decltype(masked)::value>(Qs, Ds, Ss, kvs, kvs + TILE, dvacc, dkacc, qh, kh, li, lg, key0, qa0, nc2,
+                                            p.scale);
+    MOTE_STAMP(2, qb - qb_lo);
     __builtin_amdgcn_s_waitcnt(0);
+    MOTE_STAMP(3, qb - qb_lo);
     __syncthreads();
-  }
+    MOTE_STAMP(4, qb - qb_lo);
+  };
+  // unmasked for every wave once the block's first query position exceeds the last key
+  const int qb_m = min(nqb, max(qb_lo, k0 + 63 - p.q_start >= 0 ? (k0 + 63 - p.q_start) / 64 + 1 : 0));
+  int qb = qb_lo;
+  for (; qb < qb_m; ++qb) step(qb, std::true_type{});
+  for (; qb < nqb; ++qb) step(qb, std::false_type{});
 
   // add the two query halves through LDS: R[0] = dV, R[1] = dK, [64 keys][DP] fp32
   float* R = reinterpret_cast<float*>(smem);
@@ -338,7 +350,8 @@ bwd_q_kernel(const BwdParams p) {
   constexpr int RLD = DP + 4;      // fp32 row stride of the reduction buffer
   __shared__ __align__(16) bf16_t smem[2 * STAGE];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: staging in scalar registers
   const int li = lane & 15, lg = lane >> 4;
   const int kh = wave & 1, qh = wave >> 1;
   const int BH = p.B * p.H;
@@ -378,36 +391,43 @@ bwd_q_kernel(const BwdParams p) {
 #pragma unroll
     for (int s = 0; s < 2; ++s) dqacc[dt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  TileStager<DP, 4, 2> st;
-  st.init(wave, lane);
   const bf16_t* srcs[2] = {kbase, vbase};
   const int64_t strides[2] = {p.k_sr, p.v_sr};
+  TileStager<DP, 4, 2> st;
+  st.init(wave, lane, strides);
   const int qlast = min(p.TQ, i0 + 64) - 1;
   const int nkb = (p.q_start + qlast + 63) / 64;  // keys j < q_start + qlast
   const int wq_last = min(q0 + 31, p.TQ - 1);     // the wave's last query row
   const float nc2 = -p.scale * kLog2e;
 
   if (nkb > 0) {
-    st.issue(smem, srcs, strides, 0, p.TK - 1, wave);
+    st.issue(smem, srcs, strides, 0, p.TK - 1, wave, lane);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
-  for (int kb = 0; kb < nkb; ++kb) {
+  // key blocks wholly before the workgroup's first query position first (unmasked block math), then
+  // the diagonal ones (masked): two loops keep one register assignment of the accumulators each
+  auto step = [&](int kb, auto masked) {
+    MOTE_STAMP(0, kb);
     const int stage = kb & 1;
-    if (kb + 1 < nkb) st.issue(smem + (stage ^ 1) * STAGE, srcs, strides, (kb + 1) * 64, p.TK - 1, wave);
+    if (kb + 1 < nkb) st.issue(smem + (stage ^ 1) * STAGE, srcs, strides, (kb + 1) * 64, p.TK - 1, wave, lane);
+    MOTE_STAMP(1, kb);
     const bf16_t* Ks = smem + stage * STAGE;
     const bf16_t* Vs = Ks + TILE;
     const int key0 = kb * 64 + 32 * kh;
     // the quadrant has a visible pair: some key below the wave's last query position
-    if (q0 < p.TQ && key0 < p.q_start + wq_last) {
-      if (key0 + 31 >= p.q_start + q0)
-        q_block<DP, true>(Ks, Vs, qf, df, dqacc, lse2, cv, qabs, kh, li, lg, key0, nc2, p.scale);
-      else
-        q_block<DP, false>(Ks, Vs, qf, df, dqacc, lse2, cv, qabs, kh, li, lg, key0, nc2, p.scale);
-    }
+    if (q0 < p.TQ && key0 < p.q_start + wq_last)
+      q_block<DP, decltype(masked)::value>(Ks, Vs, qf, df, dqacc, lse2, cv, qabs, kh, li, lg, key0, nc2, p.scale);
+    MOTE_STAMP(2, kb);
     __builtin_amdgcn_s_waitcnt(0);
+    MOTE_STAMP(3, kb);
     __syncthreads();
-  }
+    MOTE_STAMP(4, kb);
+  };
+  const int kb_m = min(nkb, (p.q_start + i0) / 64);
+  int kb = 0;
+  for (; kb < kb_m; ++kb) step(kb, std::false_type{});
+  for (; kb < nkb; ++kb) step(kb, std::true_type{});
 
   // add the two key halves through LDS: R[64 queries][RLD] fp32
   float* R = reinterpret_cast<float*>(smem);

@@ -20,6 +20,8 @@
 // query blocks are dispatched first (longest-processing-time order) and consecutive workgroups
 // of one query block land on different XCDs, so with 8 heads every XCD's L2 holds one head's
 // P2 / I~ rows.
+#include <type_traits>
+
 #include "common.hpp"
 #include "params.hpp"
 #include "tiles.hpp"
@@ -468,7 +470,8 @@ relation_fwd_tile_kernel(const FwdParams p) {
   constexpr int RLD = DP + 4;      // fp32 row stride of the merge buffer
   __shared__ __align__(16) bf16_t smem[2 * STAGE];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: staging in scalar registers
   const int li = lane & 15, lg = lane >> 4;
   const int kh = wave & 1, qh = wave >> 1;
   const int bid = blockIdx.x;
@@ -520,10 +523,10 @@ relation_fwd_tile_kernel(const FwdParams p) {
   const int nkb = (qs + qlast + 63) / 64;       // keys j < qs + qlast
   const int wq_last = min(q0 + 31, TQs - 1);    // the wave's last query row
 
-  TileStager<DP, 4, 2> st;
-  st.init(wave, lane);
   const bf16_t* srcs[2] = {kbase, vbase};
   const int64_t strides[2] = {p.k_sr, p.v_sr};
+  TileStager<DP, 4, 2> st;
+  st.init(wave, lane, strides);
   const float c2 = p.scale * kLog2e;
   float m_run[2] = {kNegInf, kNegInf};
   float l_run[2] = {0.f, 0.f};
@@ -534,25 +537,32 @@ relation_fwd_tile_kernel(const FwdParams p) {
     for (int s = 0; s < 2; ++s) oacc[dt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   if (nkb > 0) {
-    st.issue(smem, srcs, strides, 0, TKs - 1, wave);
+    st.issue(smem, srcs, strides, 0, TKs - 1, wave, lane);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
-  for (int kb = 0; kb < nkb; ++kb) {
+  // key blocks wholly before the workgroup's first query position first (unmasked block math), then
+  // the diagonal ones (masked): two loops keep one register assignment of the accumulators each
+  auto step = [&](int kb, auto masked) {
+    MOTE_STAMP(0, kb);
     const int stage = kb & 1;
-    if (kb + 1 < nkb) st.issue(smem + (stage ^ 1) * STAGE, srcs, strides, (kb + 1) * 64, TKs - 1, wave);
+    if (kb + 1 < nkb) st.issue(smem + (stage ^ 1) * STAGE, srcs, strides, (kb + 1) * 64, TKs - 1, wave, lane);
+    MOTE_STAMP(1, kb);
     const bf16_t* Ks = smem + stage * STAGE;
     const bf16_t* Vs = Ks + TILE;
     const int key0 = kb * 64 + 32 * kh;
-    if (q0 < TQs && key0 < qs + wq_last) {
-      if (key0 + 31 >= qs + q0)
-        fwd_quad<DP, true>(Ks, Vs, qf, oacc, m_run, l_run, key0, qabs, c2, kh, li, lg);
-      else
-        fwd_quad<DP, false>(Ks, Vs, qf, oacc, m_run, l_run, key0, qabs, c2, kh, li, lg);
-    }
+    if (q0 < TQs && key0 < qs + wq_last)
+      fwd_quad<DP, decltype(masked)::value>(Ks, Vs, qf, oacc, m_run, l_run, key0, qabs, c2, kh, li, lg);
+    MOTE_STAMP(2, kb);
     __builtin_amdgcn_s_waitcnt(0);
+    MOTE_STAMP(3, kb);
     __syncthreads();
-  }
+    MOTE_STAMP(4, kb);
+  };
+  const int kb_m = min(nkb, (qs + qb * 64) / 64);
+  int kb = 0;
+  for (; kb < kb_m; ++kb) step(kb, std::false_type{});
+  for (; kb < nkb; ++kb) step(kb, std::true_type{});
 
   // per-lane row sums over the four lane groups
 #pragma unroll
@@ -708,7 +718,7 @@ int launch_fwd(const mote_relation_fwd_args* a, hipStream_t stream) {
   const int64_t units = int64_t(a->B) * a->H;
   const int nqb4 = (a->TQ + 127) / 128;
   const bool wide = units * nqb4 >= 512;
-  if (a->dtype == MOTE_BF16 && DP == a->D) {
+  if (a->dtype == MOTE_BF16 && DP == a->D && tile_strides_ok(a->p1, a->p2, a->info)) {
     fp.nqb = (a->TQ + 63) / 64;
     const int nb = int(units * fp.nqb);
     switch (DP) {

@@ -54,41 +54,64 @@ __device__ __forceinline__ typename Elem<bf16_t>::Frag tile_row_frag(const bf16_
 }
 
 // Staging of NT tiles per stage by the NW waves of a workgroup: the NT * CPR wave instructions are
-// dealt round-robin over the waves; each lane precomputes its row and source column per instruction.
+// dealt round-robin over the waves; each lane precomputes, per instruction, its row in the block and
+// the element offset of its source chunk from the block's first row (row * stride + column), so a
+// full block costs one 64-bit add per instruction. `wave` must be wave-uniform (readfirstlane), which
+// keeps the LDS destinations and the per-block bases in scalar registers. Row strides must stay below
+// 2^24 elements (checked by the host launchers).
 template <int DP, int NW, int NT>
 struct TileStager {
   static constexpr int CPR = DP / 8;
   static constexpr int NINS = NT * CPR;
   static constexpr int PER = (NINS + NW - 1) / NW;
-  int row[PER];
-  int col[PER];
+  int off[PER];
 
-  __device__ __forceinline__ void init(int wave, int lane) {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int n = (wave + NW * i) % CPR;
-      const int q = 64 * n + lane;
-      row[i] = q / CPR;
-      col[i] = ((q % CPR) ^ tile_swz<DP>(row[i])) * 8;
-    }
+  __device__ __forceinline__ static int row_of(int n, int lane) { return (64 * n + lane) / CPR; }
+  __device__ __forceinline__ static int col_of(int n, int lane) {
+    const int q = 64 * n + lane;
+    return ((q % CPR) ^ tile_swz<DP>(q / CPR)) * 8;
   }
 
-  // Rows r0 .. r0+63 of every source (row index clamped to rlast: rows past the end load a finite
-  // copy of the last row, which the kernels mask) into dst, tiles back to back.
-  __device__ __forceinline__ void issue(bf16_t* dst, const bf16_t* const (&src)[NT], const int64_t (&stride)[NT], int r0,
-                                        int rlast, int wave) const {
+  __device__ __forceinline__ void init(int wave, int lane, const int64_t (&stride)[NT]) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int ins = wave + NW * i;
-      if (ins < NINS) {
-        const int t = ins / CPR, n = ins % CPR;
-        const int j = min(r0 + row[i], rlast);
-        const bf16_t* g = src[t] + int64_t(j) * stride[t] + col[i];
-        bf16_t* l = dst + t * 64 * DP + n * 512;
-        __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)g,
-                                         (void __attribute__((address_space(3)))*)l, 16, 0, 0);
+      const int t = ins < NINS ? ins / CPR : 0, n = ins % CPR;
+      off[i] = row_of(n, lane) * int(stride[t]) + col_of(n, lane);
+    }
+  }
+
+  // Rows r0 .. r0+63 of every source into dst, tiles back to back. Rows past rlast load a finite
+  // copy of row rlast instead (the kernels mask them).
+  __device__ __forceinline__ void issue(bf16_t* dst, const bf16_t* const (&src)[NT], const int64_t (&stride)[NT], int r0,
+                                        int rlast, int wave, int lane) const {
+    if (r0 + 63 <= rlast) {
+      // whole block in range: scalar base + the precomputed lane offset
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int ins = wave + NW * i;
+        if (NINS % NW == 0 || ins < NINS) {
+          const int t = ins / CPR, n = ins % CPR;
+          const bf16_t* g = src[t] + int64_t(r0) * stride[t] + off[i];
+          load(g, dst + t * 64 * DP + n * 512);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int ins = wave + NW * i;
+        if (NINS % NW == 0 || ins < NINS) {
+          const int t = ins / CPR, n = ins % CPR;
+          const int j = min(r0 + row_of(n, lane), rlast);
+          load(src[t] + int64_t(j) * stride[t] + col_of(n, lane), dst + t * 64 * DP + n * 512);
+        }
       }
     }
+  }
+
+  __device__ __forceinline__ static void load(const bf16_t* g, bf16_t* l) {
+    __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)g,
+                                     (void __attribute__((address_space(3)))*)l, 16, 0, 0);
   }
 };
 
