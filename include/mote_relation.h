@@ -59,6 +59,11 @@ const char* mote_version(void);
  * mote/model/dc.py:192-218): B sequences packed along the row axis, sequence b owning rows
  * [cu_seqlens[b], cu_seqlens[b+1]); q_start must be 0, TQ = TK = the longest sequence, total_rows =
  * cu_seqlens[B]; stride_b is ignored; ibar is [H, total_rows, D], lse/g are [H, total_rows].
+ * Workspace (optional): with at least mote_relation_fwd_workspace() bytes of device memory the
+ * longest query blocks are split over two workgroups whose partial softmax states merge in a
+ * second launch, which evens out the causal imbalance; with workspace == NULL every query block
+ * runs in one workgroup. Results are identical up to float rounding of the merge; contents of the
+ * workspace on entry do not matter. Calls that share a workspace must not overlap.
  * ------------------------------------------------------------------------------------------------ */
 typedef struct mote_relation_fwd_args {
   int dtype;          /* MOTE_F32 or MOTE_BF16, for p1, p2, info and y */
@@ -71,8 +76,11 @@ typedef struct mote_relation_fwd_args {
   const float* lam;   /* device pointer to the fp32 count-calibration scalar */
   const int32_t* cu_seqlens;
   int total_rows;
+  void* workspace;
+  size_t workspace_bytes;
 } mote_relation_fwd_args;
 
+size_t mote_relation_fwd_workspace(const mote_relation_fwd_args* args);
 int mote_relation_fwd(const mote_relation_fwd_args* args, void* stream);
 
 /* ------------------------------------------------------------------------------------------------

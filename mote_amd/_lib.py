@@ -36,6 +36,7 @@ class FwdArgs(C.Structure):
         ("p1", View), ("p2", View), ("info", View), ("y", View),
         ("ibar", C.c_void_p), ("lse", C.c_void_p), ("g", C.c_void_p), ("lam", C.c_void_p),
         ("cu_seqlens", C.c_void_p), ("total_rows", C.c_int),
+        ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
     ]
 
 
@@ -87,6 +88,7 @@ class DecodeArgs(C.Structure):
 EXPORTS = {
     "mote_last_error": ([], C.c_char_p),
     "mote_version": ([], C.c_char_p),
+    "mote_relation_fwd_workspace": ([C.POINTER(FwdArgs)], C.c_size_t),
     "mote_relation_fwd": ([C.POINTER(FwdArgs), C.c_void_p], C.c_int),
     "mote_relation_bwd_workspace": ([C.POINTER(BwdArgs)], C.c_size_t),
     "mote_relation_bwd": ([C.POINTER(BwdArgs), C.c_void_p], C.c_int),

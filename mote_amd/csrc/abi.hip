@@ -34,6 +34,10 @@ const char* mote_last_error(void) { return mote::g_err; }
 
 const char* mote_version(void) { return "mote_relation 0.1 gfx950"; }
 
+size_t mote_relation_fwd_workspace(const mote_relation_fwd_args* args) {
+  return args ? mote::fwd_workspace_bytes(args) : 0;
+}
+
 int mote_relation_fwd(const mote_relation_fwd_args* args, void* stream) {
   mote::g_err[0] = 0;
   return mote::launch_fwd(args, reinterpret_cast<hipStream_t>(stream));

@@ -48,6 +48,27 @@ __device__ __forceinline__ float sigmoid_acc(float x) { return 1.0f / (1.0f + ex
 
 __device__ __forceinline__ float wave_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
 
+// Max / sum over the four lanes li, li + 16, li + 32, li + 48 (one value per accumulator column)
+// with the gfx950 row swaps: v_permlane16_swap / v_permlane32_swap of a register with itself put
+// the partner row's value in one of the two results and the lane's own value in the other.
+typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
+__device__ __forceinline__ float lanegroup_max(float x) {
+  const unsigned u = __float_as_uint(x);
+  const u32x2 a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const unsigned v = __float_as_uint(x);
+  const u32x2 b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float lanegroup_sum(float x) {
+  const unsigned u = __float_as_uint(x);
+  const u32x2 a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const unsigned v = __float_as_uint(x);
+  const u32x2 b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // ------------------------------------------------------------------------------------------------
 // Element traits: fragments and the K32 matrix step
 // ------------------------------------------------------------------------------------------------

@@ -19,6 +19,8 @@ struct FwdParams {
   float* g;
   const float* lam;
   const int32_t* cu;  // null in dense mode
+  float* part;        // split partials [nseq][H][nqb][2][64 * DP + 128] (null: no split)
+  int split_c;        // query blocks with more key blocks than this run as two halves
   int64_t q_sb, q_sh, q_sr;
   int64_t k_sb, k_sh, k_sr;
   int64_t v_sb, v_sh, v_sr;
@@ -28,6 +30,7 @@ struct FwdParams {
 };
 
 int launch_fwd(const mote_relation_fwd_args* a, hipStream_t stream);
+size_t fwd_workspace_bytes(const mote_relation_fwd_args* a);
 int launch_bwd(const mote_relation_bwd_args* a, hipStream_t stream);
 size_t bwd_workspace_bytes(const mote_relation_bwd_args* a);
 int launch_rope_givens_fwd(const mote_rope_givens_args* a, hipStream_t stream);

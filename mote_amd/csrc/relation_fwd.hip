@@ -383,14 +383,20 @@ __global__ void __launch_bounds__(NW * 64) relation_fwd_kernel(const FwdParams p
 //                     (a lane holds one query and keys 4g + r of each 16-key tile: the permuted k
 //                     order both fragments share)
 // ------------------------------------------------------------------------------------------------
-template <int DP, bool MASKED>
-__device__ __forceinline__ void fwd_quad(const bf16_t* Ks, const bf16_t* Vs, const typename Elem<bf16_t>::Frag (&qf)[2][DP / 32],
-                                         f32x4 (&oacc)[DP / 16][2], float (&m_run)[2], float (&l_run)[2], int key0,
-                                         const int (&qabs)[2], float c2, int kh, int li, int lg) {
+// The running reference m of a query's online softmax is an upper bound of its exponents rather
+// than their maximum: with u2 = U log2e, the exponent SiLU(U) log2e = u2 sigmoid(U) never exceeds
+// max(u2, 0), so the block's bound comes from the raw dot products (one max per element, no SiLU
+// needed first) and m starts at 0. Exponents then stay in [-0.4, 0] below the bound for u2 >= 0
+// and the row sum l is exact up to rounding whatever m is; LSE = (m + log2 l) ln2.
+// The row sums come from the P^T fragments too: one more product with a fragment whose row 0 is
+// all ones adds sum_k P[k][q] into row 0 of `lacc`.
+// S^T = K Q^T for the wave's quadrant: keys 32 kh + 16 kt + 4 lg + r (rows), query 16 s + li.
+template <int DP>
+__device__ __forceinline__ void fwd_scores(const bf16_t* Ks, const typename Elem<bf16_t>::Frag (&qf)[2][DP / 32],
+                                           f32x4 (&sacc)[2][2], int kh, int li, int lg) {
   using E = Elem<bf16_t>;
   using Frag = E::Frag;
-  constexpr int KS = DP / 32, DT = DP / 16;
-  f32x4 sacc[2][2];  // [key tile][query tile]
+  constexpr int KS = DP / 32;
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
@@ -404,34 +410,52 @@ __device__ __forceinline__ void fwd_quad(const bf16_t* Ks, const bf16_t* Vs, con
       for (int s = 0; s < 2; ++s) sacc[kt][s] = E::mma(kf, qf[s][ks], sacc[kt][s]);
     }
   }
-  // keys key0 + 16 kt + 4 lg + r (rows), query 16 s + li (column)
-  float bmax[2];
+}
+
+// Online softmax of one quadrant's scores and O^T += V^T P^T.
+// The running reference m of a query's online softmax is an upper bound of its exponents rather
+// than their maximum: with u2 = U log2e, the exponent SiLU(U) log2e = u2 sigmoid(U) never exceeds
+// max(u2, 0), so the block's bound comes from the raw dot products (one max per element, no SiLU
+// needed first) and m starts at 0. Exponents then stay within 0.4 below the bound for u2 >= 0, and
+// the row sum l is exact up to rounding whatever m is; LSE = (m + log2 l) ln2.
+// The row sums come from the P^T fragments too: one more product with a fragment whose row 0 is
+// all ones adds sum_k P[k][q] into row 0 of `lacc`.
+template <int DP, bool MASKED>
+__device__ __forceinline__ void fwd_softmax_pv(const bf16_t* Vs, const f32x4 (&sacc)[2][2], f32x4 (&oacc)[DP / 16][2],
+                                               f32x4 (&lacc)[2], float (&m_run)[2], const typename Elem<bf16_t>::Frag& ones,
+                                               int key0, const int (&qabs)[2], float c2, int kh, int li, int lg) {
+  using E = Elem<bf16_t>;
+  using Frag = E::Frag;
+  constexpr int DT = DP / 16;
+  Frag vfr[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) vfr[dt] = tile_tr_frag<DP>(Vs, 32 * kh, dt, li, lg);
+  __builtin_amdgcn_sched_barrier(0);
+  bool keep[2][2][4];
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) keep[s][kt][r] = !MASKED || key0 + 16 * kt + 4 * lg + r < qabs[s];
+  float bnd[2];
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
     float mx = kNegInf;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float u2 = sacc[kt][s][r] * c2;
-        float e = u2 * frcp(1.0f + fexp2(-u2));
-        if constexpr (MASKED) {
-          if (key0 + 16 * kt + 4 * lg + r >= qabs[s]) e = kNegInf;
-        }
-        sacc[kt][s][r] = e;
-        mx = fmaxf(mx, e);
-      }
-    mx = fmaxf(mx, wave_xor(mx, 16));
-    mx = fmaxf(mx, wave_xor(mx, 32));
-    bmax[s] = mx;
+      for (int r = 0; r < 4; ++r) mx = fmaxf(mx, keep[s][kt][r] ? sacc[kt][s][r] : kNegInf);
+    bnd[s] = fmaxf(lanegroup_max(mx) * c2, 0.f);
   }
-  const bool need = (bmax[0] > m_run[0] + kRescale) || (bmax[1] > m_run[1] + kRescale);
+  const bool need = (bnd[0] > m_run[0] + kRescale) || (bnd[1] > m_run[1] + kRescale);
   if (__ballot(need) != 0ull) {
+    asm volatile("" ::: "memory");  // a real branch: the rescale is rare
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      const float mn = bmax[s] > m_run[s] + kRescale ? bmax[s] : m_run[s];
-      const float alpha = fexp2(m_run[s] - (mn == kNegInf ? 0.f : mn));
-      l_run[s] *= alpha;
+      const float mn = bnd[s] > m_run[s] + kRescale ? bnd[s] : m_run[s];
+      const float alpha = fexp2(m_run[s] - mn);
+      lacc[s] *= alpha;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) oacc[dt][s] *= alpha;
       m_run[s] = mn;
@@ -440,23 +464,23 @@ __device__ __forceinline__ void fwd_quad(const bf16_t* Ks, const bf16_t* Vs, con
   Frag pf[2];
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
-    const float ms = m_run[s] == kNegInf ? 0.f : m_run[s];
     float pv[8];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float pr = fexp2(sacc[kt][s][r] - ms);
-        l_run[s] += pr;
-        pv[4 * kt + r] = pr;
+        const float u2 = sacc[kt][s][r] * c2;
+        const float sg = frcp(1.0f + fexp2(-u2));
+        const float pr = fexp2(fmaf(u2, sg, -m_run[s]));
+        pv[4 * kt + r] = keep[s][kt][r] ? pr : 0.f;
       }
     pf[s] = E::from_f32(pv);
+    lacc[s] = E::mma(ones, pf[s], lacc[s]);
   }
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) {
-    const Frag vf = tile_tr_frag<DP>(Vs, 32 * kh, dt, li, lg);
 #pragma unroll
-    for (int s = 0; s < 2; ++s) oacc[dt][s] = E::mma(vf, pf[s], oacc[dt][s]);
+    for (int s = 0; s < 2; ++s) oacc[dt][s] = E::mma(vfr[dt], pf[s], oacc[dt][s]);
   }
 }
 
@@ -474,9 +498,12 @@ relation_fwd_tile_kernel(const FwdParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: staging in scalar registers
   const int li = lane & 15, lg = lane >> 4;
   const int kh = wave & 1, qh = wave >> 1;
+  // block id: head fastest, then (when split) the two halves of a query block, then query blocks
+  // (longest first)
   const int bid = blockIdx.x;
   const int h = bid % p.H;
-  const int rest = bid / p.H;
+  const int half = p.part ? (bid / p.H) & 1 : 0;
+  const int rest = p.part ? bid / p.H / 2 : bid / p.H;
   const int seq = rest % p.nseq;
   const int qb = p.nqb - 1 - rest / p.nseq;
 
@@ -522,22 +549,32 @@ relation_fwd_tile_kernel(const FwdParams p) {
   const int qlast = min(TQs, qb * 64 + 64) - 1;
   const int nkb = (qs + qlast + 63) / 64;       // keys j < qs + qlast
   const int wq_last = min(q0 + 31, TQs - 1);    // the wave's last query row
+  // long query blocks run as two workgroups over the two halves of their key blocks
+  const bool split = p.part != nullptr && nkb > p.split_c;
+  if (half == 1 && !split) return;
+  const int kb_mid = split ? (nkb + 1) / 2 : nkb;
+  const int kb_lo = half ? kb_mid : 0, kb_hi = half ? nkb : kb_mid;
 
   const bf16_t* srcs[2] = {kbase, vbase};
   const int64_t strides[2] = {p.k_sr, p.v_sr};
   TileStager<DP, 4, 2> st;
   st.init(wave, lane, strides);
   const float c2 = p.scale * kLog2e;
-  float m_run[2] = {kNegInf, kNegInf};
-  float l_run[2] = {0.f, 0.f};
+  float m_run[2] = {0.f, 0.f};
+  f32x4 lacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
   f32x4 oacc[DT][2];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
     for (int s = 0; s < 2; ++s) oacc[dt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
+  Frag ones;  // row 0 of the A operand all ones: the product sums P^T over its keys
+  {
+    const __bf16 one = (__bf16)(li == 0 ? 1.0f : 0.0f);
+    ones.v = bf16x8{one, one, one, one, one, one, one, one};
+  }
 
-  if (nkb > 0) {
-    st.issue(smem, srcs, strides, 0, TKs - 1, wave, lane);
+  if (kb_lo < kb_hi) {
+    st.issue(smem + (kb_lo & 1) * STAGE, srcs, strides, kb_lo * 64, TKs - 1, wave, lane);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
@@ -546,30 +583,31 @@ relation_fwd_tile_kernel(const FwdParams p) {
   auto step = [&](int kb, auto masked) {
     MOTE_STAMP(0, kb);
     const int stage = kb & 1;
-    if (kb + 1 < nkb) st.issue(smem + (stage ^ 1) * STAGE, srcs, strides, (kb + 1) * 64, TKs - 1, wave, lane);
+    if (kb + 1 < kb_hi) st.issue(smem + (stage ^ 1) * STAGE, srcs, strides, (kb + 1) * 64, TKs - 1, wave, lane);
     MOTE_STAMP(1, kb);
     const bf16_t* Ks = smem + stage * STAGE;
-    const bf16_t* Vs = Ks + TILE;
     const int key0 = kb * 64 + 32 * kh;
-    if (q0 < TQs && key0 < qs + wq_last)
-      fwd_quad<DP, decltype(masked)::value>(Ks, Vs, qf, oacc, m_run, l_run, key0, qabs, c2, kh, li, lg);
+    if (q0 < TQs && key0 < qs + wq_last) {
+      f32x4 sacc[2][2];
+      fwd_scores<DP>(Ks, qf, sacc, kh, li, lg);
+      fwd_softmax_pv<DP, decltype(masked)::value>(Ks + TILE, sacc, oacc, lacc, m_run, ones, key0, qabs, c2, kh, li,
+                                                  lg);
+    }
     MOTE_STAMP(2, kb);
     __builtin_amdgcn_s_waitcnt(0);
     MOTE_STAMP(3, kb);
     __syncthreads();
     MOTE_STAMP(4, kb);
   };
-  const int kb_m = min(nkb, (qs + qb * 64) / 64);
-  int kb = 0;
+  const int kb_m = min(kb_hi, (qs + qb * 64) / 64);
+  int kb = kb_lo;
   for (; kb < kb_m; ++kb) step(kb, std::false_type{});
-  for (; kb < nkb; ++kb) step(kb, std::true_type{});
+  for (; kb < kb_hi; ++kb) step(kb, std::true_type{});
 
-  // per-lane row sums over the four lane groups
+  // row sums: row 0 of lacc, held by lanes 0..15 (query li); broadcast to the other lane groups
+  float l_run[2];
 #pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    l_run[s] += wave_xor(l_run[s], 16);
-    l_run[s] += wave_xor(l_run[s], 32);
-  }
+  for (int s = 0; s < 2; ++s) l_run[s] = __shfl(lacc[s][0], li, 64);
   // merge the key halves: kh = 1 hands (m, l, O) to kh = 0 through LDS
   float* R = reinterpret_cast<float*>(smem);     // [64 queries][RLD]
   float* RM = R + 64 * RLD;                      // [64] m, then [64] l
@@ -593,13 +631,27 @@ relation_fwd_tile_kernel(const FwdParams p) {
     const int row = 32 * qh + 16 * s + li;
     const float m1 = RM[row], l1 = RM[64 + row];
     const float mm = fmaxf(m_run[s], m1);
-    const float ref = mm == kNegInf ? 0.f : mm;
-    const float a0 = fexp2(m_run[s] - ref), a1 = fexp2(m1 - ref);
+    const float a0 = fexp2(m_run[s] - mm), a1 = fexp2(m1 - mm);
     l_run[s] = l_run[s] * a0 + l1 * a1;
     m_run[s] = mm;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
       oacc[dt][s] = oacc[dt][s] * a0 + *reinterpret_cast<const f32x4*>(&R[row * RLD + 16 * dt + 4 * lg]) * a1;
+  }
+  if (split) {
+    // unnormalised state (O, m, l) of this half for the merge kernel
+    float* part = p.part + ((((int64_t)seq * p.H + h) * p.nqb + qb) * 2 + half) * (64 * DP + 128);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int row = 32 * qh + 16 * s + li;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4*>(&part[row * DP + 16 * dt + 4 * lg]) = oacc[dt][s];
+      if (lg == 0) {
+        part[64 * DP + row] = m_run[s];
+        part[64 * DP + 64 + row] = l_run[s];
+      }
+    }
+    return;
   }
 
   const float lam = *p.lam;
@@ -653,6 +705,102 @@ relation_fwd_tile_kernel(const FwdParams p) {
   }
 }
 
+// Merge of the two halves of a split query block, then the epilogue of relation_fwd_tile_kernel:
+// four threads per row, each owning DP / 4 head-dim elements.
+template <int DP>
+__global__ void __launch_bounds__(256) relation_fwd_merge_kernel(const FwdParams p) {
+  constexpr int PER = DP / 4;  // elements per thread
+  const int tid = threadIdx.x;
+  const int row = tid >> 2, quarter = tid & 3;
+  const int bid = blockIdx.x;
+  const int h = bid % p.H;
+  const int rest = bid / p.H;
+  const int seq = rest % p.nseq;
+  const int qb = rest / p.nseq;
+
+  int TQs, qs;
+  int64_t qoff, koff, voff, yoff, soff;
+  if (p.cu) {
+    const int r0 = p.cu[seq];
+    TQs = p.cu[seq + 1] - r0;
+    qs = 0;
+    qoff = int64_t(r0) * p.q_sr;
+    koff = int64_t(r0) * p.k_sr;
+    voff = int64_t(r0) * p.v_sr;
+    yoff = int64_t(r0) * p.y_sr;
+    soff = int64_t(h) * p.total_rows + r0;
+  } else {
+    TQs = p.TQ;
+    qs = p.q_start;
+    qoff = int64_t(seq) * p.q_sb;
+    koff = int64_t(seq) * p.k_sb;
+    voff = int64_t(seq) * p.v_sb;
+    yoff = int64_t(seq) * p.y_sb;
+    soff = (int64_t(seq) * p.H + h) * p.TQ;
+  }
+  if (qb * 64 >= TQs) return;
+  const int qlast = min(TQs, qb * 64 + 64) - 1;
+  const int nkb = (qs + qlast + 63) / 64;
+  if (!(nkb > p.split_c)) return;  // this query block ran whole
+  const float* P0 = p.part + (((int64_t)seq * p.H + h) * p.nqb + qb) * 2 * (64 * DP + 128);
+  const float* P1 = P0 + (64 * DP + 128);
+  const int qi = qb * 64 + row;
+  const bool qv = qi < TQs;
+  const int qa = qs + qi;
+  const float m0 = P0[64 * DP + row], l0 = P0[64 * DP + 64 + row];
+  const float m1 = P1[64 * DP + row], l1 = P1[64 * DP + 64 + row];
+  const float mm = fmaxf(m0, m1);
+  const float a0 = fexp2(m0 - mm), a1 = fexp2(m1 - mm);
+  const float lt = l0 * a0 + l1 * a1;
+  const bool has = lt > 0.f;
+  const float lse = has ? (mm + __log2f(lt)) * kLn2 : kNegInf;
+  const float inv_l = has ? 1.0f / lt : 0.f;
+  const int d0 = quarter * PER;
+  const bf16_t* qrow = reinterpret_cast<const bf16_t*>(p.p1) + qoff + int64_t(h) * p.q_sh + int64_t(qv ? qi : 0) * p.q_sr;
+  const bf16_t* krow = reinterpret_cast<const bf16_t*>(p.p2) + koff + int64_t(h) * p.k_sh + int64_t(qv ? qa : 0) * p.k_sr;
+  float ud = 0.f;
+  if (qv) {
+#pragma unroll
+    for (int c = 0; c < PER; c += 8) {
+      const bf16x8 q8 = *reinterpret_cast<const bf16x8*>(qrow + d0 + c);
+      const bf16x8 k8 = *reinterpret_cast<const bf16x8*>(krow + d0 + c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ud = fmaf((float)q8[e], (float)k8[e], ud);
+    }
+  }
+  ud += wave_xor(ud, 1);
+  ud += wave_xor(ud, 2);
+  const float sself = sigmoid_acc(ud * p.scale * p.tau_inv);
+  const float gate = has ? sigmoid_acc(lse - *p.lam * logf((float)qa + 1.0f) - sself) : 0.f;
+  if (!qv) return;
+  const bf16_t* irow = reinterpret_cast<const bf16_t*>(p.info) + voff + int64_t(h) * p.v_sh + int64_t(qa) * p.v_sr;
+  bf16_t* yrow = reinterpret_cast<bf16_t*>(p.y) + yoff + int64_t(h) * p.y_sh + int64_t(qi) * p.y_sr;
+  float* brow = p.ibar + (soff + qi) * int64_t(DP);
+#pragma unroll
+  for (int c = 0; c < PER; c += 8) {
+    const bf16x8 i8 = *reinterpret_cast<const bf16x8*>(irow + d0 + c);
+    float ib[8], yv[8];
+#pragma unroll
+    for (int e = 0; e < 8; e += 4) {
+      const float4 o0 = *reinterpret_cast<const float4*>(&P0[row * DP + d0 + c + e]);
+      const float4 o1 = *reinterpret_cast<const float4*>(&P1[row * DP + d0 + c + e]);
+      ib[e] = (o0.x * a0 + o1.x * a1) * inv_l;
+      ib[e + 1] = (o0.y * a0 + o1.y * a1) * inv_l;
+      ib[e + 2] = (o0.z * a0 + o1.z * a1) * inv_l;
+      ib[e + 3] = (o0.w * a0 + o1.w * a1) * inv_l;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) yv[e] = (1.0f - gate) * (float)i8[e] + gate * ib[e];
+    *reinterpret_cast<bf16x8*>(yrow + d0 + c) = Elem<bf16_t>::from_f32(yv).v;
+    *reinterpret_cast<float4*>(brow + d0 + c) = make_float4(ib[0], ib[1], ib[2], ib[3]);
+    *reinterpret_cast<float4*>(brow + d0 + c + 4) = make_float4(ib[4], ib[5], ib[6], ib[7]);
+  }
+  if (quarter == 0) {
+    p.lse[soff + qi] = lse;
+    p.g[soff + qi] = gate;
+  }
+}
+
 // ------------------------------------------------------------------------------------------------
 // host launcher
 // ------------------------------------------------------------------------------------------------
@@ -673,6 +821,29 @@ static void launch_fwd_dp(const FwdParams& fp, int DP, int nblocks, hipStream_t 
 
 static bool view_ok(const mote_view& v) { return v.data != nullptr; }
 
+// The tile kernel serves bf16 with D in {32, 64, 96, 128} and row strides below 2^24.
+static bool fwd_tiles(const mote_relation_fwd_args* a) {
+  return a->dtype == MOTE_BF16 && padded_dim(a->D) == a->D && tile_strides_ok(a->p1, a->p2, a->info);
+}
+
+// Key blocks of the longest query block; query blocks with more than split_c of them run as halves.
+static int fwd_max_key_blocks(const mote_relation_fwd_args* a) {
+  const int qs = a->cu_seqlens ? 0 : a->q_start;
+  return (qs + a->TQ - 1 + 63) / 64;
+}
+// Measured at the Mote-96M shape (78 key blocks), splitting does not pay for the merge launch; rows
+// beyond 96 key blocks (6144 positions) split.
+static int fwd_split_c(const mote_relation_fwd_args* a) {
+  const int n = fwd_max_key_blocks(a);
+  return n > 96 ? (n + 1) / 2 : 1 << 30;
+}
+
+size_t fwd_workspace_bytes(const mote_relation_fwd_args* a) {
+  if (!a || a->TQ <= 0 || a->D <= 0 || a->D > 128 || !fwd_tiles(a) || fwd_split_c(a) >= (1 << 30)) return 0;
+  const size_t nqb = (size_t(a->TQ) + 63) / 64;
+  return size_t(a->B) * a->H * nqb * 2 * (64 * size_t(a->D) + 128) * sizeof(float);
+}
+
 int launch_fwd(const mote_relation_fwd_args* a, hipStream_t stream) {
   if (!a) return set_error(MOTE_ERR_ARGUMENT, "relation_fwd: null args");
   if (a->dtype != MOTE_F32 && a->dtype != MOTE_BF16) return set_error(MOTE_ERR_ARGUMENT, "relation_fwd: bad dtype %d", a->dtype);
@@ -689,7 +860,7 @@ int launch_fwd(const mote_relation_fwd_args* a, hipStream_t stream) {
   if (a->TQ == 0) return MOTE_OK;  // empty outputs: nothing to launch (their pointers may be null)
   if (!view_ok(a->p1) || !view_ok(a->p2) || !view_ok(a->info) || !view_ok(a->y) || !a->ibar || !a->lse || !a->g || !a->lam)
     return set_error(MOTE_ERR_ARGUMENT, "relation_fwd: null tensor pointer");
-  FwdParams fp;
+  FwdParams fp{};
   fp.p1 = a->p1.data;
   fp.p2 = a->p2.data;
   fp.info = a->info.data;
@@ -718,15 +889,23 @@ int launch_fwd(const mote_relation_fwd_args* a, hipStream_t stream) {
   const int64_t units = int64_t(a->B) * a->H;
   const int nqb4 = (a->TQ + 127) / 128;
   const bool wide = units * nqb4 >= 512;
-  if (a->dtype == MOTE_BF16 && DP == a->D && tile_strides_ok(a->p1, a->p2, a->info)) {
+  if (fwd_tiles(a)) {
     fp.nqb = (a->TQ + 63) / 64;
+    const size_t need = fwd_workspace_bytes(a);
+    const bool split = need > 0 && a->workspace && a->workspace_bytes >= need;
+    fp.part = split ? reinterpret_cast<float*>(a->workspace) : nullptr;
+    fp.split_c = split ? fwd_split_c(a) : (1 << 30);
     const int nb = int(units * fp.nqb);
+#define MOTE_FWD_TILE(DPV)                                                                                \
+  hipLaunchKernelGGL((relation_fwd_tile_kernel<DPV>), dim3(split ? 2 * nb : nb), dim3(256), 0, stream, fp); \
+  if (split) hipLaunchKernelGGL((relation_fwd_merge_kernel<DPV>), dim3(nb), dim3(256), 0, stream, fp);
     switch (DP) {
-      case 32: hipLaunchKernelGGL((relation_fwd_tile_kernel<32>), dim3(nb), dim3(256), 0, stream, fp); break;
-      case 64: hipLaunchKernelGGL((relation_fwd_tile_kernel<64>), dim3(nb), dim3(256), 0, stream, fp); break;
-      case 96: hipLaunchKernelGGL((relation_fwd_tile_kernel<96>), dim3(nb), dim3(256), 0, stream, fp); break;
-      default: hipLaunchKernelGGL((relation_fwd_tile_kernel<128>), dim3(nb), dim3(256), 0, stream, fp); break;
+      case 32: MOTE_FWD_TILE(32) break;
+      case 64: MOTE_FWD_TILE(64) break;
+      case 96: MOTE_FWD_TILE(96) break;
+      default: MOTE_FWD_TILE(128) break;
     }
+#undef MOTE_FWD_TILE
   } else if (a->dtype == MOTE_BF16) {
     if (wide) {
       fp.nqb = nqb4;

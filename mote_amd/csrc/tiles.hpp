@@ -17,6 +17,15 @@
 
 namespace mote {
 
+// s_waitcnt immediate (gfx9 encoding) that waits until at most N vector-memory operations of the
+// wave are outstanding, leaving the export and LDS/scalar counters unconstrained. Vector loads
+// return in issue order, so after issuing stage A then stage B (N instructions), waiting for N
+// leaves stage A complete.
+template <int N>
+__device__ constexpr int kVmWaitStage() {
+  return (N & 0xF) | (0x7 << 4) | (0xF << 8) | (((N >> 4) & 0x3) << 14);
+}
+
 template <int DP>
 __device__ __forceinline__ int tile_swz(int row) {
   if constexpr (DP == 64) return (row >> 1) & 7;
@@ -85,7 +94,7 @@ struct TileStager {
   // copy of row rlast instead (the kernels mask them).
   __device__ __forceinline__ void issue(bf16_t* dst, const bf16_t* const (&src)[NT], const int64_t (&stride)[NT], int r0,
                                         int rlast, int wave, int lane) const {
-    if (r0 + 63 <= rlast) {
+    if (__builtin_expect(r0 + 63 <= rlast, 1)) {
       // whole block in range: scalar base + the precomputed lane offset
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
@@ -97,6 +106,7 @@ struct TileStager {
         }
       }
     } else {
+      asm volatile("" ::: "memory");  // a separate path: keeps the full-block addresses free of clamping
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
         const int ins = wave + NW * i;

@@ -55,6 +55,18 @@ def _token_major(B, H, T, D, like: torch.Tensor, dtype) -> torch.Tensor:
     return torch.empty(B, T, H, D, device=like.device, dtype=dtype).transpose(1, 2)
 
 
+def _fwd_workspace(a, device):
+    """Scratch for the split of the longest query blocks (partial softmax states); the caller keeps
+    the returned tensor alive until the launch is queued (the caching allocator orders reuse)."""
+    n = int(L.lib().mote_relation_fwd_workspace(a))
+    if n == 0:
+        a.workspace, a.workspace_bytes = None, 0
+        return None
+    ws = torch.empty(n, device=device, dtype=torch.uint8)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), n
+    return ws
+
+
 def _launch_fwd(p1, p2, info, lam, tau_s: float, q_start: int):
     B, H, TQ, D = p1.shape
     TK = p2.shape[2]
@@ -76,6 +88,7 @@ def _launch_fwd(p1, p2, info, lam, tau_s: float, q_start: int):
     a.p1, a.p2, a.info, a.y = L.view(p1), L.view(p2), L.view(info), L.view(y)
     a.ibar, a.lse, a.g, a.lam = ibar.data_ptr(), lse.data_ptr(), g.data_ptr(), lam32.data_ptr()
     a.cu_seqlens, a.total_rows = None, 0
+    ws = _fwd_workspace(a, p1.device)
     L.check(L.lib().mote_relation_fwd(a, L.stream_of(p1)), "mote_relation_fwd")
     return y, g, ibar, lse
 
@@ -195,6 +208,7 @@ def _relation_fwd_varlen(p1: torch.Tensor, p2: torch.Tensor, info: torch.Tensor,
     a.y = L.view(y.unsqueeze(0))
     a.ibar, a.lse, a.g, a.lam = ibar.data_ptr(), lse.data_ptr(), g.data_ptr(), lam32.data_ptr()
     a.cu_seqlens, a.total_rows = cu.data_ptr(), total
+    ws = _fwd_workspace(a, p1.device)
     L.check(L.lib().mote_relation_fwd(a, L.stream_of(p1)), "mote_relation_fwd (varlen)")
     return y, g, ibar, lse
 

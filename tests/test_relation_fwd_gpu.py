@@ -66,7 +66,7 @@ def test_rescale_branch_large_scores(cuda):
     assert float((g.cpu().double() - gr).abs().max()) < 1e-5
 
 
-@pytest.mark.parametrize("D", [48, 64, 96])
+@pytest.mark.parametrize("D", [32, 48, 64, 96, 128])
 @pytest.mark.parametrize("TQ", [33, 257])
 def test_bf16_forward(cuda, D, TQ):
     from mote_amd.flash_relation import flash_relation
@@ -90,6 +90,55 @@ def test_bf16_prefix_flagship_shape(cuda):
     yr, gr = _oracle(p1, p2, info, 0.5, 64)
     assert rel_err(y, yr) < 2e-2
     assert float((g.cpu().double() - gr).abs().max()) < 2e-2
+
+
+@pytest.mark.parametrize("D,TQ,S", [(96, 6300, 0), (64, 1200, 5100), (128, 6200, 37)])
+def test_bf16_long_rows_split(cuda, D, TQ, S):
+    """Rows long enough that the longest query blocks run as two workgroups whose partial softmax
+    states merge in a second launch."""
+    from mote_amd.flash_relation import flash_relation
+
+    print(f"case bf16 split D={D} TQ={TQ} S={S}", flush=True)
+    p1, p2, info = _inputs(1, 2, TQ, S, D, torch.bfloat16, seed=13)
+    y, g = flash_relation(p1, p2, info, torch.tensor(0.4, device=cuda), 2.0, q_start=S)
+    yr, gr = _oracle(p1, p2, info, 0.4, S)
+    assert rel_err(y, yr) < 2e-2, rel_err(y, yr)
+    assert float((g.cpu().double() - gr).abs().max()) < 2e-2
+
+
+def test_split_and_whole_rows_agree(cuda):
+    """The same launch with and without the workspace (split halves merged vs one workgroup per
+    query block) gives the same statistics to float rounding."""
+    from mote_amd import _lib as L
+
+    B, H, T, D = 1, 2, 6400, 96
+    p1, p2, info = _inputs(B, H, T, 0, D, torch.bfloat16, seed=14)
+    lam = torch.tensor([0.5], device=cuda)
+    outs = []
+    for use_ws in (False, True):
+        y = torch.empty(B, H, T, D, device=cuda, dtype=torch.bfloat16)
+        ibar = torch.empty(B, H, T, D, device=cuda)
+        lse = torch.empty(B, H, T, device=cuda)
+        g = torch.empty(B, H, T, device=cuda)
+        a = L.FwdArgs()
+        a.dtype, a.B, a.H, a.TQ, a.TK, a.D, a.q_start, a.tau_s = L.MOTE_BF16, B, H, T, T, D, 0, 2.0
+        a.p1, a.p2, a.info, a.y = L.view(p1), L.view(p2), L.view(info), L.view(y)
+        a.ibar, a.lse, a.g, a.lam = ibar.data_ptr(), lse.data_ptr(), g.data_ptr(), lam.data_ptr()
+        n = int(L.lib().mote_relation_fwd_workspace(a))
+        assert n > 0
+        ws = torch.empty(n, device=cuda, dtype=torch.uint8)
+        if use_ws:
+            a.workspace, a.workspace_bytes = ws.data_ptr(), n
+        L.check(L.lib().mote_relation_fwd(a, L.stream_of(p1)), "fwd")
+        torch.cuda.synchronize()
+        outs.append((ibar, lse, g, y))
+    (ib0, l0, g0, y0), (ib1, l1, g1, y1) = outs
+    assert rel_err(ib1, ib0) < 1e-5
+    assert torch.equal(torch.isinf(l1), torch.isinf(l0))  # rows without a past: LSE = -inf in both
+    fin = torch.isfinite(l0)
+    assert float((l1[fin] - l0[fin]).abs().max()) < 1e-4
+    assert float((g1 - g0).abs().max()) < 1e-5
+    assert float((y1.float() - y0.float()).abs().max()) <= 2 ** -6 * float(y0.float().abs().max())
 
 
 def test_first_position_is_pure_self(cuda):
@@ -120,7 +169,7 @@ def test_varlen_equals_per_sequence(cuda):
     from mote_amd.flash_relation import flash_relation_varlen
 
     H, D = 4, 96
-    lens = [37, 200, 1, 129, 64]
+    lens = [37, 200, 1, 129, 64, 6300]
     cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32)
     total = int(cu[-1])
     g = torch.Generator().manual_seed(12)
