@@ -195,18 +195,15 @@ __global__ void __launch_bounds__(256) rope_givens_bwd_kernel(const RopeBwdParam
 }
 
 __global__ void __launch_bounds__(256) sum_partials_kernel(const float* partial, int rows, int npair, float* out) {
-  // one block per pair; fixed-order strided sums, then a fixed tree
-  __shared__ float red[256];
-  const int pr = blockIdx.x;
-  float acc = 0.f;
-  for (int r = threadIdx.x; r < rows; r += 256) acc += partial[int64_t(r) * npair + pr];
-  red[threadIdx.x] = acc;
-  __syncthreads();
-  for (int w = 128; w >= 1; w >>= 1) {
-    if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
-    __syncthreads();
+  // one wave per pair (pairs strided over the waves): fixed-order strided sums, then a fixed tree
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int pr = blockIdx.x * 4 + wave; pr < npair; pr += gridDim.x * 4) {
+    float acc = 0.f;
+    for (int r = lane; r < rows; r += 64) acc += partial[int64_t(r) * npair + pr];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if (lane == 0) out[pr] = acc;
   }
-  if (threadIdx.x == 0) out[pr] = red[0];
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -237,36 +234,65 @@ __device__ __forceinline__ void rope_chunk_fwd(const T* x, T* o, int half, int k
   store_chunk(o + half + k0, rb);
 }
 
+// The block's RoPE factors for its kRopeRows positions and the Givens factors of every head pair,
+// once per block in LDS (the angles do not depend on the head): rounded to the element type as the
+// reference casts its tables. Returns through `tc` / `ts` ([kRopeRows][half]) and `gc` / `gs`
+// ([H/2]); the exact fp32 Givens sin/cos go to `gce` / `gse` when those are given.
+template <typename T>
+__device__ __forceinline__ void rope_tables_lds(const float* inv_freq, const float* theta, int pos0, int row0, int T_,
+                                                int half, int npair, float* tc, float* ts, float* gc, float* gs,
+                                                float* gce, float* gse) {
+  for (int q = threadIdx.x; q < kRopeRows * half; q += blockDim.x) {
+    const int rl = q / half, k = q % half;
+    float c = 1.f, sn = 0.f;
+    if (inv_freq) {
+      const int t = (row0 + rl) % T_;
+      sincosf((float)(pos0 + t) * inv_freq[k], &sn, &c);
+      c = rnd<T>(c);
+      sn = rnd<T>(sn);
+    }
+    tc[q] = c;
+    ts[q] = sn;
+  }
+  for (int q = threadIdx.x; q < npair; q += blockDim.x) {
+    float c = 1.f, sn = 0.f;
+    if (theta) sincosf(theta[q], &sn, &c);
+    if (gce) {
+      gce[q] = c;
+      gse[q] = sn;
+    }
+    gc[q] = rnd<T>(c);
+    gs[q] = rnd<T>(sn);
+  }
+  __syncthreads();
+}
+
+constexpr int kRopeMaxHalf = 64;   // D <= 128
+constexpr int kRopeMaxPairs = 64;  // H <= 128
+
 template <typename T>
 __global__ void __launch_bounds__(256) rope_givens_fwd_vec_kernel(const RopeParams p) {
   using E = Elem<T>;
   constexpr int EPC = 16 / sizeof(T);
+  __shared__ __align__(16) float tc[kRopeRows * kRopeMaxHalf], ts[kRopeRows * kRopeMaxHalf];
+  __shared__ float gc[kRopeMaxPairs], gs[kRopeMaxPairs];
   const int HD = p.H * p.D, half = p.D / 2;
   const int ur = p.H * (half / EPC);          // RoPE units per row
   const int ug = (p.H / 2) * (p.D / EPC);     // Givens units per row
   const int upr = ur + ug;
   const int rows = p.B * p.T;
   const int row0 = blockIdx.x * kRopeRows;
+  rope_tables_lds<T>(p.inv_freq, p.theta, p.pos0, row0, p.T, half, p.H / 2, tc, ts, gc, gs, nullptr, nullptr);
   for (int u = threadIdx.x; u < kRopeRows * upr; u += blockDim.x) {
-    const int row = row0 + u / upr, k = u % upr;
+    const int rl = u / upr, k = u % upr;
+    const int row = row0 + rl;
     if (row >= rows) break;
     const int b = row / p.T, t = row % p.T;
     const T* x = reinterpret_cast<const T*>(p.qkv) + int64_t(b) * p.qkv_sb + int64_t(t) * p.qkv_sr;
     if (k < ur) {
       const int hd = k / (half / EPC), k0 = (k % (half / EPC)) * EPC;
-      float cs[EPC], sn[EPC];
-      const float pos = (float)(p.pos0 + t);
-#pragma unroll
-      for (int e = 0; e < EPC; ++e) {
-        if (p.inv_freq) {
-          sincosf(pos * p.inv_freq[k0 + e], &sn[e], &cs[e]);
-          cs[e] = rnd<T>(cs[e]);
-          sn[e] = rnd<T>(sn[e]);
-        } else {
-          cs[e] = 1.f;
-          sn[e] = 0.f;
-        }
-      }
+      const float* cs = tc + rl * half + k0;
+      const float* sn = ts + rl * half + k0;
       T* o1 = reinterpret_cast<T*>(p.o1) + int64_t(b) * p.o1_sb + int64_t(hd) * p.o1_sh + int64_t(t) * p.o1_sr;
       T* o2 = reinterpret_cast<T*>(p.o2) + int64_t(b) * p.o2_sb + int64_t(hd) * p.o2_sh + int64_t(t) * p.o2_sr;
       rope_chunk_fwd<T>(x + hd * p.D, o1, half, k0, cs, sn);
@@ -286,10 +312,7 @@ __global__ void __launch_bounds__(256) rope_givens_fwd_vec_kernel(const RopePara
       const Chunk ca = load_chunk(xi + ha * p.D + d0), cb = load_chunk(xi + hb * p.D + d0);
       Chunk ra = ca, rb = cb;
       if (p.theta) {
-        float sn, c;
-        sincosf(p.theta[pr], &sn, &c);
-        c = rnd<T>(c);
-        sn = rnd<T>(sn);
+        const float c = gc[pr], sn = gs[pr];
         const T* ea = reinterpret_cast<const T*>(&ca);
         const T* eb = reinterpret_cast<const T*>(&cb);
         T* oa = reinterpret_cast<T*>(&ra);
@@ -314,6 +337,8 @@ __global__ void __launch_bounds__(256) rope_givens_bwd_vec_kernel(const RopeBwdP
   constexpr int EPC = 16 / sizeof(T);
   constexpr int kMaxPairChunks = 2048;  // LDS slots for d theta partials (kRopeRows * H/2 * D/EPC)
   __shared__ float dth[kMaxPairChunks];
+  __shared__ __align__(16) float tc[kRopeRows * kRopeMaxHalf], ts[kRopeRows * kRopeMaxHalf];
+  __shared__ float gc[kRopeMaxPairs], gs[kRopeMaxPairs], gce[kRopeMaxPairs], gse[kRopeMaxPairs];
   const int HD = p.H * p.D, half = p.D / 2;
   const int npair = p.H / 2, cpg = p.D / EPC;   // chunks per head
   const int ur = p.H * (half / EPC);
@@ -321,6 +346,7 @@ __global__ void __launch_bounds__(256) rope_givens_bwd_vec_kernel(const RopeBwdP
   const int upr = ur + ug;
   const int rows = p.B * p.T;
   const int row0 = blockIdx.x * kRopeRows;
+  rope_tables_lds<T>(p.inv_freq, p.theta, p.pos0, row0, p.T, half, npair, tc, ts, gc, gs, gce, gse);
   for (int u = threadIdx.x; u < kRopeRows * upr; u += blockDim.x) {
     const int rl = u / upr, k = u % upr;
     const int row = row0 + rl;
@@ -329,23 +355,11 @@ __global__ void __launch_bounds__(256) rope_givens_bwd_vec_kernel(const RopeBwdP
     T* dx = reinterpret_cast<T*>(p.dqkv) + int64_t(b) * p.dq_sb + int64_t(t) * p.dq_sr;
     if (k < ur) {
       const int hd = k / (half / EPC), k0 = (k % (half / EPC)) * EPC;
-      float cs[EPC], sn[EPC];
-      const float pos = (float)(p.pos0 + t);
-#pragma unroll
-      for (int e = 0; e < EPC; ++e) {
-        if (p.inv_freq) {
-          sincosf(pos * p.inv_freq[k0 + e], &sn[e], &cs[e]);
-          cs[e] = rnd<T>(cs[e]);
-          sn[e] = rnd<T>(sn[e]);
-        } else {
-          cs[e] = 1.f;
-          sn[e] = 0.f;
-        }
-      }
+      const float* cs = tc + rl * half + k0;
       // transposed rotation: dx_k = d_k c + d_{k+h} s, dx_{k+h} = d_{k+h} c - d_k s
       float msn[EPC];
 #pragma unroll
-      for (int e = 0; e < EPC; ++e) msn[e] = -sn[e];
+      for (int e = 0; e < EPC; ++e) msn[e] = -ts[rl * half + k0 + e];
       const T* g1 = reinterpret_cast<const T*>(p.g1) + int64_t(b) * p.g1_sb + int64_t(hd) * p.g1_sh + int64_t(t) * p.g1_sr;
       const T* g2 = reinterpret_cast<const T*>(p.g2) + int64_t(b) * p.g2_sb + int64_t(hd) * p.g2_sh + int64_t(t) * p.g2_sr;
       rope_chunk_fwd<T>(g1, dx + hd * p.D, half, k0, cs, msn);
@@ -365,9 +379,8 @@ __global__ void __launch_bounds__(256) rope_givens_bwd_vec_kernel(const RopeBwdP
       const Chunk ga = load_chunk(g3 + int64_t(ha) * p.g3_sh + d0), gb = load_chunk(g3 + int64_t(hb) * p.g3_sh + d0);
       Chunk ra = ga, rb = gb;
       if (p.theta) {
-        float sn, c;
-        sincosf(p.theta[pr], &sn, &c);
-        const float cr = rnd<T>(c), sr = rnd<T>(sn);
+        const float c = gce[pr], sn = gse[pr];      // exact: the derivative of the unrounded function
+        const float cr = gc[pr], sr = gs[pr];       // rounded: the rotation that was applied
         const T* xi = reinterpret_cast<const T*>(p.qkv) + int64_t(b) * p.qkv_sb + int64_t(t) * p.qkv_sr + 2 * HD;
         const Chunk xa = load_chunk(xi + ha * p.D + d0), xb = load_chunk(xi + hb * p.D + d0);
         const T* ega = reinterpret_cast<const T*>(&ga);
@@ -393,14 +406,14 @@ __global__ void __launch_bounds__(256) rope_givens_bwd_vec_kernel(const RopeBwdP
   }
   if (!p.theta) return;
   __syncthreads();
-  // per (row, pair): fixed-order sum over the head's chunks
-  for (int q = threadIdx.x; q < kRopeRows * npair; q += blockDim.x) {
-    const int rl = q / npair, pr = q % npair;
-    const int row = row0 + rl;
-    if (row >= rows) continue;
+  // per pair: fixed-order sum over the block's rows and the head's chunks (one partial per block)
+  for (int pr = threadIdx.x; pr < npair; pr += blockDim.x) {
     float acc = 0.f;
-    for (int c = 0; c < cpg; ++c) acc += dth[(rl * npair + pr) * cpg + c];
-    p.partial[int64_t(row) * npair + pr] = acc;
+    for (int rl = 0; rl < kRopeRows; ++rl) {
+      if (row0 + rl >= rows) break;
+      for (int c = 0; c < cpg; ++c) acc += dth[(rl * npair + pr) * cpg + c];
+    }
+    p.partial[int64_t(blockIdx.x) * npair + pr] = acc;
   }
 }
 
@@ -446,7 +459,7 @@ int launch_rope_givens_fwd(const mote_rope_givens_args* a, hipStream_t stream) {
   p.B = a->B; p.T = a->T; p.H = a->H; p.D = a->D; p.pos0 = a->pos0; p.parity = a->layer_parity & 1;
   const int rows = a->B * a->T;
   const int epc = a->dtype == MOTE_BF16 ? 8 : 4;
-  const bool vec = (a->D / 2) % epc == 0 && aligned16(a);
+  const bool vec = (a->D / 2) % epc == 0 && a->D / 2 <= kRopeMaxHalf && a->H / 2 <= kRopeMaxPairs && aligned16(a);
   const int vblocks = (rows + kRopeRows - 1) / kRopeRows;
   if (a->dtype == MOTE_BF16) {
     if (vec) hipLaunchKernelGGL(rope_givens_fwd_vec_kernel<bf16_t>, dim3(vblocks), dim3(256), 0, stream, p);
@@ -482,7 +495,8 @@ int launch_rope_givens_bwd(const mote_rope_givens_bwd_args* a, hipStream_t strea
   p.B = a->B; p.T = a->T; p.H = a->H; p.D = a->D; p.pos0 = a->pos0; p.parity = a->layer_parity & 1;
   const int rows = a->B * a->T;
   const int epc = a->dtype == MOTE_BF16 ? 8 : 4;
-  const bool vec = (a->D / 2) % epc == 0 && aligned16_bwd(a) && kRopeRows * (a->H / 2) * (a->D / epc) <= 2048;
+  const bool vec = (a->D / 2) % epc == 0 && a->D / 2 <= kRopeMaxHalf && a->H / 2 <= kRopeMaxPairs &&
+                   aligned16_bwd(a) && kRopeRows * (a->H / 2) * (a->D / epc) <= 2048;
   const int vblocks = (rows + kRopeRows - 1) / kRopeRows;
   if (a->dtype == MOTE_BF16) {
     if (vec) hipLaunchKernelGGL(rope_givens_bwd_vec_kernel<bf16_t>, dim3(vblocks), dim3(256), 0, stream, p);
@@ -493,7 +507,9 @@ int launch_rope_givens_bwd(const mote_rope_givens_bwd_args* a, hipStream_t strea
   }
   rc = check_launch("rope_givens_bwd");
   if (rc || !a->theta) return rc;
-  hipLaunchKernelGGL(sum_partials_kernel, dim3(a->H / 2), dim3(256), 0, stream, p.partial, rows, a->H / 2, a->dtheta);
+  const int nparts = vec ? vblocks : rows;  // the vectorised kernel leaves one partial per block
+  hipLaunchKernelGGL(sum_partials_kernel, dim3((a->H / 2 + 3) / 4), dim3(256), 0, stream, p.partial, nparts, a->H / 2,
+                     a->dtheta);
   return check_launch("rope_givens_bwd/sum");
 }
 
