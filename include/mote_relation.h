@@ -186,9 +186,10 @@ int mote_rope_givens_bwd(const mote_rope_givens_bwd_args* args, void* stream);
  * never read. S[b] >= capacity writes NaN into y[b] and skips the append.
  * flags bit 0 (MOTE_DECODE_ADVANCE): add 1 to every S[b] once the step has read it (graph.py's
  * S += 1, :189-190), so a captured step needs no separate kernel for it.
- * Two launches on `stream` (a split-S sweep, then a per-sequence merge). The workspace
- * (mote_relation_decode_workspace() bytes) holds the per-split partials; its contents on entry do
- * not matter. Calls that share a workspace must not overlap.
+ * One launch on `stream`: a split-S sweep whose last workgroup per (sequence, head) merges the
+ * partials. The workspace (mote_relation_decode_workspace() bytes) holds the per-split partials and
+ * completion counters: zero-fill it once before its first call (every call leaves the counters at
+ * zero again). Calls that share a workspace must not overlap.
  * ------------------------------------------------------------------------------------------------ */
 #define MOTE_DECODE_ADVANCE 1
 

@@ -1,21 +1,22 @@
-// One decode step of one Relation layer (mote/infer/graph.py:151-187): two launches.
+// One decode step of one Relation layer (mote/infer/graph.py:151-187), one launch.
 //
-// Split kernel. Grid: nsplit x (B*H) workgroups, block id = split * (B*H) + head index. Split s owns
-// the past rows [s*R, (s+1)*R) of its head, R = 64 * rows_mult (a host choice that keeps ~2k
-// workgroups in flight); splits that start at or past S leave at once, so the launch shape only
-// depends on the cache capacity and can be captured in a HIP graph. Each workgroup (4 waves; a wave
-// reads 16 rows per step, 4 lanes per row, 16-byte loads of P2 and I~ issued together with a one-step
-// register prefetch) computes U_j = <q, P2_j> / sqrt(D), e_j = SiLU(U_j) in log2 units and an online
-// softmax per row group (running max raised lazily, by more than 2^8 only), merges its row groups and
-// waves, and writes (max, l, z[D]) to the workspace.
+// Grid: nsplit x (B*H) workgroups, block id = split * (B*H) + head index. Split s owns the past rows
+// [s*R, (s+1)*R) of its head, R = 64 * rows_mult (a host choice that keeps a few hundred workgroups
+// in flight); the launch shape depends only on the cache capacity, so it can be captured in a HIP
+// graph. Each workgroup (4 waves; a wave reads 16 rows per step, 4 lanes per row, 16-byte loads of
+// P2 and I~ issued together with a one-step register prefetch) computes U_j = <q, P2_j> / sqrt(D),
+// e_j = SiLU(U_j) in log2 units and an online softmax per row group (running max raised lazily, by
+// more than 2^8 only), merges its row groups and waves, and publishes (max, l, z[D]).
 //
-// Merge kernel. One workgroup per (sequence, head): it loads the head's partials into LDS (parallel,
-// coalesced), merges them in a fixed order, computes the Self score from the new row,
-// g = sigmoid(LSE - lam ln(S+1) - S_self) and Y = (1-g) I~_S + g z/l, and appends the new P2 / I~ row
-// at S. The split kernel copies S[b] to S_used[b] and the merge reads only that copy, so with
-// MOTE_DECODE_ADVANCE the head-0 workgroup can add 1 to S[b] without racing the other heads.
-// The kernel boundary orders the partials; there is no in-kernel device-scope handshake (on gfx950
-// a device-scope release writes back the XCD's whole L2, which costs ~0.1 us per workgroup).
+// Publication without a device-scope fence (which on gfx950 writes back the XCD's whole L2): the
+// partial goes out with agent-coherent stores, the wave waits for their completion, and one atomic
+// add per workgroup counts the head's splits. Every split counts, rows or not, so the count never
+// depends on S. The workgroup that brings the count to nsplit reads all partials back with
+// agent-coherent loads and finishes the head: merge in a fixed order, the Self score from the new
+// row, g = sigmoid(LSE - lam ln(S+1) - S_self), Y = (1-g) I~_S + g z/l, the append of the new P2 / I~
+// row at S, and the reset of the counter. A second counter per sequence picks the last head to
+// finish; with MOTE_DECODE_ADVANCE it adds 1 to S[b]: by then every workgroup of the sequence has
+// read S[b]. Counters start at zero (the workspace is zeroed once) and every call leaves them zero.
 //
 // The query is RoPE'd at S and rounded to the cache dtype (graph.py:158-172) by every workgroup; the
 // new P2 row gets the same rotation and I~ the Givens rotation with its partner head's raw row.
@@ -40,16 +41,154 @@ struct DecParams {
   int64_t y_sb;
   float* g;
   float* part;        // [BH][nsplit][D + 2]  (max, l, z)
-  int64_t* S_used;    // [B] the positions the split kernel read (the merge reads these)
+  int* cnt;           // [BH] splits published in this call (zero between calls)
+  int* cnt_seq;       // [B] heads finished in this call (zero between calls)
   int B, H, D, cap, parity, flags, nsplit, rps;  // rps: rows per split
   float scale, tau_inv;
 };
 
 constexpr int kDecMaxSplits = 120;  // partials one merge holds in LDS (D <= 128: at most 62 KB)
 
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <typename T>
 __device__ __forceinline__ float round_to(float x) {
   return Elem<T>::to_f(Elem<T>::from_f(x));
+}
+
+// ------------------------------------------------------------------------------------------------
+// finish of a head by the last of its workgroups: merge, epilogue, append
+// ------------------------------------------------------------------------------------------------
+template <typename T, int DP>
+__device__ __forceinline__ void decode_finish(const DecParams& p, int bh, int64_t S64) {
+  using E = Elem<T>;
+  __shared__ float sq[DP];
+  __shared__ float knew[DP];
+  __shared__ float inew[DP];
+  __shared__ float sred[4];
+  __shared__ float sML[2];
+  extern __shared__ float spart[];  // [nsplit][D + 2], then the split weights [nsplit]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int b = bh / p.H, h = bh % p.H;
+  const int D = p.D, half = D / 2;
+  const int stride = D + 2;
+  const bool bad = S64 < 0 || S64 >= p.cap;
+  const int S = bad ? 0 : int(S64);
+  const int nact = p.nsplit;
+  float* wsp = spart + nact * stride;
+  const float* pb = p.part + int64_t(bh) * p.nsplit * stride;
+  for (int i = tid; i < nact * stride; i += 256) spart[i] = load_coherent(pb + i);
+  // new rows: query and P2 RoPE'd at S, I~ Givens'd with its partner head's raw row
+  const T* q_raw = reinterpret_cast<const T*>(p.p1) + b * p.in_sb + h * D;
+  const T* k_raw = reinterpret_cast<const T*>(p.p2) + b * p.in_sb + h * D;
+  const T* i_raw = reinterpret_cast<const T*>(p.info) + b * p.in_sb + h * D;
+  if (tid < half) {
+    float cs = 1.f, sn = 0.f;
+    if (p.inv_freq) {
+      sincosf((float)S * p.inv_freq[tid], &sn, &cs);
+      cs = round_to<T>(cs);
+      sn = round_to<T>(sn);
+    }
+    const float q0 = E::to_f(q_raw[tid]), q1 = E::to_f(q_raw[tid + half]);
+    const float k0 = E::to_f(k_raw[tid]), k1 = E::to_f(k_raw[tid + half]);
+    sq[tid] = round_to<T>(q0 * cs - q1 * sn);
+    sq[tid + half] = round_to<T>(q1 * cs + q0 * sn);
+    knew[tid] = round_to<T>(k0 * cs - k1 * sn);
+    knew[tid + half] = round_to<T>(k1 * cs + k0 * sn);
+  }
+  if (tid < D) {
+    const float self = E::to_f(i_raw[tid]);
+    float out = self;
+    if (p.theta) {
+      int pair, other;
+      bool first;
+      if (p.parity == 0) {
+        pair = h >> 1;
+        first = (h & 1) == 0;
+        other = first ? h + 1 : h - 1;
+      } else if (h & 1) {
+        first = true;
+        pair = h >> 1;
+        other = (h + 1) % p.H;
+      } else {
+        first = false;
+        other = (h + p.H - 1) % p.H;
+        pair = other >> 1;
+      }
+      float sn, cs;
+      sincosf(p.theta[pair], &sn, &cs);
+      cs = round_to<T>(cs);
+      sn = round_to<T>(sn);
+      const float oth = E::to_f(reinterpret_cast<const T*>(p.info)[b * p.in_sb + other * D + tid]);
+      out = first ? (cs * self - sn * oth) : (sn * oth + cs * self);
+    }
+    inew[tid] = round_to<T>(out);
+  }
+  __syncthreads();
+  // split weights 2^(m_s - M) and L = sum_s l_s 2^(m_s - M): wave 0, lanes over splits (fixed order)
+  if (wave == 0) {
+    float mx = kNegInf;
+    for (int s = lane; s < nact; s += 64) mx = fmaxf(mx, spart[s * stride]);
+#pragma unroll
+    for (int msk = 32; msk >= 1; msk >>= 1) mx = fmaxf(mx, __shfl_xor(mx, msk, 64));
+    const float Ms = mx == kNegInf ? 0.f : mx;
+    float ls = 0.f;
+    for (int s = lane; s < nact; s += 64) {
+      const float w = fexp2(spart[s * stride] - Ms);
+      wsp[s] = w;
+      ls += spart[s * stride + 1] * w;
+    }
+#pragma unroll
+    for (int msk = 32; msk >= 1; msk >>= 1) ls += __shfl_xor(ls, msk, 64);
+    if (lane == 0) {
+      sML[0] = Ms;
+      sML[1] = ls;
+    }
+  } else if (wave == 1) {
+    // Self score U_SS = <q, P2_S> / sqrt(D)
+    float u = 0.f;
+    for (int d = lane; d < D; d += 64) u = fmaf(sq[d], knew[d], u);
+#pragma unroll
+    for (int msk = 32; msk >= 1; msk >>= 1) u += __shfl_xor(u, msk, 64);
+    if (lane == 0) sred[0] = u;
+  }
+  __syncthreads();
+  const float Ms = sML[0], L = sML[1];
+  const float sself = sigmoid_acc(sred[0] * p.scale * p.tau_inv);
+  const bool has = L > 0.f;
+  const float lse = has ? (Ms + __log2f(L)) * kLn2 : kNegInf;
+  const float gate = has ? sigmoid_acc(lse - (*p.lam) * logf((float)S + 1.0f) - sself) : 0.f;
+  const float invL = has ? 1.0f / L : 0.f;
+  T* y = reinterpret_cast<T*>(p.y) + b * p.y_sb + h * D;
+  T* kw = reinterpret_cast<T*>(p.kc) + b * p.kc_sb + h * p.kc_sh + int64_t(S) * p.kc_sr;
+  T* vw = reinterpret_cast<T*>(p.vc) + b * p.vc_sb + h * p.vc_sh + int64_t(S) * p.vc_sr;
+  for (int d = tid; d < D; d += 256) {
+    float zsum = 0.f;
+#pragma unroll 8
+    for (int s = 0; s < nact; ++s) zsum = fmaf(spart[s * stride + 2 + d], wsp[s], zsum);
+    const float yv = (1.0f - gate) * inew[d] + gate * zsum * invL;
+    y[d] = E::from_f(bad ? __builtin_nanf("") : yv);
+    if (!bad) {
+      kw[d] = E::from_f(knew[d]);
+      vw[d] = E::from_f(inew[d]);
+    }
+  }
+  if (tid == 0) {
+    p.g[bh] = bad ? __builtin_nanf("") : gate;
+    __hip_atomic_store(p.cnt + bh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the last head of the sequence: every workgroup of the sequence has read S[b] by now
+    const int before = __hip_atomic_fetch_add(p.cnt_seq + b, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (before == p.H - 1) {
+      __hip_atomic_store(p.cnt_seq + b, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (p.flags & MOTE_DECODE_ADVANCE) p.S[b] = S64 + 1;
+    }
+  }
 }
 
 template <typename T, int DP>
@@ -69,9 +208,8 @@ __global__ void __launch_bounds__(256) relation_decode_kernel(const DecParams p)
   const int64_t S64 = p.S[b];
   const bool bad = S64 < 0 || S64 >= p.cap;
   const int S = bad ? 0 : int(S64);
-  const int nact = S > 0 ? (S + p.rps - 1) / p.rps : 1;  // splits with rows (split 0 always takes part)
-  if (split >= nact) return;
-  if (split == 0 && h == 0 && tid == 0) p.S_used[b] = S64;
+  // every split takes part (those at or past S publish an empty partial), so the count of published
+  // splits never depends on S
 
   // query: RoPE at S, rounded to the cache dtype
   const T* q_raw = reinterpret_cast<const T*>(p.p1) + b * p.in_sb + h * D;
@@ -213,151 +351,33 @@ __global__ void __launch_bounds__(256) relation_decode_kernel(const DecParams p)
       float zs = 0.f;
 #pragma unroll
       for (int w = 0; w < 4; ++w) zs += red[w * (DP + 2) + 2 + d] * fexp2(mw[w] - Ms);
-      part[2 + d] = zs;
+      store_coherent(part + 2 + d, zs);
     }
     if (tid == 0) {
       float L = 0.f;
 #pragma unroll
       for (int w = 0; w < 4; ++w) L += red[w * (DP + 2) + 1] * fexp2(mw[w] - Ms);
-      part[0] = M;
-      part[1] = L;
+      store_coherent(part, M);
+      store_coherent(part + 1, L);
     }
   }
-
-}
-
-// ------------------------------------------------------------------------------------------------
-// merge: one workgroup per (sequence, head)
-// ------------------------------------------------------------------------------------------------
-template <typename T, int DP>
-__global__ void __launch_bounds__(256) relation_decode_merge_kernel(const DecParams p) {
-  using E = Elem<T>;
-  __shared__ float sq[DP];
-  __shared__ float knew[DP];
-  __shared__ float inew[DP];
-  __shared__ float sred[4];
-  __shared__ float sML[2];
-  extern __shared__ float spart[];  // [nact][D + 2], then the split weights [nact]
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int bh = blockIdx.x;
-  const int b = bh / p.H, h = bh % p.H;
-  const int D = p.D, half = D / 2;
-  const int stride = D + 2;
-  const int64_t S64 = p.S_used[b];
-  const bool bad = S64 < 0 || S64 >= p.cap;
-  const int S = bad ? 0 : int(S64);
-  const int nact = S > 0 ? (S + p.rps - 1) / p.rps : 1;
-  float* wsp = spart + nact * stride;
-  const float* pb = p.part + int64_t(bh) * p.nsplit * stride;
-  for (int i = tid; i < nact * stride; i += 256) spart[i] = pb[i];
-  // new rows: query and P2 RoPE'd at S, I~ Givens'd with its partner head's raw row
-  const T* q_raw = reinterpret_cast<const T*>(p.p1) + b * p.in_sb + h * D;
-  const T* k_raw = reinterpret_cast<const T*>(p.p2) + b * p.in_sb + h * D;
-  const T* i_raw = reinterpret_cast<const T*>(p.info) + b * p.in_sb + h * D;
-  if (tid < half) {
-    float cs = 1.f, sn = 0.f;
-    if (p.inv_freq) {
-      sincosf((float)S * p.inv_freq[tid], &sn, &cs);
-      cs = round_to<T>(cs);
-      sn = round_to<T>(sn);
-    }
-    const float q0 = E::to_f(q_raw[tid]), q1 = E::to_f(q_raw[tid + half]);
-    const float k0 = E::to_f(k_raw[tid]), k1 = E::to_f(k_raw[tid + half]);
-    sq[tid] = round_to<T>(q0 * cs - q1 * sn);
-    sq[tid + half] = round_to<T>(q1 * cs + q0 * sn);
-    knew[tid] = round_to<T>(k0 * cs - k1 * sn);
-    knew[tid + half] = round_to<T>(k1 * cs + k0 * sn);
-  }
-  if (tid < D) {
-    const float self = E::to_f(i_raw[tid]);
-    float out = self;
-    if (p.theta) {
-      int pair, other;
-      bool first;
-      if (p.parity == 0) {
-        pair = h >> 1;
-        first = (h & 1) == 0;
-        other = first ? h + 1 : h - 1;
-      } else if (h & 1) {
-        first = true;
-        pair = h >> 1;
-        other = (h + 1) % p.H;
-      } else {
-        first = false;
-        other = (h + p.H - 1) % p.H;
-        pair = other >> 1;
-      }
-      float sn, cs;
-      sincosf(p.theta[pair], &sn, &cs);
-      cs = round_to<T>(cs);
-      sn = round_to<T>(sn);
-      const float oth = E::to_f(reinterpret_cast<const T*>(p.info)[b * p.in_sb + other * D + tid]);
-      out = first ? (cs * self - sn * oth) : (sn * oth + cs * self);
-    }
-    inew[tid] = round_to<T>(out);
-  }
+  // publish: every wave's coherent stores complete, then one count per workgroup
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  // split weights 2^(m_s - M) and L = sum_s l_s 2^(m_s - M): wave 0, lanes over splits (fixed order)
-  if (wave == 0) {
-    float mx = kNegInf;
-    for (int s = lane; s < nact; s += 64) mx = fmaxf(mx, spart[s * stride]);
-#pragma unroll
-    for (int msk = 32; msk >= 1; msk >>= 1) mx = fmaxf(mx, __shfl_xor(mx, msk, 64));
-    const float Ms = mx == kNegInf ? 0.f : mx;
-    float ls = 0.f;
-    for (int s = lane; s < nact; s += 64) {
-      const float w = fexp2(spart[s * stride] - Ms);
-      wsp[s] = w;
-      ls += spart[s * stride + 1] * w;
-    }
-#pragma unroll
-    for (int msk = 32; msk >= 1; msk >>= 1) ls += __shfl_xor(ls, msk, 64);
-    if (lane == 0) {
-      sML[0] = Ms;
-      sML[1] = ls;
-    }
-  } else if (wave == 1) {
-    // Self score U_SS = <q, P2_S> / sqrt(D)
-    float u = 0.f;
-    for (int d = lane; d < D; d += 64) u = fmaf(sq[d], knew[d], u);
-#pragma unroll
-    for (int msk = 32; msk >= 1; msk >>= 1) u += __shfl_xor(u, msk, 64);
-    if (lane == 0) sred[0] = u;
-  }
-  __syncthreads();
-  const float Ms = sML[0], L = sML[1];
-  const float sself = sigmoid_acc(sred[0] * p.scale * p.tau_inv);
-  const bool has = L > 0.f;
-  const float lse = has ? (Ms + __log2f(L)) * kLn2 : kNegInf;
-  const float gate = has ? sigmoid_acc(lse - (*p.lam) * logf((float)S + 1.0f) - sself) : 0.f;
-  const float invL = has ? 1.0f / L : 0.f;
-  T* y = reinterpret_cast<T*>(p.y) + b * p.y_sb + h * D;
-  T* kw = reinterpret_cast<T*>(p.kc) + b * p.kc_sb + h * p.kc_sh + int64_t(S) * p.kc_sr;
-  T* vw = reinterpret_cast<T*>(p.vc) + b * p.vc_sb + h * p.vc_sh + int64_t(S) * p.vc_sr;
-  for (int d = tid; d < D; d += 256) {
-    float zsum = 0.f;
-#pragma unroll 8
-    for (int s = 0; s < nact; ++s) zsum = fmaf(spart[s * stride + 2 + d], wsp[s], zsum);
-    const float yv = (1.0f - gate) * inew[d] + gate * zsum * invL;
-    y[d] = E::from_f(bad ? __builtin_nanf("") : yv);
-    if (!bad) {
-      kw[d] = E::from_f(knew[d]);
-      vw[d] = E::from_f(inew[d]);
-    }
-  }
+  __shared__ int s_last;
   if (tid == 0) {
-    p.g[bh] = bad ? __builtin_nanf("") : gate;
-    // every reader of S[b] in this step is done: the split kernel ran before this one, and the
-    // merge workgroups read the copy in S_used
-    if (h == 0 && (p.flags & MOTE_DECODE_ADVANCE)) p.S[b] = S64 + 1;
+    const int before = __hip_atomic_fetch_add(p.cnt + bh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = before == p.nsplit - 1;
   }
+  __syncthreads();
+  if (!s_last) return;
+  decode_finish<T, DP>(p, bh, S64);
 }
 
-// rows per split: a multiple of 64 chosen so that about 2048 workgroups cover a full cache
+// rows per split: a multiple of 64 chosen so that about 320 workgroups cover a full cache
 static void decode_shape(const mote_relation_decode_args* a, int& rps, int& nsplit) {
   const int64_t BH = int64_t(a->B) * a->H;
-  int64_t mult = (BH * ((a->capacity + 63) / 64) + 2047) / 2048;
+  int64_t mult = (BH * ((a->capacity + 63) / 64) + 319) / 320;
   if (mult < 1) mult = 1;
   rps = int(64 * mult);
   nsplit = (a->capacity + rps - 1) / rps;
@@ -367,13 +387,22 @@ static void decode_shape(const mote_relation_decode_args* a, int& rps, int& nspl
   }
 }
 
-size_t decode_workspace_bytes(const mote_relation_decode_args* a) {
+struct DecWs {
+  size_t part, cnt, cnt_seq, total;
+};
+static DecWs decode_ws(const mote_relation_decode_args* a) {
   int rps, nsplit;
   decode_shape(a, rps, nsplit);
   const size_t BH = size_t(a->B) * a->H;
-  const size_t parts = (BH * size_t(nsplit) * size_t(a->D + 2) * sizeof(float) + 255) & ~size_t(255);
-  return parts + size_t(a->B) * sizeof(int64_t);
+  DecWs w;
+  w.part = 0;
+  w.cnt = (BH * size_t(nsplit) * size_t(a->D + 2) * sizeof(float) + 255) & ~size_t(255);
+  w.cnt_seq = w.cnt + ((BH * sizeof(int) + 255) & ~size_t(255));
+  w.total = w.cnt_seq + ((size_t(a->B) * sizeof(int) + 255) & ~size_t(255));
+  return w;
 }
+
+size_t decode_workspace_bytes(const mote_relation_decode_args* a) { return decode_ws(a).total; }
 
 int launch_decode(const mote_relation_decode_args* a, hipStream_t stream) {
   if (!a) return set_error(MOTE_ERR_ARGUMENT, "relation_decode: null args");
@@ -394,9 +423,11 @@ int launch_decode(const mote_relation_decode_args* a, hipStream_t stream) {
   p.y = a->y; p.y_sb = a->y_sb; p.g = a->g;
   const size_t BH = size_t(a->B) * a->H;
   decode_shape(a, p.rps, p.nsplit);
-  p.part = reinterpret_cast<float*>(a->workspace);
-  const size_t parts = (BH * size_t(p.nsplit) * size_t(a->D + 2) * sizeof(float) + 255) & ~size_t(255);
-  p.S_used = reinterpret_cast<int64_t*>(reinterpret_cast<char*>(a->workspace) + parts);
+  const DecWs w = decode_ws(a);
+  char* ws = reinterpret_cast<char*>(a->workspace);
+  p.part = reinterpret_cast<float*>(ws + w.part);
+  p.cnt = reinterpret_cast<int*>(ws + w.cnt);
+  p.cnt_seq = reinterpret_cast<int*>(ws + w.cnt_seq);
   p.B = a->B; p.H = a->H; p.D = a->D; p.cap = a->capacity; p.parity = a->layer_parity & 1; p.flags = a->flags;
   p.scale = 1.0f / sqrtf((float)a->D);
   p.tau_inv = 1.0f / a->tau_s;
@@ -405,8 +436,7 @@ int launch_decode(const mote_relation_decode_args* a, hipStream_t stream) {
   const int DP = padded_dim(a->D);
 #define MOTE_DEC_LAUNCH(T_, DP_)                                                                               \
   do {                                                                                                       \
-    hipLaunchKernelGGL((relation_decode_kernel<T_, DP_>), dim3(grid), dim3(256), 0, stream, p);              \
-    hipLaunchKernelGGL((relation_decode_merge_kernel<T_, DP_>), dim3(BH), dim3(256), shmem, stream, p);      \
+    hipLaunchKernelGGL((relation_decode_kernel<T_, DP_>), dim3(grid), dim3(256), shmem, stream, p);          \
   } while (0)
   if (a->dtype == MOTE_BF16) {
     switch (DP) {

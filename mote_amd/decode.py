@@ -22,12 +22,12 @@ from .arena import RelationArena
 
 
 def decode_workspace(B: int, H: int, D: int, capacity: int, device, dtype=torch.bfloat16) -> torch.Tensor:
-    """A workspace for `relation_decode` (per-split partials; contents on entry do not matter).
-    Calls that share one must not overlap."""
+    """A workspace for `relation_decode`: per-split partials and the completion counters, zeroed
+    here once; every call leaves the counters at zero again. Calls that share one must not overlap."""
     a = L.DecodeArgs()
     a.dtype, a.B, a.H, a.D, a.capacity = L.dtype_code(torch.empty(0, dtype=dtype)), B, H, D, capacity
     n = int(L.lib().mote_relation_decode_workspace(a))
-    return torch.empty(max(n, 16), device=device, dtype=torch.uint8)
+    return torch.zeros(max(n, 16), device=device, dtype=torch.uint8)
 
 
 def relation_decode(p1: torch.Tensor, p2: torch.Tensor, info: torch.Tensor, S: torch.Tensor, cache_p2: torch.Tensor,
