@@ -155,17 +155,36 @@ def bench_stack(steps: int, warmup: int, dev):
     torch.cuda.synchronize()
     avg = {k: sum(a.elapsed_time(b) for a, b in zip(*v)) / len(v[0]) for k, v in timers.items()}
     # per-kernel work (units of H*dh*T^2, one per causal product): forward U and P I~ (2); key kernel
-    # U, dW, dV, dK (4); query kernel dQ plus the recomputed U and dW (3, of which 1 is not done elsewhere)
+    # U, dW, dV, dK (4); query kernel dQ (1), which reads the key kernel's dU^T tiles and is HBM-bound
     unit = N_HEADS * D_HEAD * T * T
+    dq_bytes = dq_kernel_bytes(T)
     res = dict(T=T, ms_per_step=ms, wall_s=wall, tflops=flops / (ms * 1e-3) / 1e12, flops_per_step=flops,
                keys_ms=avg["bwd_keys"], queries_ms=avg["bwd_queries"], fwd_ms=avg["fwd"],
                keys_tflops=4.0 * unit / (avg["bwd_keys"] * 1e-3) / 1e12,
-               queries_tflops=3.0 * unit / (avg["bwd_queries"] * 1e-3) / 1e12,
+               queries_tflops=1.0 * unit / (avg["bwd_queries"] * 1e-3) / 1e12,
+               queries_bytes=dq_bytes, queries_gbs=dq_bytes / (avg["bwd_queries"] * 1e-3) / 1e9,
                fwd_tflops=2.0 * unit / (avg["fwd"] * 1e-3) / 1e12)
     log(f"[bench] stack: {ms:.3f} ms/step = {res['tflops']:.1f} TFLOP/s; fwd kernel {avg['fwd']*1e3:.1f} us "
         f"({res['fwd_tflops']:.1f} TF/s), bwd key kernel {avg['bwd_keys']*1e3:.1f} us ({res['keys_tflops']:.1f} TF/s), "
-        f"bwd query kernel {avg['bwd_queries']*1e3:.1f} us ({res['queries_tflops']:.1f} TF/s executed)")
+        f"bwd dQ kernel {avg['bwd_queries']*1e3:.1f} us ({res['queries_gbs']:.0f} GB/s of dU^T tiles + P2 + dP1)")
     return res
+
+
+def pair_total(TQ: int, q_start: int = 0) -> int:
+    """Visible (query block, key block) pairs of 64 x 64 per head (the backward's dU^T tile count)."""
+    if TQ <= 0:
+        return 0
+    nqb = (TQ + 63) // 64
+    A = (q_start + 126) // 64
+    last = nqb - 1
+    qlast = min(TQ, 64 * last + 64) - 1
+    return last * (last - 1) // 2 + A * last + (q_start + qlast + 63) // 64
+
+
+def dq_kernel_bytes(T: int) -> float:
+    """Algorithmic HBM bytes of one dQ-kernel launch at the stack shape: the dU^T tiles (8 KB per
+    visible 64 x 64 pair and head, written by the key kernel), P2 read once and dP1 written once."""
+    return N_HEADS * (pair_total(T) * 8192 + 2 * T * D_HEAD * 2)
 
 
 def copy_calibration(dev, mib: int = 1024):
@@ -371,12 +390,11 @@ def main():
                      "achieved": round(st["keys_tflops"], 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(st["keys_tflops"] / PEAK_BF16_TFLOPS, 4), "traffic": measured_traffic("bwd_kv_kernel"),
                      "flop_per_launch": 4.0 * N_HEADS * D_HEAD * st["T"] ** 2, "avg_launch_ms": round(st["keys_ms"], 4)},
-        "roofline_bwd_q": {"kernel": "bwd_q_kernel (query-stationary dQ; recomputes U and dW)", "bound": "mfma",
-                           "achieved": round(st["queries_tflops"], 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                           "frac": round(st["queries_tflops"] / PEAK_BF16_TFLOPS, 4),
-                           "traffic": measured_traffic("bwd_q_kernel"),
-                           "flop_per_launch": 3.0 * N_HEADS * D_HEAD * st["T"] ** 2,
-                           "avg_launch_ms": round(st["queries_ms"], 4)},
+        "roofline_bwd_dq": {"kernel": "bwd_dq_kernel (query-stationary dQ from the stored dU^T tiles)", "bound": "hbm",
+                            "achieved": round(st["queries_gbs"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                            "frac": round(st["queries_gbs"] / PEAK_HBM_GBS, 4),
+                            "traffic": measured_traffic("bwd_dq_kernel"),
+                            "bytes_per_launch": st["queries_bytes"], "avg_launch_ms": round(st["queries_ms"], 4)},
         "roofline_fwd": {"kernel": "relation_fwd_tile_kernel", "bound": "mfma", "achieved": round(st["fwd_tflops"], 2),
                          "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(st["fwd_tflops"] / PEAK_BF16_TFLOPS, 4),

@@ -28,11 +28,33 @@ struct BwdParams {
   float* duii;   // [BH][TQp]
   float* dp1acc; // [BH][TQ][D]                                 (register-staged kernels)
   float* dlam_part;  // [BH][TQp / 64]
+  void* dut;     // [BH][npairs][8][64 lanes][8] bf16: dU^T as dQ-product B fragments (tile kernels)
+  int64_t npairs;    // (query block, key block) pairs per (batch, head), PairTable::total
   int B, H, TQ, TK, D, q_start, TQp;
   float scale, tau_inv;
 };
 
 constexpr int kRowBlock = 64;  // rows per workgroup in the rows stage; also TQp's granularity
+
+// The (query block, key block) pairs of 64 x 64 that hold a visible element (key position below the
+// query position): query block qb sees key blocks [0, nkb(qb)). Every block but the last holds 64
+// queries, so nkb(qb) = qb + A with A = (q_start + 126) / 64 there and the pairs of query block qb
+// start at qb (qb - 1) / 2 + A qb.
+struct PairTable {
+  __host__ __device__ static int nkb(int qb, int TQ, int q_start) {
+    const int qlast = (TQ < 64 * qb + 64 ? TQ : 64 * qb + 64) - 1;
+    return (q_start + qlast + 63) / 64;  // keys j < q_start + qlast
+  }
+  __host__ __device__ static int64_t offset(int qb, int q_start) {
+    const int64_t A = (q_start + 126) / 64;
+    return int64_t(qb) * (qb - 1) / 2 + A * qb;
+  }
+  __host__ __device__ static int64_t total(int TQ, int q_start) {
+    if (TQ <= 0) return 0;
+    const int nqb = (TQ + 63) / 64;
+    return offset(nqb - 1, q_start) + nkb(nqb - 1, TQ, q_start);
+  }
+};
 
 // bf16 with D in {32, 64, 96, 128}: the atomic-free tile kernels (dP2 / dI~ key-stationary, then dP1
 // query-stationary), for the stages selected in `stages` (MOTE_BWD_KEYS, MOTE_BWD_QUERIES).

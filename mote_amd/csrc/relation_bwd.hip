@@ -722,7 +722,7 @@ __global__ void __launch_bounds__(256) bwd_dlam_kernel(const float* part, int n,
 // host side
 // ------------------------------------------------------------------------------------------------
 struct WsLayout {
-  size_t wq, wdib, wqT, wdibT, lse2, cvec, stat, duii, dp1acc, dlam_part, total;
+  size_t wq, wdib, wqT, wdibT, lse2, cvec, stat, dut, duii, dp1acc, dlam_part, total;
 };
 
 static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -743,6 +743,8 @@ static WsLayout ws_layout(const mote_relation_bwd_args* a) {
   w.wdib = o; o = align256(o + BH * TQp * DP * es);
   if (tiles) {
     w.stat = o; o = align256(o + BH * (TQp / kRowBlock) * 128 * 4);
+    // dU^T fragments: 8 KB per visible (query block, key block) pair
+    w.dut = o; o = align256(o + BH * size_t(PairTable::total(a->TQ, a->q_start)) * 8192);
   } else {
     w.wq = o; o = align256(o + BH * TQp * DP * es);
     w.wqT = o; o = align256(o + BH * TQp * DP * es);
@@ -840,6 +842,8 @@ int launch_bwd(const mote_relation_bwd_args* a, hipStream_t stream) {
   p.dlam_part = reinterpret_cast<float*>(ws + w.dlam_part);
   if (tiles) {
     p.stat = reinterpret_cast<float*>(ws + w.stat);
+    p.dut = ws + w.dut;
+    p.npairs = PairTable::total(a->TQ, a->q_start);
   } else {
     p.wq = ws + w.wq; p.wqT = ws + w.wqT; p.wdibT = ws + w.wdibT;
     p.lse2 = reinterpret_cast<float*>(ws + w.lse2);

@@ -48,13 +48,48 @@ __device__ __forceinline__ float bwd_elem(float u, float dw, float lse2, float c
   return de * sp;
 }
 
+__device__ __forceinline__ int lane_of(int li, int lg) { return 16 * lg + li; }
+
+// dU^T of the wave's quadrant as the B fragments of dQ^T += K^T dU^T (bwd_dq_kernel). au[kt] holds
+// key 16 kt + li and, in slots 4 qt + r, query 16 qt + 4 lg + r; a 16x16x16 product with the identity
+// (eye: slot r is 1 where li == 4 lg + r) moves the queries of one query tile into the accumulator
+// columns, exactly (one bf16 term per sum). Fragment qt then holds, for query 16 qt + li, keys
+// 4 lg + r (slots 0..3, kt = 0) and 16 + 4 lg + r (slots 4..7, kt = 1): the k order of tile_tr_frag.
+// One 16-byte store per lane and fragment: the wave writes 1 KB contiguous.
+__device__ __forceinline__ void store_dut(const Elem<bf16_t>::Frag (&au)[2], s16x4 eye, bf16_t* dst, int lane) {
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    f32x4 t[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      const bf16x8 v = au[kt].v;
+      const bf16x4 h = qt ? bf16x4{v[4], v[5], v[6], v[7]} : bf16x4{v[0], v[1], v[2], v[3]};
+      t[kt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, h), eye,
+                                                        f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+    }
+    bf16x8 o;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      o[r] = (__bf16)t[0][r];
+      o[4 + r] = (__bf16)t[1][r];
+    }
+    *reinterpret_cast<bf16x8*>(dst + qt * 512 + lane * 8) = o;
+  }
+}
+
+__device__ __forceinline__ void store_dut_zero(bf16_t* dst, int lane) {
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) *reinterpret_cast<bf16x8*>(dst + qt * 512 + lane * 8) = bf16x8{};
+}
+
 // ------------------------------------------------------------------------------------------------
 // key-stationary kernel: dP2 and dI~
 // ------------------------------------------------------------------------------------------------
 template <int DP, bool MASKED>
 __device__ __forceinline__ void kv_block(const bf16_t* Qs, const bf16_t* Ds, const float* Ss, const bf16_t* Ks,
                                          const bf16_t* Vs, f32x4 (&dvacc)[2][DP / 16], f32x4 (&dkacc)[2][DP / 16],
-                                         int qh, int kh, int li, int lg, int key0, int qa0, float nc2, float scale) {
+                                         bf16_t* dut_w, s16x4 eye, int qh, int kh, int li, int lg, int key0, int qa0,
+                                         float nc2, float scale) {
   using E = Elem<bf16_t>;
   using Frag = E::Frag;
   constexpr int KS = DP / 32, DT = DP / 16;
@@ -112,6 +147,7 @@ __device__ __forceinline__ void kv_block(const bf16_t* Qs, const bf16_t* Ds, con
     aw[kt] = E::from_f32(wv[kt]);
     au[kt] = E::from_f32(uv[kt]);
   }
+  if (dut_w) store_dut(au, eye, dut_w, lane_of(li, lg));
   // dV += W^T dI-bar, dK += dU^T Q over the wave's 32 queries (k in permuted order)
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) {
@@ -170,13 +206,18 @@ bwd_kv_kernel(const BwdParams p) {
     st.issue(dst, srcs, strides, qb * 64, p.TQ - 1, wave, lane);
     if (wave == 3 && lane < 32) {
       const float* src = sbase + int64_t(qb) * 128 + 4 * lane;
-      __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)src,
-                                       (void __attribute__((address_space(3)))*)(dst + 2 * TILE), 16, 0, 0);
+      lds_dma16(src, dst + 2 * TILE);
     }
   };
 
   const float nc2 = -p.scale * kLog2e;
   const int qb_lo = max(0, k0 + 1 - p.q_start) / 64;
+  // dU^T fragments of this key block: pair (qb, kb) at PairTable::offset(qb) + kb, 8 fragments of
+  // 64 lanes x 8 bf16 each, fragment kh * 4 + query tile; the wave writes fragments (kh, 2 qh + qt)
+  bf16_t* dut_bh = reinterpret_cast<bf16_t*>(p.dut) + int64_t(bh) * p.npairs * 4096 + (kh * 4 + 2 * qh) * 512;
+  s16x4 eye;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) eye[r] = li == 4 * lg + r ? short(0x3F80) : short(0);
   {
     // the key rows once (rows past the keys: finite copies whose results are never stored)
     const bf16_t* ksrc[2] = {kbase, vbase};
@@ -201,10 +242,15 @@ bwd_kv_kernel(const BwdParams p) {
     const float* Ss = reinterpret_cast<const float*>(Qs + 2 * TILE);
     const int i0 = qb * 64 + 32 * qh;   // the wave's first query row
     const int qa0 = p.q_start + i0;     // its position
+    bf16_t* dut_w = kb < PairTable::nkb(qb, p.TQ, p.q_start)
+                        ? dut_bh + (PairTable::offset(qb, p.q_start) + kb) * 4096
+                        : nullptr;
     // quadrant visible at all (some key < some query position), and not wholly padding rows
     if (i0 < p.TQ && key0 < qa0 + 31)
-      kv_block<DP, decltype(masked)::value>(Qs, Ds, Ss, kvs, kvs + TILE, dvacc, dkacc, qh, kh, li, lg, key0, qa0, nc2,
-                                            p.scale);
+      kv_block<DP, decltype(masked)::value>(Qs, Ds, Ss, kvs, kvs + TILE, dvacc, dkacc, dut_w, eye, qh, kh, li, lg,
+                                            key0, qa0, nc2, p.scale);
+    else if (dut_w)
+      store_dut_zero(dut_w, lane);
     MOTE_STAMP(2, qb - qb_lo);
     __builtin_amdgcn_s_waitcnt(0);
     MOTE_STAMP(3, qb - qb_lo);
@@ -283,75 +329,31 @@ bwd_kv_kernel(const BwdParams p) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// query-stationary kernel: dP1
+// query-stationary kernel: dP1 = (dU P2 + dU_ii P2_i) / sqrt(D) from the stored dU^T fragments
 // ------------------------------------------------------------------------------------------------
-template <int DP, bool MASKED>
-__device__ __forceinline__ void q_block(const bf16_t* Ks, const bf16_t* Vs, const Elem<bf16_t>::Frag (&qf)[2][DP / 32],
-                                        const Elem<bf16_t>::Frag (&df)[2][DP / 32], f32x4 (&dqacc)[DP / 16][2],
-                                        const float (&lse2)[2], const float (&cv)[2], const int (&qabs)[2], int kh,
-                                        int li, int lg, int key0, float nc2, float scale) {
-  using E = Elem<bf16_t>;
-  using Frag = E::Frag;
-  constexpr int KS = DP / 32, DT = DP / 16;
-  f32x4 sacc[2][2], wacc[2][2];  // [key tile][query tile]
-#pragma unroll
-  for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      sacc[kt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
-      wacc[kt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      const int row = 32 * kh + 16 * kt + li;
-      const Frag ak = tile_row_frag<DP>(Ks, row, 4 * ks + lg);
-      const Frag av = tile_row_frag<DP>(Vs, row, 4 * ks + lg);
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        sacc[kt][s] = E::mma(ak, qf[s][ks], sacc[kt][s]);
-        wacc[kt][s] = E::mma(av, df[s][ks], wacc[kt][s]);
-      }
-    }
-  }
-  // keys 16 kt + 4 lg + r of the wave's half (rows), query 16 s + li (column)
-  Frag bu[2];
-#pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    float uv[8];
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        bool keep = true;
-        if constexpr (MASKED) keep = key0 + 16 * kt + 4 * lg + r < qabs[s];
-        float w;
-        uv[4 * kt + r] = bwd_elem(sacc[kt][s][r], wacc[kt][s][r], lse2[s], cv[s], nc2, scale, keep, w);
-      }
-    bu[s] = E::from_f32(uv);
-  }
-  // dQ^T += K^T dU^T over the wave's 32 keys (k in permuted order)
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt) {
-    const Frag ak = tile_tr_frag<DP>(Ks, 32 * kh, dt, li, lg);
-#pragma unroll
-    for (int s = 0; s < 2; ++s) dqacc[dt][s] = E::mma(ak, bu[s], dqacc[dt][s]);
-  }
-}
-
+// One workgroup per 64 queries of one (batch, head), longest first. Wave w = (qh, kh) accumulates
+// dQ^T of queries 32 qh .. +31 over key half kh of every key block: A = K^T by transposed LDS reads
+// of the staged P2 tile, B = the key kernel's dU^T fragments straight from global memory (16 bytes per
+// lane). No elementwise work: the kernel streams the fragments, with NS key blocks in flight (P2 tiles
+// in an NS-deep LDS ring, fragments in NS register sets; the loop is unrolled by NS so that every
+// buffer index is a constant). The key halves add through LDS before the Self term and the stores.
 template <int DP>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
-bwd_q_kernel(const BwdParams p) {
+__global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
   using E = Elem<bf16_t>;
   using Frag = E::Frag;
-  constexpr int KS = DP / 32, DT = DP / 16, CPR = DP / 8, TILE = 64 * DP;
-  constexpr int STAGE = 2 * TILE;  // K tile, V tile
-  constexpr int RLD = DP + 4;      // fp32 row stride of the reduction buffer
-  __shared__ __align__(16) bf16_t smem[2 * STAGE];
+  constexpr int DT = DP / 16, CPR = DP / 8, TILE = 64 * DP;
+  constexpr int NS = 4;             // key blocks in flight
+  constexpr int SLOT = TILE + 4096; // bf16 per ring slot: the P2 tile, then the pair's 8 dU^T fragments
+  constexpr int VMS = DP / 32 + 2;  // vector-memory instructions per block and wave (P2 staging + 2 fragments)
+  constexpr int HALF = DP / 2;      // fp32 columns per half of the reduction buffer
+  // one array per ring slot (each slot holds half of the final reduction buffer)
+  __shared__ __align__(16) bf16_t ks0[SLOT];
+  __shared__ __align__(16) bf16_t ks1[SLOT];
+  __shared__ __align__(16) bf16_t ks2[SLOT];
+  __shared__ __align__(16) bf16_t ks3[SLOT];
 
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: staging in scalar registers
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15, lg = lane >> 4;
   const int kh = wave & 1, qh = wave >> 1;
   const int BH = p.B * p.H;
@@ -360,77 +362,79 @@ bwd_q_kernel(const BwdParams p) {
   const int qb = nqb - 1 - blockIdx.x / BH;  // the last query block sees the most keys: longest first
   const int b = bh / p.H, h = bh % p.H;
   const int i0 = qb * 64;
-  const bf16_t* qbase = reinterpret_cast<const bf16_t*>(p.p1) + b * p.q_sb + h * p.q_sh;
   const bf16_t* kbase = reinterpret_cast<const bf16_t*>(p.p2) + b * p.k_sb + h * p.k_sh;
-  const bf16_t* vbase = reinterpret_cast<const bf16_t*>(p.info) + b * p.v_sb + h * p.v_sh;
-  const bf16_t* dbase = reinterpret_cast<const bf16_t*>(p.wdib) + int64_t(bh) * p.TQp * DP;
-  const float* sblk = p.stat + (int64_t(bh) * nqb + qb) * 128;
+  const int nkb = PairTable::nkb(qb, p.TQ, p.q_start);
+  // the wave's two fragments (kh, 2 qh) and (kh, 2 qh + 1) of each pair: 2 KB contiguous
+  const int fo = (kh * 4 + 2 * qh) * 512;
+  const bf16_t* fr = reinterpret_cast<const bf16_t*>(p.dut) +
+                     (int64_t(bh) * p.npairs + PairTable::offset(qb, p.q_start)) * 4096 + fo + lane * 8;
+  auto slot = [&](auto u) -> bf16_t* {
+    constexpr int U = decltype(u)::value;
+    if constexpr (U == 0) return ks0;
+    else if constexpr (U == 1) return ks1;
+    else if constexpr (U == 2) return ks2;
+    else return ks3;
+  };
 
-  // the wave's 32 queries as B fragments (k = head dim, column = query), with their row terms
-  const int q0 = i0 + 32 * qh;
-  Frag qf[2][KS], df[2][KS];
-  float lse2[2], cv[2];
-  int qabs[2];
-#pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    const int qi = q0 + 16 * s + li;
-    const bool ok = qi < p.TQ;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int d0 = 32 * ks + 8 * lg;
-      qf[s][ks] = ok ? E::load8(qbase + int64_t(qi) * p.q_sr + d0) : E::zero();
-      df[s][ks] = E::load8(dbase + int64_t(qi) * DP + d0);  // rows up to TQp exist (zero padding)
-    }
-    lse2[s] = sblk[32 * qh + 16 * s + li];      // +inf for padding rows and rows without a past
-    cv[s] = sblk[64 + 32 * qh + 16 * s + li];
-    qabs[s] = p.q_start + qi;
-  }
   f32x4 dqacc[DT][2];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
     for (int s = 0; s < 2; ++s) dqacc[dt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const bf16_t* srcs[2] = {kbase, vbase};
-  const int64_t strides[2] = {p.k_sr, p.v_sr};
-  TileStager<DP, 4, 2> st;
+  const bf16_t* srcs[1] = {kbase};
+  const int64_t strides[1] = {p.k_sr};
+  TileStager<DP, 4, 1> st;
   st.init(wave, lane, strides);
-  const int qlast = min(p.TQ, i0 + 64) - 1;
-  const int nkb = (p.q_start + qlast + 63) / 64;  // keys j < q_start + qlast
-  const int wq_last = min(q0 + 31, p.TQ - 1);     // the wave's last query row
-  const float nc2 = -p.scale * kLog2e;
-
-  if (nkb > 0) {
-    st.issue(smem, srcs, strides, 0, p.TK - 1, wave, lane);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-  }
-  // key blocks wholly before the workgroup's first query position first (unmasked block math), then
-  // the diagonal ones (masked): two loops keep one register assignment of the accumulators each
-  auto step = [&](int kb, auto masked) {
-    MOTE_STAMP(0, kb);
-    const int stage = kb & 1;
-    if (kb + 1 < nkb) st.issue(smem + (stage ^ 1) * STAGE, srcs, strides, (kb + 1) * 64, p.TK - 1, wave, lane);
-    MOTE_STAMP(1, kb);
-    const bf16_t* Ks = smem + stage * STAGE;
-    const bf16_t* Vs = Ks + TILE;
-    const int key0 = kb * 64 + 32 * kh;
-    // the quadrant has a visible pair: some key below the wave's last query position
-    if (q0 < p.TQ && key0 < p.q_start + wq_last)
-      q_block<DP, decltype(masked)::value>(Ks, Vs, qf, df, dqacc, lse2, cv, qabs, kh, li, lg, key0, nc2, p.scale);
-    MOTE_STAMP(2, kb);
-    __builtin_amdgcn_s_waitcnt(0);
-    MOTE_STAMP(3, kb);
-    __syncthreads();
-    MOTE_STAMP(4, kb);
+  // Block kb: P2 rows and the wave's fragments into ring slot kb % NS. Every step issues one block
+  // and waits for one, the same count each time (blocks past the end reload the last block's
+  // addresses), so the wait before a read is always "all but the two newest blocks".
+  auto issue = [&](int kb, auto u) {
+    const int kc = min(kb, nkb - 1);
+    bf16_t* dst = slot(u);
+    st.issue(dst, srcs, strides, kc * 64, p.TK - 1, wave, lane);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) TileStager<DP, 4, 1>::load(fr + int64_t(kc) * 4096 + s * 512, dst + TILE + fo + s * 512);
   };
-  const int kb_m = min(nkb, (p.q_start + i0) / 64);
-  int kb = 0;
-  for (; kb < kb_m; ++kb) step(kb, std::false_type{});
-  for (; kb < nkb; ++kb) step(kb, std::true_type{});
+  static_assert(NS == 4, "four ring slots");
+  auto step = [&](int kb, auto u) {
+    constexpr int U = decltype(u)::value;
+    __builtin_amdgcn_s_waitcnt(kVmWaitStage<(NS - 2) * VMS>());  // this wave's part of block kb is in
+    lds_barrier();  // every wave's part of block kb is in; every wave is done with block kb - 1's slot
+    issue(kb + NS - 1, std::integral_constant<int, (U + NS - 1) % NS>{});
+    if (kb < nkb) {
+      const bf16_t* Ks = slot(u);
+      Frag bf[2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) bf[s] = E::load8(Ks + TILE + fo + s * 512 + lane * 8);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const Frag ak = tile_tr_frag<DP>(Ks, 32 * kh, dt, li, lg);
+#pragma unroll
+        for (int s = 0; s < 2; ++s) dqacc[dt][s] = E::mma(ak, bf[s], dqacc[dt][s]);
+      }
+    }
+  };
+  if (nkb > 0) {
+    issue(0, std::integral_constant<int, 0>{});
+    issue(1, std::integral_constant<int, 1>{});
+    issue(2, std::integral_constant<int, 2>{});
+    for (int kb0 = 0; kb0 < nkb; kb0 += NS) {
+      step(kb0, std::integral_constant<int, 0>{});
+      step(kb0 + 1, std::integral_constant<int, 1>{});
+      step(kb0 + 2, std::integral_constant<int, 2>{});
+      step(kb0 + 3, std::integral_constant<int, 3>{});
+    }
+  }
 
-  // add the two key halves through LDS: R[64 queries][RLD] fp32
-  float* R = reinterpret_cast<float*>(smem);
+  // add the two key halves through LDS: head-dim columns [0, DP/2) in slot 0, the rest in slot 1,
+  // each [64 queries][DP/2] fp32 (exactly one slot)
+  float* R0 = reinterpret_cast<float*>(ks0);
+  float* R1 = reinterpret_cast<float*>(ks1);
+  auto rptr = [&](int row, int col) -> float* {
+    return col < HALF ? R0 + row * HALF + col : R1 + row * HALF + (col - HALF);
+  };
+  __builtin_amdgcn_s_waitcnt(0);  // the last (past-the-end) prefetches into slots 0 and 1 have landed
   __syncthreads();
   if (kh == 1) {
 #pragma unroll
@@ -438,7 +442,7 @@ bwd_q_kernel(const BwdParams p) {
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         const int row = 32 * qh + 16 * s + li;
-        *reinterpret_cast<f32x4*>(&R[row * RLD + 16 * dt + 4 * lg]) = dqacc[dt][s];
+        *reinterpret_cast<f32x4*>(rptr(row, 16 * dt + 4 * lg)) = dqacc[dt][s];
       }
   }
   __syncthreads();
@@ -448,7 +452,7 @@ bwd_q_kernel(const BwdParams p) {
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         const int row = 32 * qh + 16 * s + li;
-        f32x4* q = reinterpret_cast<f32x4*>(&R[row * RLD + 16 * dt + 4 * lg]);
+        f32x4* q = reinterpret_cast<f32x4*>(rptr(row, 16 * dt + 4 * lg));
         *q = *q + dqacc[dt][s];
       }
   }
@@ -464,7 +468,7 @@ bwd_q_kernel(const BwdParams p) {
     float o[8];
 #pragma unroll
     for (int e = 0; e < 8; e += 4) {
-      const float4 a = *reinterpret_cast<const float4*>(&R[row * RLD + d0 + e]);
+      const float4 a = *reinterpret_cast<const float4*>(rptr(row, d0 + e));
       o[e] = a.x; o[e + 1] = a.y; o[e + 2] = a.z; o[e + 3] = a.w;
     }
 #pragma unroll
@@ -486,7 +490,7 @@ static void launch_tiles_dp(const BwdParams& p, int stages, hipStream_t stream) 
   }
   if (stages & MOTE_BWD_QUERIES) {
     const int nqb = p.TQp / 64;
-    hipLaunchKernelGGL((bwd_q_kernel<DP>), dim3(nqb * BH), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((bwd_dq_kernel<DP>), dim3(nqb * BH), dim3(256), 0, stream, p);
   }
 }
 

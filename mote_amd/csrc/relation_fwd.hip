@@ -573,11 +573,9 @@ relation_fwd_tile_kernel(const FwdParams p) {
     ones.v = bf16x8{one, one, one, one, one, one, one, one};
   }
 
-  if (kb_lo < kb_hi) {
-    st.issue(smem + (kb_lo & 1) * STAGE, srcs, strides, kb_lo * 64, TKs - 1, wave, lane);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-  }
+  if (kb_lo < kb_hi) st.issue(smem + (kb_lo & 1) * STAGE, srcs, strides, kb_lo * 64, TKs - 1, wave, lane);
+  __builtin_amdgcn_s_waitcnt(0);  // unconditional: no query-fragment load stays pending into the loop
+  __syncthreads();
   // key blocks wholly before the workgroup's first query position first (unmasked block math), then
   // the diagonal ones (masked): two loops keep one register assignment of the accumulators each
   auto step = [&](int kb, auto masked) {

@@ -26,6 +26,23 @@ __device__ constexpr int kVmWaitStage() {
   return (N & 0xF) | (0x7 << 4) | (0xF << 8) | (((N >> 4) & 0x3) << 14);
 }
 
+// Workgroup barrier of the staging loops. __syncthreads() carries a workgroup-scope release fence,
+// which waits for every outstanding vector-memory operation of the wave, prefetches included; the
+// loops instead wait for the stage they are about to read with kVmWaitStage and then need only
+// their LDS operations complete before the barrier, so later stages stay in flight across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// One global -> LDS transfer of 16 bytes per active lane (lane l writes at l_base + 16 l, l_base
+// wave-uniform), issued as inline assembly: the compiler does not track it, so it never adds a wait
+// for it before unrelated LDS reads (its alias tracking of LDS DMA gives up at control-flow merges
+// and then waits for every outstanding load, prefetches included). The kernels wait for each stage
+// explicitly (kVmWaitStage, s_waitcnt 0); the compiler's own waits for register loads stay correct
+// because vector-memory operations retire in issue order and it can only undercount younger ones.
+__device__ __forceinline__ void lds_dma16(const void* g, void* l) {
+  const uint32_t la = uint32_t(reinterpret_cast<uintptr_t>((void __attribute__((address_space(3)))*)l));
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(la) : "memory", "m0");
+}
+
 template <int DP>
 __device__ __forceinline__ int tile_swz(int row) {
   if constexpr (DP == 64) return (row >> 1) & 7;
@@ -119,10 +136,7 @@ struct TileStager {
     }
   }
 
-  __device__ __forceinline__ static void load(const bf16_t* g, bf16_t* l) {
-    __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)g,
-                                     (void __attribute__((address_space(3)))*)l, 16, 0, 0);
-  }
+  __device__ __forceinline__ static void load(const bf16_t* g, bf16_t* l) { lds_dma16(g, l); }
 };
 
 }  // namespace mote
