@@ -205,8 +205,7 @@ bwd_kv_kernel(const BwdParams p) {
     bf16_t* dst = smem + stage * STAGE;
     st.issue(dst, srcs, strides, qb * 64, p.TQ - 1, wave, lane);
     if (wave == 3 && lane < 32) {
-      const float* src = sbase + int64_t(qb) * 128 + 4 * lane;
-      lds_dma16(src, dst + 2 * TILE);
+      lds_dma16_s(sbase + int64_t(qb) * 128, 16u * lane, dst + 2 * TILE);
     }
   };
 

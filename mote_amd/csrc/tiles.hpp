@@ -43,6 +43,15 @@ __device__ __forceinline__ void lds_dma16(const void* g, void* l) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(la) : "memory", "m0");
 }
 
+// The same transfer from a wave-uniform base (SGPR pair) plus a per-lane byte offset. The offset
+// registers can stay constant across a whole loop: a VMEM instruction reads its address registers
+// only when the address unit takes it, so rewriting an address register right after an issue (the
+// 64-bit form, one address per transfer) stalls the wave until the previous transfer has been taken.
+__device__ __forceinline__ void lds_dma16_s(const void* base, uint32_t voff, void* l) {
+  const uint32_t la = uint32_t(reinterpret_cast<uintptr_t>((void __attribute__((address_space(3)))*)l));
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(la) : "memory", "m0");
+}
+
 template <int DP>
 __device__ __forceinline__ int tile_swz(int row) {
   if constexpr (DP == 64) return (row >> 1) & 7;
@@ -80,17 +89,17 @@ __device__ __forceinline__ typename Elem<bf16_t>::Frag tile_row_frag(const bf16_
 }
 
 // Staging of NT tiles per stage by the NW waves of a workgroup: the NT * CPR wave instructions are
-// dealt round-robin over the waves; each lane precomputes, per instruction, its row in the block and
-// the element offset of its source chunk from the block's first row (row * stride + column), so a
-// full block costs one 64-bit add per instruction. `wave` must be wave-uniform (readfirstlane), which
+// dealt round-robin over the waves; each lane precomputes, per instruction, the byte offset of its
+// source chunk from the block's first row (row * stride + column), so a full block issues from a
+// scalar base with constant offset registers. `wave` must be wave-uniform (readfirstlane), which
 // keeps the LDS destinations and the per-block bases in scalar registers. Row strides must stay below
-// 2^24 elements (checked by the host launchers).
+// 2^24 elements (checked by the host launchers), so the offsets fit 32 bits.
 template <int DP, int NW, int NT>
 struct TileStager {
   static constexpr int CPR = DP / 8;
   static constexpr int NINS = NT * CPR;
   static constexpr int PER = (NINS + NW - 1) / NW;
-  int off[PER];
+  uint32_t voff[PER];  // bytes
 
   __device__ __forceinline__ static int row_of(int n, int lane) { return (64 * n + lane) / CPR; }
   __device__ __forceinline__ static int col_of(int n, int lane) {
@@ -103,7 +112,7 @@ struct TileStager {
     for (int i = 0; i < PER; ++i) {
       const int ins = wave + NW * i;
       const int t = ins < NINS ? ins / CPR : 0, n = ins % CPR;
-      off[i] = row_of(n, lane) * int(stride[t]) + col_of(n, lane);
+      voff[i] = uint32_t(row_of(n, lane) * int(stride[t]) + col_of(n, lane)) * 2u;
     }
   }
 
@@ -118,8 +127,7 @@ struct TileStager {
         const int ins = wave + NW * i;
         if (NINS % NW == 0 || ins < NINS) {
           const int t = ins / CPR, n = ins % CPR;
-          const bf16_t* g = src[t] + int64_t(r0) * stride[t] + off[i];
-          load(g, dst + t * 64 * DP + n * 512);
+          lds_dma16_s(src[t] + int64_t(r0) * stride[t], voff[i], dst + t * 64 * DP + n * 512);
         }
       }
     } else {
