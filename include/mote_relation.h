@@ -100,7 +100,8 @@ int mote_relation_fwd(const mote_relation_fwd_args* args, void* stream);
  * bytes; its contents on entry do not matter.
  * `stages` selects which launches run (MOTE_BWD_ROWS: per-row terms and operand copies;
  * MOTE_BWD_KEYS: the key-stationary kernel; MOTE_BWD_QUERIES: the query-stationary dp1 kernel,
- * where the path has one; MOTE_BWD_FINISH: dp1 cast and dlam); 0 runs all of them. A caller that
+ * where the path has one; MOTE_BWD_FINISH: dp1 cast and dlam, which the bf16 tile path computes in
+ * its MOTE_BWD_QUERIES launch instead); 0 runs all of them. A caller that
  * splits them (to time or overlap them) issues them in that order on one stream with one workspace.
  * ------------------------------------------------------------------------------------------------ */
 #define MOTE_BWD_ROWS 1

@@ -56,6 +56,20 @@ struct PairTable {
   }
 };
 
+// dlam = the fixed-order sum of the n row-block partials (the rows stage writes them), by the 256
+// threads of one workgroup through `red` (256 floats of LDS); every thread must call it.
+__device__ __forceinline__ void dlam_sum(const float* part, int n, float* out, float* red) {
+  float acc = 0.f;
+  for (int i = threadIdx.x; i < n; i += 256) acc += part[i];
+  red[threadIdx.x] = acc;
+  __syncthreads();
+  for (int w = 128; w >= 1; w >>= 1) {
+    if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) *out = red[0];
+}
+
 // bf16 with D in {32, 64, 96, 128}: the atomic-free tile kernels (dP2 / dI~ key-stationary, then dP1
 // query-stationary), for the stages selected in `stages` (MOTE_BWD_KEYS, MOTE_BWD_QUERIES).
 void launch_bwd_tiles(const BwdParams& p, int stages, hipStream_t stream);

@@ -707,15 +707,7 @@ __global__ void __launch_bounds__(256) bwd_zero_rows_kernel(mote_view v, int H, 
 
 __global__ void __launch_bounds__(256) bwd_dlam_kernel(const float* part, int n, float* out) {
   __shared__ float red[256];
-  float acc = 0.f;
-  for (int i = threadIdx.x; i < n; i += 256) acc += part[i];
-  red[threadIdx.x] = acc;
-  __syncthreads();
-  for (int w = 128; w >= 1; w >>= 1) {
-    if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) *out = red[0];
+  dlam_sum(part, n, out, red);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -790,14 +782,14 @@ static void launch_bwd_t(const BwdParams& p, bool deterministic, int stages, hip
   }
 }
 
+// dlam is summed by the last workgroup of the query-stationary kernel (MOTE_BWD_QUERIES): the finish
+// stage has nothing left to do on this path.
 template <int DP>
 static void launch_bwd_tile_path(const BwdParams& p, int stages, hipStream_t stream) {
   const int BH = p.B * p.H;
   if (stages & MOTE_BWD_ROWS)
     hipLaunchKernelGGL((bwd_rows_kernel<bf16_t, DP, true>), dim3(p.TQp / kRowBlock, BH), dim3(256), 0, stream, p);
   launch_bwd_tiles(p, stages, stream);
-  if (stages & MOTE_BWD_FINISH)
-    hipLaunchKernelGGL(bwd_dlam_kernel, dim3(1), dim3(256), 0, stream, p.dlam_part, BH * (p.TQp / kRowBlock), p.dlam);
 }
 
 int launch_bwd(const mote_relation_bwd_args* a, hipStream_t stream) {

@@ -475,6 +475,10 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
     const Frag ov = E::from_f32(o);
     *reinterpret_cast<bf16x8*>(dqout + int64_t(i) * p.dq_sr + d0) = ov.v;
   }
+  // the last workgroup (query block 0, the shortest) also sums dlam: the rows stage has written
+  // every partial before this launch
+  if (blockIdx.x == gridDim.x - 1)
+    dlam_sum(p.dlam_part, BH * nqb, p.dlam, reinterpret_cast<float*>(ks2));
 }
 
 // ------------------------------------------------------------------------------------------------

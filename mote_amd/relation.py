@@ -87,7 +87,8 @@ def _rope_givens_bwd(dp1: torch.Tensor, dp2: torch.Tensor, dinfo: torch.Tensor, 
     qkv = qkv if qkv.stride(-1) == 1 else qkv.contiguous()
     dp1, dp2, dinfo = (t.to(qkv.dtype) if t.stride(-1) == 1 else t.to(qkv.dtype).contiguous() for t in (dp1, dp2, dinfo))
     dqkv = torch.empty(B, T, D3, device=qkv.device, dtype=qkv.dtype)
-    dtheta = torch.zeros(max(H // 2, 1), device=qkv.device, dtype=torch.float32)
+    # written whole by the kernel when theta is given
+    dtheta = (torch.empty if theta is not None else torch.zeros)(max(H // 2, 1), device=qkv.device, dtype=torch.float32)
     a = L.RopeBwdArgs()
     a.dtype = L.dtype_code(qkv)
     a.B, a.T, a.H, a.D, a.pos0, a.layer_parity = B, T, H, D, int(pos0), int(parity)
