@@ -1,12 +1,14 @@
 // One decode step of one Relation layer (mote/infer/graph.py:151-187), one launch.
 //
-// Grid: nsplit x (B*H) workgroups, block id = split * (B*H) + head index. Split s owns the past rows
-// [s*R, (s+1)*R) of its head, R = 64 * rows_mult (a host choice that keeps a few hundred workgroups
-// in flight); the launch shape depends only on the cache capacity, so it can be captured in a HIP
-// graph. Each workgroup (4 waves; a wave reads 16 rows per step, 4 lanes per row, 16-byte loads of
-// P2 and I~ issued together with a one-step register prefetch) computes U_j = <q, P2_j> / sqrt(D),
-// e_j = SiLU(U_j) in log2 units and an online softmax per row group (running max raised lazily, by
-// more than 2^8 only), merges its row groups and waves, and publishes (max, l, z[D]).
+// Grid: nsplit x (B*H) workgroups, block id = split * (B*H) + head index; nsplit is a host choice
+// from the shape only (about three workgroups per CU over the batch, no split shorter than 512 rows
+// at full capacity), so the launch can be captured in a HIP graph. On the device each head's S past
+// rows are cut into nsplit equal runs (multiples of the 64-row step) from S itself, so the splits
+// stay balanced as S grows. Each workgroup (4 waves; a wave reads 16 rows per step, 4 lanes per row,
+// 16-byte loads of P2 and I~, with a ring of four register sets keeping three steps of loads in
+// flight) computes U_j = <q, P2_j> / sqrt(D), e_j = SiLU(U_j) in log2 units and an online softmax
+// per row group (running max raised lazily, by more than 2^8 only), merges its row groups and waves,
+// and publishes (max, l, z[D]).
 //
 // Publication without a device-scope fence (which on gfx950 writes back the XCD's whole L2): the
 // partial goes out with agent-coherent stores, the wave waits for their completion, and one atomic
@@ -21,6 +23,8 @@
 // The query is RoPE'd at S and rounded to the cache dtype (graph.py:158-172) by every workgroup; the
 // new P2 row gets the same rotation and I~ the Givens rotation with its partner head's raw row.
 // Bandwidth-bound by design: no MFMA, wavefront reductions only.
+#include <type_traits>
+
 #include "common.hpp"
 #include "params.hpp"
 
@@ -43,11 +47,13 @@ struct DecParams {
   float* part;        // [BH][nsplit][D + 2]  (max, l, z)
   int* cnt;           // [BH] splits published in this call (zero between calls)
   int* cnt_seq;       // [B] heads finished in this call (zero between calls)
-  int B, H, D, cap, parity, flags, nsplit, rps;  // rps: rows per split
+  int B, H, D, cap, parity, flags, nsplit;
   float scale, tau_inv;
 };
 
 constexpr int kDecMaxSplits = 120;  // partials one merge holds in LDS (D <= 128: at most 62 KB)
+constexpr int kDecWaves = 4;  // waves per workgroup: 16 rows each per step (8 and 16 measured slower)
+constexpr int kDecThreads = 64 * kDecWaves;
 
 __device__ __forceinline__ void store_coherent(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -83,7 +89,7 @@ __device__ __forceinline__ void decode_finish(const DecParams& p, int bh, int64_
   const int nact = p.nsplit;
   float* wsp = spart + nact * stride;
   const float* pb = p.part + int64_t(bh) * p.nsplit * stride;
-  for (int i = tid; i < nact * stride; i += 256) spart[i] = load_coherent(pb + i);
+  for (int i = tid; i < nact * stride; i += kDecThreads) spart[i] = load_coherent(pb + i);
   // new rows: query and P2 RoPE'd at S, I~ Givens'd with its partner head's raw row
   const T* q_raw = reinterpret_cast<const T*>(p.p1) + b * p.in_sb + h * D;
   const T* k_raw = reinterpret_cast<const T*>(p.p2) + b * p.in_sb + h * D;
@@ -168,7 +174,7 @@ __device__ __forceinline__ void decode_finish(const DecParams& p, int bh, int64_
   T* y = reinterpret_cast<T*>(p.y) + b * p.y_sb + h * D;
   T* kw = reinterpret_cast<T*>(p.kc) + b * p.kc_sb + h * p.kc_sh + int64_t(S) * p.kc_sr;
   T* vw = reinterpret_cast<T*>(p.vc) + b * p.vc_sb + h * p.vc_sh + int64_t(S) * p.vc_sr;
-  for (int d = tid; d < D; d += 256) {
+  for (int d = tid; d < D; d += kDecThreads) {
     float zsum = 0.f;
 #pragma unroll 8
     for (int s = 0; s < nact; ++s) zsum = fmaf(spart[s * stride + 2 + d], wsp[s], zsum);
@@ -192,12 +198,13 @@ __device__ __forceinline__ void decode_finish(const DecParams& p, int bh, int64_
 }
 
 template <typename T, int DP>
-__global__ void __launch_bounds__(256) relation_decode_kernel(const DecParams p) {
+__global__ void __launch_bounds__(kDecThreads)
+relation_decode_kernel(const DecParams p) {
   using E = Elem<T>;
   constexpr int EPC = 16 / sizeof(T);
   constexpr int MAXC = (DP / EPC + 3) / 4;  // 16-byte chunks per lane (lane c owns chunks c, c+4, ...)
   __shared__ float sq[DP];
-  __shared__ float red[4 * (DP + 2)];
+  __shared__ float red[kDecWaves * (DP + 2)];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int BH = p.B * p.H;
@@ -205,16 +212,55 @@ __global__ void __launch_bounds__(256) relation_decode_kernel(const DecParams p)
   const int split = blockIdx.x / BH;
   const int b = bh / p.H, h = bh % p.H;
   const int D = p.D, half = D / 2;
+  // Order of the prologue: the raw query loads, then the first NR - 1 cache steps, and only then the
+  // position S (the split's rows do not depend on S, only where its valid rows end), the RoPE of the
+  // query at S and the masks: the cache loads are in flight while S and the query arrive.
+  const T* q_raw = reinterpret_cast<const T*>(p.p1) + b * p.in_sb + h * D;
+  const int qi = min(tid, half - 1);
+  const float x0 = E::to_f(q_raw[qi]), x1 = E::to_f(q_raw[qi + half]);
+
+  // The head's S past rows are cut into nsplit equal runs (a multiple of the 64-row step) from S
+  // itself, so every split carries the same load whatever S is; the grid depends only on the shape.
   const int64_t S64 = p.S[b];
   const bool bad = S64 < 0 || S64 >= p.cap;
   const int S = bad ? 0 : int(S64);
+  const int rps = ((S + p.nsplit - 1) / p.nsplit + 63) & ~63;
+  const int r0 = split * rps;
+  const int rf = min(p.cap, r0 + rps);  // rows this split may load (the cache holds them all)
+  const T* kbase = reinterpret_cast<const T*>(p.kc) + b * p.kc_sb + h * p.kc_sh;
+  const T* vbase = reinterpret_cast<const T*>(p.vc) + b * p.vc_sb + h * p.vc_sh;
+  const int rr = lane >> 2, c = lane & 3;
+  const int nch = D / EPC;
+  const float c2 = p.scale * kLog2e;
+
+  // A ring of NR register sets, one 64-row step each (16 rows per wave, 4 lanes per row): the loads
+  // of the next NR - 1 steps are in flight while a step computes, and the loop is unrolled by NR so
+  // every set is named by a constant (a copy between sets would make the compiler wait for the
+  // newest loads before issuing the next ones).
+  constexpr int NR = 4;
+  Chunk kr[NR][MAXC], vr[NR][MAXC];
+  // Loads are unconditional (rows past the split and chunks past the head dim read a clamped, valid
+  // address whose values the math ignores): a load under a lane condition would hide it from the
+  // compiler's count of outstanding loads, and it would then wait for every one of them.
+  auto fetch = [&](int row, auto u) {
+    constexpr int U = decltype(u)::value;
+    const int rc = max(0, min(row, rf - 1));
+#pragma unroll
+    for (int k = 0; k < MAXC; ++k) {
+      const int kc = min(c + 4 * k, nch - 1);
+      kr[U][k] = load_chunk(kbase + int64_t(rc) * p.kc_sr + kc * EPC);
+      vr[U][k] = load_chunk(vbase + int64_t(rc) * p.vc_sr + kc * EPC);
+    }
+  };
+  const int row0 = r0 + wave * 16 + rr;
+  fetch(row0, std::integral_constant<int, 0>{});
+  fetch(row0 + 16 * kDecWaves, std::integral_constant<int, 1>{});
+  fetch(row0 + 32 * kDecWaves, std::integral_constant<int, 2>{});
+
   // every split takes part (those at or past S publish an empty partial), so the count of published
   // splits never depends on S
-
   // query: RoPE at S, rounded to the cache dtype
-  const T* q_raw = reinterpret_cast<const T*>(p.p1) + b * p.in_sb + h * D;
   if (tid < half) {
-    const float x0 = E::to_f(q_raw[tid]), x1 = E::to_f(q_raw[tid + half]);
     float o0 = x0, o1 = x1;
     if (p.inv_freq) {
       float sn, cs;
@@ -227,16 +273,10 @@ __global__ void __launch_bounds__(256) relation_decode_kernel(const DecParams p)
     sq[tid] = round_to<T>(o0);
     sq[tid + half] = round_to<T>(o1);
   }
-  for (int d = D + tid; d < DP; d += 256) sq[d] = 0.f;
+  for (int d = D + tid; d < DP; d += kDecThreads) sq[d] = 0.f;
   __syncthreads();
 
-  const int r0 = split * p.rps;
-  const int r1 = min(S, r0 + p.rps);
-  const T* kbase = reinterpret_cast<const T*>(p.kc) + b * p.kc_sb + h * p.kc_sh;
-  const T* vbase = reinterpret_cast<const T*>(p.vc) + b * p.vc_sb + h * p.vc_sh;
-  const int rr = lane >> 2, c = lane & 3;
-  const int nch = D / EPC;
-  const float c2 = p.scale * kLog2e;
+  const int r1 = min(S, r0 + rps);  // valid rows of this split: [r0, r1)
   float qv[MAXC][EPC];
 #pragma unroll
   for (int k = 0; k < MAXC; ++k)
@@ -250,39 +290,16 @@ __global__ void __launch_bounds__(256) relation_decode_kernel(const DecParams p)
 #pragma unroll
     for (int j = 0; j < EPC; ++j) z[k][j] = 0.f;
 
-  Chunk kr[MAXC], vr[MAXC];
-  auto fetch = [&](int row) {
+  auto consume = [&](int cur, auto u) {
+    constexpr int U = decltype(u)::value;
+    float dot2[2] = {0.f, 0.f};  // two independent chains
 #pragma unroll
     for (int k = 0; k < MAXC; ++k) {
-      const int kc = c + 4 * k;
-      if (row < r1 && kc < nch) {
-        kr[k] = load_chunk(kbase + int64_t(row) * p.kc_sr + kc * EPC);
-        vr[k] = load_chunk(vbase + int64_t(row) * p.vc_sr + kc * EPC);
-      } else {
-        kr[k] = zero_chunk();
-        vr[k] = zero_chunk();
-      }
-    }
-  };
-  int row = r0 + wave * 16 + rr;
-  fetch(row);
-  for (int base = r0; base < r1; base += 64) {
-    Chunk kc_[MAXC], vc_[MAXC];
+      const T* e = reinterpret_cast<const T*>(&kr[U][k]);
 #pragma unroll
-    for (int k = 0; k < MAXC; ++k) {
-      kc_[k] = kr[k];
-      vc_[k] = vr[k];
+      for (int j = 0; j < EPC; ++j) dot2[j & 1] = fmaf(E::to_f(e[j]), qv[k][j], dot2[j & 1]);
     }
-    const int cur = row;
-    row += 64;
-    if (base + 64 < r1) fetch(row);  // prefetch the next step while this one computes
-    float dot = 0.f;
-#pragma unroll
-    for (int k = 0; k < MAXC; ++k) {
-      const T* e = reinterpret_cast<const T*>(&kc_[k]);
-#pragma unroll
-      for (int j = 0; j < EPC; ++j) dot = fmaf(E::to_f(e[j]), qv[k][j], dot);
-    }
+    float dot = dot2[0] + dot2[1];
     dot += __shfl_xor(dot, 1, 64);
     dot += __shfl_xor(dot, 2, 64);
     if (cur < r1) {
@@ -301,11 +318,26 @@ __global__ void __launch_bounds__(256) relation_decode_kernel(const DecParams p)
       l += pr;
 #pragma unroll
       for (int k = 0; k < MAXC; ++k) {
-        const T* e = reinterpret_cast<const T*>(&vc_[k]);
+        const T* e = reinterpret_cast<const T*>(&vr[U][k]);
 #pragma unroll
         for (int j = 0; j < EPC; ++j) z[k][j] = fmaf(pr, E::to_f(e[j]), z[k][j]);
       }
     }
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  constexpr int RS = 16 * kDecWaves;  // rows per step of the workgroup
+  for (int row = row0; row - wave * 16 - rr < r1; row += 4 * RS) {
+    fetch(row + 3 * RS, I3{});
+    consume(row, I0{});
+    fetch(row + 4 * RS, I0{});
+    consume(row + RS, I1{});
+    fetch(row + 5 * RS, I1{});
+    consume(row + 2 * RS, I2{});
+    fetch(row + 6 * RS, I2{});
+    consume(row + 3 * RS, I3{});
   }
   // merge the 16 row groups of the wave (lanes with equal c hold the same chunks)
 #pragma unroll
@@ -336,27 +368,27 @@ __global__ void __launch_bounds__(256) relation_decode_kernel(const DecParams p)
     }
   }
   __syncthreads();
-  // merge the 4 waves -> this split's partial
+  // merge the waves -> this split's partial
   {
-    float mw[4];
+    float mw[kDecWaves];
     float M = kNegInf;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
+    for (int w = 0; w < kDecWaves; ++w) {
       mw[w] = red[w * (DP + 2)];
       M = fmaxf(M, mw[w]);
     }
     const float Ms = M == kNegInf ? 0.f : M;
     float* part = p.part + (int64_t(bh) * p.nsplit + split) * (D + 2);
-    for (int d = tid; d < D; d += 256) {
+    for (int d = tid; d < D; d += kDecThreads) {
       float zs = 0.f;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) zs += red[w * (DP + 2) + 2 + d] * fexp2(mw[w] - Ms);
+      for (int w = 0; w < kDecWaves; ++w) zs += red[w * (DP + 2) + 2 + d] * fexp2(mw[w] - Ms);
       store_coherent(part + 2 + d, zs);
     }
     if (tid == 0) {
       float L = 0.f;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) L += red[w * (DP + 2) + 1] * fexp2(mw[w] - Ms);
+      for (int w = 0; w < kDecWaves; ++w) L += red[w * (DP + 2) + 1] * fexp2(mw[w] - Ms);
       store_coherent(part, M);
       store_coherent(part + 1, L);
     }
@@ -374,25 +406,30 @@ __global__ void __launch_bounds__(256) relation_decode_kernel(const DecParams p)
   decode_finish<T, DP>(p, bh, S64);
 }
 
-// rows per split: a multiple of 64 chosen so that about 320 workgroups cover a full cache
-static void decode_shape(const mote_relation_decode_args* a, int& rps, int& nsplit) {
+// Splits per head: about three workgroups per CU over the whole batch (a multiple of the CU count,
+// so no CU runs one more than the others), but no split shorter than 512 rows at full capacity
+// (every split costs a published partial, a completion count and a share of the merge).
+static int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    return 256;
+  return cus;
+}
+static int decode_splits(const mote_relation_decode_args* a) {
   const int64_t BH = int64_t(a->B) * a->H;
-  int64_t mult = (BH * ((a->capacity + 63) / 64) + 319) / 320;
-  if (mult < 1) mult = 1;
-  rps = int(64 * mult);
-  nsplit = (a->capacity + rps - 1) / rps;
-  while (nsplit > kDecMaxSplits) {
-    rps += 64;
-    nsplit = (a->capacity + rps - 1) / rps;
-  }
+  int64_t n = (3 * int64_t(device_cus()) + BH - 1) / BH;
+  const int64_t by_rows = (int64_t(a->capacity) + 511) / 512;
+  if (n > by_rows) n = by_rows;
+  if (n > kDecMaxSplits) n = kDecMaxSplits;
+  return int(n < 1 ? 1 : n);
 }
 
 struct DecWs {
   size_t part, cnt, cnt_seq, total;
 };
 static DecWs decode_ws(const mote_relation_decode_args* a) {
-  int rps, nsplit;
-  decode_shape(a, rps, nsplit);
+  const int nsplit = decode_splits(a);
   const size_t BH = size_t(a->B) * a->H;
   DecWs w;
   w.part = 0;
@@ -422,7 +459,7 @@ int launch_decode(const mote_relation_decode_args* a, hipStream_t stream) {
   p.vc = a->cache_info.data; p.vc_sb = a->cache_info.stride_b; p.vc_sh = a->cache_info.stride_h; p.vc_sr = a->cache_info.stride_r;
   p.y = a->y; p.y_sb = a->y_sb; p.g = a->g;
   const size_t BH = size_t(a->B) * a->H;
-  decode_shape(a, p.rps, p.nsplit);
+  p.nsplit = decode_splits(a);
   const DecWs w = decode_ws(a);
   char* ws = reinterpret_cast<char*>(a->workspace);
   p.part = reinterpret_cast<float*>(ws + w.part);
@@ -436,7 +473,7 @@ int launch_decode(const mote_relation_decode_args* a, hipStream_t stream) {
   const int DP = padded_dim(a->D);
 #define MOTE_DEC_LAUNCH(T_, DP_)                                                                               \
   do {                                                                                                       \
-    hipLaunchKernelGGL((relation_decode_kernel<T_, DP_>), dim3(grid), dim3(256), shmem, stream, p);          \
+    hipLaunchKernelGGL((relation_decode_kernel<T_, DP_>), dim3(grid), dim3(kDecThreads), shmem, stream, p);          \
   } while (0)
   if (a->dtype == MOTE_BF16) {
     switch (DP) {
