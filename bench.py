@@ -408,6 +408,7 @@ def main():
                 "avg_S": round(v["avg_S"], 1), "step_GBs": round(v["gbs"], 1),
                 "step_frac_hbm": round(v["gbs"] / PEAK_HBM_GBS, 4), "kernel_us": round(v["kernel_us"], 2),
                 "kernel_GBs": round(v["kernel_gbs"], 1), "kernel_frac_hbm": round(v["kernel_gbs"] / PEAK_HBM_GBS, 4),
+                "traffic": measured_traffic(f"relation_decode_kernel_{k}"),
                 "cache_copies_rotated": v["copies"]}
             for k, v in dec.items()}
     if cpu is not None:
