@@ -1,28 +1,32 @@
 // One decode step of one Relation layer (mote/infer/graph.py:151-187), one launch.
 //
 // Grid: nsplit x (B*H) workgroups, block id = split * (B*H) + head index; nsplit is a host choice
-// from the shape only (about three workgroups per CU over the batch, no split shorter than 512 rows
-// at full capacity), so the launch can be captured in a HIP graph. On the device each head's S past
-// rows are cut into nsplit equal runs (multiples of the 64-row step) from S itself, so the splits
-// stay balanced as S grows. Each workgroup (4 waves; a wave reads 16 rows per step, 4 lanes per row,
-// 16-byte loads of P2 and I~, with a ring of four register sets keeping three steps of loads in
-// flight) computes U_j = <q, P2_j> / sqrt(D), e_j = SiLU(U_j) in log2 units and an online softmax
-// per row group (running max raised lazily, by more than 2^8 only), merges its row groups and waves,
-// and publishes (max, l, z[D]).
+// from the shape only, so the launch can be captured in a HIP graph. Each head's cache is read in
+// steps of 64 rows (4 waves, 16 rows per wave, 4 lanes per row, 16-byte loads of P2 and I~), and
+// the steps are dealt to the splits round-robin: split s takes steps s, s + nsplit, s + 2 nsplit, ...
+// Two things follow. The addresses of a split's first steps do not depend on the position S, so
+// the first three steps of loads are issued at the very start, while S and the new row are still
+// in flight; and for every S the splits' step counts differ by at most one. A ring of four register
+// sets keeps three steps of loads in flight while one step computes U_j = <q, P2_j> / sqrt(D),
+// e_j = SiLU(U_j) in log2 units and an online softmax per row group (running max raised lazily, by
+// more than 2^8 only).
 //
-// Publication without a device-scope fence (which on gfx950 writes back the XCD's whole L2): the
-// partial goes out with agent-coherent stores, the wave waits for their completion, and one atomic
-// add per workgroup counts the head's splits. Every split counts, rows or not, so the count never
-// depends on S. The workgroup that brings the count to nsplit reads all partials back with
-// agent-coherent loads and finishes the head: merge in a fixed order, the Self score from the new
-// row, g = sigmoid(LSE - lam ln(S+1) - S_self), Y = (1-g) I~_S + g z/l, the append of the new P2 / I~
-// row at S, and the reset of the counter. A second counter per sequence picks the last head to
-// finish; with MOTE_DECODE_ADVANCE it adds 1 to S[b]: by then every workgroup of the sequence has
-// read S[b]. Counters start at zero (the workspace is zeroed once) and every call leaves them zero.
+// Merge within the workgroup through LDS: the workgroup's largest running max M, every row group
+// rescaled to it, the 64 row groups' z written as rows of an LDS table and summed per column in a
+// fixed order. The split publishes (M, l, z[D]) with agent-coherent stores, waits for their
+// completion, then counts itself with one atomic add on its head's counter (each counter on a
+// cache line of its own: counters that share a line serialise every split of every head). Every
+// split counts, rows or not, so the count never depends on S. The workgroup that brings the count
+// to nsplit reads all partials back with agent-coherent loads (one batch) and finishes the head:
+// merge in a fixed order, the Self score from the new row, g = sigmoid(LSE - lam ln(S+1) - S_self),
+// Y = (1-g) I~_S + g z/l, the append of the new P2 / I~ row at S and the reset of the counter. A
+// second counter per sequence picks the last head to finish; with MOTE_DECODE_ADVANCE it adds 1 to
+// S[b]: by then every workgroup of the sequence has read S[b]. Counters start at zero (the
+// workspace is zeroed once) and every call leaves them zero.
 //
-// The query is RoPE'd at S and rounded to the cache dtype (graph.py:158-172) by every workgroup; the
-// new P2 row gets the same rotation and I~ the Givens rotation with its partner head's raw row.
-// Bandwidth-bound by design: no MFMA, wavefront reductions only.
+// The new rows (graph.py:158-172) are computed by every workgroup in its prologue, under the
+// latency of the first loads: the query and the new P2 row RoPE'd at S, I~ Givens-rotated with its
+// partner head's raw row, all rounded to the cache dtype. Bandwidth-bound by design: no MFMA.
 #include <type_traits>
 
 #include "common.hpp"
@@ -32,8 +36,9 @@ namespace mote {
 
 struct DecParams {
   const float* lam;
-  const float* inv_freq;
+  const float* inv_freq;  // never null: without RoPE / Givens the launcher points both at lam
   const float* theta;
+  int rope, givens;       // whether inv_freq / theta are the real tables
   int64_t* S;
   const void* p1;
   const void* p2;
@@ -45,15 +50,17 @@ struct DecParams {
   int64_t y_sb;
   float* g;
   float* part;        // [BH][nsplit][D + 2]  (max, l, z)
-  int* cnt;           // [BH] splits published in this call (zero between calls)
-  int* cnt_seq;       // [B] heads finished in this call (zero between calls)
+  int* cnt;           // [BH] splits published in this call, kDecCntStride ints apart (zero between calls)
+  int* cnt_seq;       // [B] heads finished in this call, kDecCntStride ints apart (zero between calls)
   int B, H, D, cap, parity, flags, nsplit;
   float scale, tau_inv;
 };
 
-constexpr int kDecMaxSplits = 120;  // partials one merge holds in LDS (D <= 128: at most 62 KB)
-constexpr int kDecWaves = 4;  // waves per workgroup: 16 rows each per step (8 and 16 measured slower)
+constexpr int kDecMaxSplits = 64;   // the merge gives every split one lane of a wave
+constexpr int kDecWaves = 4;        // waves per workgroup
 constexpr int kDecThreads = 64 * kDecWaves;
+constexpr int kDecRows = 16 * kDecWaves;  // rows of one step
+constexpr int kDecCntStride = 64;   // ints between two completion counters: 256 bytes
 
 __device__ __forceinline__ void store_coherent(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -67,144 +74,20 @@ __device__ __forceinline__ float round_to(float x) {
   return Elem<T>::to_f(Elem<T>::from_f(x));
 }
 
-// ------------------------------------------------------------------------------------------------
-// finish of a head by the last of its workgroups: merge, epilogue, append
-// ------------------------------------------------------------------------------------------------
-template <typename T, int DP>
-__device__ __forceinline__ void decode_finish(const DecParams& p, int bh, int64_t S64) {
-  using E = Elem<T>;
-  __shared__ float sq[DP];
-  __shared__ float knew[DP];
-  __shared__ float inew[DP];
-  __shared__ float sred[4];
-  __shared__ float sML[2];
-  extern __shared__ float spart[];  // [nsplit][D + 2], then the split weights [nsplit]
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int b = bh / p.H, h = bh % p.H;
-  const int D = p.D, half = D / 2;
-  const int stride = D + 2;
-  const bool bad = S64 < 0 || S64 >= p.cap;
-  const int S = bad ? 0 : int(S64);
-  const int nact = p.nsplit;
-  float* wsp = spart + nact * stride;
-  const float* pb = p.part + int64_t(bh) * p.nsplit * stride;
-  for (int i = tid; i < nact * stride; i += kDecThreads) spart[i] = load_coherent(pb + i);
-  // new rows: query and P2 RoPE'd at S, I~ Givens'd with its partner head's raw row
-  const T* q_raw = reinterpret_cast<const T*>(p.p1) + b * p.in_sb + h * D;
-  const T* k_raw = reinterpret_cast<const T*>(p.p2) + b * p.in_sb + h * D;
-  const T* i_raw = reinterpret_cast<const T*>(p.info) + b * p.in_sb + h * D;
-  if (tid < half) {
-    float cs = 1.f, sn = 0.f;
-    if (p.inv_freq) {
-      sincosf((float)S * p.inv_freq[tid], &sn, &cs);
-      cs = round_to<T>(cs);
-      sn = round_to<T>(sn);
-    }
-    const float q0 = E::to_f(q_raw[tid]), q1 = E::to_f(q_raw[tid + half]);
-    const float k0 = E::to_f(k_raw[tid]), k1 = E::to_f(k_raw[tid + half]);
-    sq[tid] = round_to<T>(q0 * cs - q1 * sn);
-    sq[tid + half] = round_to<T>(q1 * cs + q0 * sn);
-    knew[tid] = round_to<T>(k0 * cs - k1 * sn);
-    knew[tid + half] = round_to<T>(k1 * cs + k0 * sn);
-  }
-  if (tid < D) {
-    const float self = E::to_f(i_raw[tid]);
-    float out = self;
-    if (p.theta) {
-      int pair, other;
-      bool first;
-      if (p.parity == 0) {
-        pair = h >> 1;
-        first = (h & 1) == 0;
-        other = first ? h + 1 : h - 1;
-      } else if (h & 1) {
-        first = true;
-        pair = h >> 1;
-        other = (h + 1) % p.H;
-      } else {
-        first = false;
-        other = (h + p.H - 1) % p.H;
-        pair = other >> 1;
-      }
-      float sn, cs;
-      sincosf(p.theta[pair], &sn, &cs);
-      cs = round_to<T>(cs);
-      sn = round_to<T>(sn);
-      const float oth = E::to_f(reinterpret_cast<const T*>(p.info)[b * p.in_sb + other * D + tid]);
-      out = first ? (cs * self - sn * oth) : (sn * oth + cs * self);
-    }
-    inew[tid] = round_to<T>(out);
-  }
-  __syncthreads();
-  // split weights 2^(m_s - M) and L = sum_s l_s 2^(m_s - M): wave 0, lanes over splits (fixed order)
-  if (wave == 0) {
-    float mx = kNegInf;
-    for (int s = lane; s < nact; s += 64) mx = fmaxf(mx, spart[s * stride]);
-#pragma unroll
-    for (int msk = 32; msk >= 1; msk >>= 1) mx = fmaxf(mx, __shfl_xor(mx, msk, 64));
-    const float Ms = mx == kNegInf ? 0.f : mx;
-    float ls = 0.f;
-    for (int s = lane; s < nact; s += 64) {
-      const float w = fexp2(spart[s * stride] - Ms);
-      wsp[s] = w;
-      ls += spart[s * stride + 1] * w;
-    }
-#pragma unroll
-    for (int msk = 32; msk >= 1; msk >>= 1) ls += __shfl_xor(ls, msk, 64);
-    if (lane == 0) {
-      sML[0] = Ms;
-      sML[1] = ls;
-    }
-  } else if (wave == 1) {
-    // Self score U_SS = <q, P2_S> / sqrt(D)
-    float u = 0.f;
-    for (int d = lane; d < D; d += 64) u = fmaf(sq[d], knew[d], u);
-#pragma unroll
-    for (int msk = 32; msk >= 1; msk >>= 1) u += __shfl_xor(u, msk, 64);
-    if (lane == 0) sred[0] = u;
-  }
-  __syncthreads();
-  const float Ms = sML[0], L = sML[1];
-  const float sself = sigmoid_acc(sred[0] * p.scale * p.tau_inv);
-  const bool has = L > 0.f;
-  const float lse = has ? (Ms + __log2f(L)) * kLn2 : kNegInf;
-  const float gate = has ? sigmoid_acc(lse - (*p.lam) * logf((float)S + 1.0f) - sself) : 0.f;
-  const float invL = has ? 1.0f / L : 0.f;
-  T* y = reinterpret_cast<T*>(p.y) + b * p.y_sb + h * D;
-  T* kw = reinterpret_cast<T*>(p.kc) + b * p.kc_sb + h * p.kc_sh + int64_t(S) * p.kc_sr;
-  T* vw = reinterpret_cast<T*>(p.vc) + b * p.vc_sb + h * p.vc_sh + int64_t(S) * p.vc_sr;
-  for (int d = tid; d < D; d += kDecThreads) {
-    float zsum = 0.f;
-#pragma unroll 8
-    for (int s = 0; s < nact; ++s) zsum = fmaf(spart[s * stride + 2 + d], wsp[s], zsum);
-    const float yv = (1.0f - gate) * inew[d] + gate * zsum * invL;
-    y[d] = E::from_f(bad ? __builtin_nanf("") : yv);
-    if (!bad) {
-      kw[d] = E::from_f(knew[d]);
-      vw[d] = E::from_f(inew[d]);
-    }
-  }
-  if (tid == 0) {
-    p.g[bh] = bad ? __builtin_nanf("") : gate;
-    __hip_atomic_store(p.cnt + bh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // the last head of the sequence: every workgroup of the sequence has read S[b] by now
-    const int before = __hip_atomic_fetch_add(p.cnt_seq + b, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (before == p.H - 1) {
-      __hip_atomic_store(p.cnt_seq + b, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (p.flags & MOTE_DECODE_ADVANCE) p.S[b] = S64 + 1;
-    }
-  }
-}
-
 template <typename T, int DP>
 __global__ void __launch_bounds__(kDecThreads)
 relation_decode_kernel(const DecParams p) {
   using E = Elem<T>;
   constexpr int EPC = 16 / sizeof(T);
   constexpr int MAXC = (DP / EPC + 3) / 4;  // 16-byte chunks per lane (lane c owns chunks c, c+4, ...)
-  __shared__ float sq[DP];
-  __shared__ float red[kDecWaves * (DP + 2)];
+  constexpr int ZS = DP + 4;                // LDS row of one row group's z (16-byte aligned)
+  __shared__ __align__(16) float zred[kDecRows * ZS];  // row-group z, then the head's partials
+  __shared__ float sq[DP], knew[DP], inew[DP];
+  __shared__ float csum[2][DP];
+  __shared__ float sm[kDecWaves], sl[kDecWaves];
+  __shared__ float wsp[kDecMaxSplits];
+  __shared__ float sML[3];
+  __shared__ int s_last;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int BH = p.B * p.H;
@@ -212,39 +95,54 @@ relation_decode_kernel(const DecParams p) {
   const int split = blockIdx.x / BH;
   const int b = bh / p.H, h = bh % p.H;
   const int D = p.D, half = D / 2;
-  // Order of the prologue: the raw query loads, then the first NR - 1 cache steps, and only then the
-  // position S (the split's rows do not depend on S, only where its valid rows end), the RoPE of the
-  // query at S and the masks: the cache loads are in flight while S and the query arrive.
-  const T* q_raw = reinterpret_cast<const T*>(p.p1) + b * p.in_sb + h * D;
-  const int qi = min(tid, half - 1);
-  const float x0 = E::to_f(q_raw[qi]), x1 = E::to_f(q_raw[qi + half]);
-
-  // The head's S past rows are cut into nsplit equal runs (a multiple of the 64-row step) from S
-  // itself, so every split carries the same load whatever S is; the grid depends only on the shape.
-  const int64_t S64 = p.S[b];
-  const bool bad = S64 < 0 || S64 >= p.cap;
-  const int S = bad ? 0 : int(S64);
-  const int rps = ((S + p.nsplit - 1) / p.nsplit + 63) & ~63;
-  const int r0 = split * rps;
-  const int rf = min(p.cap, r0 + rps);  // rows this split may load (the cache holds them all)
+  const int nch = D / EPC;
+  const int nsp = p.nsplit;
+  const int rr = lane >> 2, c = lane & 3;
+  const int roff = wave * 16 + rr;  // this lane's row within a step
   const T* kbase = reinterpret_cast<const T*>(p.kc) + b * p.kc_sb + h * p.kc_sh;
   const T* vbase = reinterpret_cast<const T*>(p.vc) + b * p.vc_sb + h * p.vc_sh;
-  const int rr = lane >> 2, c = lane & 3;
-  const int nch = D / EPC;
-  const float c2 = p.scale * kLog2e;
 
-  // A ring of NR register sets, one 64-row step each (16 rows per wave, 4 lanes per row): the loads
-  // of the next NR - 1 steps are in flight while a step computes, and the loop is unrolled by NR so
-  // every set is named by a constant (a copy between sets would make the compiler wait for the
-  // newest loads before issuing the next ones).
-  constexpr int NR = 4;
-  Chunk kr[NR][MAXC], vr[NR][MAXC];
-  // Loads are unconditional (rows past the split and chunks past the head dim read a clamped, valid
-  // address whose values the math ignores): a load under a lane condition would hide it from the
-  // compiler's count of outstanding loads, and it would then wait for every one of them.
-  auto fetch = [&](int row, auto u) {
+  // The small loads go first and unconditionally (lanes past the row read a clamped element):
+  // loads complete in order, so the new rows can be computed while the cache loads issued after
+  // them are still in flight. Wave 0 takes the query and P2 halves, waves 2-3 the I~ row and its
+  // Givens partner: pairing by layer parity (relation.py:150-174), even layers (0,1),(2,3)...,
+  // odd layers (1,2),...,(H-1,0); the first head of a pair gets c a - s b, the second s a + c b.
+  // lam and theta are read per lane through an index the compiler cannot see is zero: as scalar
+  // loads they would be waited for at the first barrier (whose wait for the LDS writes also waits
+  // for every scalar load in flight).
+  int vzero;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(vzero));
+  const float lam = p.lam[vzero];
+  // Written as integer arithmetic: the compiler turns selects here into branches, and a branch
+  // would split the kernel-argument loads over two waits.
+  const int odd = h & 1, par = p.parity;
+  const bool first = (odd ^ par) == 0;
+  int nb = h + 2 * odd - 1;  // odd layers: h + 1 for odd h, h - 1 for even h, modulo H
+  nb += int(nb < 0) * p.H - int(nb >= p.H) * p.H;
+  const int other = (h ^ 1) + par * (nb - (h ^ 1));
+  const int pair = (h >> 1) + (par & (odd ^ 1)) * ((other >> 1) - (h >> 1));
+  const float th = p.theta[(p.givens ? pair : 0) + vzero];
+  const int qi = min(tid, half - 1);
+  const int di = min(tid & 127, D - 1);
+  const T* in_b = reinterpret_cast<const T*>(p.p1) + b * p.in_sb + h * D;
+  const float q0 = E::to_f(in_b[qi]), q1 = E::to_f(in_b[qi + half]);
+  const T* kn_b = reinterpret_cast<const T*>(p.p2) + b * p.in_sb + h * D;
+  const float k0 = E::to_f(kn_b[qi]), k1 = E::to_f(kn_b[qi + half]);
+  const T* i_raw = reinterpret_cast<const T*>(p.info) + b * p.in_sb;
+  const float iself = E::to_f(i_raw[h * D + di]), ioth = E::to_f(i_raw[other * D + di]);
+  const float invf = p.inv_freq[p.rope ? qi : 0];
+
+  // A ring of four register sets, one step each, named by constants (a copy between sets would
+  // make the compiler wait for the newest loads before issuing the next ones). Loads are
+  // unconditional: rows are clamped to rlim (the cache's last row until S is known, then the
+  // split's last valid row, so loads past the split re-read lines already fetched), and chunks
+  // past the head dim to its last chunk; the math ignores both. A load under a lane condition would
+  // hide from the compiler's count of outstanding loads, and it would then wait for all of them.
+  Chunk kr[4][MAXC], vr[4][MAXC];
+  int rlim = p.cap - 1;
+  auto fetch = [&](int j, auto u) {
     constexpr int U = decltype(u)::value;
-    const int rc = max(0, min(row, rf - 1));
+    const int rc = min((split + j * nsp) * kDecRows + roff, rlim);
 #pragma unroll
     for (int k = 0; k < MAXC; ++k) {
       const int kc = min(c + 4 * k, nch - 1);
@@ -252,31 +150,47 @@ relation_decode_kernel(const DecParams p) {
       vr[U][k] = load_chunk(vbase + int64_t(rc) * p.vc_sr + kc * EPC);
     }
   };
-  const int row0 = r0 + wave * 16 + rr;
-  fetch(row0, std::integral_constant<int, 0>{});
-  fetch(row0 + 16 * kDecWaves, std::integral_constant<int, 1>{});
-  fetch(row0 + 32 * kDecWaves, std::integral_constant<int, 2>{});
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  fetch(0, I0{});
+  fetch(1, I1{});
+  fetch(2, I2{});
 
-  // every split takes part (those at or past S publish an empty partial), so the count of published
-  // splits never depends on S
-  // query: RoPE at S, rounded to the cache dtype
+  const int64_t S64 = p.S[b];  // after the cache loads: their addresses do not depend on it
+  const bool bad = S64 < 0 || S64 >= p.cap;
+  const int S = bad ? 0 : int(S64);
+
+  // the new rows at S, computed on every lane (a use under a lane condition would let the compiler
+  // sink the small loads behind the cache loads); only the owning lanes write them to LDS
+  float cs, sn;
+  sincosf((float)S * invf, &sn, &cs);
+  cs = p.rope ? round_to<T>(cs) : 1.f;
+  sn = p.rope ? round_to<T>(sn) : 0.f;
+  const float rq0 = round_to<T>(q0 * cs - q1 * sn), rq1 = round_to<T>(q1 * cs + q0 * sn);
+  const float rk0 = round_to<T>(k0 * cs - k1 * sn), rk1 = round_to<T>(k1 * cs + k0 * sn);
+  float gc, gs;
+  sincosf(th, &gs, &gc);
+  gc = p.givens ? round_to<T>(gc) : 1.f;
+  gs = p.givens ? round_to<T>(gs) : 0.f;
+  const float rin = round_to<T>(p.givens ? (first ? (gc * iself - gs * ioth) : (gs * ioth + gc * iself)) : iself);
   if (tid < half) {
-    float o0 = x0, o1 = x1;
-    if (p.inv_freq) {
-      float sn, cs;
-      sincosf((float)S * p.inv_freq[tid], &sn, &cs);
-      cs = round_to<T>(cs);
-      sn = round_to<T>(sn);
-      o0 = x0 * cs - x1 * sn;
-      o1 = x1 * cs + x0 * sn;
-    }
-    sq[tid] = round_to<T>(o0);
-    sq[tid + half] = round_to<T>(o1);
+    sq[tid] = rq0;
+    sq[tid + half] = rq1;
+    knew[tid] = rk0;
+    knew[tid + half] = rk1;
+  } else if (tid >= 128 && tid < 128 + D) {
+    inew[tid - 128] = rin;
   }
   for (int d = D + tid; d < DP; d += kDecThreads) sq[d] = 0.f;
   __syncthreads();
 
-  const int r1 = min(S, r0 + rps);  // valid rows of this split: [r0, r1)
+  // this split's steps: s + j nsplit for j < ns, rows below S
+  const int nst = (S + kDecRows - 1) / kDecRows;
+  const int ns = nst > split ? (nst - split + nsp - 1) / nsp : 0;
+  rlim = ns > 0 ? min((split + (ns - 1) * nsp) * kDecRows + kDecRows, S) - 1 : 0;
+
   float qv[MAXC][EPC];
 #pragma unroll
   for (int k = 0; k < MAXC; ++k)
@@ -290,8 +204,12 @@ relation_decode_kernel(const DecParams p) {
 #pragma unroll
     for (int j = 0; j < EPC; ++j) z[k][j] = 0.f;
 
-  auto consume = [&](int cur, auto u) {
+  const float c2 = p.scale * kLog2e;
+  // Steps past the split are skipped whole (ns is uniform): their loads, clamped to lines already
+  // fetched, are never waited for.
+  auto consume = [&](int jstep, auto u) {
     constexpr int U = decltype(u)::value;
+    if (jstep >= ns) return;
     float dot2[2] = {0.f, 0.f};  // two independent chains
 #pragma unroll
     for (int k = 0; k < MAXC; ++k) {
@@ -302,7 +220,8 @@ relation_decode_kernel(const DecParams p) {
     float dot = dot2[0] + dot2[1];
     dot += __shfl_xor(dot, 1, 64);
     dot += __shfl_xor(dot, 2, 64);
-    if (cur < r1) {
+    const int row = (split + jstep * nsp) * kDecRows + roff;
+    if (row < S) {
       const float u2 = dot * c2;
       const float ev = u2 * frcp(1.0f + fexp2(-u2));
       if (ev > m + kRescale) {
@@ -324,71 +243,61 @@ relation_decode_kernel(const DecParams p) {
       }
     }
   };
-  using I0 = std::integral_constant<int, 0>;
-  using I1 = std::integral_constant<int, 1>;
-  using I2 = std::integral_constant<int, 2>;
-  using I3 = std::integral_constant<int, 3>;
-  constexpr int RS = 16 * kDecWaves;  // rows per step of the workgroup
-  for (int row = row0; row - wave * 16 - rr < r1; row += 4 * RS) {
-    fetch(row + 3 * RS, I3{});
-    consume(row, I0{});
-    fetch(row + 4 * RS, I0{});
-    consume(row + RS, I1{});
-    fetch(row + 5 * RS, I1{});
-    consume(row + 2 * RS, I2{});
-    fetch(row + 6 * RS, I2{});
-    consume(row + 3 * RS, I3{});
+  for (int j = 0; j < ns; j += 4) {
+    fetch(j + 3, I3{});
+    consume(j, I0{});
+    fetch(j + 4, I0{});
+    consume(j + 1, I1{});
+    fetch(j + 5, I1{});
+    consume(j + 2, I2{});
+    fetch(j + 6, I2{});
+    consume(j + 3, I3{});
   }
-  // merge the 16 row groups of the wave (lanes with equal c hold the same chunks)
+
+  // ---- merge of the 64 row groups (lanes of one row group hold the same m and l) ----
+  float mw = m;
 #pragma unroll
-  for (int msk = 4; msk <= 32; msk <<= 1) {
-    const float mo = __shfl_xor(m, msk, 64);
-    const float lo = __shfl_xor(l, msk, 64);
-    const float mn = fmaxf(m, mo);
-    const float ms = mn == kNegInf ? 0.f : mn;
-    const float a = fexp2(m - ms), ao = fexp2(mo - ms);
-    l = l * a + lo * ao;
+  for (int msk = 4; msk <= 32; msk <<= 1) mw = fmaxf(mw, __shfl_xor(mw, msk, 64));
+  if (lane == 0) sm[wave] = mw;
+  __syncthreads();
+  float M = sm[0];
 #pragma unroll
-    for (int k = 0; k < MAXC; ++k)
+  for (int w = 1; w < kDecWaves; ++w) M = fmaxf(M, sm[w]);
+  const float a = fexp2(m - (M == kNegInf ? 0.f : M));  // 0 for a row group without rows
+  float lw = l * a;
 #pragma unroll
-      for (int j = 0; j < EPC; ++j) z[k][j] = z[k][j] * a + __shfl_xor(z[k][j], msk, 64) * ao;
-    m = mn;
+  for (int msk = 4; msk <= 32; msk <<= 1) lw += __shfl_xor(lw, msk, 64);
+  if (lane == 0) sl[wave] = lw;
+  float* zg = zred + roff * ZS;
+#pragma unroll
+  for (int k = 0; k < MAXC; ++k) {
+    const int kc = c + 4 * k;
+    if (kc < nch)
+#pragma unroll
+      for (int j = 0; j < EPC; ++j) zg[kc * EPC + j] = z[k][j] * a;
   }
-  if (rr == 0) {
+  __syncthreads();
+  {
+    const int d = tid & 127, hf = tid >> 7;  // two halves of 32 row groups per column
+    if (d < D) {
+      const float* col = zred + hf * 32 * ZS + d;
+      float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-    for (int k = 0; k < MAXC; ++k) {
-      const int kc = c + 4 * k;
-      if (kc < nch)
-#pragma unroll
-        for (int j = 0; j < EPC; ++j) red[wave * (DP + 2) + 2 + kc * EPC + j] = z[k][j];
-    }
-    if (c == 0) {
-      red[wave * (DP + 2)] = m;
-      red[wave * (DP + 2) + 1] = l;
+      for (int g2 = 0; g2 < 32; g2 += 2) {
+        s0 += col[g2 * ZS];
+        s1 += col[(g2 + 1) * ZS];
+      }
+      csum[hf][d] = s0 + s1;
     }
   }
   __syncthreads();
-  // merge the waves -> this split's partial
   {
-    float mw[kDecWaves];
-    float M = kNegInf;
-#pragma unroll
-    for (int w = 0; w < kDecWaves; ++w) {
-      mw[w] = red[w * (DP + 2)];
-      M = fmaxf(M, mw[w]);
-    }
-    const float Ms = M == kNegInf ? 0.f : M;
-    float* part = p.part + (int64_t(bh) * p.nsplit + split) * (D + 2);
-    for (int d = tid; d < D; d += kDecThreads) {
-      float zs = 0.f;
-#pragma unroll
-      for (int w = 0; w < kDecWaves; ++w) zs += red[w * (DP + 2) + 2 + d] * fexp2(mw[w] - Ms);
-      store_coherent(part + 2 + d, zs);
-    }
+    float* part = p.part + (int64_t(bh) * nsp + split) * (D + 2);
+    if (tid < D) store_coherent(part + 2 + tid, csum[0][tid] + csum[1][tid]);
     if (tid == 0) {
       float L = 0.f;
 #pragma unroll
-      for (int w = 0; w < kDecWaves; ++w) L += red[w * (DP + 2) + 1] * fexp2(mw[w] - Ms);
+      for (int w = 0; w < kDecWaves; ++w) L += sl[w];
       store_coherent(part, M);
       store_coherent(part + 1, L);
     }
@@ -396,19 +305,87 @@ relation_decode_kernel(const DecParams p) {
   // publish: every wave's coherent stores complete, then one count per workgroup
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  __shared__ int s_last;
   if (tid == 0) {
-    const int before = __hip_atomic_fetch_add(p.cnt + bh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = before == p.nsplit - 1;
+    const int before = __hip_atomic_fetch_add(p.cnt + bh * kDecCntStride, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = before == nsp - 1;
   }
   __syncthreads();
   if (!s_last) return;
-  decode_finish<T, DP>(p, bh, S64);
+
+  // ---- the last workgroup of the head: all partials in one batch of loads ----
+  const int np = nsp * (D + 2);
+  const float* pb = p.part + int64_t(bh) * np;
+  constexpr int KP = (kDecMaxSplits * (DP + 2) + kDecThreads - 1) / kDecThreads;
+  float pv[KP];
+#pragma unroll
+  for (int k = 0; k < KP; ++k) pv[k] = load_coherent(pb + min(tid + k * kDecThreads, np - 1));
+#pragma unroll
+  for (int k = 0; k < KP; ++k)
+    if (tid + k * kDecThreads < np) zred[tid + k * kDecThreads] = pv[k];
+  __syncthreads();
+  const int stride = D + 2;
+  if (wave == 0) {
+    // split weights 2^(m_s - Mh) and L = sum_s l_s 2^(m_s - Mh), one split per lane
+    const float ms = lane < nsp ? zred[lane * stride] : kNegInf;
+    float mx = ms;
+#pragma unroll
+    for (int msk = 32; msk >= 1; msk >>= 1) mx = fmaxf(mx, __shfl_xor(mx, msk, 64));
+    const float Mh = mx == kNegInf ? 0.f : mx;
+    const float w = fexp2(ms - Mh);
+    if (lane < nsp) wsp[lane] = w;
+    float ls = lane < nsp ? zred[lane * stride + 1] * w : 0.f;
+#pragma unroll
+    for (int msk = 32; msk >= 1; msk >>= 1) ls += __shfl_xor(ls, msk, 64);
+    if (lane == 0) {
+      sML[0] = Mh;
+      sML[1] = ls;
+    }
+  } else if (wave == 1) {
+    // Self score U_SS = <q, P2_S> / sqrt(D)
+    float u = 0.f;
+    for (int d = lane; d < D; d += 64) u = fmaf(sq[d], knew[d], u);
+#pragma unroll
+    for (int msk = 32; msk >= 1; msk >>= 1) u += __shfl_xor(u, msk, 64);
+    if (lane == 0) sML[2] = u;
+  }
+  __syncthreads();
+  const float Mh = sML[0], L = sML[1];
+  const float sself = sigmoid_acc(sML[2] * p.scale * p.tau_inv);
+  const bool has = L > 0.f;
+  const float lse = has ? (Mh + __log2f(L)) * kLn2 : kNegInf;
+  const float gate = has ? sigmoid_acc(lse - lam * logf((float)S + 1.0f) - sself) : 0.f;
+  const float invL = has ? 1.0f / L : 0.f;
+  T* y = reinterpret_cast<T*>(p.y) + b * p.y_sb + h * D;
+  T* kw = reinterpret_cast<T*>(p.kc) + b * p.kc_sb + h * p.kc_sh + int64_t(S) * p.kc_sr;
+  T* vw = reinterpret_cast<T*>(p.vc) + b * p.vc_sb + h * p.vc_sh + int64_t(S) * p.vc_sr;
+  for (int d = tid; d < D; d += kDecThreads) {
+    float zsum = 0.f;
+#pragma unroll 8
+    for (int s2 = 0; s2 < nsp; ++s2) zsum = fmaf(zred[s2 * stride + 2 + d], wsp[s2], zsum);
+    const float yv = (1.0f - gate) * inew[d] + gate * zsum * invL;
+    y[d] = E::from_f(bad ? __builtin_nanf("") : yv);
+    if (!bad) {
+      kw[d] = E::from_f(knew[d]);
+      vw[d] = E::from_f(inew[d]);
+    }
+  }
+  if (tid == 0) {
+    p.g[bh] = bad ? __builtin_nanf("") : gate;
+    __hip_atomic_store(p.cnt + bh * kDecCntStride, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the last head of the sequence: every workgroup of the sequence has read S[b] by now
+    const int before =
+        __hip_atomic_fetch_add(p.cnt_seq + b * kDecCntStride, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (before == p.H - 1) {
+      __hip_atomic_store(p.cnt_seq + b * kDecCntStride, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (p.flags & MOTE_DECODE_ADVANCE) p.S[b] = S64 + 1;
+    }
+  }
 }
 
-// Splits per head: about three workgroups per CU over the whole batch (a multiple of the CU count,
-// so no CU runs one more than the others), but no split shorter than 512 rows at full capacity
-// (every split costs a published partial, a completion count and a share of the merge).
+// Splits per head: one workgroup per CU over the whole batch (measured at Mote-96M, batch 1 and
+// 16: more splits add completion counts and merge work without speeding up the sweep, fewer leave
+// CUs idle), at least two steps per split at full capacity, and at most one split per lane of the
+// merging wave.
 static int device_cus() {
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
@@ -418,8 +395,8 @@ static int device_cus() {
 }
 static int decode_splits(const mote_relation_decode_args* a) {
   const int64_t BH = int64_t(a->B) * a->H;
-  int64_t n = (3 * int64_t(device_cus()) + BH - 1) / BH;
-  const int64_t by_rows = (int64_t(a->capacity) + 511) / 512;
+  int64_t n = int64_t(device_cus()) / BH;
+  const int64_t by_rows = (int64_t(a->capacity) + 2 * kDecRows - 1) / (2 * kDecRows);
   if (n > by_rows) n = by_rows;
   if (n > kDecMaxSplits) n = kDecMaxSplits;
   return int(n < 1 ? 1 : n);
@@ -431,11 +408,12 @@ struct DecWs {
 static DecWs decode_ws(const mote_relation_decode_args* a) {
   const int nsplit = decode_splits(a);
   const size_t BH = size_t(a->B) * a->H;
+  const size_t line = kDecCntStride * sizeof(int);
   DecWs w;
   w.part = 0;
-  w.cnt = (BH * size_t(nsplit) * size_t(a->D + 2) * sizeof(float) + 255) & ~size_t(255);
-  w.cnt_seq = w.cnt + ((BH * sizeof(int) + 255) & ~size_t(255));
-  w.total = w.cnt_seq + ((size_t(a->B) * sizeof(int) + 255) & ~size_t(255));
+  w.cnt = (BH * size_t(nsplit) * size_t(a->D + 2) * sizeof(float) + line - 1) / line * line;
+  w.cnt_seq = w.cnt + BH * line;
+  w.total = w.cnt_seq + size_t(a->B) * line;
   return w;
 }
 
@@ -453,7 +431,11 @@ int launch_decode(const mote_relation_decode_args* a, hipStream_t stream) {
     return set_error(MOTE_ERR_WORKSPACE, "relation_decode: workspace of %zu bytes, %zu needed", a->workspace_bytes,
                      decode_workspace_bytes(a));
   DecParams p;
-  p.lam = a->lam; p.inv_freq = a->inv_freq; p.theta = a->theta; p.S = a->S;
+  p.lam = a->lam; p.S = a->S;
+  p.rope = a->inv_freq != nullptr;
+  p.givens = a->theta != nullptr;
+  p.inv_freq = p.rope ? a->inv_freq : a->lam;
+  p.theta = p.givens ? a->theta : a->lam;
   p.p1 = a->p1; p.p2 = a->p2; p.info = a->info; p.in_sb = a->in_sb;
   p.kc = a->cache_p2.data; p.kc_sb = a->cache_p2.stride_b; p.kc_sh = a->cache_p2.stride_h; p.kc_sr = a->cache_p2.stride_r;
   p.vc = a->cache_info.data; p.vc_sb = a->cache_info.stride_b; p.vc_sh = a->cache_info.stride_h; p.vc_sr = a->cache_info.stride_r;
@@ -469,11 +451,10 @@ int launch_decode(const mote_relation_decode_args* a, hipStream_t stream) {
   p.scale = 1.0f / sqrtf((float)a->D);
   p.tau_inv = 1.0f / a->tau_s;
   const int grid = int(BH) * p.nsplit;
-  const size_t shmem = size_t(p.nsplit) * (a->D + 3) * sizeof(float);
   const int DP = padded_dim(a->D);
 #define MOTE_DEC_LAUNCH(T_, DP_)                                                                               \
   do {                                                                                                       \
-    hipLaunchKernelGGL((relation_decode_kernel<T_, DP_>), dim3(grid), dim3(kDecThreads), shmem, stream, p);          \
+    hipLaunchKernelGGL((relation_decode_kernel<T_, DP_>), dim3(grid), dim3(kDecThreads), 0, stream, p);          \
   } while (0)
   if (a->dtype == MOTE_BF16) {
     switch (DP) {
