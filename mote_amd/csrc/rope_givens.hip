@@ -23,6 +23,9 @@ struct RopeParams {
   void* o3; int64_t o3_sb, o3_sh, o3_sr;
   const float* inv_freq;
   const float* theta;
+  const float* inv_safe;    // never null: the tables, or any valid fp32 address when absent
+  const float* theta_safe;
+  int rope, givens;
   int B, T, H, D, pos0, parity;
 };
 
@@ -115,7 +118,10 @@ struct RopeBwdParams {
   int64_t dq_sb, dq_sr;
   const float* inv_freq;
   const float* theta;
-  float* partial;  // [B*T, H/2]
+  const float* inv_safe;    // never null: the tables, or any valid fp32 address when absent
+  const float* theta_safe;
+  int rope, givens;
+  float* partial;  // [blocks or rows][H/2]
   int B, T, H, D, pos0, parity;
 };
 
@@ -194,226 +200,254 @@ __global__ void __launch_bounds__(256) rope_givens_bwd_kernel(const RopeBwdParam
   }
 }
 
+// d theta: one block per pair; thread j sums partials j, j + 256, ... (eight loads in flight per
+// batch), then a fixed tree over the block: the order is fixed, so the result is reproducible.
 __global__ void __launch_bounds__(256) sum_partials_kernel(const float* partial, int rows, int npair, float* out) {
-  // one wave per pair (pairs strided over the waves): fixed-order strided sums, then a fixed tree
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int pr = blockIdx.x * 4 + wave; pr < npair; pr += gridDim.x * 4) {
-    float acc = 0.f;
-    for (int r = lane; r < rows; r += 64) acc += partial[int64_t(r) * npair + pr];
+  __shared__ float red[256];
+  const int tid = threadIdx.x, pr = blockIdx.x;
+  float acc = 0.f;
+  for (int base = 0; base < rows; base += 256 * 8) {
+    float v[8];
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
-    if (lane == 0) out[pr] = acc;
+    for (int m = 0; m < 8; ++m) v[m] = partial[int64_t(min(base + m * 256 + tid, rows - 1)) * npair + pr];
+#pragma unroll
+    for (int m = 0; m < 8; ++m)
+      if (base + m * 256 + tid < rows) acc += v[m];
   }
+  red[tid] = acc;
+  __syncthreads();
+  for (int w = 128; w >= 1; w >>= 1) {
+    if (tid < w) red[tid] += red[tid + w];
+    __syncthreads();
+  }
+  if (tid == 0) out[pr] = red[0];
 }
 
 // ------------------------------------------------------------------------------------------------
-// Vectorised kernels (16-byte chunks), used when D/2 is a multiple of the chunk. A block handles
-// kRopeRows rows; each thread loops over (row, unit) pairs: a RoPE unit is one chunk k..k+EPC of
-// the first half of one head, for p1 and p2 together (the angles are shared); a Givens unit is one
-// chunk of both heads of one pair.
+// Streaming kernels (16-byte chunks), used when D/2 is a multiple of the chunk, every view is 16-byte
+// aligned and a [p1 | p2 | I~] row has at most 1024 chunks. A block takes up to kRopeR rows and has
+// one thread per chunk position of the row, so every index of a thread (tensor, head, chunk, partner
+// chunk, output address) is worked out once; per row the thread loads its own chunk and its partner
+// (the other RoPE half of its head, or the same chunk of the Givens partner head; the partner's
+// lines are the neighbouring threads', so they come from L2), and stores one output chunk. Every
+// load of the block is issued before any math (the table value first: loads complete in order), the
+// RoPE factors of the block's rows go through LDS, and the only barrier waits for them.
 // ------------------------------------------------------------------------------------------------
-constexpr int kRopeRows = 8;
+constexpr int kRopeR = 4;       // rows per block, forward (two loads per row in flight)
+constexpr int kRopeRB = 2;      // rows per block, backward (four loads per row in flight)
+constexpr int kRopeMaxCh = 1024;
 
-template <typename T>
-__device__ __forceinline__ void rope_chunk_fwd(const T* x, T* o, int half, int k0, const float* ang_c, const float* ang_s) {
-  using E = Elem<T>;
-  constexpr int EPC = 16 / sizeof(T);
-  const Chunk a = load_chunk(x + k0), b = load_chunk(x + half + k0);
-  const T* ea = reinterpret_cast<const T*>(&a);
-  const T* eb = reinterpret_cast<const T*>(&b);
-  Chunk ra, rb;
-  T* oa = reinterpret_cast<T*>(&ra);
-  T* ob = reinterpret_cast<T*>(&rb);
+// The RoPE factors of a block's NR rows, [NR][D/2] cos then sin in LDS, rounded to the element type
+// as the reference casts its tables: thread k < D/2 computes column k for every row, from its
+// inverse frequency `invk`, loaded before the chunk loads so that the sincos runs while they arrive.
+template <typename T, int NR>
+__device__ __forceinline__ void rope_factors(float invk, int rope, int pos0, int row0, int nrow, int T_, int half,
+                                             float* tc, float* ts) {
+  const int k = threadIdx.x;
+  if (k >= half) return;
 #pragma unroll
-  for (int e = 0; e < EPC; ++e) {
-    const float x0 = E::to_f(ea[e]), x1 = E::to_f(eb[e]);
-    oa[e] = E::from_f(x0 * ang_c[e] - x1 * ang_s[e]);
-    ob[e] = E::from_f(x1 * ang_c[e] + x0 * ang_s[e]);
+  for (int r = 0; r < NR; ++r) {
+    const int t = (row0 + min(r, nrow - 1)) % T_;
+    float sn, cs;
+    sincosf((float)(pos0 + t) * invk, &sn, &cs);
+    tc[r * half + k] = rope ? rnd<T>(cs) : 1.f;
+    ts[r * half + k] = rope ? rnd<T>(sn) : 0.f;
   }
-  store_chunk(o + k0, ra);
-  store_chunk(o + half + k0, rb);
 }
 
-// The block's RoPE factors for its kRopeRows positions and the Givens factors of every head pair,
-// once per block in LDS (the angles do not depend on the head): rounded to the element type as the
-// reference casts its tables. Returns through `tc` / `ts` ([kRopeRows][half]) and `gc` / `gs`
-// ([H/2]); the exact fp32 Givens sin/cos go to `gce` / `gse` when those are given.
-template <typename T>
-__device__ __forceinline__ void rope_tables_lds(const float* inv_freq, const float* theta, int pos0, int row0, int T_,
-                                                int half, int npair, float* tc, float* ts, float* gc, float* gs,
-                                                float* gce, float* gse) {
-  for (int q = threadIdx.x; q < kRopeRows * half; q += blockDim.x) {
-    const int rl = q / half, k = q % half;
-    float c = 1.f, sn = 0.f;
-    if (inv_freq) {
-      const int t = (row0 + rl) % T_;
-      sincosf((float)(pos0 + t) * inv_freq[k], &sn, &c);
-      c = rnd<T>(c);
-      sn = rnd<T>(sn);
-    }
-    tc[q] = c;
-    ts[q] = sn;
-  }
-  for (int q = threadIdx.x; q < npair; q += blockDim.x) {
-    float c = 1.f, sn = 0.f;
-    if (theta) sincosf(theta[q], &sn, &c);
-    if (gce) {
-      gce[q] = c;
-      gse[q] = sn;
-    }
-    gc[q] = rnd<T>(c);
-    gs[q] = rnd<T>(sn);
-  }
-  __syncthreads();
+// The thread's place in the [p1 | p2 | I~] row: tensor, head, chunk in the head, partner chunk and
+// the Givens pairing (relation.py:150-174).
+struct RopeLane {
+  int which, hd, k, pc, pair, other, a0;
+  bool lo, first;
+};
+__device__ __forceinline__ RopeLane rope_lane(int c, int H, int D, int EPC, int parity) {
+  RopeLane L;
+  const int cph = D / EPC, hch = cph / 2, cpt = H * cph;
+  L.which = c / cpt;
+  const int cc = c - L.which * cpt;
+  L.hd = cc / cph;
+  L.k = cc - L.hd * cph;
+  L.lo = L.k < hch;
+  L.a0 = (L.lo ? L.k : L.k - hch) * EPC;  // RoPE factor index of the chunk's first element
+  givens_pair(L.hd, H, parity, L.pair, L.other, L.first);
+  L.pc = L.which < 2 ? c + (L.lo ? hch : -hch) : 2 * cpt + L.other * cph + L.k;
+  return L;
 }
 
-constexpr int kRopeMaxHalf = 64;   // D <= 128
-constexpr int kRopeMaxPairs = 64;  // H <= 128
-
 template <typename T>
-__global__ void __launch_bounds__(256) rope_givens_fwd_vec_kernel(const RopeParams p) {
+__global__ void __launch_bounds__(kRopeMaxCh) rope_givens_fwd_stream_kernel(const RopeParams p) {
   using E = Elem<T>;
   constexpr int EPC = 16 / sizeof(T);
-  __shared__ __align__(16) float tc[kRopeRows * kRopeMaxHalf], ts[kRopeRows * kRopeMaxHalf];
-  __shared__ float gc[kRopeMaxPairs], gs[kRopeMaxPairs];
-  const int HD = p.H * p.D, half = p.D / 2;
-  const int ur = p.H * (half / EPC);          // RoPE units per row
-  const int ug = (p.H / 2) * (p.D / EPC);     // Givens units per row
-  const int upr = ur + ug;
+  extern __shared__ float rope_tab[];  // [kRopeR][D/2] cos, then [kRopeR][D/2] sin
+  const int tid = threadIdx.x;
+  const int H = p.H, D = p.D, half = D / 2, npair = H / 2;
+  const int nch = 3 * H * D / EPC;
   const int rows = p.B * p.T;
-  const int row0 = blockIdx.x * kRopeRows;
-  rope_tables_lds<T>(p.inv_freq, p.theta, p.pos0, row0, p.T, half, p.H / 2, tc, ts, gc, gs, nullptr, nullptr);
-  for (int u = threadIdx.x; u < kRopeRows * upr; u += blockDim.x) {
-    const int rl = u / upr, k = u % upr;
-    const int row = row0 + rl;
-    if (row >= rows) break;
-    const int b = row / p.T, t = row % p.T;
-    const T* x = reinterpret_cast<const T*>(p.qkv) + int64_t(b) * p.qkv_sb + int64_t(t) * p.qkv_sr;
-    if (k < ur) {
-      const int hd = k / (half / EPC), k0 = (k % (half / EPC)) * EPC;
-      const float* cs = tc + rl * half + k0;
-      const float* sn = ts + rl * half + k0;
-      T* o1 = reinterpret_cast<T*>(p.o1) + int64_t(b) * p.o1_sb + int64_t(hd) * p.o1_sh + int64_t(t) * p.o1_sr;
-      T* o2 = reinterpret_cast<T*>(p.o2) + int64_t(b) * p.o2_sb + int64_t(hd) * p.o2_sh + int64_t(t) * p.o2_sr;
-      rope_chunk_fwd<T>(x + hd * p.D, o1, half, k0, cs, sn);
-      rope_chunk_fwd<T>(x + HD + hd * p.D, o2, half, k0, cs, sn);
-    } else {
-      const int kg = k - ur;
-      const int pr = kg / (p.D / EPC), d0 = (kg % (p.D / EPC)) * EPC;
-      int ha, hb;
-      if (p.parity == 0) {
-        ha = 2 * pr;
-        hb = 2 * pr + 1;
-      } else {
-        ha = 2 * pr + 1;
-        hb = (2 * pr + 2) % p.H;
-      }
-      const T* xi = x + 2 * HD;
-      const Chunk ca = load_chunk(xi + ha * p.D + d0), cb = load_chunk(xi + hb * p.D + d0);
-      Chunk ra = ca, rb = cb;
-      if (p.theta) {
-        const float c = gc[pr], sn = gs[pr];
-        const T* ea = reinterpret_cast<const T*>(&ca);
-        const T* eb = reinterpret_cast<const T*>(&cb);
-        T* oa = reinterpret_cast<T*>(&ra);
-        T* ob = reinterpret_cast<T*>(&rb);
+  const int row0 = blockIdx.x * kRopeR;
+  const int nrow = min(kRopeR, rows - row0);
+  const int ntab = kRopeR * half;
+  float* tc = rope_tab;
+  float* ts = rope_tab + ntab;
+  const RopeLane L = rope_lane(min(tid, nch - 1), H, D, EPC, p.parity);
+
+  // table values first (indices by multiplication with the 0/1 flags: a select becomes a branch)
+  const float invk = p.inv_safe[min(tid, half - 1) * p.rope];
+  const float th = p.theta_safe[min(L.pair, npair - 1) * p.givens];
+  Chunk xv[kRopeR], pv[kRopeR];
+  const T* q = reinterpret_cast<const T*>(p.qkv);
 #pragma unroll
-        for (int e = 0; e < EPC; ++e) {
-          const float a = E::to_f(ea[e]), bb = E::to_f(eb[e]);
-          oa[e] = E::from_f(c * a - sn * bb);
-          ob[e] = E::from_f(sn * a + c * bb);
-        }
-      }
-      T* o3 = reinterpret_cast<T*>(p.o3) + int64_t(b) * p.o3_sb + int64_t(t) * p.o3_sr;
-      store_chunk(o3 + int64_t(ha) * p.o3_sh + d0, ra);
-      store_chunk(o3 + int64_t(hb) * p.o3_sh + d0, rb);
+  for (int r = 0; r < kRopeR; ++r) {
+    const int row = row0 + min(r, nrow - 1), b = row / p.T, t = row - b * p.T;
+    const T* base = q + int64_t(b) * p.qkv_sb + int64_t(t) * p.qkv_sr;
+    xv[r] = load_chunk(base + min(tid, nch - 1) * EPC);
+    pv[r] = load_chunk(base + L.pc * EPC);
+  }
+  // the RoPE factors of the block's rows and the Givens factor of the thread's pair
+  rope_factors<T, kRopeR>(invk, p.rope, p.pos0, row0, nrow, p.T, half, tc, ts);
+  float gsn, gcs;
+  sincosf(th, &gsn, &gcs);
+  const float gc = p.givens ? rnd<T>(gcs) : 1.f, gs = p.givens ? rnd<T>(gsn) : 0.f;
+  __syncthreads();
+  if (tid >= nch) return;
+
+  // out = x C + y S with, per element: RoPE first half C = c, S = -s; second half C = c, S = s;
+  // Givens first member C = c, S = -s (out_a = c a - s b); second C = c, S = s (out_b = s a + c b)
+  const bool rope_part = L.which < 2;
+  const float sgn = rope_part ? (L.lo ? -1.f : 1.f) : (L.first ? -1.f : 1.f);
+  T* obase;
+  int64_t osb, osr;
+  if (L.which == 0) {
+    obase = reinterpret_cast<T*>(p.o1) + int64_t(L.hd) * p.o1_sh;
+    osb = p.o1_sb;
+    osr = p.o1_sr;
+  } else if (L.which == 1) {
+    obase = reinterpret_cast<T*>(p.o2) + int64_t(L.hd) * p.o2_sh;
+    osb = p.o2_sb;
+    osr = p.o2_sr;
+  } else {
+    obase = reinterpret_cast<T*>(p.o3) + int64_t(L.hd) * p.o3_sh;
+    osb = p.o3_sb;
+    osr = p.o3_sr;
+  }
+  obase += L.k * EPC;
+#pragma unroll
+  for (int r = 0; r < kRopeR; ++r) {
+    if (r >= nrow) break;
+    const int row = row0 + r, b = row / p.T, t = row - b * p.T;
+    const T* ex = reinterpret_cast<const T*>(&xv[r]);
+    const T* ey = reinterpret_cast<const T*>(&pv[r]);
+    Chunk out;
+    T* eo = reinterpret_cast<T*>(&out);
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) {
+      const float C = rope_part ? tc[r * half + L.a0 + e] : gc;
+      const float S = sgn * (rope_part ? ts[r * half + L.a0 + e] : gs);
+      eo[e] = E::from_f(E::to_f(ex[e]) * C + E::to_f(ey[e]) * S);
     }
+    store_chunk(obase + int64_t(b) * osb + int64_t(t) * osr, out);
   }
 }
 
 template <typename T>
-__global__ void __launch_bounds__(256) rope_givens_bwd_vec_kernel(const RopeBwdParams p) {
+__global__ void __launch_bounds__(kRopeMaxCh) rope_givens_bwd_stream_kernel(const RopeBwdParams p) {
   using E = Elem<T>;
   constexpr int EPC = 16 / sizeof(T);
-  constexpr int kMaxPairChunks = 2048;  // LDS slots for d theta partials (kRopeRows * H/2 * D/EPC)
-  __shared__ float dth[kMaxPairChunks];
-  __shared__ __align__(16) float tc[kRopeRows * kRopeMaxHalf], ts[kRopeRows * kRopeMaxHalf];
-  __shared__ float gc[kRopeMaxPairs], gs[kRopeMaxPairs], gce[kRopeMaxPairs], gse[kRopeMaxPairs];
-  const int HD = p.H * p.D, half = p.D / 2;
-  const int npair = p.H / 2, cpg = p.D / EPC;   // chunks per head
-  const int ur = p.H * (half / EPC);
-  const int ug = npair * cpg;
-  const int upr = ur + ug;
+  extern __shared__ float rope_tab[];  // [kRopeRB][D/2] cos, [kRopeRB][D/2] sin, [chunks] d theta
+  const int tid = threadIdx.x;
+  const int H = p.H, D = p.D, half = D / 2, npair = H / 2;
+  const int cph = D / EPC, cpt = H * cph, nch = 3 * cpt;
   const int rows = p.B * p.T;
-  const int row0 = blockIdx.x * kRopeRows;
-  rope_tables_lds<T>(p.inv_freq, p.theta, p.pos0, row0, p.T, half, npair, tc, ts, gc, gs, gce, gse);
-  for (int u = threadIdx.x; u < kRopeRows * upr; u += blockDim.x) {
-    const int rl = u / upr, k = u % upr;
-    const int row = row0 + rl;
-    if (row >= rows) break;
-    const int b = row / p.T, t = row % p.T;
-    T* dx = reinterpret_cast<T*>(p.dqkv) + int64_t(b) * p.dq_sb + int64_t(t) * p.dq_sr;
-    if (k < ur) {
-      const int hd = k / (half / EPC), k0 = (k % (half / EPC)) * EPC;
-      const float* cs = tc + rl * half + k0;
-      // transposed rotation: dx_k = d_k c + d_{k+h} s, dx_{k+h} = d_{k+h} c - d_k s
-      float msn[EPC];
+  const int row0 = blockIdx.x * kRopeRB;
+  const int nrow = min(kRopeRB, rows - row0);
+  const int ntab = kRopeRB * half;
+  float* tc = rope_tab;
+  float* ts = rope_tab + ntab;
+  float* red = rope_tab + 2 * ntab;
+  const RopeLane L = rope_lane(min(tid, nch - 1), H, D, EPC, p.parity);
+
+  const float invk = p.inv_safe[min(tid, half - 1) * p.rope];
+  const float th = p.theta_safe[min(L.pair, npair - 1) * p.givens];
+  // gradient chunks: the thread's own and its partner's, from the view of its tensor
+  const T* gb;
+  int64_t gsb, gsh, gsr;
+  if (L.which == 0) {
+    gb = reinterpret_cast<const T*>(p.g1); gsb = p.g1_sb; gsh = p.g1_sh; gsr = p.g1_sr;
+  } else if (L.which == 1) {
+    gb = reinterpret_cast<const T*>(p.g2); gsb = p.g2_sb; gsh = p.g2_sh; gsr = p.g2_sr;
+  } else {
+    gb = reinterpret_cast<const T*>(p.g3); gsb = p.g3_sb; gsh = p.g3_sh; gsr = p.g3_sr;
+  }
+  const int hch = cph / 2;
+  const T* gself = gb + int64_t(L.hd) * gsh + L.k * EPC;
+  const T* gpart = L.which < 2 ? gself + (L.lo ? hch : -hch) * EPC : gb + int64_t(L.other) * gsh + L.k * EPC;
+  // I~ inputs of the pair (for d theta): every thread loads two chunks of the I~ part of qkv (those
+  // of p1 / p2 threads repeat an I~ thread's lines), so no load sits under a condition
+  const int xa = L.which == 2 ? L.hd : L.hd % H, xb = L.which == 2 ? L.other : L.hd % H;
+  const T* xq = reinterpret_cast<const T*>(p.qkv) + 2 * H * D + L.k * EPC;
+  Chunk g0[kRopeRB], g1[kRopeRB], x0[kRopeRB], x1[kRopeRB];
 #pragma unroll
-      for (int e = 0; e < EPC; ++e) msn[e] = -ts[rl * half + k0 + e];
-      const T* g1 = reinterpret_cast<const T*>(p.g1) + int64_t(b) * p.g1_sb + int64_t(hd) * p.g1_sh + int64_t(t) * p.g1_sr;
-      const T* g2 = reinterpret_cast<const T*>(p.g2) + int64_t(b) * p.g2_sb + int64_t(hd) * p.g2_sh + int64_t(t) * p.g2_sr;
-      rope_chunk_fwd<T>(g1, dx + hd * p.D, half, k0, cs, msn);
-      rope_chunk_fwd<T>(g2, dx + HD + hd * p.D, half, k0, cs, msn);
-    } else {
-      const int kg = k - ur;
-      const int pr = kg / cpg, d0 = (kg % cpg) * EPC;
-      int ha, hb;
-      if (p.parity == 0) {
-        ha = 2 * pr;
-        hb = 2 * pr + 1;
-      } else {
-        ha = 2 * pr + 1;
-        hb = (2 * pr + 2) % p.H;
-      }
-      const T* g3 = reinterpret_cast<const T*>(p.g3) + int64_t(b) * p.g3_sb + int64_t(t) * p.g3_sr;
-      const Chunk ga = load_chunk(g3 + int64_t(ha) * p.g3_sh + d0), gb = load_chunk(g3 + int64_t(hb) * p.g3_sh + d0);
-      Chunk ra = ga, rb = gb;
-      if (p.theta) {
-        const float c = gce[pr], sn = gse[pr];      // exact: the derivative of the unrounded function
-        const float cr = gc[pr], sr = gs[pr];       // rounded: the rotation that was applied
-        const T* xi = reinterpret_cast<const T*>(p.qkv) + int64_t(b) * p.qkv_sb + int64_t(t) * p.qkv_sr + 2 * HD;
-        const Chunk xa = load_chunk(xi + ha * p.D + d0), xb = load_chunk(xi + hb * p.D + d0);
-        const T* ega = reinterpret_cast<const T*>(&ga);
-        const T* egb = reinterpret_cast<const T*>(&gb);
-        const T* exa = reinterpret_cast<const T*>(&xa);
-        const T* exb = reinterpret_cast<const T*>(&xb);
-        T* oa = reinterpret_cast<T*>(&ra);
-        T* ob = reinterpret_cast<T*>(&rb);
-        float acc = 0.f;
+  for (int r = 0; r < kRopeRB; ++r) {
+    const int row = row0 + min(r, nrow - 1), b = row / p.T, t = row - b * p.T;
+    const int64_t go = int64_t(b) * gsb + int64_t(t) * gsr;
+    g0[r] = load_chunk(gself + go);
+    g1[r] = load_chunk(gpart + go);
+    const T* xr = xq + int64_t(b) * p.qkv_sb + int64_t(t) * p.qkv_sr;
+    x0[r] = load_chunk(xr + xa * D);
+    x1[r] = load_chunk(xr + xb * D);
+  }
+  rope_factors<T, kRopeRB>(invk, p.rope, p.pos0, row0, nrow, p.T, half, tc, ts);
+  float gsn, gcs;
+  sincosf(th, &gsn, &gcs);
+  const float ce = p.givens ? gcs : 1.f, se = p.givens ? gsn : 0.f;     // exact: the derivative
+  const float cr = p.givens ? rnd<T>(gcs) : 1.f, sr = p.givens ? rnd<T>(gsn) : 0.f;  // applied rotation
+  __syncthreads();
+
+  // dx = g C + g' S: RoPE^T first half C = c, S = s (dx_k = d_k c + d_{k+h} s), second half
+  // C = c, S = -s (dx_{k+h} = d_{k+h} c - d_k s); Givens^T first member C = c, S = s
+  // (da = c ga + s gb), second C = c, S = -s (db = c gb - s ga)
+  const bool act = tid < nch;
+  const bool rope_part = L.which < 2;
+  const float sgn = rope_part ? (L.lo ? 1.f : -1.f) : (L.first ? 1.f : -1.f);
+  const bool dth_lane = act && !rope_part && L.first && p.givens;
+  T* dbase = reinterpret_cast<T*>(p.dqkv) + min(tid, nch - 1) * EPC;
+  float acc = 0.f;
 #pragma unroll
-        for (int e = 0; e < EPC; ++e) {
-          const float a = E::to_f(exa[e]), bb = E::to_f(exb[e]);
-          const float da = E::to_f(ega[e]), db = E::to_f(egb[e]);
-          oa[e] = E::from_f(cr * da + sr * db);
-          ob[e] = E::from_f(cr * db - sr * da);
-          acc += da * (-sn * a - c * bb) + db * (c * a - sn * bb);
-        }
-        dth[(rl * npair + pr) * cpg + kg % cpg] = acc;
+  for (int r = 0; r < kRopeRB; ++r) {
+    if (r >= nrow) break;
+    const int row = row0 + r, b = row / p.T, t = row - b * p.T;
+    const T* e0 = reinterpret_cast<const T*>(&g0[r]);
+    const T* e1 = reinterpret_cast<const T*>(&g1[r]);
+    Chunk out;
+    T* eo = reinterpret_cast<T*>(&out);
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) {
+      const float C = rope_part ? tc[r * half + L.a0 + e] : cr;
+      const float S = sgn * (rope_part ? ts[r * half + L.a0 + e] : sr);
+      eo[e] = E::from_f(E::to_f(e0[e]) * C + E::to_f(e1[e]) * S);
+    }
+    if (act) store_chunk(dbase + int64_t(b) * p.dq_sb + int64_t(t) * p.dq_sr, out);
+    if (dth_lane) {
+      // d theta of the pair from its first member: ga (-s a - c b) + gb (c a - s b), exact s, c
+      const T* ea = reinterpret_cast<const T*>(&x0[r]);
+      const T* eb = reinterpret_cast<const T*>(&x1[r]);
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) {
+        const float a = E::to_f(ea[e]), bb = E::to_f(eb[e]);
+        const float da = E::to_f(e0[e]), db = E::to_f(e1[e]);
+        acc += da * (-se * a - ce * bb) + db * (ce * a - se * bb);
       }
-      store_chunk(dx + 2 * HD + ha * p.D + d0, ra);
-      store_chunk(dx + 2 * HD + hb * p.D + d0, rb);
     }
   }
-  if (!p.theta) return;
+  if (!p.givens) return;
+  // per pair: the first member's chunks in a fixed order (one partial per block)
+  if (act) red[tid] = acc;
   __syncthreads();
-  // per pair: fixed-order sum over the block's rows and the head's chunks (one partial per block)
-  for (int pr = threadIdx.x; pr < npair; pr += blockDim.x) {
-    float acc = 0.f;
-    for (int rl = 0; rl < kRopeRows; ++rl) {
-      if (row0 + rl >= rows) break;
-      for (int c = 0; c < cpg; ++c) acc += dth[(rl * npair + pr) * cpg + c];
-    }
-    p.partial[int64_t(blockIdx.x) * npair + pr] = acc;
+  for (int pr = tid; pr < npair; pr += blockDim.x) {
+    const int ha = p.parity == 0 ? 2 * pr : 2 * pr + 1;
+    float s2 = 0.f;
+    for (int k = 0; k < cph; ++k) s2 += red[2 * cpt + ha * cph + k];
+    p.partial[int64_t(blockIdx.x) * npair + pr] = s2;
   }
 }
 
@@ -456,17 +490,27 @@ int launch_rope_givens_fwd(const mote_rope_givens_args* a, hipStream_t stream) {
   p.o2 = a->p2.data; p.o2_sb = a->p2.stride_b; p.o2_sh = a->p2.stride_h; p.o2_sr = a->p2.stride_r;
   p.o3 = a->info.data; p.o3_sb = a->info.stride_b; p.o3_sh = a->info.stride_h; p.o3_sr = a->info.stride_r;
   p.inv_freq = a->inv_freq; p.theta = a->theta;
+  p.rope = a->inv_freq != nullptr;
+  p.givens = a->theta != nullptr;
+  p.inv_safe = p.rope ? a->inv_freq : reinterpret_cast<const float*>(a->qkv);
+  p.theta_safe = p.givens ? a->theta : reinterpret_cast<const float*>(a->qkv);
   p.B = a->B; p.T = a->T; p.H = a->H; p.D = a->D; p.pos0 = a->pos0; p.parity = a->layer_parity & 1;
   const int rows = a->B * a->T;
   const int epc = a->dtype == MOTE_BF16 ? 8 : 4;
-  const bool vec = (a->D / 2) % epc == 0 && a->D / 2 <= kRopeMaxHalf && a->H / 2 <= kRopeMaxPairs && aligned16(a);
-  const int vblocks = (rows + kRopeRows - 1) / kRopeRows;
-  if (a->dtype == MOTE_BF16) {
-    if (vec) hipLaunchKernelGGL(rope_givens_fwd_vec_kernel<bf16_t>, dim3(vblocks), dim3(256), 0, stream, p);
-    else hipLaunchKernelGGL(rope_givens_fwd_kernel<bf16_t>, dim3(rows), dim3(256), 0, stream, p);
+  const int nch = 3 * a->H * a->D / epc;
+  const bool vec = (a->D / 2) % epc == 0 && a->D % epc == 0 && nch <= kRopeMaxCh && aligned16(a);
+  if (vec) {
+    const int blocks = (rows + kRopeR - 1) / kRopeR;
+    const int threads = (nch + 63) / 64 * 64;
+    const size_t lds = size_t(2) * kRopeR * (a->D / 2) * sizeof(float);
+    if (a->dtype == MOTE_BF16)
+      hipLaunchKernelGGL(rope_givens_fwd_stream_kernel<bf16_t>, dim3(blocks), dim3(threads), lds, stream, p);
+    else
+      hipLaunchKernelGGL(rope_givens_fwd_stream_kernel<float>, dim3(blocks), dim3(threads), lds, stream, p);
+  } else if (a->dtype == MOTE_BF16) {
+    hipLaunchKernelGGL(rope_givens_fwd_kernel<bf16_t>, dim3(rows), dim3(256), 0, stream, p);
   } else {
-    if (vec) hipLaunchKernelGGL(rope_givens_fwd_vec_kernel<float>, dim3(vblocks), dim3(256), 0, stream, p);
-    else hipLaunchKernelGGL(rope_givens_fwd_kernel<float>, dim3(rows), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(rope_givens_fwd_kernel<float>, dim3(rows), dim3(256), 0, stream, p);
   }
   return check_launch("rope_givens_fwd");
 }
@@ -491,25 +535,33 @@ int launch_rope_givens_bwd(const mote_rope_givens_bwd_args* a, hipStream_t strea
   p.g3 = a->dinfo.data; p.g3_sb = a->dinfo.stride_b; p.g3_sh = a->dinfo.stride_h; p.g3_sr = a->dinfo.stride_r;
   p.dqkv = a->dqkv; p.dq_sb = a->dqkv_sb; p.dq_sr = a->dqkv_sr;
   p.inv_freq = a->inv_freq; p.theta = a->theta;
+  p.rope = a->inv_freq != nullptr;
+  p.givens = a->theta != nullptr;
+  p.inv_safe = p.rope ? a->inv_freq : reinterpret_cast<const float*>(a->qkv);
+  p.theta_safe = p.givens ? a->theta : reinterpret_cast<const float*>(a->qkv);
   p.partial = reinterpret_cast<float*>(a->workspace);
   p.B = a->B; p.T = a->T; p.H = a->H; p.D = a->D; p.pos0 = a->pos0; p.parity = a->layer_parity & 1;
   const int rows = a->B * a->T;
   const int epc = a->dtype == MOTE_BF16 ? 8 : 4;
-  const bool vec = (a->D / 2) % epc == 0 && a->D / 2 <= kRopeMaxHalf && a->H / 2 <= kRopeMaxPairs &&
-                   aligned16_bwd(a) && kRopeRows * (a->H / 2) * (a->D / epc) <= 2048;
-  const int vblocks = (rows + kRopeRows - 1) / kRopeRows;
-  if (a->dtype == MOTE_BF16) {
-    if (vec) hipLaunchKernelGGL(rope_givens_bwd_vec_kernel<bf16_t>, dim3(vblocks), dim3(256), 0, stream, p);
-    else hipLaunchKernelGGL(rope_givens_bwd_kernel<bf16_t>, dim3(rows), dim3(256), 0, stream, p);
+  const int nch = 3 * a->H * a->D / epc;
+  const bool vec = (a->D / 2) % epc == 0 && a->D % epc == 0 && nch <= kRopeMaxCh && aligned16_bwd(a);
+  const int blocks = vec ? (rows + kRopeRB - 1) / kRopeRB : rows;
+  if (vec) {
+    const int threads = (nch + 63) / 64 * 64;
+    const size_t lds = (size_t(2) * kRopeRB * (a->D / 2) + size_t(nch)) * sizeof(float);
+    if (a->dtype == MOTE_BF16)
+      hipLaunchKernelGGL(rope_givens_bwd_stream_kernel<bf16_t>, dim3(blocks), dim3(threads), lds, stream, p);
+    else
+      hipLaunchKernelGGL(rope_givens_bwd_stream_kernel<float>, dim3(blocks), dim3(threads), lds, stream, p);
+  } else if (a->dtype == MOTE_BF16) {
+    hipLaunchKernelGGL(rope_givens_bwd_kernel<bf16_t>, dim3(rows), dim3(256), 0, stream, p);
   } else {
-    if (vec) hipLaunchKernelGGL(rope_givens_bwd_vec_kernel<float>, dim3(vblocks), dim3(256), 0, stream, p);
-    else hipLaunchKernelGGL(rope_givens_bwd_kernel<float>, dim3(rows), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(rope_givens_bwd_kernel<float>, dim3(rows), dim3(256), 0, stream, p);
   }
   rc = check_launch("rope_givens_bwd");
   if (rc || !a->theta) return rc;
-  const int nparts = vec ? vblocks : rows;  // the vectorised kernel leaves one partial per block
-  hipLaunchKernelGGL(sum_partials_kernel, dim3((a->H / 2 + 3) / 4), dim3(256), 0, stream, p.partial, nparts, a->H / 2,
-                     a->dtheta);
+  const int nparts = blocks;  // one partial per block (the per-row kernel: one per row)
+  hipLaunchKernelGGL(sum_partials_kernel, dim3(a->H / 2), dim3(256), 0, stream, p.partial, nparts, a->H / 2, a->dtheta);
   return check_launch("rope_givens_bwd/sum");
 }
 

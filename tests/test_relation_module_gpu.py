@@ -27,12 +27,16 @@ def _pair(d_model, n_heads, layer_idx, seed=0, **kw):
     return mine, ref
 
 
+# (H, D, T): the row-staged kernels at several row widths and partial last blocks, and D = 40
+# (D/2 not a multiple of the 16-byte chunk in bf16), which takes the per-row kernels
+@pytest.mark.parametrize("H,D,T", [(8, 64, 37), (8, 96, 301), (2, 48, 53), (4, 32, 9), (2, 40, 23)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("layer_idx", [0, 1])
-def test_rope_givens_forward_and_grads(cuda, dtype, layer_idx):
+def test_rope_givens_forward_and_grads(cuda, dtype, layer_idx, H, D, T):
     from mote_amd.relation import rope_givens, rope_inv_freq
 
-    B, T, H, D, S = 2, 37, 8, 64, 11
+    print(f"case rope_givens {dtype} layer={layer_idx} H={H} D={D} T={T}", flush=True)
+    B, S = 2, 11
     g = torch.Generator().manual_seed(layer_idx)
     qkv = (torch.randn(B, T, 3 * H * D, generator=g) * 0.8).to(dtype)
     theta = torch.rand(H // 2, generator=g) * 0.6 - 0.3
