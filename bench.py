@@ -56,21 +56,26 @@ def chunk_count(seed: int, nbytes: int, batch: int = 1) -> int:
 # fwd + bwd (C3)
 # ------------------------------------------------------------------------------------------------
 class StackInputs:
-    def __init__(self, T: int, seed: int, dev):
+    """Per layer: the fused projection output of RMSNorm'd N(0,1) hidden states through random-init
+    FullRelation weights (bf16, [B, T, 3 D]) and an N(0,1) upstream gradient dY, resident on the GPU."""
+
+    def __init__(self, T: int, seed: int, dev, B: int = 1, d_model: int = D_MODEL, heads: int = N_HEADS,
+                 layers: int = N_LAYERS):
         from mote_amd.relation import FullRelation
 
         torch.manual_seed(seed)
-        x = rmsnorm(torch.randn(1, T, D_MODEL))
+        x = rmsnorm(torch.randn(B, T, d_model))
+        dh = d_model // heads
         self.layers = []
-        for li in range(N_LAYERS):
-            m = FullRelation(D_MODEL, N_HEADS, li)
+        for li in range(layers):
+            m = FullRelation(d_model, heads, li)
             with torch.no_grad():
                 m.theta.uniform_(-0.3, 0.3)
             w = torch.cat([m.w1.weight, m.w2.weight, m.wi.weight], 0).detach()
             qkv = (x @ w.t()).to(torch.bfloat16).to(dev)
-            dy = torch.randn(1, N_HEADS, T, D_HEAD).to(torch.bfloat16).to(dev)
+            dy = torch.randn(B, heads, T, dh).to(torch.bfloat16).to(dev)
             self.layers.append(dict(qkv=qkv, dy=dy, theta=m.theta.detach().to(dev), lam=m.lam.detach().to(dev),
-                                    inv=m.inv_freq.to(dev), parity=li % 2))
+                                    inv=m.inv_freq.to(dev), parity=li % 2, heads=heads))
         self.T = T
 
 
@@ -78,7 +83,7 @@ def stack_step(inp: StackInputs, timers=None):
     """One fwd+bwd pass of the 12-layer stack through the HIP ops."""
     ops = torch.ops.mote
     for L in inp.layers:
-        p1, p2, info = ops.rope_givens(L["qkv"], L["inv"], L["theta"], N_HEADS, L["parity"], 0)
+        p1, p2, info = ops.rope_givens(L["qkv"], L["inv"], L["theta"], L["heads"], L["parity"], 0)
         if timers is not None:
             timers["fwd"][0].append(torch.cuda.Event(enable_timing=True))
             timers["fwd"][0][-1].record()
@@ -89,7 +94,7 @@ def stack_step(inp: StackInputs, timers=None):
             dp = staged_bwd(p1, p2, info, ibar, lse, g, L["dy"], timers)
         else:
             dp = ops.relation_bwd(p1, p2, info, ibar, lse, g, L["dy"], 2.0, 0)
-        ops.rope_givens_bwd(dp[0], dp[1], dp[2], L["qkv"], L["inv"], L["theta"], N_HEADS, L["parity"], 0)
+        ops.rope_givens_bwd(dp[0], dp[1], dp[2], L["qkv"], L["inv"], L["theta"], L["heads"], L["parity"], 0)
 
 
 def staged_bwd(p1, p2, info, ibar, lse, g, dy, timers):
@@ -315,6 +320,88 @@ def bench_decode(batch: int, steps: int, dev, copies: int):
 
 
 # ------------------------------------------------------------------------------------------------
+# C2 (Mote-32M stack) and C5 (Mote-138M ragged prefill): reported beside the headline
+# ------------------------------------------------------------------------------------------------
+def bench_c2(steps: int, warmup: int, dev):
+    """Mote-32M Relation stack (d_model 512, 8 heads, dh 64, 8 layers), bf16 fwd+bwd, B = 4, a
+    2048-byte window with Bernoulli(1/3.3) chunk boundaries (seed 1): every sequence padded to the
+    longest (T = max M_b); FLOPs count the real rows only, 7 H dh sum_b M_b^2 per layer."""
+    g = torch.Generator().manual_seed(1)
+    mask = torch.rand(4, 2048, generator=g) < (1.0 / 3.3)
+    mask[:, 0] = True
+    M = mask.sum(-1).tolist()
+    T = max(M)
+    inp = StackInputs(T, 1, dev, B=4, d_model=512, heads=8, layers=8)
+    for _ in range(warmup):
+        stack_step(inp)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(steps):
+        stack_step(inp)
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    flops = 8 * 7.0 * 8 * 64 * sum(m * m for m in M)
+    log(f"[bench] C2 Mote-32M stack: chunks {M} (T = {T}), {ms:.3f} ms/step = {flops / ms / 1e9:.1f} TFLOP/s")
+    return dict(workload="Mote-32M Relation stack fwd+bwd (8 layers, B=4, 2048-byte window, seed 1)", chunks=M,
+                T_padded=T, ms_per_step=round(ms, 4), tflops=round(flops / (ms * 1e-3) / 1e12, 2),
+                flop_per_step=flops, frac_bf16_peak=round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4))
+
+
+def bench_c5(steps: int, warmup: int, dev):
+    """Mote-138M Relation prefill (d_model 768, 8 heads, dh 96, 18 layers), bf16 forward over a
+    ragged packed batch: 8 sequences of U[1000, 5000] chunks (seed 4) in cu_seqlens layout. Per layer
+    the varlen core (mote::relation_fwd_varlen) on resident P1 / P2 / I~ ([H, total, dh] views of
+    [total, H, dh] memory from RMSNorm'd N(0,1) hidden states through random-init projections, RoPE
+    restarting at 0 for every sequence, Givens). FLOPs: 2 H dh sum_i T_i^2 per layer."""
+    from mote_amd.relation import FullRelation, rope_givens
+
+    lens = torch.randint(1000, 5001, (8,), generator=torch.Generator().manual_seed(4)).tolist()
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32)
+    total = int(cu[-1])
+    torch.manual_seed(4)
+    x = rmsnorm(torch.randn(total, D_MODEL))
+    layers = []
+    for li in range(18):
+        m = FullRelation(D_MODEL, N_HEADS, li)
+        with torch.no_grad():
+            m.theta.uniform_(-0.3, 0.3)
+        w = torch.cat([m.w1.weight, m.w2.weight, m.wi.weight], 0).detach()
+        qkv = (x @ w.t()).to(torch.bfloat16).to(dev)
+        bufs = [torch.empty(total, N_HEADS, D_HEAD, device=dev, dtype=torch.bfloat16) for _ in range(3)]
+        for b, n in enumerate(lens):  # RoPE positions restart at every sequence
+            r0 = int(cu[b])
+            outs = rope_givens(qkv[None, r0:r0 + n], N_HEADS, m.inv_freq.to(dev), m.theta.detach().to(dev), li, 0)
+            for dst, o in zip(bufs, outs):
+                dst[r0:r0 + n] = o[0].transpose(0, 1)
+        layers.append(([t.permute(1, 0, 2) for t in bufs], m.lam.detach().to(dev)))
+    cud = cu.to(dev)
+    ops = torch.ops.mote
+
+    def step():
+        for (p1, p2, info), lam in layers:
+            ops.relation_fwd_varlen(p1, p2, info, lam, cud, max(lens), 2.0)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(steps):
+        step()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    flops = 18 * 2.0 * N_HEADS * D_HEAD * sum(n * n for n in lens)
+    log(f"[bench] C5 Mote-138M prefill: lens {lens} (total {total}), {ms:.3f} ms/step = "
+        f"{flops / ms / 1e9:.1f} TFLOP/s")
+    return dict(workload="Mote-138M Relation prefill, varlen core forward (18 layers, 8 ragged sequences, seed 4)",
+                lens=lens, total_chunks=total, ms_per_step=round(ms, 4), tflops=round(flops / (ms * 1e-3) / 1e12, 2),
+                flop_per_step=flops, frac_bf16_peak=round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4))
+
+
+# ------------------------------------------------------------------------------------------------
 # CPU baseline: the oracle on the host cores
 # ------------------------------------------------------------------------------------------------
 def bench_cpu(T: int):
@@ -355,6 +442,7 @@ def main():
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the C2 / C5 lines")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the Relation path is built and measured on a single GPU "
@@ -372,6 +460,10 @@ def main():
     if not args.no_decode:
         dec["b1"] = bench_decode(1, args.decode_steps, dev, copies=4)
         dec["b16"] = bench_decode(16, args.decode_steps, dev, copies=1)
+    extra = {}
+    if not args.no_extra:
+        extra["c2_mote32m_stack"] = bench_c2(args.steps, args.warmup, dev)
+        extra["c5_mote138m_prefill"] = bench_c5(max(3, args.steps // 4), min(args.warmup, 2), dev)
     cpu = None if args.no_cpu else bench_cpu(st["T"])
     out = {
         "metric": METRIC,
@@ -415,6 +507,7 @@ def main():
                 "traffic": measured_traffic(f"relation_decode_kernel_{k}"),
                 "cache_copies_rotated": v["copies"]}
             for k, v in dec.items()}
+    out.update(extra)
     if cpu is not None:
         out["cpu_baseline"] = {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")}
     print(json.dumps(out), flush=True)

@@ -184,6 +184,30 @@ def test_varlen_equals_per_sequence(cuda):
         assert float((gg[:, sl].cpu().double() - gr[0]).abs().max()) < 2e-2
 
 
+def test_c5_varlen_full_size_equals_dense(cuda):
+    """BASELINE config C5 at full size: 8 packed sequences of U[1000, 5000] chunks (seed 4), H = 8,
+    dh = 96, bf16. The oracle cannot run at this size; the packed path must equal the dense path run
+    on each sequence alone (the small varlen test above pins both against the oracle)."""
+    from mote_amd.flash_relation import flash_relation, flash_relation_varlen
+
+    H, D = 8, 96
+    lens = torch.randint(1000, 5001, (8,), generator=torch.Generator().manual_seed(4)).tolist()
+    print(f"case C5 lens={lens}", flush=True)
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32)
+    total = int(cu[-1])
+    g = torch.Generator().manual_seed(14)
+    x = [torch.randn(total, H, D, generator=g).to(torch.bfloat16).to(cuda) for _ in range(3)]
+    p1, p2, info = (t.permute(1, 0, 2) for t in x)  # [H, total, D] views of [total, H, D] memory
+    lam = torch.tensor(0.5, device=cuda)
+    y, gg = flash_relation_varlen(p1, p2, info, lam, cu.to(cuda), max(lens), 2.0)
+    assert torch.isfinite(y.float()).all() and torch.isfinite(gg).all()
+    for b, n in enumerate(lens):
+        sl = slice(int(cu[b]), int(cu[b]) + n)
+        yd, gd = flash_relation(p1[None, :, sl], p2[None, :, sl], info[None, :, sl], lam, 2.0, 0)
+        assert rel_err(y[:, sl], yd[0]) < 1e-3, (b, rel_err(y[:, sl], yd[0]))
+        assert float((gg[:, sl] - gd[0]).abs().max()) < 1e-3
+
+
 def test_empty_query_block_and_shapes(cuda):
     from mote_amd.flash_relation import flash_relation
 

@@ -94,6 +94,21 @@ def test_module_matches_oracle_fp32(cuda, d_model, n_heads, T, layer_idx):
         assert rel_err(p.grad, grads_r[n].grad) < 1e-5, (n, rel_err(p.grad, grads_r[n].grad))
 
 
+@pytest.mark.parametrize("layer_idx", [0, 1])
+def test_c1_mote1m_layer_matches_oracle(cuda, layer_idx):
+    """the Mote-1M Relation layer (d_model 192, 4 heads, dh 48), fp32, B = 2,
+    T = 256, hidden N(0,1) then RMSNorm (eps 1e-5, unit weight), weights from seed 0, theta ~
+    U(-0.3, 0.3) and lam = 0.4; the forward output and the gates against the oracle module."""
+    print(f"case C1 layer={layer_idx}", flush=True)
+    mine, ref = _pair(192, 4, layer_idx, seed=0)
+    x = torch.randn(2, 256, 192, generator=torch.Generator().manual_seed(0))
+    x = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-5)
+    out, g = mine(x.cuda(), return_gates=True)
+    outr, gr = ref(x, return_gates=True)
+    assert rel_err(out, outr) < 1e-5, rel_err(out, outr)
+    assert float((g.cpu() - gr).abs().max()) < 1e-5
+
+
 def test_module_bf16_autocast(cuda):
     mine, ref = _pair(768, 8, 1, seed=3)
     x = torch.randn(1, 500, 768, generator=torch.Generator().manual_seed(2))
