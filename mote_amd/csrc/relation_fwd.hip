@@ -492,7 +492,10 @@ relation_fwd_tile_kernel(const FwdParams p) {
   constexpr int KS = DP / 32, DT = DP / 16, TILE = 64 * DP;
   constexpr int STAGE = 2 * TILE;  // P2 tile, I~ tile
   constexpr int RLD = DP + 4;      // fp32 row stride of the merge buffer
-  __shared__ __align__(16) bf16_t smem[2 * STAGE];
+  // A ring of NSTG stages: a block waits only for its own stage, the next NSTG - 2 stay in flight
+  // across its math (three stages: 72 KB at DP = 96, so two workgroups still share a CU).
+  constexpr int NSTG = DP <= 96 ? 3 : 2;
+  __shared__ __align__(16) bf16_t smem[NSTG * STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: staging in scalar registers
@@ -573,17 +576,34 @@ relation_fwd_tile_kernel(const FwdParams p) {
     ones.v = bf16x8{one, one, one, one, one, one, one, one};
   }
 
-  if (kb_lo < kb_hi) st.issue(smem + (kb_lo & 1) * STAGE, srcs, strides, kb_lo * 64, TKs - 1, wave, lane);
+  // Block kb goes to ring slot (kb - kb_lo) % NSTG. Every step issues one block, past the end a
+  // reload of the last one, so that the wait before a step always leaves the same count in flight.
+  constexpr int PER = TileStager<DP, 4, 2>::PER;  // transfers per stage and wave
+  auto issue_kb = [&](int kb, int slot) {
+    st.issue(smem + slot * STAGE, srcs, strides, min(kb, kb_hi - 1) * 64, TKs - 1, wave, lane);
+  };
+  if (kb_lo < kb_hi) issue_kb(kb_lo, 0);
   __builtin_amdgcn_s_waitcnt(0);  // unconditional: no query-fragment load stays pending into the loop
-  __syncthreads();
+  // The fragments pass through an empty asm: the compiler's own count of outstanding loads then has
+  // no load of them left to wait for inside the loop (it otherwise waited for every load in flight,
+  // the ring's prefetches included, before the first product of each block).
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(qf[s][ks].v));
+  if (kb_lo < kb_hi && NSTG > 2) issue_kb(kb_lo + 1, 1);
   // key blocks wholly before the workgroup's first query position first (unmasked block math), then
   // the diagonal ones (masked): two loops keep one register assignment of the accumulators each
+  int slot = 0;
   auto step = [&](int kb, auto masked) {
     MOTE_STAMP(0, kb);
-    const int stage = kb & 1;
-    if (kb + 1 < kb_hi) st.issue(smem + (stage ^ 1) * STAGE, srcs, strides, (kb + 1) * 64, TKs - 1, wave, lane);
+    __builtin_amdgcn_s_waitcnt(kVmWaitStage<(NSTG - 2) * PER>());  // this wave's part of block kb is in
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0) only (vmcnt and expcnt at their maxima)
+    __builtin_amdgcn_s_barrier();  // every wave's part of block kb is in; every wave is done with block kb - 1's slot
+    MOTE_STAMP(3, kb);
+    issue_kb(kb + NSTG - 1, slot == 0 ? NSTG - 1 : slot - 1);
     MOTE_STAMP(1, kb);
-    const bf16_t* Ks = smem + stage * STAGE;
+    const bf16_t* Ks = smem + slot * STAGE;
     const int key0 = kb * 64 + 32 * kh;
     if (q0 < TQs && key0 < qs + wq_last) {
       f32x4 sacc[2][2];
@@ -592,10 +612,7 @@ relation_fwd_tile_kernel(const FwdParams p) {
                                                   lg);
     }
     MOTE_STAMP(2, kb);
-    __builtin_amdgcn_s_waitcnt(0);
-    MOTE_STAMP(3, kb);
-    __syncthreads();
-    MOTE_STAMP(4, kb);
+    slot = slot + 1 == NSTG ? 0 : slot + 1;
   };
   const int kb_m = min(kb_hi, (qs + qb * 64) / 64);
   int kb = kb_lo;
@@ -609,6 +626,7 @@ relation_fwd_tile_kernel(const FwdParams p) {
   // merge the key halves: kh = 1 hands (m, l, O) to kh = 0 through LDS
   float* R = reinterpret_cast<float*>(smem);     // [64 queries][RLD]
   float* RM = R + 64 * RLD;                      // [64] m, then [64] l
+  __builtin_amdgcn_s_waitcnt(0);  // the reloads past the end have landed before the ring is reused
   __syncthreads();
   if (kh == 1) {
 #pragma unroll
