@@ -402,6 +402,75 @@ def bench_c5(steps: int, warmup: int, dev):
 
 
 # ------------------------------------------------------------------------------------------------
+# fused add + RMSNorm (the pre-norm of every H-Net block)
+# ------------------------------------------------------------------------------------------------
+def bench_norm(rows: int, dev, copies: int, launches: int = 24):
+    """mote::add_rms_norm / _bwd at the H-Net block's pre-norm: x bf16 [rows, 768] plus the fp32
+    residual stream, prenorm (y bf16 and the new fp32 stream out); backward with the gradients of
+    both outputs. Each direction is a HIP graph of `launches` launches rotating over `copies` input
+    sets (so that the 256 MB Infinity Cache cannot hold them); time per launch = replay time / launches.
+    Algorithmic bytes per row: forward 2D + 4D in, 2D + 4D out, 4 (rstd); backward 2D + 4D + 4D + 4
+    in (dy, d stream, s, rstd), 2D + 4D out (dx, d residual)."""
+    import mote_amd.norm  # noqa: F401  (registers the ops)
+
+    D = D_MODEL
+    g = torch.Generator(device="cpu").manual_seed(5)
+    w = (torch.randn(D, generator=g) * 0.2 + 1.0).to(dev)
+    sets = []
+    for _ in range(copies):
+        x = torch.randn(rows, D, generator=g).to(torch.bfloat16).to(dev)
+        res = torch.randn(rows, D, generator=g).to(dev)
+        y, s_, rstd = torch.ops.mote.add_rms_norm(x, w, res, 1e-5, True, True)
+        dy = torch.randn(rows, D, generator=g).to(torch.bfloat16).to(dev)
+        dro = torch.randn(rows, D, generator=g).to(dev)
+        sets.append((x, res, s_, rstd, dy, dro))
+    torch.cuda.synchronize()
+    ops = torch.ops.mote
+
+    def fwd(i):
+        x, res = sets[i % copies][:2]
+        ops.add_rms_norm(x, w, res, 1e-5, True, True)
+
+    def bwd(i):
+        _, _, s_, rstd, dy, dro = sets[i % copies]
+        ops.add_rms_norm_bwd(dy, dro, s_, rstd, w, torch.bfloat16, True, torch.float32)
+
+    out = {}
+    side = torch.cuda.Stream()
+    for name, fn, per_row in (("fwd", fwd, 12 * D + 4), ("bwd", bwd, 16 * D + 4)):
+        for i in range(copies):
+            fn(i)
+        torch.cuda.synchronize()
+        side.wait_stream(torch.cuda.current_stream())
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(gr, stream=side):
+                for i in range(launches):
+                    fn(i)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        for _ in range(2):
+            gr.replay()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 10
+        t0.record()
+        for _ in range(reps):
+            gr.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        us = t0.elapsed_time(t1) * 1e3 / (reps * launches)
+        gbs = rows * per_row / (us * 1e-6) / 1e9
+        out[name] = dict(us_per_launch=round(us, 2), bytes_per_launch=rows * per_row, GBs=round(gbs, 1),
+                         frac_hbm=round(gbs / PEAK_HBM_GBS, 4))
+        del gr
+    log(f"[bench] add_rms_norm rows {rows} x {D}: fwd {out['fwd']['us_per_launch']:.2f} us "
+        f"({out['fwd']['GBs']:.0f} GB/s), bwd {out['bwd']['us_per_launch']:.2f} us ({out['bwd']['GBs']:.0f} GB/s)")
+    return dict(workload=f"add+RMSNorm pre-norm, {rows} rows x {D} (bf16 x, fp32 residual stream), HIP graph "
+                         f"of {launches} launches over {copies} input sets", rows=rows, D=D, **out)
+
+
+# ------------------------------------------------------------------------------------------------
 # CPU baseline: the oracle on the host cores
 # ------------------------------------------------------------------------------------------------
 def bench_cpu(T: int):
@@ -442,7 +511,7 @@ def main():
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--no-extra", action="store_true", help="skip the C2 / C5 lines")
+    ap.add_argument("--no-extra", action="store_true", help="skip the C2 / C5 / add+RMSNorm lines")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the Relation path is built and measured on a single GPU "
@@ -464,6 +533,8 @@ def main():
     if not args.no_extra:
         extra["c2_mote32m_stack"] = bench_c2(args.steps, args.warmup, dev)
         extra["c5_mote138m_prefill"] = bench_c5(max(3, args.steps // 4), min(args.warmup, 2), dev)
+        extra["add_rms_norm"] = {"T": bench_norm(st["T"], dev, copies=8),
+                                 "16T": bench_norm(16 * st["T"], dev, copies=1)}
     cpu = None if args.no_cpu else bench_cpu(st["T"])
     out = {
         "metric": METRIC,

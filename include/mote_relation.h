@@ -217,6 +217,63 @@ typedef struct mote_relation_decode_args {
 size_t mote_relation_decode_workspace(const mote_relation_decode_args* args);
 int mote_relation_decode(const mote_relation_decode_args* args, void* stream);
 
+/* ------------------------------------------------------------------------------------------------
+ * Fused residual add + RMSNorm (the pre-norm of every H-Net block and the final norm).
+ * Replaces: RMSNorm.forward(x, residual, prenorm, residual_in_fp32) (mote/model/norm.py:36-59), whose
+ * CUDA path calls mamba_ssm's Triton rms_norm_fn with the same semantics (norm.py:17-23, 48-50).
+ * Per row of D elements, in fp32: s = x + residual (residual == NULL: s = x), r = 1/sqrt(mean(s^2) +
+ * eps), y = s r weight. x, residual, y and residual_out are [rows, D] with unit element stride and a
+ * row stride each (elements); every dtype is MOTE_F32 or MOTE_BF16 independently (residual_in_fp32:
+ * residual and residual_out MOTE_F32). The sum is held in res_out_dtype: MOTE_BF16 rounds it before
+ * the norm, as `x + residual` in bf16 does (norm.py:51). residual_out (the new residual stream s) and
+ * rstd (r, fp32 [rows], kept for the backward) may be NULL. weight is fp32 [D]. Rows must start on
+ * 8-byte (bf16) / 16-byte (fp32) boundaries; 4 <= D <= 2048, D % 4 == 0. rows == 0 launches nothing
+ * (the data pointers may then be NULL); the backward then only sets dweight to 0.
+ * ------------------------------------------------------------------------------------------------ */
+typedef struct mote_add_rms_norm_args {
+  int dtype;            /* x */
+  int res_dtype;        /* residual */
+  int out_dtype;        /* y */
+  int res_out_dtype;    /* residual_out */
+  int rows, D;
+  float eps;
+  const void* x; int64_t x_sr;
+  const void* residual; int64_t res_sr;
+  const float* weight;
+  void* y; int64_t y_sr;
+  void* residual_out; int64_t res_out_sr;
+  float* rstd;
+} mote_add_rms_norm_args;
+
+int mote_add_rms_norm_fwd(const mote_add_rms_norm_args* args, void* stream);
+
+/* Backward of mote_add_rms_norm_fwd. With g = dy weight and the saved s (residual_out) and r (rstd):
+ * ds = r g - (r^3 / D) s sum(g s) + dres_out; dx = ds, dresidual = ds (NULL: no residual input),
+ * dweight = sum over rows of dy s r (fp32 [D], overwritten, fixed-order sum: reproducible).
+ * dres_out (the gradient reaching the returned residual stream) may be NULL. Workspace:
+ * mote_add_rms_norm_bwd_workspace() bytes of device memory, contents on entry do not matter. */
+typedef struct mote_add_rms_norm_bwd_args {
+  int dtype;            /* dy */
+  int dres_out_dtype;
+  int s_dtype;
+  int dx_dtype;
+  int dres_dtype;
+  int rows, D;
+  const void* dy; int64_t dy_sr;
+  const void* dres_out; int64_t dres_out_sr;
+  const void* s; int64_t s_sr;
+  const float* rstd;
+  const float* weight;
+  void* dx; int64_t dx_sr;
+  void* dresidual; int64_t dres_sr;
+  float* dweight;
+  void* workspace;
+  size_t workspace_bytes;
+} mote_add_rms_norm_bwd_args;
+
+size_t mote_add_rms_norm_bwd_workspace(const mote_add_rms_norm_bwd_args* args);
+int mote_add_rms_norm_bwd(const mote_add_rms_norm_bwd_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -84,6 +84,27 @@ class DecodeArgs(C.Structure):
     ]
 
 
+class NormArgs(C.Structure):
+    _fields_ = [
+        ("dtype", C.c_int), ("res_dtype", C.c_int), ("out_dtype", C.c_int), ("res_out_dtype", C.c_int),
+        ("rows", C.c_int), ("D", C.c_int), ("eps", C.c_float),
+        ("x", C.c_void_p), ("x_sr", C.c_int64), ("residual", C.c_void_p), ("res_sr", C.c_int64),
+        ("weight", C.c_void_p), ("y", C.c_void_p), ("y_sr", C.c_int64),
+        ("residual_out", C.c_void_p), ("res_out_sr", C.c_int64), ("rstd", C.c_void_p),
+    ]
+
+
+class NormBwdArgs(C.Structure):
+    _fields_ = [
+        ("dtype", C.c_int), ("dres_out_dtype", C.c_int), ("s_dtype", C.c_int), ("dx_dtype", C.c_int),
+        ("dres_dtype", C.c_int), ("rows", C.c_int), ("D", C.c_int),
+        ("dy", C.c_void_p), ("dy_sr", C.c_int64), ("dres_out", C.c_void_p), ("dres_out_sr", C.c_int64),
+        ("s", C.c_void_p), ("s_sr", C.c_int64), ("rstd", C.c_void_p), ("weight", C.c_void_p),
+        ("dx", C.c_void_p), ("dx_sr", C.c_int64), ("dresidual", C.c_void_p), ("dres_sr", C.c_int64),
+        ("dweight", C.c_void_p), ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
+    ]
+
+
 # every symbol the header declares, with its argument types
 EXPORTS = {
     "mote_last_error": ([], C.c_char_p),
@@ -97,6 +118,9 @@ EXPORTS = {
     "mote_rope_givens_bwd": ([C.POINTER(RopeBwdArgs), C.c_void_p], C.c_int),
     "mote_relation_decode_workspace": ([C.POINTER(DecodeArgs)], C.c_size_t),
     "mote_relation_decode": ([C.POINTER(DecodeArgs), C.c_void_p], C.c_int),
+    "mote_add_rms_norm_fwd": ([C.POINTER(NormArgs), C.c_void_p], C.c_int),
+    "mote_add_rms_norm_bwd_workspace": ([C.POINTER(NormBwdArgs)], C.c_size_t),
+    "mote_add_rms_norm_bwd": ([C.POINTER(NormBwdArgs), C.c_void_p], C.c_int),
 }
 
 _lock = threading.Lock()

@@ -75,4 +75,18 @@ int mote_relation_decode(const mote_relation_decode_args* args, void* stream) {
   return mote::launch_decode(args, reinterpret_cast<hipStream_t>(stream));
 }
 
+int mote_add_rms_norm_fwd(const mote_add_rms_norm_args* args, void* stream) {
+  mote::g_err[0] = 0;
+  return mote::launch_add_rms_norm_fwd(args, reinterpret_cast<hipStream_t>(stream));
+}
+
+size_t mote_add_rms_norm_bwd_workspace(const mote_add_rms_norm_bwd_args* args) {
+  return args ? mote::add_rms_norm_bwd_workspace_bytes(args) : 0;
+}
+
+int mote_add_rms_norm_bwd(const mote_add_rms_norm_bwd_args* args, void* stream) {
+  mote::g_err[0] = 0;
+  return mote::launch_add_rms_norm_bwd(args, reinterpret_cast<hipStream_t>(stream));
+}
+
 }  // extern "C"
