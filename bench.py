@@ -471,6 +471,82 @@ def bench_norm(rows: int, dev, copies: int, launches: int = 24):
 
 
 # ------------------------------------------------------------------------------------------------
+# chunk gather and EMA dechunk (either side of the main network)
+# ------------------------------------------------------------------------------------------------
+def bench_dc(B: int, dev, copies: int, launches: int = 20):
+    """mote::chunk_route / chunk_gather / chunk_gather_bwd / dechunk / dechunk_bwd at the Mote-96M
+    shape: B windows of 16384 bytes, Bernoulli(1/3.3) boundaries (seed 2, first byte forced), D0 = 512,
+    bf16 hidden states, fp32 boundary probabilities, chunk rows padded to a multiple of 64. Each op is a
+    HIP graph of `launches` launches rotating over `copies` input sets. Algorithmic bytes per launch:
+    route L (mask) + 8 L (cum, perm); gather 2 M D 2 (rows in and out); gather_bwd M D 2 + L D 2;
+    dechunk M D 2 (x) + L D 2 (bytes out) + M D 4 (z kept) + 8 M (p and positions); dechunk_bwd L D 2
+    (dout) + M D 2 (x) + M D 4 (z) + M D 2 (dx) + 16 L (dprob) + 8 M."""
+    from mote_amd import dc
+
+    Ln, D = 16384, 512
+    g = torch.Generator().manual_seed(2)
+    sets = []
+    for _ in range(copies):
+        mask = torch.rand(B, Ln, generator=g) < (1.0 / 3.3)
+        mask[:, 0] = True
+        mask = mask.to(dev)
+        x = torch.randn(B, Ln, D, generator=g).to(torch.bfloat16).to(dev)
+        prob = torch.rand(B, Ln, 2, generator=g).to(dev)
+        cum, perm, num, _ = dc.chunk_route(mask)
+        M = min(Ln, -(-int(num.max()) // 64) * 64)
+        hc = dc.chunk_gather(x, perm, num, mask, cum, M)
+        out, w = dc.dechunk(hc, prob, perm, num, mask, cum, 1e-4, None)
+        dy = torch.randn(B, Ln, D, generator=g).to(torch.bfloat16).to(dev)
+        sets.append(dict(mask=mask, x=x, prob=prob, cum=cum, perm=perm, num=num, M=M, hc=hc, w=w, dy=dy))
+    torch.cuda.synchronize()
+    Ms = sorted({s_["M"] for s_ in sets})
+    M = sum(s_["M"] for s_ in sets) / copies
+    ops = {
+        "route": (lambda s_: dc.chunk_route(s_["mask"]), B * Ln * 9),
+        "gather": (lambda s_: dc.chunk_gather(s_["x"], s_["perm"], s_["num"], s_["mask"], s_["cum"], s_["M"]),
+                   2 * B * M * D * 2),
+        "gather_bwd": (lambda s_: dc.chunk_gather_bwd(s_["hc"], s_["mask"], s_["cum"], s_["num"], Ln),
+                       B * M * D * 2 + B * Ln * D * 2),
+        "dechunk": (lambda s_: dc.dechunk(s_["hc"], s_["prob"], s_["perm"], s_["num"], s_["mask"], s_["cum"], 1e-4,
+                                          None), B * (M * D * 2 + Ln * D * 2 + M * D * 4 + 8 * M)),
+        "dechunk_bwd": (lambda s_: dc.dechunk_bwd(s_["dy"], s_["hc"], s_["prob"], s_["perm"], s_["num"], s_["mask"],
+                                                  s_["cum"], s_["w"], 1e-4),
+                        B * (Ln * D * 2 + M * D * 2 + M * D * 4 + M * D * 2 + 16 * Ln + 8 * M)),
+    }
+    res = {}
+    side = torch.cuda.Stream()
+    for name, (fn, nbytes) in ops.items():
+        for s_ in sets:
+            fn(s_)
+        torch.cuda.synchronize()
+        side.wait_stream(torch.cuda.current_stream())
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(gr, stream=side):
+                for i in range(launches):
+                    fn(sets[i % copies])
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        gr.replay()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 10
+        t0.record()
+        for _ in range(reps):
+            gr.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        us = t0.elapsed_time(t1) * 1e3 / (reps * launches)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        res[name] = dict(us_per_launch=round(us, 2), bytes_per_launch=int(nbytes), GBs=round(gbs, 1),
+                         frac_hbm=round(gbs / PEAK_HBM_GBS, 4))
+        del gr
+    log(f"[bench] chunk/dechunk B={B} (M {Ms}): " + ", ".join(f"{k} {v['us_per_launch']:.1f} us" for k, v in res.items()))
+    return dict(workload=f"chunk gather + EMA dechunk, {B} x 16384 bytes, D0 = 512 (bf16 hidden, fp32 p), bucket 64, "
+                         f"HIP graph of {launches} launches over {copies} input sets", B=B, L=Ln, D=D, M=Ms, **res)
+
+
+# ------------------------------------------------------------------------------------------------
 # CPU baseline: the oracle on the host cores
 # ------------------------------------------------------------------------------------------------
 def bench_cpu(T: int):
@@ -511,7 +587,7 @@ def main():
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--no-extra", action="store_true", help="skip the C2 / C5 / add+RMSNorm lines")
+    ap.add_argument("--no-extra", action="store_true", help="skip the C2 / C5 / add+RMSNorm / dechunk lines")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the Relation path is built and measured on a single GPU "
@@ -535,6 +611,7 @@ def main():
         extra["c5_mote138m_prefill"] = bench_c5(max(3, args.steps // 4), min(args.warmup, 2), dev)
         extra["add_rms_norm"] = {"T": bench_norm(st["T"], dev, copies=8),
                                  "16T": bench_norm(16 * st["T"], dev, copies=1)}
+        extra["chunk_dechunk"] = {"B1": bench_dc(1, dev, copies=8), "B8": bench_dc(8, dev, copies=1)}
     cpu = None if args.no_cpu else bench_cpu(st["T"])
     out = {
         "metric": METRIC,

@@ -274,6 +274,144 @@ typedef struct mote_add_rms_norm_bwd_args {
 size_t mote_add_rms_norm_bwd_workspace(const mote_add_rms_norm_bwd_args* args);
 int mote_add_rms_norm_bwd(const mote_add_rms_norm_bwd_args* args, void* stream);
 
+/* ------------------------------------------------------------------------------------------------
+ * Chunking either side of the main network (mote/model/dc.py:192-352).
+ *
+ * mote_chunk_route: per row of the boundary mask (bool / uint8 [B, L], row stride mask_sr bytes),
+ * cum[b, t] = number of boundaries in [0, t] (int32 [B, L]), perm[b, :] = the boundary positions in
+ * order followed by the other positions in order (int32 [B, L]; the reference's
+ * argsort(arange(L) + L * !mask), dc.py:212-213 and :320-322) and num[b] = the row's boundary count
+ * (dc.py:209). cu_seqlens (int32 [B + 1], may be NULL) receives 0, num[0], num[0] + num[1], ...: the
+ * packed layout of the Relation varlen entry point. No host synchronisation: a caller that needs M
+ * on the host (the reference's int(num.max()), dc.py:210) reads num.
+ * Replaces: the index computation of ChunkLayer.forward and DeChunkLayer.forward (dc.py:209-214, 320-327).
+ * ------------------------------------------------------------------------------------------------ */
+typedef struct mote_chunk_route_args {
+  int B, L;
+  const uint8_t* mask; int64_t mask_sr;
+  int32_t* cum;
+  int32_t* perm;
+  int32_t* num;
+  int32_t* cu_seqlens;
+} mote_chunk_route_args;
+
+int mote_chunk_route(const mote_chunk_route_args* args, void* stream);
+
+/* mote_chunk_gather: out[b, m] = hidden[b, perm[b, m]] for m < M (M <= L; rows past num[b] are the
+ * first non-boundary positions, the reference's padded tail, dc.py:196-199, 214-216). With cu_seqlens
+ * given, only rows m < num[b] are written, to out row cu_seqlens[b] + m (o_sb unused): the packed
+ * varlen layout. hidden [B, L, D] and out have unit element stride, strides in elements; rows are
+ * whole 16-byte units (D % 4 == 0 fp32, D % 8 == 0 bf16) on 16-byte boundaries.
+ * Replaces: ChunkLayer.forward's gather (dc.py:214-216). */
+typedef struct mote_chunk_gather_args {
+  int dtype;
+  int B, L, M, D;
+  const void* hidden; int64_t h_sb, h_sr;
+  const int32_t* perm;
+  const int32_t* num;
+  const int32_t* cu_seqlens;
+  void* out; int64_t o_sb, o_sr;
+} mote_chunk_gather_args;
+
+int mote_chunk_gather(const mote_chunk_gather_args* args, void* stream);
+
+/* Backward of mote_chunk_gather: dhidden[b, t] = dout row of t when t was gathered, else 0 (every
+ * row of dhidden is written). Same layout rules; dout is [B, M, D] or packed [total, D].
+ * Replaces: autograd of torch.gather in ChunkLayer.forward. */
+typedef struct mote_chunk_gather_bwd_args {
+  int dtype;
+  int B, L, M, D;
+  const void* dout; int64_t g_sb, g_sr;
+  const uint8_t* mask; int64_t mask_sr;
+  const int32_t* cum;
+  const int32_t* num;
+  const int32_t* cu_seqlens;
+  void* dhidden; int64_t dh_sb, dh_sr;
+} mote_chunk_gather_bwd_args;
+
+int mote_chunk_gather_bwd(const mote_chunk_gather_bwd_args* args, void* stream);
+
+/* mote_dechunk_fwd: DeChunkLayer.forward (dc.py:312-335). p_m = clamp(prob[b, perm[b, m], 1], eps,
+ * 1 - eps); z_m = p_m hidden[b, m] + (1 - p_m) z_{m-1} in fp32 (z_{-1} = init[b] or 0), for m <
+ * num[b]; out[b, t] = z of the last boundary at or before t (perm, num, cum from mote_chunk_route). Bytes before the first boundary read
+ * init when it is given (the decode-state form, dc.py:328-332), else z_0 (dc.py:326). hidden is
+ * [B, M, D] (M >= num[b]; rows past num[b] are not read), prob [B, L, 2] (strides in elements), out
+ * [B, L, D] in hidden's dtype (out_dtype == dtype). w (fp32 [B, M, D], may be NULL) keeps
+ * hidden_m - z_{m-1} for the backward. The arithmetic that produces z_m reads chunks <= m only, in an
+ * order fixed by m: outputs are causal bit for bit. The caller updates its state from out[:, L - 1]
+ * (dc.py:336-337). D even; rows on 2-element boundaries.
+ * Workspace: mote_dechunk_workspace() bytes, contents on entry do not matter. */
+typedef struct mote_dechunk_args {
+  int dtype;        /* hidden */
+  int prob_dtype;
+  int out_dtype;
+  int B, L, M, D;
+  float eps;
+  const void* hidden; int64_t h_sb, h_sr;
+  const void* prob; int64_t p_sb, p_sr;
+  const int32_t* perm;
+  const int32_t* num;
+  const int32_t* cum;
+  const float* init;
+  void* out; int64_t o_sb, o_sr;
+  float* w;
+  void* workspace;
+  size_t workspace_bytes;
+} mote_dechunk_args;
+
+size_t mote_dechunk_workspace(const mote_dechunk_args* args);
+int mote_dechunk_fwd(const mote_dechunk_args* args, void* stream);
+
+/* Backward of mote_dechunk_fwd without init (the training form): with ds_m the sum of dout over the
+ * bytes of chunk m, g_m = ds_m + (1 - p_{m+1}) g_{m+1}; dhidden[b, m] = p_m g_m (0 for rows no byte
+ * reads), dprob[b, t, 1] = sum_d g_m (hidden_m - z_{m-1}) at the position t of chunk m when eps <=
+ * prob <= 1 - eps (the clamp's gradient), every other dprob entry 0 (every entry is written). w is
+ * the forward's w; dout and dhidden are in hidden's dtype. Sums over channels and bytes run in a
+ * fixed order: reproducible.
+ * Replaces: autograd of DeChunkLayer.forward / _ema_chunked (dc.py:236-282, 312-335). */
+typedef struct mote_dechunk_bwd_args {
+  int dtype;        /* hidden */
+  int prob_dtype;
+  int dout_dtype;
+  int dx_dtype;
+  int dprob_dtype;
+  int B, L, M, D;
+  float eps;
+  const void* dout; int64_t g_sb, g_sr;
+  const void* hidden; int64_t h_sb, h_sr;
+  const void* prob; int64_t p_sb, p_sr;
+  const int32_t* perm;
+  const int32_t* num;
+  const uint8_t* mask; int64_t mask_sr;
+  const int32_t* cum;
+  const float* w;
+  void* dhidden; int64_t dh_sb, dh_sr;
+  void* dprob; int64_t dp_sb, dp_sr;
+  void* workspace;
+  size_t workspace_bytes;
+} mote_dechunk_bwd_args;
+
+size_t mote_dechunk_bwd_workspace(const mote_dechunk_bwd_args* args);
+int mote_dechunk_bwd(const mote_dechunk_bwd_args* args, void* stream);
+
+/* mote_dechunk_step: one decode byte (dc.py:342-352). For row b with mask[b]: p = clamp(prob[b, 1])
+ * (rounded to prob's dtype, then to the state's), cur = hidden[r] where r counts the set mask entries
+ * before b; else p = 0, cur = 0. last_value[b] = p cur + (1 - p) last_value[b], every operation
+ * rounded to the state's dtype as the reference's eager ops are; out[b] (may be NULL) gets the same.
+ * Replaces: DeChunkLayer.step. */
+typedef struct mote_dechunk_step_args {
+  int prob_dtype, hidden_dtype, state_dtype;
+  int B, D;
+  float eps;
+  const uint8_t* mask;
+  const void* prob; int64_t p_sr;
+  const void* hidden; int64_t h_sr;
+  void* last_value; int64_t l_sr;
+  void* out; int64_t o_sr;
+} mote_dechunk_step_args;
+
+int mote_dechunk_step(const mote_dechunk_step_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -105,6 +105,69 @@ class NormBwdArgs(C.Structure):
     ]
 
 
+class ChunkRouteArgs(C.Structure):
+    _fields_ = [
+        ("B", C.c_int), ("L", C.c_int), ("mask", C.c_void_p), ("mask_sr", C.c_int64),
+        ("cum", C.c_void_p), ("perm", C.c_void_p), ("num", C.c_void_p), ("cu_seqlens", C.c_void_p),
+    ]
+
+
+class ChunkGatherArgs(C.Structure):
+    _fields_ = [
+        ("dtype", C.c_int), ("B", C.c_int), ("L", C.c_int), ("M", C.c_int), ("D", C.c_int),
+        ("hidden", C.c_void_p), ("h_sb", C.c_int64), ("h_sr", C.c_int64),
+        ("perm", C.c_void_p), ("num", C.c_void_p), ("cu_seqlens", C.c_void_p),
+        ("out", C.c_void_p), ("o_sb", C.c_int64), ("o_sr", C.c_int64),
+    ]
+
+
+class ChunkGatherBwdArgs(C.Structure):
+    _fields_ = [
+        ("dtype", C.c_int), ("B", C.c_int), ("L", C.c_int), ("M", C.c_int), ("D", C.c_int),
+        ("dout", C.c_void_p), ("g_sb", C.c_int64), ("g_sr", C.c_int64),
+        ("mask", C.c_void_p), ("mask_sr", C.c_int64), ("cum", C.c_void_p), ("num", C.c_void_p),
+        ("cu_seqlens", C.c_void_p), ("dhidden", C.c_void_p), ("dh_sb", C.c_int64), ("dh_sr", C.c_int64),
+    ]
+
+
+class DechunkArgs(C.Structure):
+    _fields_ = [
+        ("dtype", C.c_int), ("prob_dtype", C.c_int), ("out_dtype", C.c_int),
+        ("B", C.c_int), ("L", C.c_int), ("M", C.c_int), ("D", C.c_int), ("eps", C.c_float),
+        ("hidden", C.c_void_p), ("h_sb", C.c_int64), ("h_sr", C.c_int64),
+        ("prob", C.c_void_p), ("p_sb", C.c_int64), ("p_sr", C.c_int64),
+        ("perm", C.c_void_p), ("num", C.c_void_p), ("cum", C.c_void_p), ("init", C.c_void_p),
+        ("out", C.c_void_p), ("o_sb", C.c_int64), ("o_sr", C.c_int64), ("w", C.c_void_p),
+        ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
+    ]
+
+
+class DechunkBwdArgs(C.Structure):
+    _fields_ = [
+        ("dtype", C.c_int), ("prob_dtype", C.c_int), ("dout_dtype", C.c_int), ("dx_dtype", C.c_int),
+        ("dprob_dtype", C.c_int), ("B", C.c_int), ("L", C.c_int), ("M", C.c_int), ("D", C.c_int),
+        ("eps", C.c_float),
+        ("dout", C.c_void_p), ("g_sb", C.c_int64), ("g_sr", C.c_int64),
+        ("hidden", C.c_void_p), ("h_sb", C.c_int64), ("h_sr", C.c_int64),
+        ("prob", C.c_void_p), ("p_sb", C.c_int64), ("p_sr", C.c_int64),
+        ("perm", C.c_void_p), ("num", C.c_void_p), ("mask", C.c_void_p), ("mask_sr", C.c_int64),
+        ("cum", C.c_void_p), ("w", C.c_void_p),
+        ("dhidden", C.c_void_p), ("dh_sb", C.c_int64), ("dh_sr", C.c_int64),
+        ("dprob", C.c_void_p), ("dp_sb", C.c_int64), ("dp_sr", C.c_int64),
+        ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
+    ]
+
+
+class DechunkStepArgs(C.Structure):
+    _fields_ = [
+        ("prob_dtype", C.c_int), ("hidden_dtype", C.c_int), ("state_dtype", C.c_int),
+        ("B", C.c_int), ("D", C.c_int), ("eps", C.c_float),
+        ("mask", C.c_void_p), ("prob", C.c_void_p), ("p_sr", C.c_int64),
+        ("hidden", C.c_void_p), ("h_sr", C.c_int64), ("last_value", C.c_void_p), ("l_sr", C.c_int64),
+        ("out", C.c_void_p), ("o_sr", C.c_int64),
+    ]
+
+
 # every symbol the header declares, with its argument types
 EXPORTS = {
     "mote_last_error": ([], C.c_char_p),
@@ -121,6 +184,14 @@ EXPORTS = {
     "mote_add_rms_norm_fwd": ([C.POINTER(NormArgs), C.c_void_p], C.c_int),
     "mote_add_rms_norm_bwd_workspace": ([C.POINTER(NormBwdArgs)], C.c_size_t),
     "mote_add_rms_norm_bwd": ([C.POINTER(NormBwdArgs), C.c_void_p], C.c_int),
+    "mote_chunk_route": ([C.POINTER(ChunkRouteArgs), C.c_void_p], C.c_int),
+    "mote_chunk_gather": ([C.POINTER(ChunkGatherArgs), C.c_void_p], C.c_int),
+    "mote_chunk_gather_bwd": ([C.POINTER(ChunkGatherBwdArgs), C.c_void_p], C.c_int),
+    "mote_dechunk_workspace": ([C.POINTER(DechunkArgs)], C.c_size_t),
+    "mote_dechunk_fwd": ([C.POINTER(DechunkArgs), C.c_void_p], C.c_int),
+    "mote_dechunk_bwd_workspace": ([C.POINTER(DechunkBwdArgs)], C.c_size_t),
+    "mote_dechunk_bwd": ([C.POINTER(DechunkBwdArgs), C.c_void_p], C.c_int),
+    "mote_dechunk_step": ([C.POINTER(DechunkStepArgs), C.c_void_p], C.c_int),
 }
 
 _lock = threading.Lock()

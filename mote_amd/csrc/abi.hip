@@ -89,4 +89,42 @@ int mote_add_rms_norm_bwd(const mote_add_rms_norm_bwd_args* args, void* stream) 
   return mote::launch_add_rms_norm_bwd(args, reinterpret_cast<hipStream_t>(stream));
 }
 
+int mote_chunk_route(const mote_chunk_route_args* args, void* stream) {
+  mote::g_err[0] = 0;
+  return mote::launch_chunk_route(args, reinterpret_cast<hipStream_t>(stream));
+}
+
+int mote_chunk_gather(const mote_chunk_gather_args* args, void* stream) {
+  mote::g_err[0] = 0;
+  return mote::launch_chunk_gather(args, reinterpret_cast<hipStream_t>(stream));
+}
+
+int mote_chunk_gather_bwd(const mote_chunk_gather_bwd_args* args, void* stream) {
+  mote::g_err[0] = 0;
+  return mote::launch_chunk_gather_bwd(args, reinterpret_cast<hipStream_t>(stream));
+}
+
+size_t mote_dechunk_workspace(const mote_dechunk_args* args) {
+  return args ? mote::dechunk_workspace_bytes(args) : 0;
+}
+
+int mote_dechunk_fwd(const mote_dechunk_args* args, void* stream) {
+  mote::g_err[0] = 0;
+  return mote::launch_dechunk_fwd(args, reinterpret_cast<hipStream_t>(stream));
+}
+
+size_t mote_dechunk_bwd_workspace(const mote_dechunk_bwd_args* args) {
+  return args ? mote::dechunk_bwd_workspace_bytes(args) : 0;
+}
+
+int mote_dechunk_bwd(const mote_dechunk_bwd_args* args, void* stream) {
+  mote::g_err[0] = 0;
+  return mote::launch_dechunk_bwd(args, reinterpret_cast<hipStream_t>(stream));
+}
+
+int mote_dechunk_step(const mote_dechunk_step_args* args, void* stream) {
+  mote::g_err[0] = 0;
+  return mote::launch_dechunk_step(args, reinterpret_cast<hipStream_t>(stream));
+}
+
 }  // extern "C"

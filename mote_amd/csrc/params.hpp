@@ -41,6 +41,14 @@ size_t decode_workspace_bytes(const mote_relation_decode_args* a);
 int launch_add_rms_norm_fwd(const mote_add_rms_norm_args* a, hipStream_t stream);
 int launch_add_rms_norm_bwd(const mote_add_rms_norm_bwd_args* a, hipStream_t stream);
 size_t add_rms_norm_bwd_workspace_bytes(const mote_add_rms_norm_bwd_args* a);
+int launch_chunk_route(const mote_chunk_route_args* a, hipStream_t stream);
+int launch_chunk_gather(const mote_chunk_gather_args* a, hipStream_t stream);
+int launch_chunk_gather_bwd(const mote_chunk_gather_bwd_args* a, hipStream_t stream);
+size_t dechunk_workspace_bytes(const mote_dechunk_args* a);
+int launch_dechunk_fwd(const mote_dechunk_args* a, hipStream_t stream);
+size_t dechunk_bwd_workspace_bytes(const mote_dechunk_bwd_args* a);
+int launch_dechunk_bwd(const mote_dechunk_bwd_args* a, hipStream_t stream);
+int launch_dechunk_step(const mote_dechunk_step_args* a, hipStream_t stream);
 
 // Error reporting shared by the launchers (thread-local text, see abi.cpp).
 int set_error(int code, const char* fmt, ...);
