@@ -159,8 +159,9 @@ typedef struct mote_rope_givens_bwd_args {
   int B, T, H, D, pos0, layer_parity;
   const float* inv_freq;
   const float* theta;
-  const void* qkv;
+  const void* qkv;       /* only its I~ columns are read (for d theta) */
   int64_t qkv_sb, qkv_sr;
+  int qkv_info_only;     /* 1: qkv holds the I~ projections alone ([B, T, H*D], e.g. mote_qkv_rope_fwd's info_raw) */
   mote_view dp1, dp2, dinfo;
   void* dqkv;
   int64_t dqkv_sb, dqkv_sr;
@@ -273,6 +274,34 @@ typedef struct mote_add_rms_norm_bwd_args {
 
 size_t mote_add_rms_norm_bwd_workspace(const mote_add_rms_norm_bwd_args* args);
 int mote_add_rms_norm_bwd(const mote_add_rms_norm_bwd_args* args, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * Fused projection prologue (bf16): qkv = x [w1; w2; wi]^T, RoPE on p1 / p2 and the Givens rotation
+ * on I~ in the product's epilogue, written into the three [B, H, T, D] head views; the same results as
+ * the projection (x [w1; w2; wi]^T rounded to bf16) followed by mote_rope_givens_fwd.
+ * Replaces: the three projections and the RoPE / Givens of FullRelation.forward
+ * (mote/model/relation.py:199-215); the unfused path stays for QK-Norm, fp32 and other head dims.
+ * x: [B, T, H*D] bf16 with the batches back to back (x_sb == T x_sr); w: [3 H D, H D] bf16 rows
+ * w1 | w2 | wi (row stride w_sr); D in {64, 96, 128}; H even; H D % 32 == 0. inv_freq NULL: no RoPE;
+ * theta NULL: no Givens. info_raw (may be NULL) receives the I~ projections before the rotation,
+ * for mote_rope_givens_bwd (qkv_info_only = 1). Workspace: mote_qkv_rope_workspace() bytes (the
+ * cos / sin table of the T positions). All rows on 16-byte boundaries.
+ * ------------------------------------------------------------------------------------------------ */
+typedef struct mote_qkv_rope_args {
+  int B, T, H, D;
+  int pos0, layer_parity;
+  const void* x; int64_t x_sb, x_sr;
+  const void* w; int64_t w_sr;
+  const float* inv_freq;
+  const float* theta;
+  mote_view p1, p2, info;
+  void* info_raw; int64_t ir_sb, ir_sr;
+  void* workspace;
+  size_t workspace_bytes;
+} mote_qkv_rope_args;
+
+size_t mote_qkv_rope_workspace(const mote_qkv_rope_args* args);
+int mote_qkv_rope_fwd(const mote_qkv_rope_args* args, void* stream);
 
 /* ------------------------------------------------------------------------------------------------
  * Chunking either side of the main network (mote/model/dc.py:192-352).

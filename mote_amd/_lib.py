@@ -65,7 +65,7 @@ class RopeBwdArgs(C.Structure):
     _fields_ = [
         ("dtype", C.c_int), ("B", C.c_int), ("T", C.c_int), ("H", C.c_int), ("D", C.c_int), ("pos0", C.c_int),
         ("layer_parity", C.c_int), ("inv_freq", C.c_void_p), ("theta", C.c_void_p),
-        ("qkv", C.c_void_p), ("qkv_sb", C.c_int64), ("qkv_sr", C.c_int64),
+        ("qkv", C.c_void_p), ("qkv_sb", C.c_int64), ("qkv_sr", C.c_int64), ("qkv_info_only", C.c_int),
         ("dp1", View), ("dp2", View), ("dinfo", View),
         ("dqkv", C.c_void_p), ("dqkv_sb", C.c_int64), ("dqkv_sr", C.c_int64),
         ("dtheta", C.c_void_p), ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
@@ -102,6 +102,16 @@ class NormBwdArgs(C.Structure):
         ("s", C.c_void_p), ("s_sr", C.c_int64), ("rstd", C.c_void_p), ("weight", C.c_void_p),
         ("dx", C.c_void_p), ("dx_sr", C.c_int64), ("dresidual", C.c_void_p), ("dres_sr", C.c_int64),
         ("dweight", C.c_void_p), ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
+    ]
+
+
+class QkvRopeArgs(C.Structure):
+    _fields_ = [
+        ("B", C.c_int), ("T", C.c_int), ("H", C.c_int), ("D", C.c_int), ("pos0", C.c_int), ("layer_parity", C.c_int),
+        ("x", C.c_void_p), ("x_sb", C.c_int64), ("x_sr", C.c_int64), ("w", C.c_void_p), ("w_sr", C.c_int64),
+        ("inv_freq", C.c_void_p), ("theta", C.c_void_p), ("p1", View), ("p2", View), ("info", View),
+        ("info_raw", C.c_void_p), ("ir_sb", C.c_int64), ("ir_sr", C.c_int64),
+        ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
     ]
 
 
@@ -184,6 +194,8 @@ EXPORTS = {
     "mote_add_rms_norm_fwd": ([C.POINTER(NormArgs), C.c_void_p], C.c_int),
     "mote_add_rms_norm_bwd_workspace": ([C.POINTER(NormBwdArgs)], C.c_size_t),
     "mote_add_rms_norm_bwd": ([C.POINTER(NormBwdArgs), C.c_void_p], C.c_int),
+    "mote_qkv_rope_workspace": ([C.POINTER(QkvRopeArgs)], C.c_size_t),
+    "mote_qkv_rope_fwd": ([C.POINTER(QkvRopeArgs), C.c_void_p], C.c_int),
     "mote_chunk_route": ([C.POINTER(ChunkRouteArgs), C.c_void_p], C.c_int),
     "mote_chunk_gather": ([C.POINTER(ChunkGatherArgs), C.c_void_p], C.c_int),
     "mote_chunk_gather_bwd": ([C.POINTER(ChunkGatherBwdArgs), C.c_void_p], C.c_int),

@@ -89,6 +89,15 @@ int mote_add_rms_norm_bwd(const mote_add_rms_norm_bwd_args* args, void* stream) 
   return mote::launch_add_rms_norm_bwd(args, reinterpret_cast<hipStream_t>(stream));
 }
 
+size_t mote_qkv_rope_workspace(const mote_qkv_rope_args* args) {
+  return args ? mote::qkv_rope_workspace_bytes(args) : 0;
+}
+
+int mote_qkv_rope_fwd(const mote_qkv_rope_args* args, void* stream) {
+  mote::g_err[0] = 0;
+  return mote::launch_qkv_rope_fwd(args, reinterpret_cast<hipStream_t>(stream));
+}
+
 int mote_chunk_route(const mote_chunk_route_args* args, void* stream) {
   mote::g_err[0] = 0;
   return mote::launch_chunk_route(args, reinterpret_cast<hipStream_t>(stream));

@@ -1,0 +1,324 @@
+// Fused projection prologue of FullRelation (mote/model/relation.py:199-215): the QKV product
+// x [w1; w2; wi]^T with RoPE on p1 / p2 and the Givens head-pair rotation on I~ in its epilogue,
+// written straight into the [B, T, H, dh] layout the Relation kernels and the arena read.
+//
+// Product. C^T = W X^T on v_mfma_f32_16x16x32_bf16: a workgroup (8 waves) owns 256 tokens and the
+// 2 dh output features of one head pair of one projection (p1, p2: heads 2k, 2k+1; I~: the Givens
+// pair of the layer's parity, (2k, 2k+1) or (2k+1, 2k+2 mod H)). Wave w holds head (w & 1) for tokens
+// 64 (w >> 1) .. +63: dh/16 x 4 accumulator tiles, features in the rows, tokens in the columns, so
+// a lane ends with 4 consecutive features of one token. k advances 32 at a time through a ring of
+// four LDS stages filled by direct global -> LDS transfers (16 token or weight rows x 64 bytes per
+// wave instruction, chunks XOR-swizzled within a row). 256 x 2 dh outputs per 32-wide stage keep the
+// L2 -> LDS traffic at about 110 flop per byte (dh 96).
+//
+// Epilogue. The product, rounded to bf16 (the projection output the reference rotates), goes to a
+// padded LDS tile [256 tokens][2 dh]; then every thread takes 16-byte chunks of it with their partner
+// chunks (RoPE: the other half of the head, relation.py:53-58; Givens: the same chunk of the pair's
+// other head, :160-174) and stores out = x C + y S, with C, S the bf16-rounded factors (cos / sin of
+// float(pos) * inv_freq[k] from a table kernel, cos / sin of theta), exactly as the unfused
+// rope_givens kernels compute them. Optionally the pre-rotation I~ is kept for the backward (d theta).
+#include "common.hpp"
+#include "params.hpp"
+#include "tiles.hpp"
+
+namespace mote {
+
+constexpr int kQkvTok = 256;     // tokens per workgroup
+constexpr int kQkvNW = 8;        // waves per workgroup
+constexpr int kQkvK = 32;        // k per stage
+constexpr int kQkvStg = 4;       // ring depth
+constexpr int kQkvPad = 8;       // bf16 elements of padding per output-tile row
+
+struct QkvParams {
+  const bf16_t* x; int64_t x_sr;           // [M, K] token rows (M = B * T)
+  const bf16_t* w; int64_t w_sr;           // [3 H dh, K]
+  const uint32_t* tab;                     // [T][dh / 2] bf16 cos | bf16 sin << 16, or null (no RoPE)
+  const float* theta;                      // [H / 2] or null (no Givens)
+  bf16_t* o1; int64_t o1_sb, o1_sh, o1_sr;
+  bf16_t* o2; int64_t o2_sb, o2_sh, o2_sr;
+  bf16_t* o3; int64_t o3_sb, o3_sh, o3_sr;
+  bf16_t* iraw; int64_t ir_sb, ir_sr;      // [B, T, H dh] pre-rotation I~, or null
+  int B, T, H, K, M, parity, nk;
+  int ntok, ncol;                          // token tiles, column tiles (3 H / 2)
+};
+
+template <int DH>
+struct QkvShape {
+  static constexpr int NF = DH / 16;                  // feature tiles per head
+  static constexpr int ROWS = 2 * DH + kQkvTok;       // staged rows per stage: W head 0 | W head 1 | X
+  static constexpr int NINS = ROWS / 16;              // wave instructions per stage
+  static constexpr int PER = (NINS + kQkvNW - 1) / kQkvNW;  // per wave (waves >= NINS % NW issue one
+  static constexpr int FULL = NINS % kQkvNW == 0 ? kQkvNW : NINS % kQkvNW;  // fewer when NINS % NW != 0)
+  static constexpr int STAGE = ROWS * kQkvK;          // bf16 elements
+  static constexpr int OUTW = 2 * DH + kQkvPad;
+  static constexpr int NCH = 2 * DH / 8;              // 16-byte chunks per output-tile row
+  static constexpr int LDS = kQkvStg * STAGE > kQkvTok * OUTW ? kQkvStg * STAGE : kQkvTok * OUTW;
+};
+
+// rope table: tab[t][k] = bf16(cos a) | bf16(sin a) << 16, a = float(pos0 + t) * inv_freq[k]
+__global__ void __launch_bounds__(256) rope_table_kernel(const float* inv_freq, int pos0, int T, int half,
+                                                         uint32_t* tab) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= int64_t(T) * half) return;
+  const int t = int(i / half), k = int(i % half);
+  float sn, cs;
+  sincosf((float)(pos0 + t) * inv_freq[k], &sn, &cs);
+  tab[i] = uint32_t(f2bf(cs)) | (uint32_t(f2bf(sn)) << 16);
+}
+
+template <int DH>
+__global__ void __launch_bounds__(64 * kQkvNW) qkv_rope_kernel(const QkvParams p) {
+  using S = QkvShape<DH>;
+  using E = Elem<bf16_t>;
+  __shared__ __align__(16) bf16_t smem[S::LDS];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // workgroup id -> (token tile, column tile): workgroups go round-robin over the 8 XCDs, so XCD j
+  // takes the j-th contiguous run of the (token tile, column) order: a few token tiles with all their
+  // column tiles, which its L2 holds while they are in use
+  const int nwg = p.ntok * p.ncol, per = (nwg + 7) / 8;
+  const int seq = (blockIdx.x % 8) * per + blockIdx.x / 8;
+  if (seq >= nwg) return;
+  const int r0 = (seq / p.ncol) * kQkvTok;
+  const int colt = seq % p.ncol;
+  const int npair = p.H / 2;
+  const int part = colt / npair, hp = colt % npair;
+  int h0 = 2 * hp, h1 = 2 * hp + 1;
+  if (part == 2 && p.parity) {
+    h0 = 2 * hp + 1;
+    h1 = (2 * hp + 2) % p.H;
+  }
+  const int HD = p.H * DH;
+  const bf16_t* wb0 = p.w + int64_t(part * HD + h0 * DH) * p.w_sr;
+  const bf16_t* wb1 = p.w + int64_t(part * HD + h1 * DH) * p.w_sr;
+  const bf16_t* xb = p.x + int64_t(r0) * p.x_sr;
+  const bool full = r0 + kQkvTok <= p.M;
+
+  // staging: instruction g covers stage rows 16 g .. 16 g + 15; lane l takes row 16 g + l / 4 and
+  // physical chunk l % 4, i.e. logical chunk (l % 4) ^ swz, swz = (row >> 2) & 3 = (l >> 4) & 3
+  const int lrow = lane >> 2, lch = (lane & 3) ^ ((lane >> 4) & 3);
+  uint32_t voff[S::PER];
+#pragma unroll
+  for (int i = 0; i < S::PER; ++i) {
+    const int g = wave + kQkvNW * i;
+    const int64_t sr = g < 2 * S::NF ? p.w_sr : p.x_sr;
+    voff[i] = uint32_t(lrow * int(sr) + lch * 8) * 2u;
+  }
+  const bool more = wave < S::FULL;  // this wave issues PER transfers per stage (else PER - 1)
+  auto issue = [&](int kb, int slot) {
+    kb = min(kb, p.nk - 1);  // past the end: the last stage again (keeps every wave's count equal)
+    const int k0 = kb * kQkvK;
+    bf16_t* dst = smem + slot * S::STAGE;
+#pragma unroll
+    for (int i = 0; i < S::PER; ++i) {
+      const int g = wave + kQkvNW * i;
+      if (i == S::PER - 1 && !more) break;
+      bf16_t* d = dst + g * 512;
+      if (g < S::NF) {
+        lds_dma16_s(wb0 + int64_t(16 * g) * p.w_sr + k0, voff[i], d);
+      } else if (g < 2 * S::NF) {
+        lds_dma16_s(wb1 + int64_t(16 * (g - S::NF)) * p.w_sr + k0, voff[i], d);
+      } else if (full) {
+        lds_dma16_s(xb + int64_t(16 * (g - 2 * S::NF)) * p.x_sr + k0, voff[i], d);
+      } else {
+        const int r = min(r0 + 16 * (g - 2 * S::NF) + lrow, p.M - 1);
+        lds_dma16(p.x + int64_t(r) * p.x_sr + k0 + lch * 8, d);
+      }
+    }
+  };
+
+  const int hw = wave & 1, tw = wave >> 1;
+  f32x4 acc[S::NF][4];
+#pragma unroll
+  for (int f = 0; f < S::NF; ++f)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[f][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int i = 0; i < kQkvStg - 1; ++i) issue(i, i);
+  int slot = 0;
+  for (int kb = 0; kb < p.nk; ++kb) {
+    // stage kb is complete once at most kQkvStg - 2 younger stages of this wave are outstanding
+    if (more) __builtin_amdgcn_s_waitcnt(kVmWaitStage<(kQkvStg - 2) * S::PER>());
+    else __builtin_amdgcn_s_waitcnt(kVmWaitStage<(kQkvStg - 2) * (S::PER - 1)>());
+    lds_barrier();
+    issue(kb + kQkvStg - 1, slot == 0 ? kQkvStg - 1 : slot - 1);
+    const bf16_t* st = smem + slot * S::STAGE;
+    typename E::Frag a[S::NF], bq[4];
+#pragma unroll
+    for (int f = 0; f < S::NF; ++f) a[f] = tile_row_frag<32>(st, hw * DH + 16 * f + (lane & 15), lane >> 4);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) bq[t] = tile_row_frag<32>(st, 2 * DH + 64 * tw + 16 * t + (lane & 15), lane >> 4);
+#pragma unroll
+    for (int f = 0; f < S::NF; ++f)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc[f][t] = E::mma(a[f], bq[t], acc[f][t]);
+    slot = slot == kQkvStg - 1 ? 0 : slot + 1;
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // the ring's last transfers land before the tile reuses the LDS
+  __syncthreads();
+
+  // product -> bf16 -> output tile [token][2 dh] (padded rows)
+#pragma unroll
+  for (int f = 0; f < S::NF; ++f)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int tok = 64 * tw + 16 * t + (lane & 15);
+      const int col = hw * DH + 16 * f + 4 * (lane >> 4);
+      uint2 v;
+      v.x = uint32_t(f2bf(acc[f][t][0])) | (uint32_t(f2bf(acc[f][t][1])) << 16);
+      v.y = uint32_t(f2bf(acc[f][t][2])) | (uint32_t(f2bf(acc[f][t][3])) << 16);
+      *reinterpret_cast<uint2*>(smem + tok * S::OUTW + col) = v;
+    }
+  __syncthreads();
+
+  // rotations and stores: chunk c of token row `tok`, partner chunk from the tile
+  const bool rope = part < 2 && p.tab != nullptr;
+  const bool giv = part == 2 && p.theta != nullptr;
+  float gc = 1.f, gs = 0.f;
+  if (giv) {
+    float sn, cs;
+    sincosf(p.theta[hp], &sn, &cs);
+    gc = bf2f(f2bf(cs));
+    gs = bf2f(f2bf(sn));
+  }
+  constexpr int HC = DH / 16;  // chunks per half head
+  constexpr int CPH = DH / 8;  // chunks per head
+  bf16_t* obase = part == 0 ? p.o1 : (part == 1 ? p.o2 : p.o3);
+  const int64_t osb = part == 0 ? p.o1_sb : (part == 1 ? p.o2_sb : p.o3_sb);
+  const int64_t osh = part == 0 ? p.o1_sh : (part == 1 ? p.o2_sh : p.o3_sh);
+  const int64_t osr = part == 0 ? p.o1_sr : (part == 1 ? p.o2_sr : p.o3_sr);
+  // every table load of the thread's tasks first (one latency for all of them), then the rotations
+  constexpr int NTASK = kQkvTok * S::NCH / (64 * kQkvNW);
+  const int rlast = p.M - 1;
+  uint4 tabv[NTASK][2];
+  if (rope) {
+#pragma unroll
+    for (int i = 0; i < NTASK; ++i) {
+      const int q = threadIdx.x + 64 * kQkvNW * i;
+      const int tok = q / S::NCH, cc = (q % S::NCH) % CPH;
+      const int r = min(r0 + tok, rlast);
+      const int t = p.B == 1 ? r : r % p.T;
+      const uint4* tp = reinterpret_cast<const uint4*>(p.tab + int64_t(t) * (DH / 2) + (cc % HC) * 8);
+      tabv[i][0] = tp[0];
+      tabv[i][1] = tp[1];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NTASK; ++i) {
+    const int q = threadIdx.x + 64 * kQkvNW * i;
+    const int tok = q / S::NCH, c = q % S::NCH;
+    const int r = r0 + tok;
+    if (r >= p.M) break;  // tokens are in order: every later task of this thread is past M too
+    const int b = p.B == 1 ? 0 : r / p.T, t = r - b * p.T;
+    const int hh = c / CPH, cc = c % CPH;
+    int pc;  // partner chunk in the tile row
+    if (part < 2) pc = hh * CPH + (cc < HC ? cc + HC : cc - HC);
+    else pc = (1 - hh) * CPH + cc;
+    const uint4 xv = *reinterpret_cast<const uint4*>(smem + tok * S::OUTW + c * 8);
+    const uint4 yv = *reinterpret_cast<const uint4*>(smem + tok * S::OUTW + pc * 8);
+    const int h = hh ? h1 : h0;
+    if (part == 2 && p.iraw)
+      *reinterpret_cast<uint4*>(p.iraw + b * p.ir_sb + t * p.ir_sr + h * DH + cc * 8) = xv;
+    float C[8], Sn[8];
+    if (rope) {
+      const uint32_t tv[8] = {tabv[i][0].x, tabv[i][0].y, tabv[i][0].z, tabv[i][0].w,
+                              tabv[i][1].x, tabv[i][1].y, tabv[i][1].z, tabv[i][1].w};
+      const float sg = cc < HC ? -1.f : 1.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        C[e] = bf2f(tv[e] & 0xffffu);
+        Sn[e] = sg * bf2f(tv[e] >> 16);
+      }
+    } else {
+      const float sg = hh == 0 ? -1.f : 1.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        C[e] = gc;
+        Sn[e] = sg * gs;
+      }
+    }
+    const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w}, yw[4] = {yv.x, yv.y, yv.z, yv.w};
+    uint32_t ow[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float x0 = bf2f(xw[k] & 0xffffu), x1 = bf2f(xw[k] >> 16);
+      const float y0 = bf2f(yw[k] & 0xffffu), y1 = bf2f(yw[k] >> 16);
+      const float o0 = x0 * C[2 * k] + y0 * Sn[2 * k];
+      const float o1 = x1 * C[2 * k + 1] + y1 * Sn[2 * k + 1];
+      ow[k] = uint32_t(f2bf(o0)) | (uint32_t(f2bf(o1)) << 16);
+    }
+    *reinterpret_cast<uint4*>(obase + b * osb + t * osr + h * osh + cc * 8) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// host side
+// ------------------------------------------------------------------------------------------------
+size_t qkv_rope_workspace_bytes(const mote_qkv_rope_args* a) {
+  if (!a->inv_freq || a->T <= 0 || a->D <= 0) return 0;
+  return size_t(a->T) * (a->D / 2) * sizeof(uint32_t);
+}
+
+static bool al16v(const void* ptr, int64_t s0, int64_t s1, int64_t s2) {
+  return reinterpret_cast<uintptr_t>(ptr) % 16 == 0 && (s0 * 2) % 16 == 0 && (s1 * 2) % 16 == 0 &&
+         (s2 * 2) % 16 == 0;
+}
+
+int launch_qkv_rope_fwd(const mote_qkv_rope_args* a, hipStream_t stream) {
+  if (!a) return set_error(MOTE_ERR_ARGUMENT, "qkv_rope: null args");
+  if (a->D != 64 && a->D != 96 && a->D != 128)
+    return set_error(MOTE_ERR_SHAPE, "qkv_rope: head dim %d (the fused prologue serves 64, 96, 128)", a->D);
+  if (a->B < 0 || a->T < 0 || a->H < 2 || a->H % 2)
+    return set_error(MOTE_ERR_SHAPE, "qkv_rope: B = %d, T = %d, H = %d (H even)", a->B, a->T, a->H);
+  const int K = a->H * a->D;
+  if (K % kQkvK) return set_error(MOTE_ERR_SHAPE, "qkv_rope: model width %d not a multiple of 32", K);
+  const int64_t M = int64_t(a->B) * a->T;
+  if (M == 0) return MOTE_OK;
+  if (M > (int64_t(1) << 30)) return set_error(MOTE_ERR_SHAPE, "qkv_rope: %lld tokens", (long long)M);
+  if (!a->x || !a->w || !a->p1.data || !a->p2.data || !a->info.data)
+    return set_error(MOTE_ERR_ARGUMENT, "qkv_rope: null pointer");
+  if (a->B > 1 && a->x_sb != int64_t(a->T) * a->x_sr)
+    return set_error(MOTE_ERR_ARGUMENT, "qkv_rope: x must hold its batches back to back (x_sb == T * x_sr)");
+  if (a->x_sr >= (int64_t(1) << 24) || a->w_sr >= (int64_t(1) << 24))
+    return set_error(MOTE_ERR_ARGUMENT, "qkv_rope: row strides must stay below 2^24 elements");
+  if (!al16v(a->x, a->x_sr, 0, 0) || !al16v(a->w, a->w_sr, 0, 0) ||
+      !al16v(a->p1.data, a->p1.stride_b, a->p1.stride_h, a->p1.stride_r) ||
+      !al16v(a->p2.data, a->p2.stride_b, a->p2.stride_h, a->p2.stride_r) ||
+      !al16v(a->info.data, a->info.stride_b, a->info.stride_h, a->info.stride_r) ||
+      (a->info_raw && !al16v(a->info_raw, a->ir_sb, a->ir_sr, 0)))
+    return set_error(MOTE_ERR_ARGUMENT, "qkv_rope: rows must start on 16-byte boundaries");
+  if (a->inv_freq && (!a->workspace || a->workspace_bytes < qkv_rope_workspace_bytes(a) ||
+                      reinterpret_cast<uintptr_t>(a->workspace) % 16))
+    return set_error(MOTE_ERR_WORKSPACE, "qkv_rope: workspace too small or misaligned");
+  QkvParams p;
+  p.x = reinterpret_cast<const bf16_t*>(a->x); p.x_sr = a->x_sr;
+  p.w = reinterpret_cast<const bf16_t*>(a->w); p.w_sr = a->w_sr;
+  p.tab = a->inv_freq ? reinterpret_cast<const uint32_t*>(a->workspace) : nullptr;
+  p.theta = a->theta;
+  p.o1 = reinterpret_cast<bf16_t*>(a->p1.data); p.o1_sb = a->p1.stride_b; p.o1_sh = a->p1.stride_h; p.o1_sr = a->p1.stride_r;
+  p.o2 = reinterpret_cast<bf16_t*>(a->p2.data); p.o2_sb = a->p2.stride_b; p.o2_sh = a->p2.stride_h; p.o2_sr = a->p2.stride_r;
+  p.o3 = reinterpret_cast<bf16_t*>(a->info.data); p.o3_sb = a->info.stride_b; p.o3_sh = a->info.stride_h;
+  p.o3_sr = a->info.stride_r;
+  p.iraw = reinterpret_cast<bf16_t*>(a->info_raw); p.ir_sb = a->ir_sb; p.ir_sr = a->ir_sr;
+  p.B = a->B; p.T = a->T; p.H = a->H; p.K = K; p.M = int(M); p.parity = a->layer_parity & 1; p.nk = K / kQkvK;
+  p.ntok = int((M + kQkvTok - 1) / kQkvTok);
+  p.ncol = 3 * (a->H / 2);
+  if (a->inv_freq) {
+    const int64_t n = int64_t(a->T) * (a->D / 2);
+    hipLaunchKernelGGL(rope_table_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, stream, a->inv_freq, a->pos0,
+                       a->T, a->D / 2, reinterpret_cast<uint32_t*>(a->workspace));
+    int rc = check_launch("qkv_rope/table");
+    if (rc) return rc;
+  }
+  const int nwg = p.ntok * p.ncol;
+  const dim3 grid(unsigned((nwg + 7) / 8 * 8));  // whole rounds over the 8 XCDs; the extra ids return
+  switch (a->D) {
+    case 64: hipLaunchKernelGGL(qkv_rope_kernel<64>, grid, dim3(64 * kQkvNW), 0, stream, p); break;
+    case 96: hipLaunchKernelGGL(qkv_rope_kernel<96>, grid, dim3(64 * kQkvNW), 0, stream, p); break;
+    default: hipLaunchKernelGGL(qkv_rope_kernel<128>, grid, dim3(64 * kQkvNW), 0, stream, p); break;
+  }
+  return check_launch("qkv_rope");
+}
+
+}  // namespace mote

@@ -111,6 +111,7 @@ __global__ void __launch_bounds__(256) rope_givens_fwd_kernel(const RopeParams p
 struct RopeBwdParams {
   const void* qkv;
   int64_t qkv_sb, qkv_sr;
+  int ioff;        // element offset of the I~ columns in a qkv row (2 H D, or 0 for I~ alone)
   const void* g1; int64_t g1_sb, g1_sh, g1_sr;
   const void* g2; int64_t g2_sb, g2_sh, g2_sr;
   const void* g3; int64_t g3_sb, g3_sh, g3_sr;
@@ -154,7 +155,7 @@ __global__ void __launch_bounds__(256) rope_givens_bwd_kernel(const RopeBwdParam
     o[k] = E::from_f(r0);
     o[k + half] = E::from_f(r1);
   }
-  const T* xi = reinterpret_cast<const T*>(p.qkv) + int64_t(b) * p.qkv_sb + int64_t(t) * p.qkv_sr + 2 * HD;
+  const T* xi = reinterpret_cast<const T*>(p.qkv) + int64_t(b) * p.qkv_sb + int64_t(t) * p.qkv_sr + p.ioff;
   const T* g3 = reinterpret_cast<const T*>(p.g3) + int64_t(b) * p.g3_sb + int64_t(t) * p.g3_sr;
   for (int u = threadIdx.x; u < HD; u += blockDim.x) {
     const int hd = u / p.D, d = u % p.D;
@@ -384,7 +385,7 @@ __global__ void __launch_bounds__(kRopeMaxCh) rope_givens_bwd_stream_kernel(cons
   // I~ inputs of the pair (for d theta): every thread loads two chunks of the I~ part of qkv (those
   // of p1 / p2 threads repeat an I~ thread's lines), so no load sits under a condition
   const int xa = L.which == 2 ? L.hd : L.hd % H, xb = L.which == 2 ? L.other : L.hd % H;
-  const T* xq = reinterpret_cast<const T*>(p.qkv) + 2 * H * D + L.k * EPC;
+  const T* xq = reinterpret_cast<const T*>(p.qkv) + p.ioff + L.k * EPC;
   Chunk g0[kRopeRB], g1[kRopeRB], x0[kRopeRB], x1[kRopeRB];
 #pragma unroll
   for (int r = 0; r < kRopeRB; ++r) {
@@ -530,6 +531,7 @@ int launch_rope_givens_bwd(const mote_rope_givens_bwd_args* a, hipStream_t strea
   if (a->T == 0) return MOTE_OK;
   RopeBwdParams p;
   p.qkv = a->qkv; p.qkv_sb = a->qkv_sb; p.qkv_sr = a->qkv_sr;
+  p.ioff = a->qkv_info_only ? 0 : 2 * a->H * a->D;
   p.g1 = a->dp1.data; p.g1_sb = a->dp1.stride_b; p.g1_sh = a->dp1.stride_h; p.g1_sr = a->dp1.stride_r;
   p.g2 = a->dp2.data; p.g2_sb = a->dp2.stride_b; p.g2_sh = a->dp2.stride_h; p.g2_sr = a->dp2.stride_r;
   p.g3 = a->dinfo.data; p.g3_sb = a->dinfo.stride_b; p.g3_sh = a->dinfo.stride_h; p.g3_sr = a->dinfo.stride_r;

@@ -3,8 +3,10 @@
 Same constructor, parameter names and construction order (relation.py:97-157), same forward
 signature and return convention (relation.py:184-268). What runs underneath:
 
-    qkv = x [w1; w2; wi]^T                      one GEMM (hipBLASLt) instead of three
-    p1, p2, I~ = mote::rope_givens(qkv)          HIP: RoPE on p1/p2, Givens on I~, head split
+    p1, p2, I~ = mote::qkv_rope(x, [w1; w2; wi])  HIP: one launch for the projections with RoPE on
+                                                 p1/p2 and Givens on I~ in the epilogue (bf16,
+                                                 dh 64 / 96 / 128, no QK-Norm); otherwise one
+                                                 hipBLASLt GEMM and mote::rope_givens
     Y, g = mote::relation_fwd(p1, P2, I~)        HIP: the fused Relation core (any T, decode too)
     out = wo(Y [* sigmoid(wg x)])                 Y is token-major already, so no transpose copy
 
@@ -80,10 +82,13 @@ def _rope_givens_fake(qkv, inv_freq, theta, n_heads, parity, pos0):
 @torch.library.custom_op("mote::rope_givens_bwd", mutates_args=())
 def _rope_givens_bwd(dp1: torch.Tensor, dp2: torch.Tensor, dinfo: torch.Tensor, qkv: torch.Tensor,
                      inv_freq: Optional[torch.Tensor], theta: Optional[torch.Tensor], n_heads: int, parity: int,
-                     pos0: int) -> Tuple[torch.Tensor, torch.Tensor]:
-    B, T, D3 = qkv.shape
+                     pos0: int, info_only: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(dqkv [B, T, 3 H dh], dtheta). qkv is the projection output, or with info_only its I~ part
+    alone ([B, T, H dh]): the backward reads only the I~ columns (for dtheta)."""
+    B, T, Dx = qkv.shape
     H = n_heads
-    D = D3 // (3 * H)
+    D = Dx // H if info_only else Dx // (3 * H)
+    D3 = 3 * H * D
     qkv = qkv if qkv.stride(-1) == 1 else qkv.contiguous()
     dp1, dp2, dinfo = (t.to(qkv.dtype) if t.stride(-1) == 1 else t.to(qkv.dtype).contiguous() for t in (dp1, dp2, dinfo))
     dqkv = torch.empty(B, T, D3, device=qkv.device, dtype=qkv.dtype)
@@ -96,6 +101,7 @@ def _rope_givens_bwd(dp1: torch.Tensor, dp2: torch.Tensor, dinfo: torch.Tensor, 
     th = None if theta is None else theta.detach().to(device=qkv.device, dtype=torch.float32).contiguous()
     a.inv_freq, a.theta = L.ptr(inv), L.ptr(th)
     a.qkv, a.qkv_sb, a.qkv_sr = qkv.data_ptr(), qkv.stride(0), qkv.stride(1)
+    a.qkv_info_only = int(bool(info_only))
     a.dp1, a.dp2, a.dinfo = L.view(dp1), L.view(dp2), L.view(dinfo)
     a.dqkv, a.dqkv_sb, a.dqkv_sr = dqkv.data_ptr(), dqkv.stride(0), dqkv.stride(1)
     a.dtheta = dtheta.data_ptr()
@@ -107,8 +113,10 @@ def _rope_givens_bwd(dp1: torch.Tensor, dp2: torch.Tensor, dinfo: torch.Tensor, 
 
 
 @_rope_givens_bwd.register_fake
-def _rope_givens_bwd_fake(dp1, dp2, dinfo, qkv, inv_freq, theta, n_heads, parity, pos0):
-    return qkv.new_empty(qkv.shape), qkv.new_empty((max(n_heads // 2, 1),), dtype=torch.float32)
+def _rope_givens_bwd_fake(dp1, dp2, dinfo, qkv, inv_freq, theta, n_heads, parity, pos0, info_only=False):
+    B, T, Dx = qkv.shape
+    D3 = 3 * Dx if info_only else Dx
+    return qkv.new_empty((B, T, D3)), qkv.new_empty((max(n_heads // 2, 1),), dtype=torch.float32)
 
 
 def _rg_setup(ctx, inputs, output):
@@ -140,6 +148,88 @@ def rope_givens(qkv: torch.Tensor, n_heads: int, inv_freq: Optional[torch.Tensor
     pos0.. on p1/p2 (relation.py:211-214), Givens on I~ (relation.py:215). Differentiable in qkv
     and theta."""
     return _rope_givens(qkv, inv_freq, theta, int(n_heads), int(layer_idx) % 2, int(pos0))
+
+
+# ---- mote::qkv_rope (fused projection prologue) ----------------------------------------------------
+USE_FUSED_PROLOGUE = True   # bf16 activations, head dim 64 / 96 / 128, no QK-Norm: one launch for the
+                            # projections and RoPE / Givens; the unfused path serves everything else
+
+
+@torch.library.custom_op("mote::qkv_rope", mutates_args=())
+def _qkv_rope(x: torch.Tensor, w: torch.Tensor, inv_freq: Optional[torch.Tensor], theta: Optional[torch.Tensor],
+              n_heads: int, parity: int, pos0: int, keep_info: bool
+              ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(p1, p2, I~) as [B, H, T, dh] views of x [w1; w2; wi]^T after RoPE / Givens, and (keep_info)
+    the I~ projections before the rotation ([B, T, H dh]; empty otherwise) for the backward."""
+    if not x.is_cuda:
+        raise RuntimeError("mote::qkv_rope needs the HIP library and an MI355X")
+    B, T, K = x.shape
+    H = n_heads
+    D = K // H
+    x = x.contiguous()
+    w = w.contiguous()
+    p1, p2, info = (_heads_out(B, T, H, D, x, x.dtype) for _ in range(3))
+    iraw = torch.empty(B, T, K, device=x.device, dtype=x.dtype) if keep_info else x.new_empty(0)
+    a = L.QkvRopeArgs()
+    a.B, a.T, a.H, a.D, a.pos0, a.layer_parity = B, T, H, D, int(pos0), int(parity)
+    a.x, a.x_sb, a.x_sr = x.data_ptr(), x.stride(0), x.stride(1)
+    a.w, a.w_sr = w.data_ptr(), w.stride(0)
+    inv = None if inv_freq is None else inv_freq.to(device=x.device, dtype=torch.float32).contiguous()
+    th = None if theta is None else theta.detach().to(device=x.device, dtype=torch.float32).contiguous()
+    a.inv_freq, a.theta = L.ptr(inv), L.ptr(th)
+    a.p1, a.p2, a.info = L.view(p1), L.view(p2), L.view(info)
+    if keep_info:
+        a.info_raw, a.ir_sb, a.ir_sr = iraw.data_ptr(), iraw.stride(0), iraw.stride(1)
+    ws = torch.empty(max(int(L.lib().mote_qkv_rope_workspace(a)), 16), device=x.device, dtype=torch.uint8)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    L.check(L.lib().mote_qkv_rope_fwd(a, L.stream_of(x)), "mote_qkv_rope_fwd")
+    return p1, p2, info, iraw
+
+
+@_qkv_rope.register_fake
+def _qkv_rope_fake(x, w, inv_freq, theta, n_heads, parity, pos0, keep_info):
+    B, T, K = x.shape
+    D = K // n_heads
+    mk = lambda: x.new_empty((B, T, n_heads, D)).transpose(1, 2)
+    return mk(), mk(), mk(), (x.new_empty((B, T, K)) if keep_info else x.new_empty(0))
+
+
+def _qr_setup(ctx, inputs, output):
+    x, w, inv_freq, theta, n_heads, parity, pos0, keep_info = inputs
+    ctx.save_for_backward(x, w, inv_freq, theta, output[3])
+    ctx.has_theta = theta is not None
+    ctx.keep = keep_info
+    ctx.n_heads, ctx.parity, ctx.pos0 = n_heads, parity, pos0
+
+
+def _qr_backward(ctx, dp1, dp2, dinfo, _diraw):
+    x, w, inv_freq, theta, iraw = ctx.saved_tensors
+    if ctx.has_theta and not ctx.keep:
+        raise RuntimeError("mote::qkv_rope: the backward needs keep_info=True when theta is given")
+    B, T, K = x.shape
+    H = ctx.n_heads
+    D = K // H
+    z = lambda: torch.zeros(B, H, T, D, device=x.device, dtype=x.dtype)
+    dp1 = z() if dp1 is None else dp1
+    dp2 = z() if dp2 is None else dp2
+    dinfo = z() if dinfo is None else dinfo
+    src = iraw if ctx.keep else x.new_empty(B, T, K)  # read only for dtheta
+    dqkv, dtheta = _rope_givens_bwd(dp1, dp2, dinfo, src, inv_freq, theta, H, ctx.parity, ctx.pos0, True)
+    dx = torch.matmul(dqkv, w)                                        # [B, T, 3K] x [3K, K]
+    dw = torch.matmul(dqkv.reshape(-1, 3 * K).t(), x.reshape(-1, K))  # [3K, K]
+    return dx, dw, None, (dtheta[: H // 2] if ctx.has_theta else None), None, None, None, None
+
+
+_qkv_rope.register_autograd(_qr_backward, setup_context=_qr_setup)
+
+
+def qkv_rope(x: torch.Tensor, w: torch.Tensor, n_heads: int, inv_freq: Optional[torch.Tensor],
+             theta: Optional[torch.Tensor], layer_idx: int, pos0: int = 0):
+    """The fused prologue: bf16 x [B, T, H dh] and w = [w1; w2; wi] [3 H dh, H dh] -> (p1, p2, I~),
+    the same as rope_givens(F.linear(x, w), ...) (relation.py:199-215). Differentiable in x, w, theta."""
+    keep = theta is not None and torch.is_grad_enabled()
+    p1, p2, info, _ = _qkv_rope(x, w, inv_freq, theta, int(n_heads), int(layer_idx) % 2, int(pos0), keep)
+    return p1, p2, info
 
 
 class HeadRMSNorm(nn.Module):
@@ -204,14 +294,18 @@ class FullRelation(nn.Module):
         B, T, D = x.shape
         H, dh = self.n_heads, self.d_head
         w = torch.cat([self.w1.weight, self.w2.weight, self.wi.weight], dim=0)
+        inv = self.inv_freq if self.use_rope else None
+        theta = self.theta if self.use_givens else None
+        bf16 = x.dtype == torch.bfloat16 or (torch.is_autocast_enabled() and
+                                             torch.get_autocast_dtype("cuda") == torch.bfloat16)
+        if USE_FUSED_PROLOGUE and bf16 and not self.qk_norm and dh in (64, 96, 128) and (H * dh) % 32 == 0:
+            return qkv_rope(x.to(torch.bfloat16), w.to(torch.bfloat16), H, inv, theta, self.layer_idx, S)
         qkv = F.linear(x, w)
         if self.qk_norm:
             q, k, v = qkv.split(D, dim=-1)
             q = self.p1_norm(q.reshape(B, T, H, dh)).reshape(B, T, D)
             k = self.p2_norm(k.reshape(B, T, H, dh)).reshape(B, T, D)
             qkv = torch.cat([q, k, v], dim=-1)
-        inv = self.inv_freq if self.use_rope else None
-        theta = self.theta if self.use_givens else None
         return rope_givens(qkv, H, inv, theta, self.layer_idx, S)
 
     def _out(self, y: torch.Tensor, x: torch.Tensor) -> torch.Tensor:

@@ -1,0 +1,144 @@
+"""Parity of the fused projection prologue (mote::qkv_rope: the QKV product with RoPE / Givens in its
+epilogue) with the reference's projections + RoPE + Givens (mote/model/relation.py:199-215, 37-68,
+160-174), restated in oracle/relation.py.
+
+Against the float64 oracle of bf16 inputs, outputs and gradients within the bf16 tolerance the
+Relation tests use (2e-2 relative, tests/test_flash_relation.py:84-85 of the reference); against the
+unfused path (hipBLASLt product, then mote::rope_givens) within one bf16 step of the product. Cases:
+head dims 64 / 96 / 128, both Givens parities, RoPE at pos0 > 0, RoPE or Givens off, ragged token
+counts (1 to 4964, partial token tiles), two batches, and the FullRelation module under bf16 autocast.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from conftest import rel_err
+from oracle import relation as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _ref(x, w, H, inv, theta, parity, pos0):
+    """float64: projection rounded to bf16 (the reference's F.linear output), then RoPE / Givens."""
+    B, T, K = x.shape
+    D = K // H
+    qkv = (x.double() @ w.double().t()).to(torch.bfloat16).double()
+    q, k, v = (t.reshape(B, T, H, D).transpose(1, 2) for t in qkv.split(K, dim=-1))
+    if inv is not None:
+        cos, sin = O.rope_tables(pos0, T, D, 10000.0, torch.bfloat16)
+        q, k = O.apply_rope(q, cos.double(), sin.double()), O.apply_rope(k, cos.double(), sin.double())
+    if theta is not None:
+        v = O.givens(v, theta.double(), parity)
+    return q, k, v
+
+
+@pytest.mark.parametrize("H,D,T,B,parity,pos0", [
+    (8, 96, 4964, 1, 0, 0), (8, 96, 301, 2, 1, 0), (8, 96, 1, 1, 1, 17), (4, 64, 37, 2, 0, 5),
+    (12, 64, 700, 1, 1, 0), (4, 128, 129, 1, 0, 3), (2, 96, 128, 1, 1, 0),
+])
+def test_fused_prologue_matches_oracle(cuda, H, D, T, B, parity, pos0):
+    from mote_amd.relation import qkv_rope, rope_inv_freq
+
+    print(f"case qkv_rope H={H} D={D} T={T} B={B} parity={parity} pos0={pos0}", flush=True)
+    g = torch.Generator().manual_seed(H * 1000 + T)
+    K = H * D
+    x = torch.randn(B, T, K, generator=g).bfloat16()
+    w = (torch.randn(3 * K, K, generator=g) / K ** 0.5).bfloat16()
+    theta = torch.rand(H // 2, generator=g) * 2 - 1
+    inv = rope_inv_freq(D, 10000.0)
+    xg, wg, tg = (t.to(cuda).requires_grad_(True) for t in (x, w, theta))
+    p1, p2, info = qkv_rope(xg, wg, H, inv.to(cuda), tg, parity, pos0)
+    r1, r2, r3 = _ref(x, w, H, inv, theta, parity, pos0)
+    for got, want in ((p1, r1), (p2, r2), (info, r3)):
+        assert got.shape == want.shape and got.dtype == torch.bfloat16
+        assert rel_err(got, want) < 2e-2, rel_err(got, want)
+    # gradients against float64 autograd of the same composition
+    dys = [torch.randn(B, H, T, D, generator=g).bfloat16() for _ in range(3)]
+    loss = sum((o.float() * d.to(cuda).float()).sum() for o, d in zip((p1, p2, info), dys))
+    loss.backward()
+    xr, wr, tr = (t.double().requires_grad_(True) for t in (x.float(), w.float(), theta))
+    K_ = K
+    qkv = xr @ wr.t()
+    q, k, v = (t.reshape(B, T, H, D).transpose(1, 2) for t in qkv.split(K_, dim=-1))
+    cos, sin = O.rope_tables(pos0, T, D, 10000.0, torch.bfloat16)
+    q, k = O.apply_rope(q, cos.double(), sin.double()), O.apply_rope(k, cos.double(), sin.double())
+    v = O.givens(v, tr, parity)
+    sum((o * d.double()).sum() for o, d in zip((q, k, v), dys)).backward()
+    assert rel_err(xg.grad, xr.grad) < 2e-2, rel_err(xg.grad, xr.grad)
+    assert rel_err(wg.grad, wr.grad) < 2e-2, rel_err(wg.grad, wr.grad)
+    assert rel_err(tg.grad, tr.grad) < 2e-2, rel_err(tg.grad, tr.grad)
+
+
+@pytest.mark.parametrize("rope,givens", [(False, True), (True, False), (False, False)])
+def test_fused_prologue_flags(cuda, rope, givens):
+    from mote_amd.relation import qkv_rope, rope_inv_freq
+
+    H, D, T = 8, 96, 200
+    g = torch.Generator().manual_seed(3)
+    K = H * D
+    x = torch.randn(1, T, K, generator=g).bfloat16()
+    w = (torch.randn(3 * K, K, generator=g) / K ** 0.5).bfloat16()
+    theta = torch.rand(H // 2, generator=g) if givens else None
+    inv = rope_inv_freq(D, 10000.0) if rope else None
+    outs = qkv_rope(x.to(cuda), w.to(cuda), H, inv.to(cuda) if rope else None,
+                    theta.to(cuda) if givens else None, 1, 0)
+    for got, want in zip(outs, _ref(x, w, H, inv, theta, 1, 0)):
+        assert rel_err(got, want) < 2e-2
+
+
+def test_fused_matches_unfused_path(cuda):
+    # the two device paths differ only in the product's summation order: one bf16 step at most
+    from mote_amd.relation import qkv_rope, rope_givens, rope_inv_freq
+
+    H, D, T = 8, 96, 4964
+    g = torch.Generator().manual_seed(4)
+    K = H * D
+    x = torch.randn(1, T, K, generator=g).bfloat16().to(cuda)
+    w = (torch.randn(3 * K, K, generator=g) / K ** 0.5).bfloat16().to(cuda)
+    theta = (torch.rand(H // 2, generator=g) - 0.5).to(cuda)
+    inv = rope_inv_freq(D, 10000.0).to(cuda)
+    a = qkv_rope(x, w, H, inv, theta, 1, 0)
+    b = rope_givens(F.linear(x, w), H, inv, theta, 1, 0)
+    for u, v in zip(a, b):
+        d = (u.float() - v.float()).abs()
+        assert float(d.max()) <= 2 * float((v.float().abs().max()) * 2 ** -7)
+        assert float((d > 0).float().mean()) < 0.05    # most elements bit-identical
+
+
+def test_module_fused_vs_unfused(cuda):
+    # FullRelation under bf16 autocast with and without the fused prologue: outputs and every gradient
+    import mote_amd.relation as R
+
+    torch.manual_seed(5)
+    m = R.FullRelation(768, 8, 1).to(cuda)
+    with torch.no_grad():
+        m.theta.uniform_(-0.5, 0.5)
+    x = torch.randn(1, 500, 768, device=cuda)
+    res = {}
+    for fused in (True, False):
+        R.USE_FUSED_PROLOGUE = fused
+        try:
+            m.zero_grad(set_to_none=True)
+            xx = x.clone().requires_grad_(True)
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                out = m(xx)
+            out.float().pow(2).mean().backward()
+            res[fused] = (out.float(), xx.grad.clone(), {n: p.grad.clone() for n, p in m.named_parameters()})
+        finally:
+            R.USE_FUSED_PROLOGUE = True
+    (o1, g1, p1), (o2, g2, p2) = res[True], res[False]
+    assert rel_err(o1, o2) < 2e-2 and rel_err(g1, g2) < 2e-2
+    for n in p1:
+        assert rel_err(p1[n], p2[n]) < 2e-2, (n, rel_err(p1[n], p2[n]))
+
+
+def test_unsupported_head_dim_raises(cuda):
+    from mote_amd.relation import _qkv_rope
+
+    x = torch.zeros(1, 4, 4 * 48, device=cuda, dtype=torch.bfloat16)
+    w = torch.zeros(3 * 4 * 48, 4 * 48, device=cuda, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="head dim 48"):
+        _qkv_rope(x, w, None, None, 4, 0, 0, False)
