@@ -25,8 +25,8 @@ namespace mote {
 
 constexpr int kQkvTok = 256;     // tokens per workgroup
 constexpr int kQkvNW = 8;        // waves per workgroup
-constexpr int kQkvK = 32;        // k per stage
-constexpr int kQkvStg = 4;       // ring depth
+constexpr int kQkvK = 64;        // k per stage (a 128-byte line of every staged row)
+constexpr int kQkvStg = 2;       // ring depth
 constexpr int kQkvPad = 8;       // bf16 elements of padding per output-tile row
 
 struct QkvParams {
@@ -46,7 +46,9 @@ template <int DH>
 struct QkvShape {
   static constexpr int NF = DH / 16;                  // feature tiles per head
   static constexpr int ROWS = 2 * DH + kQkvTok;       // staged rows per stage: W head 0 | W head 1 | X
-  static constexpr int NINS = ROWS / 16;              // wave instructions per stage
+  static constexpr int CPR = kQkvK / 8;              // 16-byte chunks per staged row
+  static constexpr int RPI = 64 / CPR;                // rows per wave instruction
+  static constexpr int NINS = ROWS / RPI;             // wave instructions per stage
   static constexpr int PER = (NINS + kQkvNW - 1) / kQkvNW;  // per wave (waves >= NINS % NW issue one
   static constexpr int FULL = NINS % kQkvNW == 0 ? kQkvNW : NINS % kQkvNW;  // fewer when NINS % NW != 0)
   static constexpr int STAGE = ROWS * kQkvK;          // bf16 elements
@@ -94,14 +96,18 @@ __global__ void __launch_bounds__(64 * kQkvNW) qkv_rope_kernel(const QkvParams p
   const bf16_t* xb = p.x + int64_t(r0) * p.x_sr;
   const bool full = r0 + kQkvTok <= p.M;
 
-  // staging: instruction g covers stage rows 16 g .. 16 g + 15; lane l takes row 16 g + l / 4 and
-  // physical chunk l % 4, i.e. logical chunk (l % 4) ^ swz, swz = (row >> 2) & 3 = (l >> 4) & 3
-  const int lrow = lane >> 2, lch = (lane & 3) ^ ((lane >> 4) & 3);
+  // staging: instruction g covers stage rows RPI g .. RPI g + RPI - 1; lane l takes row RPI g + l / CPR
+  // and physical chunk l % CPR, i.e. logical chunk (l % CPR) ^ tile_swz(row)
+  constexpr int GW = DH / S::RPI;  // instructions per weight head
+  const int lrow = lane / S::CPR;
   uint32_t voff[S::PER];
+  int lchs[S::PER];
 #pragma unroll
   for (int i = 0; i < S::PER; ++i) {
     const int g = wave + kQkvNW * i;
-    const int64_t sr = g < 2 * S::NF ? p.w_sr : p.x_sr;
+    const int64_t sr = g < 2 * GW ? p.w_sr : p.x_sr;
+    const int lch = (lane % S::CPR) ^ tile_swz<kQkvK>(S::RPI * g + lrow);
+    lchs[i] = lch;
     voff[i] = uint32_t(lrow * int(sr) + lch * 8) * 2u;
   }
   const bool more = wave < S::FULL;  // this wave issues PER transfers per stage (else PER - 1)
@@ -114,15 +120,15 @@ __global__ void __launch_bounds__(64 * kQkvNW) qkv_rope_kernel(const QkvParams p
       const int g = wave + kQkvNW * i;
       if (i == S::PER - 1 && !more) break;
       bf16_t* d = dst + g * 512;
-      if (g < S::NF) {
-        lds_dma16_s(wb0 + int64_t(16 * g) * p.w_sr + k0, voff[i], d);
-      } else if (g < 2 * S::NF) {
-        lds_dma16_s(wb1 + int64_t(16 * (g - S::NF)) * p.w_sr + k0, voff[i], d);
+      if (g < GW) {
+        lds_dma16_s(wb0 + int64_t(S::RPI * g) * p.w_sr + k0, voff[i], d);
+      } else if (g < 2 * GW) {
+        lds_dma16_s(wb1 + int64_t(S::RPI * (g - GW)) * p.w_sr + k0, voff[i], d);
       } else if (full) {
-        lds_dma16_s(xb + int64_t(16 * (g - 2 * S::NF)) * p.x_sr + k0, voff[i], d);
+        lds_dma16_s(xb + int64_t(S::RPI * (g - 2 * GW)) * p.x_sr + k0, voff[i], d);
       } else {
-        const int r = min(r0 + 16 * (g - 2 * S::NF) + lrow, p.M - 1);
-        lds_dma16(p.x + int64_t(r) * p.x_sr + k0 + lch * 8, d);
+        const int r = min(r0 + S::RPI * (g - 2 * GW) + lrow, p.M - 1);
+        lds_dma16(p.x + int64_t(r) * p.x_sr + k0 + lchs[i] * 8, d);
       }
     }
   };
@@ -139,20 +145,25 @@ __global__ void __launch_bounds__(64 * kQkvNW) qkv_rope_kernel(const QkvParams p
   int slot = 0;
   for (int kb = 0; kb < p.nk; ++kb) {
     // stage kb is complete once at most kQkvStg - 2 younger stages of this wave are outstanding
-    if (more) __builtin_amdgcn_s_waitcnt(kVmWaitStage<(kQkvStg - 2) * S::PER>());
+    if (kQkvStg == 2) __builtin_amdgcn_s_waitcnt(0);
+    else if (more) __builtin_amdgcn_s_waitcnt(kVmWaitStage<(kQkvStg - 2) * S::PER>());
     else __builtin_amdgcn_s_waitcnt(kVmWaitStage<(kQkvStg - 2) * (S::PER - 1)>());
     lds_barrier();
     issue(kb + kQkvStg - 1, slot == 0 ? kQkvStg - 1 : slot - 1);
     const bf16_t* st = smem + slot * S::STAGE;
-    typename E::Frag a[S::NF], bq[4];
 #pragma unroll
-    for (int f = 0; f < S::NF; ++f) a[f] = tile_row_frag<32>(st, hw * DH + 16 * f + (lane & 15), lane >> 4);
+    for (int kk = 0; kk < kQkvK / 32; ++kk) {
+      typename E::Frag a[S::NF], bq[4];
+      const int ch = 4 * kk + (lane >> 4);
 #pragma unroll
-    for (int t = 0; t < 4; ++t) bq[t] = tile_row_frag<32>(st, 2 * DH + 64 * tw + 16 * t + (lane & 15), lane >> 4);
+      for (int f = 0; f < S::NF; ++f) a[f] = tile_row_frag<kQkvK>(st, hw * DH + 16 * f + (lane & 15), ch);
 #pragma unroll
-    for (int f = 0; f < S::NF; ++f)
+      for (int t = 0; t < 4; ++t) bq[t] = tile_row_frag<kQkvK>(st, 2 * DH + 64 * tw + 16 * t + (lane & 15), ch);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) acc[f][t] = E::mma(a[f], bq[t], acc[f][t]);
+      for (int f = 0; f < S::NF; ++f)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[f][t] = E::mma(a[f], bq[t], acc[f][t]);
+    }
     slot = slot == kQkvStg - 1 ? 0 : slot + 1;
   }
   __builtin_amdgcn_s_waitcnt(0);  // the ring's last transfers land before the tile reuses the LDS
