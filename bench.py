@@ -80,8 +80,10 @@ class StackInputs:
 
 
 def stack_step(inp: StackInputs, timers=None):
-    """One fwd+bwd pass of the 12-layer stack through the HIP ops."""
+    """One fwd+bwd pass of the layer stack through the HIP ops; returns the last layer's Y and
+    d(qkv), d(theta) (for the graph-replay check)."""
     ops = torch.ops.mote
+    out = None
     for L in inp.layers:
         p1, p2, info = ops.rope_givens(L["qkv"], L["inv"], L["theta"], L["heads"], L["parity"], 0)
         if timers is not None:
@@ -94,7 +96,41 @@ def stack_step(inp: StackInputs, timers=None):
             dp = staged_bwd(p1, p2, info, ibar, lse, g, L["dy"], timers)
         else:
             dp = ops.relation_bwd(p1, p2, info, ibar, lse, g, L["dy"], 2.0, 0)
-        ops.rope_givens_bwd(dp[0], dp[1], dp[2], L["qkv"], L["inv"], L["theta"], L["heads"], L["parity"], 0)
+        dqkv, dth = ops.rope_givens_bwd(dp[0], dp[1], dp[2], L["qkv"], L["inv"], L["theta"], L["heads"], L["parity"], 0)
+        out = (y, dqkv, dth, dp[3])
+    return out
+
+
+def capture_stack(inp: StackInputs):
+    """The whole stack step as one HIP graph (torch.cuda.CUDAGraph): every launch of every layer
+    replays without the per-op Python dispatch. Returns (graph, the graph's output tensors)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        stack_step(inp)  # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(gr, stream=side):
+            outs = stack_step(inp)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    return gr, outs
+
+
+def check_replays(gr, outs, ref, n: int = 3):
+    """Replays `gr` n times with eager work and synchronisations between the replays; every replay
+    must reproduce the eager outputs bit for bit (the kernels are deterministic)."""
+    for r in range(n):
+        for t in outs:
+            t.fill_(float("nan")) if t.is_floating_point() else t.zero_()
+        torch.cuda.synchronize()
+        gr.replay()
+        torch.cuda.synchronize()
+        for a, b in zip(outs, ref):
+            if not torch.equal(a, b):
+                raise RuntimeError(f"graph replay {r} differs from the eager step")
 
 
 def staged_bwd(p1, p2, info, ibar, lse, g, dy, timers):
@@ -343,10 +379,29 @@ def bench_c2(steps: int, warmup: int, dev):
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / steps
     flops = 8 * 7.0 * 8 * 64 * sum(m * m for m in M)
-    log(f"[bench] C2 Mote-32M stack: chunks {M} (T = {T}), {ms:.3f} ms/step = {flops / ms / 1e9:.1f} TFLOP/s")
+    # the same step as one HIP graph: at T ~ 650 the eager step is bound by per-op dispatch
+    ref = [t.clone() for t in stack_step(inp)]
+    torch.cuda.synchronize()
+    gr, outs = capture_stack(inp)
+    check_replays(gr, outs, ref)
+    for _ in range(warmup):
+        gr.replay()
+    torch.cuda.synchronize()
+    t0.record()
+    for _ in range(steps):
+        gr.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    ms_g = t0.elapsed_time(t1) / steps
+    del gr, outs
+    log(f"[bench] C2 Mote-32M stack: chunks {M} (T = {T}), eager {ms:.3f} ms/step = {flops / ms / 1e9:.1f} TFLOP/s, "
+        f"HIP graph {ms_g:.3f} ms/step = {flops / ms_g / 1e9:.1f} TFLOP/s")
     return dict(workload="Mote-32M Relation stack fwd+bwd (8 layers, B=4, 2048-byte window, seed 1)", chunks=M,
                 T_padded=T, ms_per_step=round(ms, 4), tflops=round(flops / (ms * 1e-3) / 1e12, 2),
-                flop_per_step=flops, frac_bf16_peak=round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4))
+                flop_per_step=flops, frac_bf16_peak=round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                graph=dict(ms_per_step=round(ms_g, 4), tflops=round(flops / (ms_g * 1e-3) / 1e12, 2),
+                           frac_bf16_peak=round(flops / (ms_g * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                           replays_checked=3))
 
 
 def bench_c5(steps: int, warmup: int, dev):
@@ -468,6 +523,71 @@ def bench_norm(rows: int, dev, copies: int, launches: int = 24):
         f"({out['fwd']['GBs']:.0f} GB/s), bwd {out['bwd']['us_per_launch']:.2f} us ({out['bwd']['GBs']:.0f} GB/s)")
     return dict(workload=f"add+RMSNorm pre-norm, {rows} rows x {D} (bf16 x, fp32 residual stream), HIP graph "
                          f"of {launches} launches over {copies} input sets", rows=rows, D=D, **out)
+
+
+# ------------------------------------------------------------------------------------------------
+# fused projection prologue (QKV product with RoPE / Givens in the epilogue)
+# ------------------------------------------------------------------------------------------------
+def bench_qkv(rows: int, dev, copies: int, launches: int = 20):
+    """mote::qkv_rope at the Mote-96M shape (x bf16 [rows, 768], w = [w1; w2; wi] [2304, 768], an odd
+    layer: RoPE on p1 / p2, Givens pairs (1,2),...,(7,0)) against the unfused path (hipBLASLt product
+    + mote::rope_givens), each a HIP graph of `launches` launches over `copies` inputs. Work: 2 rows
+    D 3D FLOP (the product; the rotations are elementwise)."""
+    from mote_amd.relation import FullRelation, qkv_rope, rope_givens
+
+    D, H = D_MODEL, N_HEADS
+    torch.manual_seed(6)
+    m = FullRelation(D, H, 1)
+    with torch.no_grad():
+        m.theta.uniform_(-0.3, 0.3)
+    w = torch.cat([m.w1.weight, m.w2.weight, m.wi.weight], 0).detach().to(torch.bfloat16).to(dev)
+    inv, th = m.inv_freq.to(dev), m.theta.detach().to(dev)
+    xs = [torch.randn(1, rows, D).to(torch.bfloat16).to(dev) for _ in range(copies)]
+
+    def fused(i):
+        return qkv_rope(xs[i % copies], w, H, inv, th, 1, 0)
+
+    def unfused(i):
+        return rope_givens(torch.nn.functional.linear(xs[i % copies], w), H, inv, th, 1, 0)
+
+    out = {}
+    side = torch.cuda.Stream()
+    flops = 2.0 * rows * D * 3 * D
+    with torch.no_grad():
+        a, b = fused(0), unfused(0)
+        diff = max(float((u.float() - v.float()).abs().max()) / max(float(v.float().abs().max()), 1e-3)
+                   for u, v in zip(a, b))
+        for name, fn in (("fused", fused), ("unfused", unfused)):
+            for i in range(copies):
+                fn(i)
+            torch.cuda.synchronize()
+            side.wait_stream(torch.cuda.current_stream())
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.stream(side):
+                with torch.cuda.graph(gr, stream=side):
+                    for i in range(launches):
+                        fn(i)
+            torch.cuda.current_stream().wait_stream(side)
+            torch.cuda.synchronize()
+            for _ in range(2):
+                gr.replay()
+            torch.cuda.synchronize()
+            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            reps = 10
+            t0.record()
+            for _ in range(reps):
+                gr.replay()
+            t1.record()
+            torch.cuda.synchronize()
+            us = t0.elapsed_time(t1) * 1e3 / (reps * launches)
+            tf = flops / (us * 1e-6) / 1e12
+            out[name] = dict(us_per_launch=round(us, 2), tflops=round(tf, 1), frac_bf16_peak=round(tf / PEAK_BF16_TFLOPS, 4))
+            del gr
+    log(f"[bench] qkv prologue rows {rows}: fused {out['fused']['us_per_launch']:.1f} us "
+        f"({out['fused']['tflops']:.0f} TF/s), unfused {out['unfused']['us_per_launch']:.1f} us; rel diff {diff:.2e}")
+    return dict(workload=f"QKV product + RoPE/Givens, {rows} rows x {D} -> 3 x {H} heads x {D // H} (bf16, odd layer), "
+                         f"HIP graph of {launches} launches over {copies} inputs", rows=rows, flop_per_launch=flops,
+                rel_diff_fused_vs_unfused=diff, **out)
 
 
 # ------------------------------------------------------------------------------------------------
@@ -609,6 +729,7 @@ def main():
     if not args.no_extra:
         extra["c2_mote32m_stack"] = bench_c2(args.steps, args.warmup, dev)
         extra["c5_mote138m_prefill"] = bench_c5(max(3, args.steps // 4), min(args.warmup, 2), dev)
+        extra["qkv_prologue"] = {"T": bench_qkv(st["T"], dev, copies=8), "16T": bench_qkv(16 * st["T"], dev, copies=1)}
         extra["add_rms_norm"] = {"T": bench_norm(st["T"], dev, copies=8),
                                  "16T": bench_norm(16 * st["T"], dev, copies=1)}
         extra["chunk_dechunk"] = {"B1": bench_dc(1, dev, copies=8), "B8": bench_dc(8, dev, copies=1)}

@@ -6,17 +6,21 @@
 // 2 dh output features of one head pair of one projection (p1, p2: heads 2k, 2k+1; I~: the Givens
 // pair of the layer's parity, (2k, 2k+1) or (2k+1, 2k+2 mod H)). Wave w holds head (w & 1) for tokens
 // 64 (w >> 1) .. +63: dh/16 x 4 accumulator tiles, features in the rows, tokens in the columns, so
-// a lane ends with 4 consecutive features of one token. k advances 32 at a time through a ring of
-// four LDS stages filled by direct global -> LDS transfers (16 token or weight rows x 64 bytes per
-// wave instruction, chunks XOR-swizzled within a row). 256 x 2 dh outputs per 32-wide stage keep the
-// L2 -> LDS traffic at about 110 flop per byte (dh 96).
+// a lane ends with 4 consecutive features of one token. k advances 64 at a time through two LDS
+// slots filled by direct global -> LDS transfers (8 token or weight rows x 128 bytes per wave
+// instruction, chunks XOR-swizzled within a row): after the stage's barrier a wave reads all of its
+// fragments of the stage at once (one LDS latency per stage), issues the next stage's transfers into
+// the other slot, then runs the products. 256 x 2 dh outputs per stage keep the L2 -> LDS traffic
+// at about 110 flop per byte (dh 96).
 //
 // Epilogue. The product, rounded to bf16 (the projection output the reference rotates), goes to a
-// padded LDS tile [256 tokens][2 dh]; then every thread takes 16-byte chunks of it with their partner
-// chunks (RoPE: the other half of the head, relation.py:53-58; Givens: the same chunk of the pair's
-// other head, :160-174) and stores out = x C + y S, with C, S the bf16-rounded factors (cos / sin of
-// float(pos) * inv_freq[k] from a table kernel, cos / sin of theta), exactly as the unfused
-// rope_givens kernels compute them. Optionally the pre-rotation I~ is kept for the backward (d theta).
+// padded LDS tile [256 tokens][2 dh]; then every thread takes pairs of 16-byte chunks of it (RoPE:
+// chunk c and c + dh/16 of one head, the two halves that rotate together, relation.py:53-58; Givens:
+// the same chunk of the pair's two heads, :160-174) and stores both rotated chunks,
+// out_a = a C - b S, out_b = b C + a S, with C, S the bf16-rounded factors (cos / sin of
+// float(pos) * inv_freq[k] from a table kernel: one table entry serves both chunks of a RoPE pair;
+// cos / sin of theta), exactly as the unfused rope_givens kernels compute them. Optionally the
+// pre-rotation I~ is kept for the backward (d theta).
 #include "common.hpp"
 #include "params.hpp"
 #include "tiles.hpp"
@@ -24,7 +28,8 @@
 namespace mote {
 
 constexpr int kQkvTok = 256;     // tokens per workgroup
-constexpr int kQkvNW = 8;        // waves per workgroup
+constexpr int kQkvWaves = 8;     // waves per workgroup: 64 tokens x dh per wave (4 waves with 128 x dh
+                                 // tiles hold their accumulators in AGPRs at one wave per SIMD: slower)
 constexpr int kQkvK = 64;        // k per stage (a 128-byte line of every staged row)
 constexpr int kQkvStg = 2;       // ring depth
 constexpr int kQkvPad = 8;       // bf16 elements of padding per output-tile row
@@ -42,15 +47,17 @@ struct QkvParams {
   int ntok, ncol;                          // token tiles, column tiles (3 H / 2)
 };
 
-template <int DH>
+template <int DH, int NW>
 struct QkvShape {
   static constexpr int NF = DH / 16;                  // feature tiles per head
+  static constexpr int TPW = kQkvTok / (NW / 2);      // tokens per wave (waves pair up over the two heads)
+  static constexpr int NT = TPW / 16;                 // token tiles per wave
   static constexpr int ROWS = 2 * DH + kQkvTok;       // staged rows per stage: W head 0 | W head 1 | X
   static constexpr int CPR = kQkvK / 8;              // 16-byte chunks per staged row
   static constexpr int RPI = 64 / CPR;                // rows per wave instruction
   static constexpr int NINS = ROWS / RPI;             // wave instructions per stage
-  static constexpr int PER = (NINS + kQkvNW - 1) / kQkvNW;  // per wave (waves >= NINS % NW issue one
-  static constexpr int FULL = NINS % kQkvNW == 0 ? kQkvNW : NINS % kQkvNW;  // fewer when NINS % NW != 0)
+  static constexpr int PER = (NINS + NW - 1) / NW;   // per wave (waves >= NINS % NW issue one
+  static constexpr int FULL = NINS % NW == 0 ? NW : NINS % NW;  // fewer when NINS % NW != 0)
   static constexpr int STAGE = ROWS * kQkvK;          // bf16 elements
   static constexpr int OUTW = 2 * DH + kQkvPad;
   static constexpr int NCH = 2 * DH / 8;              // 16-byte chunks per output-tile row
@@ -68,9 +75,10 @@ __global__ void __launch_bounds__(256) rope_table_kernel(const float* inv_freq, 
   tab[i] = uint32_t(f2bf(cs)) | (uint32_t(f2bf(sn)) << 16);
 }
 
-template <int DH>
-__global__ void __launch_bounds__(64 * kQkvNW) qkv_rope_kernel(const QkvParams p) {
-  using S = QkvShape<DH>;
+template <int DH, int NW>
+__global__ void __launch_bounds__(64 * NW)
+qkv_rope_kernel(const QkvParams p) {
+  using S = QkvShape<DH, NW>;
   using E = Elem<bf16_t>;
   __shared__ __align__(16) bf16_t smem[S::LDS];
   const int lane = threadIdx.x & 63;
@@ -104,41 +112,42 @@ __global__ void __launch_bounds__(64 * kQkvNW) qkv_rope_kernel(const QkvParams p
   int lchs[S::PER];
 #pragma unroll
   for (int i = 0; i < S::PER; ++i) {
-    const int g = wave + kQkvNW * i;
+    const int g = wave + NW * i;
     const int64_t sr = g < 2 * GW ? p.w_sr : p.x_sr;
     const int lch = (lane % S::CPR) ^ tile_swz<kQkvK>(S::RPI * g + lrow);
     lchs[i] = lch;
     voff[i] = uint32_t(lrow * int(sr) + lch * 8) * 2u;
   }
   const bool more = wave < S::FULL;  // this wave issues PER transfers per stage (else PER - 1)
-  auto issue = [&](int kb, int slot) {
+  // transfer i of the wave's share of stage kb into ring slot `slot`
+  auto issue_i = [&](int i, int kb, int slot) {
+    const int g = wave + NW * i;
+    if (i == S::PER - 1 && !more) return;
     kb = min(kb, p.nk - 1);  // past the end: the last stage again (keeps every wave's count equal)
     const int k0 = kb * kQkvK;
-    bf16_t* dst = smem + slot * S::STAGE;
-#pragma unroll
-    for (int i = 0; i < S::PER; ++i) {
-      const int g = wave + kQkvNW * i;
-      if (i == S::PER - 1 && !more) break;
-      bf16_t* d = dst + g * 512;
-      if (g < GW) {
-        lds_dma16_s(wb0 + int64_t(S::RPI * g) * p.w_sr + k0, voff[i], d);
-      } else if (g < 2 * GW) {
-        lds_dma16_s(wb1 + int64_t(S::RPI * (g - GW)) * p.w_sr + k0, voff[i], d);
-      } else if (full) {
-        lds_dma16_s(xb + int64_t(S::RPI * (g - 2 * GW)) * p.x_sr + k0, voff[i], d);
-      } else {
-        const int r = min(r0 + S::RPI * (g - 2 * GW) + lrow, p.M - 1);
-        lds_dma16(p.x + int64_t(r) * p.x_sr + k0 + lchs[i] * 8, d);
-      }
+    bf16_t* d = smem + slot * S::STAGE + g * 512;
+    if (g < GW) {
+      lds_dma16_s(wb0 + int64_t(S::RPI * g) * p.w_sr + k0, voff[i], d);
+    } else if (g < 2 * GW) {
+      lds_dma16_s(wb1 + int64_t(S::RPI * (g - GW)) * p.w_sr + k0, voff[i], d);
+    } else if (full) {
+      lds_dma16_s(xb + int64_t(S::RPI * (g - 2 * GW)) * p.x_sr + k0, voff[i], d);
+    } else {
+      const int r = min(r0 + S::RPI * (g - 2 * GW) + lrow, p.M - 1);
+      lds_dma16(p.x + int64_t(r) * p.x_sr + k0 + lchs[i] * 8, d);
     }
+  };
+  auto issue = [&](int kb, int slot) {
+#pragma unroll
+    for (int i = 0; i < S::PER; ++i) issue_i(i, kb, slot);
   };
 
   const int hw = wave & 1, tw = wave >> 1;
-  f32x4 acc[S::NF][4];
+  f32x4 acc[S::NF][S::NT];
 #pragma unroll
   for (int f = 0; f < S::NF; ++f)
 #pragma unroll
-    for (int t = 0; t < 4; ++t) acc[f][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < S::NT; ++t) acc[f][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
 #pragma unroll
   for (int i = 0; i < kQkvStg - 1; ++i) issue(i, i);
@@ -149,21 +158,28 @@ __global__ void __launch_bounds__(64 * kQkvNW) qkv_rope_kernel(const QkvParams p
     else if (more) __builtin_amdgcn_s_waitcnt(kVmWaitStage<(kQkvStg - 2) * S::PER>());
     else __builtin_amdgcn_s_waitcnt(kVmWaitStage<(kQkvStg - 2) * (S::PER - 1)>());
     lds_barrier();
-    issue(kb + kQkvStg - 1, slot == 0 ? kQkvStg - 1 : slot - 1);
+    const int nslot = slot == 0 ? kQkvStg - 1 : slot - 1;
     const bf16_t* st = smem + slot * S::STAGE;
+    // every fragment of the stage first (one LDS latency per stage), the next stage's transfers,
+    // then the products
+    constexpr int KK = kQkvK / 32;
+    typename E::Frag a[KK][S::NF], bq[KK][S::NT];
 #pragma unroll
-    for (int kk = 0; kk < kQkvK / 32; ++kk) {
-      typename E::Frag a[S::NF], bq[4];
+    for (int kk = 0; kk < KK; ++kk) {
       const int ch = 4 * kk + (lane >> 4);
 #pragma unroll
-      for (int f = 0; f < S::NF; ++f) a[f] = tile_row_frag<kQkvK>(st, hw * DH + 16 * f + (lane & 15), ch);
+      for (int f = 0; f < S::NF; ++f) a[kk][f] = tile_row_frag<kQkvK>(st, hw * DH + 16 * f + (lane & 15), ch);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) bq[t] = tile_row_frag<kQkvK>(st, 2 * DH + 64 * tw + 16 * t + (lane & 15), ch);
+      for (int t = 0; t < S::NT; ++t)
+        bq[kk][t] = tile_row_frag<kQkvK>(st, 2 * DH + S::TPW * tw + 16 * t + (lane & 15), ch);
+    }
+    issue(kb + kQkvStg - 1, nslot);
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
 #pragma unroll
       for (int f = 0; f < S::NF; ++f)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) acc[f][t] = E::mma(a[f], bq[t], acc[f][t]);
-    }
+        for (int t = 0; t < S::NT; ++t) acc[f][t] = E::mma(a[kk][f], bq[kk][t], acc[f][t]);
     slot = slot == kQkvStg - 1 ? 0 : slot + 1;
   }
   __builtin_amdgcn_s_waitcnt(0);  // the ring's last transfers land before the tile reuses the LDS
@@ -173,8 +189,8 @@ __global__ void __launch_bounds__(64 * kQkvNW) qkv_rope_kernel(const QkvParams p
 #pragma unroll
   for (int f = 0; f < S::NF; ++f)
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int tok = 64 * tw + 16 * t + (lane & 15);
+    for (int t = 0; t < S::NT; ++t) {
+      const int tok = S::TPW * tw + 16 * t + (lane & 15);
       const int col = hw * DH + 16 * f + 4 * (lane >> 4);
       uint2 v;
       v.x = uint32_t(f2bf(acc[f][t][0])) | (uint32_t(f2bf(acc[f][t][1])) << 16);
@@ -183,7 +199,10 @@ __global__ void __launch_bounds__(64 * kQkvNW) qkv_rope_kernel(const QkvParams p
     }
   __syncthreads();
 
-  // rotations and stores: chunk c of token row `tok`, partner chunk from the tile
+  // rotations and stores. The chunks of a token row pair up: RoPE pairs chunk cc of a head with
+  // chunk cc + dh/16 of the same head (the two halves, one table entry for both), Givens pairs chunk
+  // cc of the first head with chunk cc of the second. A task is one pair of one token row: two
+  // chunks in, two rotated chunks out.
   const bool rope = part < 2 && p.tab != nullptr;
   const bool giv = part == 2 && p.theta != nullptr;
   float gc = 1.f, gs = 0.f;
@@ -195,71 +214,82 @@ __global__ void __launch_bounds__(64 * kQkvNW) qkv_rope_kernel(const QkvParams p
   }
   constexpr int HC = DH / 16;  // chunks per half head
   constexpr int CPH = DH / 8;  // chunks per head
+  constexpr int NPAIR = CPH;   // pairs per token row (2 heads x CPH chunks / 2)
   bf16_t* obase = part == 0 ? p.o1 : (part == 1 ? p.o2 : p.o3);
   const int64_t osb = part == 0 ? p.o1_sb : (part == 1 ? p.o2_sb : p.o3_sb);
   const int64_t osh = part == 0 ? p.o1_sh : (part == 1 ? p.o2_sh : p.o3_sh);
   const int64_t osr = part == 0 ? p.o1_sr : (part == 1 ? p.o2_sr : p.o3_sr);
   // every table load of the thread's tasks first (one latency for all of them), then the rotations
-  constexpr int NTASK = kQkvTok * S::NCH / (64 * kQkvNW);
+  constexpr int NTASK = kQkvTok * NPAIR / (64 * NW);
+  static_assert(kQkvTok * NPAIR % (64 * NW) == 0, "whole tasks per thread");
   const int rlast = p.M - 1;
   uint4 tabv[NTASK][2];
   if (rope) {
 #pragma unroll
     for (int i = 0; i < NTASK; ++i) {
-      const int q = threadIdx.x + 64 * kQkvNW * i;
-      const int tok = q / S::NCH, cc = (q % S::NCH) % CPH;
+      const int q = threadIdx.x + 64 * NW * i;
+      const int tok = q / NPAIR, cc = (q % NPAIR) % HC;
       const int r = min(r0 + tok, rlast);
       const int t = p.B == 1 ? r : r % p.T;
-      const uint4* tp = reinterpret_cast<const uint4*>(p.tab + int64_t(t) * (DH / 2) + (cc % HC) * 8);
+      const uint4* tp = reinterpret_cast<const uint4*>(p.tab + int64_t(t) * (DH / 2) + cc * 8);
       tabv[i][0] = tp[0];
       tabv[i][1] = tp[1];
     }
   }
 #pragma unroll
   for (int i = 0; i < NTASK; ++i) {
-    const int q = threadIdx.x + 64 * kQkvNW * i;
-    const int tok = q / S::NCH, c = q % S::NCH;
+    const int q = threadIdx.x + 64 * NW * i;
+    const int tok = q / NPAIR, j = q % NPAIR;
     const int r = r0 + tok;
     if (r >= p.M) break;  // tokens are in order: every later task of this thread is past M too
     const int b = p.B == 1 ? 0 : r / p.T, t = r - b * p.T;
-    const int hh = c / CPH, cc = c % CPH;
-    int pc;  // partner chunk in the tile row
-    if (part < 2) pc = hh * CPH + (cc < HC ? cc + HC : cc - HC);
-    else pc = (1 - hh) * CPH + cc;
-    const uint4 xv = *reinterpret_cast<const uint4*>(smem + tok * S::OUTW + c * 8);
-    const uint4 yv = *reinterpret_cast<const uint4*>(smem + tok * S::OUTW + pc * 8);
-    const int h = hh ? h1 : h0;
-    if (part == 2 && p.iraw)
-      *reinterpret_cast<uint4*>(p.iraw + b * p.ir_sb + t * p.ir_sr + h * DH + cc * 8) = xv;
+    // chunk ca (head ha, chunk cca) and its partner cb (head hb, chunk ccb); out_a = x_a C - x_b S,
+    // out_b = x_b C + x_a S
+    int ha, cca, hb, ccb;
+    if (part < 2) {
+      ha = hb = j / HC;
+      cca = j % HC;
+      ccb = cca + HC;
+    } else {
+      ha = 0;
+      hb = 1;
+      cca = ccb = j;
+    }
+    const uint4 xa = *reinterpret_cast<const uint4*>(smem + tok * S::OUTW + (ha * CPH + cca) * 8);
+    const uint4 xb = *reinterpret_cast<const uint4*>(smem + tok * S::OUTW + (hb * CPH + ccb) * 8);
+    const int gha = ha ? h1 : h0, ghb = hb ? h1 : h0;
+    if (part == 2 && p.iraw) {
+      *reinterpret_cast<uint4*>(p.iraw + b * p.ir_sb + t * p.ir_sr + gha * DH + cca * 8) = xa;
+      *reinterpret_cast<uint4*>(p.iraw + b * p.ir_sb + t * p.ir_sr + ghb * DH + ccb * 8) = xb;
+    }
     float C[8], Sn[8];
     if (rope) {
       const uint32_t tv[8] = {tabv[i][0].x, tabv[i][0].y, tabv[i][0].z, tabv[i][0].w,
                               tabv[i][1].x, tabv[i][1].y, tabv[i][1].z, tabv[i][1].w};
-      const float sg = cc < HC ? -1.f : 1.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         C[e] = bf2f(tv[e] & 0xffffu);
-        Sn[e] = sg * bf2f(tv[e] >> 16);
+        Sn[e] = bf2f(tv[e] >> 16);
       }
     } else {
-      const float sg = hh == 0 ? -1.f : 1.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         C[e] = gc;
-        Sn[e] = sg * gs;
+        Sn[e] = gs;
       }
     }
-    const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w}, yw[4] = {yv.x, yv.y, yv.z, yv.w};
-    uint32_t ow[4];
+    const uint32_t aw[4] = {xa.x, xa.y, xa.z, xa.w}, bw[4] = {xb.x, xb.y, xb.z, xb.w};
+    uint32_t oa[4], ob[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const float x0 = bf2f(xw[k] & 0xffffu), x1 = bf2f(xw[k] >> 16);
-      const float y0 = bf2f(yw[k] & 0xffffu), y1 = bf2f(yw[k] >> 16);
-      const float o0 = x0 * C[2 * k] + y0 * Sn[2 * k];
-      const float o1 = x1 * C[2 * k + 1] + y1 * Sn[2 * k + 1];
-      ow[k] = uint32_t(f2bf(o0)) | (uint32_t(f2bf(o1)) << 16);
+      const float a0 = bf2f(aw[k] & 0xffffu), a1 = bf2f(aw[k] >> 16);
+      const float b0 = bf2f(bw[k] & 0xffffu), b1 = bf2f(bw[k] >> 16);
+      const float c0 = C[2 * k], c1 = C[2 * k + 1], s0 = Sn[2 * k], s1 = Sn[2 * k + 1];
+      oa[k] = uint32_t(f2bf(a0 * c0 + b0 * -s0)) | (uint32_t(f2bf(a1 * c1 + b1 * -s1)) << 16);
+      ob[k] = uint32_t(f2bf(b0 * c0 + a0 * s0)) | (uint32_t(f2bf(b1 * c1 + a1 * s1)) << 16);
     }
-    *reinterpret_cast<uint4*>(obase + b * osb + t * osr + h * osh + cc * 8) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+    *reinterpret_cast<uint4*>(obase + b * osb + t * osr + gha * osh + cca * 8) = make_uint4(oa[0], oa[1], oa[2], oa[3]);
+    *reinterpret_cast<uint4*>(obase + b * osb + t * osr + ghb * osh + ccb * 8) = make_uint4(ob[0], ob[1], ob[2], ob[3]);
   }
 }
 
@@ -325,9 +355,9 @@ int launch_qkv_rope_fwd(const mote_qkv_rope_args* a, hipStream_t stream) {
   const int nwg = p.ntok * p.ncol;
   const dim3 grid(unsigned((nwg + 7) / 8 * 8));  // whole rounds over the 8 XCDs; the extra ids return
   switch (a->D) {
-    case 64: hipLaunchKernelGGL(qkv_rope_kernel<64>, grid, dim3(64 * kQkvNW), 0, stream, p); break;
-    case 96: hipLaunchKernelGGL(qkv_rope_kernel<96>, grid, dim3(64 * kQkvNW), 0, stream, p); break;
-    default: hipLaunchKernelGGL(qkv_rope_kernel<128>, grid, dim3(64 * kQkvNW), 0, stream, p); break;
+    case 64: hipLaunchKernelGGL((qkv_rope_kernel<64, kQkvWaves>), grid, dim3(64 * kQkvWaves), 0, stream, p); break;
+    case 96: hipLaunchKernelGGL((qkv_rope_kernel<96, kQkvWaves>), grid, dim3(64 * kQkvWaves), 0, stream, p); break;
+    default: hipLaunchKernelGGL((qkv_rope_kernel<128, kQkvWaves>), grid, dim3(64 * kQkvWaves), 0, stream, p); break;
   }
   return check_launch("qkv_rope");
 }

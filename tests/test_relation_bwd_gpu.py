@@ -151,3 +151,32 @@ def test_empty_query_rows_give_zero_prefix_grads(cuda):
     assert got[0].shape == (1, 2, 0, 32)
     assert float(got[1].abs().max()) == 0.0 and float(got[2].abs().max()) == 0.0
     assert float(got[3]) == 0.0
+
+
+def test_c3_full_size_bf16_against_fp32_kernels(cuda):
+    """Config C3 at its real size (T = 4964 chunks, H = 8, dh = 96): the bf16 tile kernels against
+    the fp32 kernels (pinned to the float64 oracle at 1e-5 by the tests above) on the same inputs,
+    upcast. Y, g and every gradient within 2e-2; dlam against the summed magnitude of its terms
+    -dA_i ln(i+1) (it cancels across rows), worked out on the device from the fp32 forward."""
+    print("case C3 full size T=4964 H=8 D=96 bf16 vs fp32 kernels", flush=True)
+    import mote_amd.flash_relation as fr
+
+    T = 4964
+    p1, p2, info, lam, dy = _inputs(1, 8, T, 0, 96, torch.bfloat16, seed=2)
+    up = lambda t: t.detach().float().requires_grad_(True)
+    p1f, p2f, infof, lamf = up(p1), up(p2), up(info), up(lam)
+    y, g = fr.flash_relation(p1, p2, info, lam, 2.0, q_start=0)
+    yf, gf = fr.flash_relation(p1f, p2f, infof, lamf, 2.0, q_start=0)
+    assert rel_err(y, yf) < 2e-2
+    assert float((g - gf).abs().max()) < 2e-2
+    got = torch.autograd.grad((y.float() * dy.float()).sum(), [p1, p2, info, lam])
+    ref = torch.autograd.grad((yf * dy.float()).sum(), [p1f, p2f, infof, lamf])
+    for a, b, n in zip(got[:3], ref[:3], NAMES):
+        assert a.shape == b.shape and a.dtype == torch.bfloat16, n
+        assert rel_err(a, b) < 2e-2, (n, rel_err(a, b))
+    with torch.no_grad():
+        _, gg, ibar, _ = torch.ops.mote.relation_fwd(p1f, p2f, infof, lamf, 2.0, 0)
+        dA = (dy.float() * (ibar - infof)).sum(-1) * gg * (1 - gg)
+        scale = float((dA * torch.log(torch.arange(1, T + 1, device=cuda, dtype=torch.float32))).abs().sum())
+    assert abs(float(got[3]) - float(ref[3])) / max(scale, 1e-3) < 2e-2
+    assert torch.isfinite(got[3])
