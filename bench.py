@@ -531,8 +531,10 @@ def bench_norm(rows: int, dev, copies: int, launches: int = 24):
 def bench_qkv(rows: int, dev, copies: int, launches: int = 20):
     """mote::qkv_rope at the Mote-96M shape (x bf16 [rows, 768], w = [w1; w2; wi] [2304, 768], an odd
     layer: RoPE on p1 / p2, Givens pairs (1,2),...,(7,0)) against the unfused path (hipBLASLt product
-    + mote::rope_givens), each a HIP graph of `launches` launches over `copies` inputs. Work: 2 rows
-    D 3D FLOP (the product; the rotations are elementwise)."""
+    + mote::rope_givens), each a HIP graph of `launches` launches over `copies` inputs. The fused
+    path's cos / sin table is memoised across calls (as every layer of a step shares it), so the
+    graph reuses the table its warm-up wrote. Work: 2 rows D 3D FLOP (the product; the rotations are
+    elementwise)."""
     from mote_amd.relation import FullRelation, qkv_rope, rope_givens
 
     D, H = D_MODEL, N_HEADS
@@ -558,10 +560,11 @@ def bench_qkv(rows: int, dev, copies: int, launches: int = 20):
         diff = max(float((u.float() - v.float()).abs().max()) / max(float(v.float().abs().max()), 1e-3)
                    for u, v in zip(a, b))
         for name, fn in (("fused", fused), ("unfused", unfused)):
-            for i in range(copies):
-                fn(i)
-            torch.cuda.synchronize()
             side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):  # warm-up on the capture stream (fills the RoPE table memo)
+                for i in range(copies):
+                    fn(i)
+            torch.cuda.synchronize()
             gr = torch.cuda.CUDAGraph()
             with torch.cuda.stream(side):
                 with torch.cuda.graph(gr, stream=side):

@@ -285,7 +285,10 @@ int mote_add_rms_norm_bwd(const mote_add_rms_norm_bwd_args* args, void* stream);
  * w1 | w2 | wi (row stride w_sr); D in {64, 96, 128}; H even; H D % 32 == 0. inv_freq NULL: no RoPE;
  * theta NULL: no Givens. info_raw (may be NULL) receives the I~ projections before the rotation,
  * for mote_rope_givens_bwd (qkv_info_only = 1). Workspace: mote_qkv_rope_workspace() bytes (the
- * cos / sin table of the T positions). All rows on 16-byte boundaries.
+ * cos / sin table of the T positions). table_ready = 1: the workspace already holds that table,
+ * written by an earlier call with the same T, pos0 and inv_freq whose work precedes this one on the
+ * stream (the caller memoises tables the way the reference memoises its RoPE tables,
+ * relation.py:45-58); the table launch is skipped. All rows on 16-byte boundaries.
  * ------------------------------------------------------------------------------------------------ */
 typedef struct mote_qkv_rope_args {
   int B, T, H, D;
@@ -298,6 +301,7 @@ typedef struct mote_qkv_rope_args {
   void* info_raw; int64_t ir_sb, ir_sr;
   void* workspace;
   size_t workspace_bytes;
+  int table_ready;
 } mote_qkv_rope_args;
 
 size_t mote_qkv_rope_workspace(const mote_qkv_rope_args* args);

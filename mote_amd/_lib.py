@@ -111,7 +111,7 @@ class QkvRopeArgs(C.Structure):
         ("x", C.c_void_p), ("x_sb", C.c_int64), ("x_sr", C.c_int64), ("w", C.c_void_p), ("w_sr", C.c_int64),
         ("inv_freq", C.c_void_p), ("theta", C.c_void_p), ("p1", View), ("p2", View), ("info", View),
         ("info_raw", C.c_void_p), ("ir_sb", C.c_int64), ("ir_sr", C.c_int64),
-        ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
+        ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t), ("table_ready", C.c_int),
     ]
 
 

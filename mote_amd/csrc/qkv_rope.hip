@@ -345,7 +345,7 @@ int launch_qkv_rope_fwd(const mote_qkv_rope_args* a, hipStream_t stream) {
   p.B = a->B; p.T = a->T; p.H = a->H; p.K = K; p.M = int(M); p.parity = a->layer_parity & 1; p.nk = K / kQkvK;
   p.ntok = int((M + kQkvTok - 1) / kQkvTok);
   p.ncol = 3 * (a->H / 2);
-  if (a->inv_freq) {
+  if (a->inv_freq && !a->table_ready) {
     const int64_t n = int64_t(a->T) * (a->D / 2);
     hipLaunchKernelGGL(rope_table_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, stream, a->inv_freq, a->pos0,
                        a->T, a->D / 2, reinterpret_cast<uint32_t*>(a->workspace));

@@ -155,6 +155,42 @@ USE_FUSED_PROLOGUE = True   # bf16 activations, head dim 64 / 96 / 128, no QK-No
                             # projections and RoPE / Givens; the unfused path serves everything else
 
 
+# cos / sin tables of the fused prologue, memoised per (device, stream, inv_freq, T, pos0) the way
+# the reference memoises its RoPE tables (at most 32 entries, relation.py:45-58): every layer of a
+# step asks for the same positions. Keyed by stream as well, so a table is only reused behind the
+# launch that wrote it. A graph capture reuses a table written before the capture began (on the
+# capture stream) and pins it, since the graph keeps its address; a table missing at capture time
+# is computed inside the graph on every replay and not memoised (its memory belongs to the graph).
+_ROPE_TABLES: "dict" = {}          # key -> (inv_freq, its version, table)
+_ROPE_TABLES_PINNED: "dict" = {}   # tables a captured graph reads, kept for the life of the process
+_ROPE_TABLES_MAX = 32
+
+
+def _rope_table_ws(a, x: torch.Tensor, inv: Optional[torch.Tensor], cacheable: bool) -> Tuple[torch.Tensor, int]:
+    """Workspace for mote_qkv_rope_fwd and whether it already holds the table (table_ready).
+    `cacheable`: inv is the caller's own frequency tensor (not a converted temporary)."""
+    n = max(int(L.lib().mote_qkv_rope_workspace(a)), 16)
+    if inv is None or not cacheable:
+        return torch.empty(n, device=x.device, dtype=torch.uint8), 0
+    key = (x.device, torch.cuda.current_stream(x.device).cuda_stream, inv.data_ptr(), a.T, a.pos0, a.D)
+    hit = _ROPE_TABLES.get(key)
+    # the entry holds the frequency tensor itself: its memory cannot be recycled for another tensor
+    # while the entry lives, and an in-place change of it shows in its version counter
+    valid = hit is not None and hit[0] is inv and hit[1] == inv._version
+    if torch.cuda.is_current_stream_capturing():
+        if valid:
+            _ROPE_TABLES_PINNED[hit[2].data_ptr()] = hit[2]
+            return hit[2], 1
+        return torch.empty(n, device=x.device, dtype=torch.uint8), 0
+    if valid:
+        return hit[2], 1
+    if hit is None and len(_ROPE_TABLES) >= _ROPE_TABLES_MAX:
+        _ROPE_TABLES.pop(next(iter(_ROPE_TABLES)))  # a pinned table stays alive through the pin
+    ws = torch.empty(n, device=x.device, dtype=torch.uint8)
+    _ROPE_TABLES[key] = (inv, inv._version, ws)
+    return ws, 0
+
+
 @torch.library.custom_op("mote::qkv_rope", mutates_args=())
 def _qkv_rope(x: torch.Tensor, w: torch.Tensor, inv_freq: Optional[torch.Tensor], theta: Optional[torch.Tensor],
               n_heads: int, parity: int, pos0: int, keep_info: bool
@@ -180,7 +216,7 @@ def _qkv_rope(x: torch.Tensor, w: torch.Tensor, inv_freq: Optional[torch.Tensor]
     a.p1, a.p2, a.info = L.view(p1), L.view(p2), L.view(info)
     if keep_info:
         a.info_raw, a.ir_sb, a.ir_sr = iraw.data_ptr(), iraw.stride(0), iraw.stride(1)
-    ws = torch.empty(max(int(L.lib().mote_qkv_rope_workspace(a)), 16), device=x.device, dtype=torch.uint8)
+    ws, a.table_ready = _rope_table_ws(a, x, inv, inv is inv_freq)
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
     L.check(L.lib().mote_qkv_rope_fwd(a, L.stream_of(x)), "mote_qkv_rope_fwd")
     return p1, p2, info, iraw

@@ -142,3 +142,85 @@ def test_unsupported_head_dim_raises(cuda):
     w = torch.zeros(3 * 4 * 48, 4 * 48, device=cuda, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="head dim 48"):
         _qkv_rope(x, w, None, None, 4, 0, 0, False)
+
+
+def test_rope_tables_are_reused_and_invalidated(cuda):
+    """The cos / sin table is memoised per (stream, inv_freq, T, pos0): a second call with the same
+    positions skips the table launch and gives identical bits; other positions, or an in-place
+    change of the frequencies, compute a new table (results against the float64 oracle)."""
+    from mote_amd import relation as R
+
+    print("case qkv_rope table reuse", flush=True)
+    R._ROPE_TABLES.clear()
+    g = torch.Generator().manual_seed(11)
+    H, D, T = 8, 96, 300
+    K = H * D
+    x = torch.randn(1, T, K, generator=g).bfloat16()
+    w = (torch.randn(3 * K, K, generator=g) / K ** 0.5).bfloat16()
+    theta = torch.rand(H // 2, generator=g) * 2 - 1
+    inv = R.rope_inv_freq(D, 10000.0).to(cuda)
+    xg, wg, tg = x.to(cuda), w.to(cuda), theta.to(cuda)
+    with torch.no_grad():
+        a = R.qkv_rope(xg, wg, H, inv, tg, 1, 3)
+        assert len(R._ROPE_TABLES) == 1
+        b = R.qkv_rope(xg, wg, H, inv, tg, 1, 3)
+        assert len(R._ROPE_TABLES) == 1
+        for u, v in zip(a, b):
+            assert torch.equal(u, v)
+        c = R.qkv_rope(xg, wg, H, inv, tg, 0, 40)
+        assert len(R._ROPE_TABLES) == 2
+        for got, want in zip(c, _ref(x, w, H, inv.cpu(), theta, 0, 40)):
+            assert rel_err(got, want) < 2e-2
+        inv.mul_(0.5)  # the same tensor, new values: its table must not be reused
+        d = R.qkv_rope(xg, wg, H, inv, tg, 1, 3)
+    q, k, _ = _ref(x, w, H, None, theta, 1, 3)
+    # the oracle's table construction (rope_cos_sin) with the halved frequencies
+    ang = torch.arange(3, 3 + T, dtype=torch.float32)[:, None] * inv.cpu()[None, :]
+    emb = torch.cat([ang, ang], dim=-1)
+    cos, sin = emb.cos().to(torch.bfloat16).double(), emb.sin().to(torch.bfloat16).double()
+    for got, want in ((d[0], O.apply_rope(q, cos, sin)), (d[1], O.apply_rope(k, cos, sin))):
+        assert rel_err(got, want) < 2e-2, rel_err(got, want)
+    assert not torch.equal(d[0], a[0])
+
+
+def test_fused_prologue_replays_in_a_hip_graph(cuda):
+    """Captured after a warm-up on the capture stream, the prologue reads the memoised table from the
+    graph (the table launch is not captured); every replay, with eager work and synchronisations
+    between replays, reproduces the eager outputs bit for bit. A capture with no table yet computes it
+    inside the graph."""
+    from mote_amd import relation as R
+
+    print("case qkv_rope graph replay", flush=True)
+    g = torch.Generator().manual_seed(12)
+    H, D, T = 8, 96, 700
+    K = H * D
+    x = torch.randn(1, T, K, generator=g).bfloat16().to(cuda)
+    w = (torch.randn(3 * K, K, generator=g) / K ** 0.5).bfloat16().to(cuda)
+    theta = (torch.rand(H // 2, generator=g) * 2 - 1).to(cuda)
+    inv = R.rope_inv_freq(D, 10000.0).to(cuda)
+    side = torch.cuda.Stream()
+    for pos0, warm in ((0, True), (9, False)):
+        R._ROPE_TABLES.clear()
+        with torch.no_grad():
+            ref = [t.clone() for t in R.qkv_rope(x, w, H, inv, theta, 1, pos0)]
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                if warm:
+                    R.qkv_rope(x, w, H, inv, theta, 1, pos0)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.stream(side):
+                with torch.cuda.graph(graph, stream=side):
+                    outs = R.qkv_rope(x, w, H, inv, theta, 1, pos0)
+            torch.cuda.current_stream().wait_stream(side)
+            torch.cuda.synchronize()
+            for _ in range(3):
+                for o in outs:
+                    o.fill_(float("nan"))
+                R.qkv_rope(x, w, H, inv, theta, 0, pos0 + 1)  # eager work between replays
+                torch.cuda.synchronize()
+                graph.replay()
+                torch.cuda.synchronize()
+                for o, r in zip(outs, ref):
+                    assert torch.equal(o, r)
+        del graph
