@@ -358,6 +358,79 @@ def bench_decode(batch: int, steps: int, dev, copies: int):
 # ------------------------------------------------------------------------------------------------
 # C2 (Mote-32M stack) and C5 (Mote-138M ragged prefill): reported beside the headline
 # ------------------------------------------------------------------------------------------------
+def bench_decode_engine(batch: int, steps: int, dev):
+    """The decode engine's per-token Relation work for the 12-layer Mote-96M stack: per layer the
+    fused projection (hipBLASLt), the decode kernel (RoPE / Givens, append at the device position S,
+    the sweep over rows [0, S]) and `wo` (graph.py:151-187 through mote_amd.decode.RelationDecodeStep),
+    layer outputs chained into the next layer's input, the whole token captured as one HIP graph
+    that advances S itself. Caches prefilled to 4096 rows as in bench_decode; `steps` tokens timed."""
+    from mote_amd.arena import RelationArena
+    from mote_amd.decode import RelationDecodeStep
+    from mote_amd.relation import FullRelation, rope_givens
+
+    S0 = 4096
+    cap = S0 + steps + 256
+    torch.manual_seed(7)
+    arena = RelationArena(N_LAYERS, N_HEADS, cap, D_HEAD, dev, torch.bfloat16, batch=batch)
+    mods, dsteps = [], []
+    for li in range(N_LAYERS):
+        m = FullRelation(D_MODEL, N_HEADS, li)
+        with torch.no_grad():
+            m.theta.uniform_(-0.3, 0.3)
+        m = m.to(dev)
+        with torch.no_grad():
+            w = torch.cat([m.w1.weight, m.w2.weight, m.wi.weight], 0).to(torch.bfloat16)
+            for b0 in range(batch):
+                x = rmsnorm(torch.randn(1, S0, D_MODEL, device=dev)).to(torch.bfloat16)
+                _, p2, info = rope_givens(x @ w.t(), N_HEADS, m.inv_freq, m.theta, li, 0)
+                arena.p2(li)[b0, :, :S0] = p2[0]
+                arena.info(li)[b0, :, :S0] = info[0]
+        for lin in (m.w1, m.w2, m.wi, m.wo):
+            lin.to(torch.bfloat16)  # bf16 weights; lam, theta and the RoPE frequencies stay fp32
+        mods.append(m)
+        dsteps.append(RelationDecodeStep(m, arena, li))
+    S = torch.full((batch,), S0, device=dev, dtype=torch.int64)
+    x0 = torch.randn(batch, 1, D_MODEL, device=dev).to(torch.bfloat16)
+
+    def token():
+        x = x0
+        for li, st in enumerate(dsteps):
+            x, _ = st(x, S, advance=(li == N_LAYERS - 1))
+        return x
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        token()  # warm-up on the capture stream (S advances once)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(gr, stream=side):
+            token()
+    torch.cuda.current_stream().wait_stream(side)
+    S.fill_(S0)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        gr.replay()
+    S.fill_(S0)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(steps):
+        gr.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    us = t0.elapsed_time(t1) * 1e3 / steps
+    if int(S[0]) != S0 + steps:
+        raise RuntimeError(f"decode engine: S = {int(S[0])} after {steps} tokens from {S0}")
+    log(f"[bench] decode engine b{batch}: {us:.1f} us per token for the 12 Relation layers (projections, decode, wo)")
+    del gr
+    return dict(workload=f"Mote-96M Relation decode step with projections and wo, 12 layers chained, batch {batch}, "
+                         f"cache 4096 -> {S0 + steps} rows, one HIP graph per token", batch=batch,
+                us_per_token=round(us, 2), tokens=steps)
+
+
 def bench_c2(steps: int, warmup: int, dev):
     """Mote-32M Relation stack (d_model 512, 8 heads, dh 64, 8 layers), bf16 fwd+bwd, B = 4, a
     2048-byte window with Bernoulli(1/3.3) chunk boundaries (seed 1): every sequence padded to the
@@ -728,6 +801,7 @@ def main():
     if not args.no_decode:
         dec["b1"] = bench_decode(1, args.decode_steps, dev, copies=4)
         dec["b16"] = bench_decode(16, args.decode_steps, dev, copies=1)
+        dec_engine = {k: bench_decode_engine(b, args.decode_steps, dev) for k, b in (("b1", 1), ("b16", 16))}
     extra = {}
     if not args.no_extra:
         extra["c2_mote32m_stack"] = bench_c2(args.steps, args.warmup, dev)
@@ -779,6 +853,8 @@ def main():
                 "traffic": measured_traffic(f"relation_decode_kernel_{k}"),
                 "cache_copies_rotated": v["copies"]}
             for k, v in dec.items()}
+    if dec:
+        out["decode_engine"] = dec_engine
     out.update(extra)
     if cpu is not None:
         out["cpu_baseline"] = {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")}

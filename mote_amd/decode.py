@@ -77,9 +77,10 @@ def relation_decode(p1: torch.Tensor, p2: torch.Tensor, info: torch.Tensor, S: t
 class RelationDecodeStep:
     """GraphDecoder._relation_step (graph.py:151-187) for one FullRelation layer over its arena rows.
 
-    Holds the static tensors a captured graph needs (fp32 lam/theta/inv_freq copies refreshed by
-    `sync_params()`, the workspace, outputs). `__call__(x [B,1,D], S)` returns (out [B,1,D],
-    xm [B] = mean over heads of the exchange mass, graph.py:186)."""
+    Holds the static tensors a captured graph needs (fp32 lam/theta/inv_freq copies and the stacked
+    projection weight [w1; w2; wi], refreshed by `sync_params()`, the workspace, outputs).
+    `__call__(x [B,1,D], S)` returns (out [B,1,D], xm [B] = mean over heads of the exchange mass,
+    graph.py:186)."""
 
     def __init__(self, mixer, arena: RelationArena, layer: int):
         self.mixer, self.arena, self.layer = mixer, arena, layer
@@ -92,10 +93,19 @@ class RelationDecodeStep:
         self.lam = torch.empty((), device=dev, dtype=torch.float32)
         self.theta = torch.empty(max(H // 2, 1), device=dev, dtype=torch.float32) if mixer.use_givens else None
         self.inv_freq = mixer.inv_freq.to(device=dev, dtype=torch.float32).clone() if mixer.use_rope else None
+        self.w_qkv = None
         self.sync_params()
 
     @torch.no_grad()
     def sync_params(self) -> None:
+        """Refresh the step's copies of the layer's parameters (after an optimiser step; a captured
+        graph keeps reading these same tensors)."""
+        m = self.mixer
+        w = torch.cat([m.w1.weight, m.w2.weight, m.wi.weight], dim=0)
+        if self.w_qkv is None or self.w_qkv.shape != w.shape or self.w_qkv.dtype != w.dtype:
+            self.w_qkv = w.detach().clone()
+        else:
+            self.w_qkv.copy_(w)
         self.lam.copy_(self.mixer.lam.detach().float())
         if self.theta is not None:
             self.theta.copy_(self.mixer.theta.detach().float())
@@ -105,8 +115,7 @@ class RelationDecodeStep:
         m = self.mixer
         B, T, Dm = x.shape
         H, dh = m.n_heads, m.d_head
-        w = torch.cat([m.w1.weight, m.w2.weight, m.wi.weight], dim=0)
-        qkv = F.linear(x, w).to(self.arena.dtype).view(B, 3, H, dh)
+        qkv = F.linear(x, self.w_qkv).to(self.arena.dtype).view(B, 3, H, dh)
         if m.qk_norm:
             q = m.p1_norm(qkv[:, 0])
             k = m.p2_norm(qkv[:, 1])

@@ -183,3 +183,16 @@ def test_decode_step_module_matches_oracle(cuda):
     assert int(Sd) == S + 1
     assert rel_err(arena.buf[0, 0, :, S], p2buf[0, :, S]) < 1e-5
     assert rel_err(arena.buf[0, 1, :, S], ibuf[0, :, S]) < 1e-5
+    # a parameter update reaches the step through sync_params() (the step keeps its own stacked
+    # projection weight and fp32 copies, which a captured graph reads)
+    with torch.no_grad():
+        for m in (mine, ref):
+            m.w2.weight.mul_(0.5)
+            m.lam.add_(0.25)
+    step.sync_params()
+    x2 = torch.randn(1, 1, 768, generator=g)
+    out2, xm2 = step(x2.cuda(), Sd, advance=True)
+    outr2, _, xmr2 = O.decode_step_ref(ref, x2, p2buf, ibuf, S + 1, Cb=cap)
+    assert rel_err(out2, outr2) < 1e-5, rel_err(out2, outr2)
+    assert abs(float(xm2) - float(xmr2)) < 1e-5
+    assert int(Sd) == S + 2
