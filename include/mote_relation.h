@@ -213,6 +213,7 @@ typedef struct mote_relation_decode_args {
   float* g;
   void* workspace;
   size_t workspace_bytes;
+  float* xm;               /* [B] mean over the heads of g (graph.py:186), or NULL */
 } mote_relation_decode_args;
 
 size_t mote_relation_decode_workspace(const mote_relation_decode_args* args);

@@ -80,7 +80,7 @@ class DecodeArgs(C.Structure):
         ("p1", C.c_void_p), ("p2", C.c_void_p), ("info", C.c_void_p), ("in_sb", C.c_int64),
         ("cache_p2", View), ("cache_info", View),
         ("y", C.c_void_p), ("y_sb", C.c_int64), ("g", C.c_void_p),
-        ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
+        ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t), ("xm", C.c_void_p),
     ]
 
 

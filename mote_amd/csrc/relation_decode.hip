@@ -49,6 +49,7 @@ struct DecParams {
   void* y;
   int64_t y_sb;
   float* g;
+  float* xm;          // [B] mean over heads of g, or null
   float* part;        // [BH][nsplit][D + 2]  (max, l, z)
   int* cnt;           // [BH] splits published in this call, kDecCntStride ints apart (zero between calls)
   int* cnt_seq;       // [B] heads finished in this call, kDecCntStride ints apart (zero between calls)
@@ -372,12 +373,21 @@ relation_decode_kernel(const DecParams p) {
   if (tid == 0) {
     p.g[bh] = bad ? __builtin_nanf("") : gate;
     __hip_atomic_store(p.cnt + bh * kDecCntStride, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // the last head of the sequence: every workgroup of the sequence has read S[b] by now
-    const int before =
-        __hip_atomic_fetch_add(p.cnt_seq + b * kDecCntStride, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the last head of the sequence: every workgroup of the sequence has read S[b] by now. With xm
+    // the count is acquire-release, so the last head also sees every other head's g.
+    int before;
+    if (p.xm)
+      before = __hip_atomic_fetch_add(p.cnt_seq + b * kDecCntStride, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    else
+      before = __hip_atomic_fetch_add(p.cnt_seq + b * kDecCntStride, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (before == p.H - 1) {
       __hip_atomic_store(p.cnt_seq + b * kDecCntStride, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (p.flags & MOTE_DECODE_ADVANCE) p.S[b] = S64 + 1;
+      if (p.xm) {
+        float sum = 0.f;  // fixed head order
+        for (int hh = 0; hh < p.H; ++hh) sum += p.g[b * p.H + hh];
+        p.xm[b] = sum / float(p.H);
+      }
     }
   }
 }
@@ -447,6 +457,7 @@ int launch_decode(const mote_relation_decode_args* a, hipStream_t stream) {
   p.part = reinterpret_cast<float*>(ws + w.part);
   p.cnt = reinterpret_cast<int*>(ws + w.cnt);
   p.cnt_seq = reinterpret_cast<int*>(ws + w.cnt_seq);
+  p.xm = a->xm;
   p.B = a->B; p.H = a->H; p.D = a->D; p.cap = a->capacity; p.parity = a->layer_parity & 1; p.flags = a->flags;
   p.scale = 1.0f / sqrtf((float)a->D);
   p.tau_inv = 1.0f / a->tau_s;

@@ -34,7 +34,7 @@ def relation_decode(p1: torch.Tensor, p2: torch.Tensor, info: torch.Tensor, S: t
                     cache_info: torch.Tensor, lam: torch.Tensor, tau_s: float = 2.0,
                     inv_freq: Optional[torch.Tensor] = None, theta: Optional[torch.Tensor] = None, layer_idx: int = 0,
                     advance: bool = False, workspace: Optional[torch.Tensor] = None, y: Optional[torch.Tensor] = None,
-                    g: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+                    g: Optional[torch.Tensor] = None, xm: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """One decode step for B sequences.
 
     p1, p2, info: raw projections of the new chunk, [B, H, dh] (head stride dh, any batch stride),
@@ -42,6 +42,8 @@ def relation_decode(p1: torch.Tensor, p2: torch.Tensor, info: torch.Tensor, S: t
         applied on the device.
     S: int64 [B] device positions; row S[b] of the caches receives the new P2 / I~ row.
     cache_p2, cache_info: [B, H, capacity, dh] views (RelationArena.p2(layer) / .info(layer)).
+    xm: optional fp32 [B] that receives the mean of g over the heads (graph.py:186), worked out by
+        the kernel's last head of each sequence.
     Returns (y [B, H, dh] in the cache dtype, g [B, H] fp32 exchange mass = 1 - F_SS).
     """
     B, H, D = p1.shape
@@ -70,6 +72,10 @@ def relation_decode(p1: torch.Tensor, p2: torch.Tensor, info: torch.Tensor, S: t
     a.cache_p2, a.cache_info = L.view(cache_p2), L.view(cache_info)
     a.y, a.y_sb, a.g = y.data_ptr(), y.stride(0), g.data_ptr()
     a.workspace, a.workspace_bytes = workspace.data_ptr(), workspace.numel()
+    if xm is not None:
+        if xm.dtype != torch.float32 or xm.numel() != B or not xm.is_contiguous():
+            raise ValueError("xm must be a contiguous fp32 tensor of B elements")
+        a.xm = xm.data_ptr()
     L.check(L.lib().mote_relation_decode(a, L.stream_of(p1)), "mote_relation_decode")
     return y, g
 
@@ -90,6 +96,7 @@ class RelationDecodeStep:
         self.workspace = decode_workspace(B, H, D, arena.capacity, dev, arena.dtype)
         self.y = torch.empty(B, H, D, device=dev, dtype=arena.dtype)
         self.g = torch.empty(B, H, device=dev, dtype=torch.float32)
+        self.xm = torch.empty(B, device=dev, dtype=torch.float32)
         self.lam = torch.empty((), device=dev, dtype=torch.float32)
         self.theta = torch.empty(max(H // 2, 1), device=dev, dtype=torch.float32) if mixer.use_givens else None
         self.inv_freq = mixer.inv_freq.to(device=dev, dtype=torch.float32).clone() if mixer.use_rope else None
@@ -122,6 +129,6 @@ class RelationDecodeStep:
             qkv = torch.stack([q, k, qkv[:, 2]], dim=1)
         relation_decode(qkv[:, 0], qkv[:, 1], qkv[:, 2], S, self.arena.p2(self.layer), self.arena.info(self.layer),
                         self.lam, m.tau_s, self.inv_freq, self.theta, m.layer_idx, advance, self.workspace,
-                        self.y, self.g)
+                        self.y, self.g, self.xm)
         y = self.y.to(x.dtype).view(B, H, 1, dh)
-        return m._out(y, x), self.g.mean(-1)
+        return m._out(y, x), self.xm

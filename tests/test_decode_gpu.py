@@ -142,3 +142,26 @@ def test_decode_replays_in_a_hip_graph(cuda):
         assert torch.equal(gb, eager[s][1]), s
         _ = (yb.float() * 2).sum()  # eager work between replays
     assert torch.equal(kg, ke) and torch.equal(vg, ve) and torch.equal(Sg, Se)
+
+
+def test_decode_exchange_mass_mean_over_heads(cuda):
+    """xm (graph.py:186): the kernel's last head of every sequence writes the mean of g over the heads
+    (fixed head order); checked against the kernel's own g and the oracle's, over two calls in a row
+    (the completion counts return to zero) with the position advancing."""
+    from mote_amd.decode import decode_workspace, relation_decode
+
+    print("case decode xm b16", flush=True)
+    S = [4096, 1, 17, 2049, 300, 4351 - 1, 64, 65, 1000, 3000, 5, 4095, 128, 129, 2500, 4000]
+    kc, vc, raw, th, inv, Sv = _setup(16, 8, 96, 4352, S, torch.bfloat16, seed=8)
+    kd, vd, Sd = kc.cuda(), vc.cuda(), Sv.cuda()
+    ws = decode_workspace(16, 8, 96, 4352, "cuda")
+    xm = torch.full((16,), float("nan"), device="cuda")
+    for call in range(2):
+        y, gg = relation_decode(*(t.cuda() for t in raw), Sd, kd, vd, torch.tensor(0.5, device="cuda"), 2.0,
+                                inv.cuda(), th.cuda(), 1, advance=True, workspace=ws, xm=xm)
+        torch.cuda.synchronize()
+        assert float((xm - gg.mean(-1)).abs().max()) < 1e-6, call
+        if call == 0:
+            _, gr, _, _ = _oracle(kc, vc, raw, th, inv, Sv, 1, 0.5, torch.bfloat16)
+            assert float((xm.cpu().double() - gr.mean(-1)).abs().max()) < 2e-2
+        assert torch.equal(Sd.cpu(), Sv + call + 1)
