@@ -309,6 +309,25 @@ size_t mote_qkv_rope_workspace(const mote_qkv_rope_args* args);
 int mote_qkv_rope_fwd(const mote_qkv_rope_args* args, void* stream);
 
 /* ------------------------------------------------------------------------------------------------
+ * Skinny product for the decode engine's per-token projections (bf16, fp32 accumulation):
+ * y [B, N] = x [B, K] W[N, K]^T rounded to bf16, B <= 16 rows (one new chunk per sequence), N a
+ * multiple of 16, K a multiple of 128 and at most 1024; x and W rows on 16-byte boundaries, row
+ * strides in elements. B == 0 launches nothing.
+ * Replaces: the projections around GraphDecoder._relation_step (F.linear of the stacked
+ * [w1; w2; wi] and wo, mote/infer/graph.py:151-187, relation.py:176-182) at decode shapes, where
+ * the general GEMM library's launch is most of the cost.
+ * ------------------------------------------------------------------------------------------------ */
+typedef struct mote_skinny_gemm_args {
+  int dtype;               /* MOTE_BF16 */
+  int B, N, K;
+  const void* x; int64_t x_sr;
+  const void* w; int64_t w_sr;
+  void* y; int64_t y_sr;
+} mote_skinny_gemm_args;
+
+int mote_skinny_gemm(const mote_skinny_gemm_args* args, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
  * Chunking either side of the main network (mote/model/dc.py:192-352).
  *
  * mote_chunk_route: per row of the boundary mask (bool / uint8 [B, L], row stride mask_sr bytes),

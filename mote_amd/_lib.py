@@ -115,6 +115,14 @@ class QkvRopeArgs(C.Structure):
     ]
 
 
+class SkinnyGemmArgs(C.Structure):
+    _fields_ = [
+        ("dtype", C.c_int), ("B", C.c_int), ("N", C.c_int), ("K", C.c_int),
+        ("x", C.c_void_p), ("x_sr", C.c_int64), ("w", C.c_void_p), ("w_sr", C.c_int64),
+        ("y", C.c_void_p), ("y_sr", C.c_int64),
+    ]
+
+
 class ChunkRouteArgs(C.Structure):
     _fields_ = [
         ("B", C.c_int), ("L", C.c_int), ("mask", C.c_void_p), ("mask_sr", C.c_int64),
@@ -196,6 +204,7 @@ EXPORTS = {
     "mote_add_rms_norm_bwd": ([C.POINTER(NormBwdArgs), C.c_void_p], C.c_int),
     "mote_qkv_rope_workspace": ([C.POINTER(QkvRopeArgs)], C.c_size_t),
     "mote_qkv_rope_fwd": ([C.POINTER(QkvRopeArgs), C.c_void_p], C.c_int),
+    "mote_skinny_gemm": ([C.POINTER(SkinnyGemmArgs), C.c_void_p], C.c_int),
     "mote_chunk_route": ([C.POINTER(ChunkRouteArgs), C.c_void_p], C.c_int),
     "mote_chunk_gather": ([C.POINTER(ChunkGatherArgs), C.c_void_p], C.c_int),
     "mote_chunk_gather_bwd": ([C.POINTER(ChunkGatherBwdArgs), C.c_void_p], C.c_int),

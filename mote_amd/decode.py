@@ -80,6 +80,32 @@ def relation_decode(p1: torch.Tensor, p2: torch.Tensor, info: torch.Tensor, S: t
     return y, g
 
 
+def skinny_linear(x: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y [B, N] = x [B, K] w[N, K]^T for the decode engine's per-token projections (bf16, B <= 16,
+    N % 16 == 0, K % 128 == 0, K <= 1024): one launch of mote_skinny_gemm."""
+    B, K = x.shape
+    N = w.shape[0]
+    if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+        raise TypeError("skinny_linear: bf16 x and w")
+    if x.stride(-1) != 1 or w.stride(-1) != 1 or w.shape[1] != K:
+        raise ValueError("skinny_linear: x [B, K] and w [N, K] with unit element stride")
+    if out is None:
+        out = torch.empty(B, N, device=x.device, dtype=x.dtype)
+    a = L.SkinnyGemmArgs()
+    a.dtype, a.B, a.N, a.K = L.dtype_code(x), B, N, K
+    a.x, a.x_sr = x.data_ptr(), x.stride(0)
+    a.w, a.w_sr = w.data_ptr(), w.stride(0)
+    a.y, a.y_sr = out.data_ptr(), out.stride(0)
+    L.check(L.lib().mote_skinny_gemm(a, L.stream_of(x)), "mote_skinny_gemm")
+    return out
+
+
+def _skinny_ok(B: int, x: torch.Tensor, *ws: torch.Tensor) -> bool:
+    return (x.is_cuda and x.dtype == torch.bfloat16 and 1 <= B <= 16 and
+            all(w.dtype == torch.bfloat16 and w.shape[0] % 16 == 0 and w.shape[1] % 128 == 0 and w.shape[1] <= 1024
+                for w in ws))
+
+
 class RelationDecodeStep:
     """GraphDecoder._relation_step (graph.py:151-187) for one FullRelation layer over its arena rows.
 
@@ -122,7 +148,12 @@ class RelationDecodeStep:
         m = self.mixer
         B, T, Dm = x.shape
         H, dh = m.n_heads, m.d_head
-        qkv = F.linear(x, self.w_qkv).to(self.arena.dtype).view(B, 3, H, dh)
+        skinny = T == 1 and _skinny_ok(B, x, self.w_qkv, m.wo.weight, *([m.wg.weight] if m.out_gate else []))
+        if skinny:  # bf16 decode shapes: the skinny product instead of the general GEMM library
+            qkv = skinny_linear(x.reshape(B, Dm), self.w_qkv).view(B, 3, H, dh)
+        else:
+            qkv = F.linear(x, self.w_qkv).view(B, 3, H, dh)
+        qkv = qkv.to(self.arena.dtype)
         if m.qk_norm:
             q = m.p1_norm(qkv[:, 0])
             k = m.p2_norm(qkv[:, 1])
@@ -130,5 +161,10 @@ class RelationDecodeStep:
         relation_decode(qkv[:, 0], qkv[:, 1], qkv[:, 2], S, self.arena.p2(self.layer), self.arena.info(self.layer),
                         self.lam, m.tau_s, self.inv_freq, self.theta, m.layer_idx, advance, self.workspace,
                         self.y, self.g, self.xm)
+        if skinny:  # _out (relation.py:176-182) on the skinny product
+            y = self.y.to(x.dtype).reshape(B, H * dh)
+            if m.out_gate:
+                y = y * torch.sigmoid(skinny_linear(x.reshape(B, Dm), m.wg.weight))
+            return skinny_linear(y, m.wo.weight).view(B, 1, Dm), self.xm
         y = self.y.to(x.dtype).view(B, H, 1, dh)
         return m._out(y, x), self.xm

@@ -56,3 +56,23 @@ def test_argument_errors_are_reported_without_a_gpu():
     a.B, a.H, a.TQ, a.TK, a.D = 1, 1, 4, 4, 100
     assert _lib.lib().mote_relation_fwd(a, None) == 2
     assert b"head dim" in _lib.lib().mote_last_error()
+
+
+def test_skinny_gemm_rejects_unsupported_shapes_without_a_gpu():
+    """mote_skinny_gemm checks dtype, row count and the N / K granularity before any launch."""
+    from mote_amd import _lib
+
+    if not _lib.available():
+        pytest.skip("libmote_relation.so not built")
+    a = _lib.SkinnyGemmArgs()
+    a.dtype, a.B, a.N, a.K = _lib.MOTE_F32, 1, 16, 128
+    a.x = a.w = a.y = 16
+    a.x_sr = a.w_sr = a.y_sr = 128
+    assert _lib.lib().mote_skinny_gemm(a, None) == 1
+    assert b"bf16" in _lib.lib().mote_last_error()
+    a.dtype = _lib.MOTE_BF16
+    for B, N, K in ((17, 16, 128), (1, 24, 128), (1, 16, 100), (1, 16, 2048)):
+        a.B, a.N, a.K = B, N, K
+        assert _lib.lib().mote_skinny_gemm(a, None) == 2, (B, N, K)
+    a.B, a.N, a.K = 0, 16, 128
+    assert _lib.lib().mote_skinny_gemm(a, None) == 0  # nothing to do, nothing launched

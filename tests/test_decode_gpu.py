@@ -165,3 +165,57 @@ def test_decode_exchange_mass_mean_over_heads(cuda):
             _, gr, _, _ = _oracle(kc, vc, raw, th, inv, Sv, 1, 0.5, torch.bfloat16)
             assert float((xm.cpu().double() - gr.mean(-1)).abs().max()) < 2e-2
         assert torch.equal(Sd.cpu(), Sv + call + 1)
+
+
+@pytest.mark.parametrize("B,N,K,xpad", [(1, 2304, 768, 0), (16, 2304, 768, 0), (5, 768, 768, 64), (3, 48, 128, 0),
+                                        (16, 64, 1024, 8)])
+def test_skinny_linear_matches_float64(cuda, B, N, K, xpad):
+    """The decode engine's skinny product against float64 x W^T rounded to bf16 (one rounding; the
+    fp32 accumulation order may move a result by one bf16 step)."""
+    from mote_amd.decode import skinny_linear
+
+    print(f"case skinny B={B} N={N} K={K} xpad={xpad}", flush=True)
+    g = torch.Generator().manual_seed(B * 7 + N + K)
+    xs = torch.randn(B, K + xpad, generator=g).bfloat16()
+    w = (torch.randn(N, K, generator=g) / K ** 0.5).bfloat16()
+    y = skinny_linear(xs.cuda()[:, :K], w.cuda())
+    ref = (xs[:, :K].double() @ w.double().t())
+    assert y.shape == (B, N) and y.dtype == torch.bfloat16
+    assert rel_err(y, ref) < 1e-2, rel_err(y, ref)
+
+
+def test_decode_step_skinny_path_matches_library_path(cuda):
+    """RelationDecodeStep in bf16 at batch 16: the skinny-product projections give the same step
+    (out, xm, the appended rows and the advanced position) as the hipBLASLt path."""
+    import mote_amd.decode as Dm
+    from mote_amd.arena import RelationArena
+    from mote_amd.relation import FullRelation
+
+    print("case decode step skinny vs library", flush=True)
+    torch.manual_seed(13)
+    m = FullRelation(768, 8, 1).cuda()
+    with torch.no_grad():
+        m.theta.uniform_(-0.3, 0.3)
+    for lin in (m.w1, m.w2, m.wi, m.wo):
+        lin.to(torch.bfloat16)
+    outs = []
+    for skinny in (True, False):
+        arena = RelationArena(1, 8, 512, 96, "cuda", torch.bfloat16, batch=16)
+        g = torch.Generator().manual_seed(14)
+        arena.buf.copy_(torch.randn(arena.buf.shape, generator=g).bfloat16())
+        step = Dm.RelationDecodeStep(m, arena, 0)
+        S = torch.tensor([300 + 7 * b for b in range(16)], device="cuda")
+        x = torch.randn(16, 1, 768, generator=g).bfloat16().cuda()
+        orig = Dm._skinny_ok
+        if not skinny:
+            Dm._skinny_ok = lambda *a: False
+        try:
+            out, xm = step(x, S, advance=True)
+        finally:
+            Dm._skinny_ok = orig
+        torch.cuda.synchronize()
+        outs.append((out.clone(), xm.clone(), arena.buf.clone(), S.clone()))
+    (o1, x1, b1, s1), (o2, x2, b2, s2) = outs
+    assert rel_err(o1, o2) < 2e-2, rel_err(o1, o2)
+    assert float((x1 - x2).abs().max()) < 2e-2
+    assert rel_err(b1, b2) < 2e-2 and torch.equal(s1, s2)
