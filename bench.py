@@ -784,6 +784,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the C2 / C5 / add+RMSNorm / dechunk lines")
+    ap.add_argument("--engine-only", action="store_true",
+                    help="only the decode-engine lines (batch 1 and 16, --decode-steps tokens), for profiling")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the Relation path is built and measured on a single GPU "
@@ -795,6 +797,10 @@ def main():
     if not fr.HAS_HIP:
         raise SystemExit("bench.py needs libmote_relation.so and a GPU")
     dev = torch.device("cuda")
+    if args.engine_only:
+        print(json.dumps({k: bench_decode_engine(b, args.decode_steps, dev) for k, b in (("b1", 1), ("b16", 16))}),
+              flush=True)
+        return
     copy_calibration(dev)
     st = bench_stack(args.steps, args.warmup, dev)
     dec = {}
