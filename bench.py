@@ -861,6 +861,13 @@ def main():
             for k, v in dec.items()}
     if dec:
         out["decode_engine"] = dec_engine
+    if "qkv_prologue" in extra:
+        q = extra["qkv_prologue"]["T"]
+        out["roofline_qkv_prologue"] = {
+            "kernel": "qkv_rope_kernel (QKV product with RoPE / Givens in the epilogue, 4964 tokens)", "bound": "mfma",
+            "achieved": q["fused"]["tflops"], "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+            "frac": q["fused"]["frac_bf16_peak"], "flop_per_launch": q["flop_per_launch"],
+            "avg_launch_ms": round(q["fused"]["us_per_launch"] / 1e3, 5)}
     out.update(extra)
     if cpu is not None:
         out["cpu_baseline"] = {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")}
