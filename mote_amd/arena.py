@@ -1,99 +1,136 @@
-"""The Relation decode arena: one preallocated, append-only home for every layer's {P2, I~} rows.
+"""The {P2, I~} decode arena: every Relation layer's cache rows in one device allocation.
 
-Same contract as mote/model/arena.py:30-186. `buf[layer, 0]` holds P2 rows and `buf[layer, 1]` I~
-rows, [H, capacity, dh] each (the reference layout, batch 1), or [batch, H, capacity, dh] when the
-arena is built for `batch` independent sequences (batched decode, which the reference defers,
-docs/shape.md:255). Per layer the rows of one head are contiguous and heads are capacity*dh apart,
-which is the head stride the HIP kernels read in place.
+Interface of mote/model/arena.py:30-143 (RelationArena, ArenaLayer, ArenaState and the members
+their callers touch); the storage and its management are this package's own.
 
-The buffer is allocated zeroed and grows zeroed (arena.py:38-44): rows past the fill are never read
-by the HIP decode kernel, but the reference's bucket-width readers multiply masked rows, so they must
-stay finite.
+Storage. One tensor `store` [n_layers, 2, batch, H, capacity, dh]: kind 0 holds P2 rows, kind 1
+I~ rows, one slot per independent sequence (batched decode; the reference serves one sequence,
+docs/shape.md:255). Within a (layer, kind, sequence) the rows of a head are contiguous and heads
+are capacity * dh elements apart, the head stride the HIP forward and decode kernels take as an
+argument, so nothing is ever gathered or transposed. `buf` is the store itself, or for batch 1 the
+reference's [n_layers, 2, H, capacity, dh] view of it (same memory).
+
+Rows at or past a sequence's fill are never read by the HIP kernels (they stop at S), but callers
+that read a whole bucket width and mask (mote/infer/graph.py:176-184) multiply masked weights into
+them, so the store is created and grown zeroed: stale values there are finite, never garbage.
+
+Growth. `ensure(rows)` reallocates to the next power-of-two multiple of the current capacity and
+bumps `generation` (captured graphs hold the old addresses and must be recaptured). Rows are carried
+over only when a prefix store has declared them live with `claim(owner, rows)`; otherwise the old
+store is released before the new one is allocated, so the peak is the new size alone.
 """
 
 from __future__ import annotations
 
-import contextlib
-from typing import Iterator, Optional
+from typing import Iterator, Optional, Tuple
 
 import torch
 
 
 class RelationArena:
+    """Cache rows of `n_layers` Relation layers for `batch` sequences (see the module docstring)."""
+
     def __init__(self, n_layers: int, n_heads: int, capacity: int, d_head: int, device, dtype, batch: int = 1):
-        self.n_layers, self.n_heads, self.d_head = n_layers, n_heads, d_head
+        if capacity <= 0 or batch <= 0:
+            raise ValueError("an arena needs a positive capacity and batch")
+        self.n_layers, self.n_heads, self.d_head = int(n_layers), int(n_heads), int(d_head)
         self.batch = int(batch)
-        self.capacity = int(capacity)
         self.device = torch.device(device)
         self.dtype = dtype
-        self.buf = torch.zeros(self._shape(self.capacity), device=self.device, dtype=dtype)
-        self.owner: Optional[int] = None
-        self.n_valid: int = 0
-        self.generation: int = 0
-        self.pool = None
+        self.generation = 0
+        self._resident: Tuple[Optional[int], int] = (None, 0)  # (prefix-store owner, live rows)
+        self.store = self._zeros(int(capacity))
 
-    def _shape(self, cap: int):
-        if self.batch == 1:
-            return (self.n_layers, 2, self.n_heads, cap, self.d_head)
-        return (self.n_layers, 2, self.batch, self.n_heads, cap, self.d_head)
-
+    # ---- sizing ---------------------------------------------------------------------------------
     @staticmethod
     def capacity_for(seq_len: int, bpic: float, bucket: int = 256, margin: float = 1.25) -> int:
-        """Rows a `seq_len`-byte context needs at `bpic` bytes per chunk, with `margin` headroom,
-        rounded up to the decode bucket (arena.py:54-62)."""
-        need = int(seq_len / max(float(bpic), 1e-6) * float(margin)) + 1
-        return max(-(-need // bucket) * bucket, bucket)
+        """Rows for a `seq_len`-byte context at `bpic` bytes per chunk: the expected chunk count
+        with `margin` headroom plus one row, in whole decode buckets (at least one). The same
+        numbers as arena.py:54-62, so an engine sizing from a checkpoint's bpic gets the same
+        capacity."""
+        expected = int(seq_len / max(float(bpic), 1e-6) * float(margin))
+        buckets = max(1, (expected + bucket) // bucket)  # ceil((expected + 1) / bucket)
+        return buckets * bucket
+
+    @property
+    def capacity(self) -> int:
+        return self.store.shape[4]
 
     @property
     def bytes_per_chunk(self) -> int:
-        return self.n_layers * 2 * self.batch * self.n_heads * self.d_head * self.buf.element_size()
+        """Bytes one more row costs across every layer, kind, sequence and head."""
+        return self.n_layers * 2 * self.batch * self.n_heads * self.d_head * self.store.element_size()
 
     def nbytes(self) -> int:
-        return self.buf.numel() * self.buf.element_size()
+        return self.store.numel() * self.store.element_size()
+
+    def _zeros(self, capacity: int) -> torch.Tensor:
+        shape = (self.n_layers, 2, self.batch, self.n_heads, capacity, self.d_head)
+        return torch.zeros(shape, device=self.device, dtype=self.dtype)
+
+    # ---- views ----------------------------------------------------------------------------------
+    @property
+    def buf(self) -> torch.Tensor:
+        """The store; for batch 1 as the reference's [n_layers, 2, H, capacity, dh] view."""
+        return self.store[:, :, 0] if self.batch == 1 else self.store
 
     def p2(self, layer: int) -> torch.Tensor:
         """[batch, H, capacity, dh] view of a layer's P2 rows."""
-        t = self.buf[layer, 0]
-        return t.unsqueeze(0) if self.batch == 1 else t
+        return self.store[layer, 0]
 
     def info(self, layer: int) -> torch.Tensor:
-        t = self.buf[layer, 1]
-        return t.unsqueeze(0) if self.batch == 1 else t
+        """[batch, H, capacity, dh] view of a layer's I~ rows."""
+        return self.store[layer, 1]
 
     def rows(self, c0: int, c1: int) -> torch.Tensor:
-        """All layers' rows [c0, c1) as a view."""
+        """Rows [c0, c1) of every layer, kind, sequence and head, as a view of `buf`'s layout."""
         return self.buf[..., c0:c1, :]
 
-    def ensure(self, n_chunks: int) -> bool:
-        """Grow (x2, at least n_chunks) when needed, keeping the owned rows (arena.py:81-115).
-        Returns True when a reallocation happened (captured graphs must be recaptured)."""
-        if n_chunks <= self.capacity:
-            return False
-        new_cap = self.capacity
-        while new_cap < n_chunks:
-            new_cap *= 2
-        ctx = torch.cuda.use_mem_pool(self.pool) if (self.pool is not None and self.device.type == "cuda") else contextlib.nullcontext()
-        keep = self.n_valid if self.owner is not None else 0
-        old = self.buf
-        if keep == 0:
-            self.buf = old = None
-        with ctx:
-            buf = torch.zeros(self._shape(new_cap), device=self.device, dtype=self.dtype)
-        if old is not None:
-            buf[..., :keep, :].copy_(old[..., :keep, :])
-        else:
-            self.owner, self.n_valid = None, 0
-        self.buf = buf
-        self.capacity = new_cap
-        self.generation += 1
-        return True
+    # ---- residency (which prefix-store branch's rows are live) ----------------------------------
+    @property
+    def owner(self) -> Optional[int]:
+        return self._resident[0]
+
+    @property
+    def n_valid(self) -> int:
+        return self._resident[1]
+
+    def claim(self, owner: int, rows: int) -> None:
+        """Declare rows [0, rows) live for prefix-store branch `owner` (kept across growth)."""
+        if not 0 <= rows <= self.capacity:
+            raise ValueError(f"claim of {rows} rows in an arena of {self.capacity}")
+        self._resident = (owner, int(rows))
 
     def invalidate(self) -> None:
-        self.owner, self.n_valid = None, 0
+        """Nothing in the arena is live any more (a new conversation, a dropped branch)."""
+        self._resident = (None, 0)
+
+    # ---- growth ---------------------------------------------------------------------------------
+    def ensure(self, n_chunks: int) -> bool:
+        """Make room for `n_chunks` rows. Returns True when the store was reallocated."""
+        if n_chunks <= self.capacity:
+            return False
+        factor = 1 << max(0, (int(n_chunks) - 1) // self.capacity).bit_length()
+        self._reallocate(self.capacity * factor)
+        return True
+
+    def _reallocate(self, capacity: int) -> None:
+        owner, live = self._resident
+        live = live if owner is not None else 0
+        if live == 0:
+            self.store = None  # drop the old rows before the new allocation: the peak is the new size
+            self.store = self._zeros(capacity)
+            self._resident = (None, 0)
+        else:
+            fresh = self._zeros(capacity)
+            fresh[..., :live, :].copy_(self.store[..., :live, :])
+            self.store = fresh
+        self.generation += 1
 
 
 class ArenaLayer:
-    """One layer's rows and the shared fill `n` (arena.py:121-143)."""
+    """What one FullRelation layer sees (arena.py:121-143): its rows and the fill `n` shared by
+    every layer of the sequence state."""
 
     __slots__ = ("arena", "layer", "state")
 
@@ -105,59 +142,43 @@ class ArenaLayer:
         return self.state.n
 
     def write(self, p2: torch.Tensor, info: torch.Tensor) -> None:
-        """Append T rows at [n, n+T); the caller advances `n` once every layer has written."""
-        T = p2.shape[2]
-        n = self.state.n
-        assert n + T <= self.arena.capacity, f"arena overflow: {n + T} > {self.arena.capacity}"
+        """Store T new rows [n, n + T) of every sequence; p2 / info are [batch, H, T, dh]. The state
+        advances `n` once every layer has written."""
+        n, T = self.state.n, p2.shape[2]
+        if n + T > self.arena.capacity:
+            raise RuntimeError(f"arena overflow: rows up to {n + T} in a capacity of {self.arena.capacity}")
         self.arena.p2(self.layer)[:, :, n : n + T].copy_(p2)
         self.arena.info(self.layer)[:, :, n : n + T].copy_(info)
 
-    def views(self, upto: int):
-        """(P2, I~) over rows [0, upto) as [batch, H, upto, dh] views."""
+    def views(self, upto: int) -> Tuple[torch.Tensor, torch.Tensor]:
+        """(P2, I~) rows [0, upto) as [batch, H, upto, dh] views (head stride capacity * dh)."""
         return self.arena.p2(self.layer)[:, :, :upto], self.arena.info(self.layer)[:, :, :upto]
 
 
-def _map(obj, fn):
-    if torch.is_tensor(obj):
-        return fn(obj)
-    if isinstance(obj, (list, tuple)):
-        return type(obj)(_map(o, fn) for o in obj)
-    if isinstance(obj, dict):
-        return {k: _map(v, fn) for k, v in obj.items()}
-    return obj
-
-
 class ArenaState:
-    """The main-network half of an inference state: the shared arena and this sequence's fill `n`
-    (arena.py:146-186). Copying it copies `n`, never the arena; recurrent states of non-Relation
-    main layers ride along in `mamba` and are copied."""
+    """The Relation part of an inference state (arena.py:146-186): the shared arena and the number
+    of rows `n` this state has written. Copies share the arena and copy `n` only. (The reference
+    also carries recurrent states of non-Relation main layers here; those layers are not part of
+    this package.)"""
 
-    __slots__ = ("arena", "n", "mamba")
+    __slots__ = ("arena", "n")
 
-    def __init__(self, arena: RelationArena, n: int = 0, mamba: Optional[dict] = None):
+    def __init__(self, arena: RelationArena, n: int = 0):
         self.arena, self.n = arena, int(n)
-        self.mamba = dict(mamba) if mamba else {}
 
     def __len__(self) -> int:
         return self.arena.n_layers
 
-    def __getitem__(self, layer: int):
-        if layer in self.mamba:
-            return self.mamba[layer]
+    def __getitem__(self, layer: int) -> ArenaLayer:
+        if not 0 <= layer < self.arena.n_layers:
+            raise IndexError(layer)
         return ArenaLayer(self.arena, layer, self)
 
-    def set(self, layer: int, state) -> None:
-        if layer in self.mamba:
-            self.mamba[layer] = state
-
-    def map(self, fn) -> "ArenaState":
-        return ArenaState(self.arena, self.n, {k: _map(v, fn) for k, v in self.mamba.items()})
-
     def __iter__(self) -> Iterator[ArenaLayer]:
-        return (self[i] for i in range(len(self)))
+        return (ArenaLayer(self.arena, i, self) for i in range(self.arena.n_layers))
 
     def copy(self) -> "ArenaState":
-        return self.map(lambda t: t.clone()) if self.mamba else ArenaState(self.arena, self.n)
+        return ArenaState(self.arena, self.n)
 
     def advance(self, T: int) -> None:
         self.n += int(T)

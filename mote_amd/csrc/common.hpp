@@ -169,4 +169,21 @@ __device__ __forceinline__ Chunk zero_chunk() {
   return c;
 }
 
+// The rotation x c + y s (RoPE: x cos + rotate_half(x) sin; Givens: c a - s b, s a + c b) with the
+// rounding points of eager tensor ops in the element type: each product is rounded to T, then the
+// sum. For bf16 that is where the reference's per-op arithmetic rounds (the products of two bf16
+// values are exact in fp32); contraction into an FMA is off, so fp32 elements get a separately
+// rounded multiply and add as well.
+template <typename T>
+__device__ __forceinline__ float round_elem(float x) {
+  return Elem<T>::to_f(Elem<T>::from_f(x));
+}
+template <typename T>
+__device__ __forceinline__ float rot_round(float x, float c, float y, float s) {
+#pragma clang fp contract(off)
+  const float a = round_elem<T>(x * c);
+  const float b = round_elem<T>(y * s);
+  return round_elem<T>(a + b);
+}
+
 }  // namespace mote

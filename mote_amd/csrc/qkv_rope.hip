@@ -285,8 +285,10 @@ qkv_rope_kernel(const QkvParams p) {
       const float a0 = bf2f(aw[k] & 0xffffu), a1 = bf2f(aw[k] >> 16);
       const float b0 = bf2f(bw[k] & 0xffffu), b1 = bf2f(bw[k] >> 16);
       const float c0 = C[2 * k], c1 = C[2 * k + 1], s0 = Sn[2 * k], s1 = Sn[2 * k + 1];
-      oa[k] = uint32_t(f2bf(a0 * c0 + b0 * -s0)) | (uint32_t(f2bf(a1 * c1 + b1 * -s1)) << 16);
-      ob[k] = uint32_t(f2bf(b0 * c0 + a0 * s0)) | (uint32_t(f2bf(b1 * c1 + a1 * s1)) << 16);
+      oa[k] = uint32_t(f2bf(rot_round<bf16_t>(a0, c0, b0, -s0))) |
+              (uint32_t(f2bf(rot_round<bf16_t>(a1, c1, b1, -s1))) << 16);
+      ob[k] = uint32_t(f2bf(rot_round<bf16_t>(b0, c0, a0, s0))) |
+              (uint32_t(f2bf(rot_round<bf16_t>(b1, c1, a1, s1))) << 16);
     }
     *reinterpret_cast<uint4*>(obase + b * osb + t * osr + gha * osh + cca * 8) = make_uint4(oa[0], oa[1], oa[2], oa[3]);
     *reinterpret_cast<uint4*>(obase + b * osb + t * osr + ghb * osh + ccb * 8) = make_uint4(ob[0], ob[1], ob[2], ob[3]);

@@ -169,13 +169,13 @@ relation_decode_kernel(const DecParams p) {
   sincosf((float)S * invf, &sn, &cs);
   cs = p.rope ? round_to<T>(cs) : 1.f;
   sn = p.rope ? round_to<T>(sn) : 0.f;
-  const float rq0 = round_to<T>(q0 * cs - q1 * sn), rq1 = round_to<T>(q1 * cs + q0 * sn);
-  const float rk0 = round_to<T>(k0 * cs - k1 * sn), rk1 = round_to<T>(k1 * cs + k0 * sn);
+  const float rq0 = rot_round<T>(q0, cs, q1, -sn), rq1 = rot_round<T>(q1, cs, q0, sn);
+  const float rk0 = rot_round<T>(k0, cs, k1, -sn), rk1 = rot_round<T>(k1, cs, k0, sn);
   float gc, gs;
   sincosf(th, &gs, &gc);
   gc = p.givens ? round_to<T>(gc) : 1.f;
   gs = p.givens ? round_to<T>(gs) : 0.f;
-  const float rin = round_to<T>(p.givens ? (first ? (gc * iself - gs * ioth) : (gs * ioth + gc * iself)) : iself);
+  const float rin = p.givens ? rot_round<T>(iself, gc, ioth, first ? -gs : gs) : iself;
   if (tid < half) {
     sq[tid] = rq0;
     sq[tid + half] = rq1;

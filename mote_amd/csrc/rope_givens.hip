@@ -344,7 +344,7 @@ __global__ void __launch_bounds__(kRopeMaxCh) rope_givens_fwd_stream_kernel(cons
     for (int e = 0; e < EPC; ++e) {
       const float C = rope_part ? tc[r * half + L.a0 + e] : gc;
       const float S = sgn * (rope_part ? ts[r * half + L.a0 + e] : gs);
-      eo[e] = E::from_f(E::to_f(ex[e]) * C + E::to_f(ey[e]) * S);
+      eo[e] = E::from_f(rot_round<T>(E::to_f(ex[e]), C, E::to_f(ey[e]), S));
     }
     store_chunk(obase + int64_t(b) * osb + int64_t(t) * osr, out);
   }

@@ -30,6 +30,12 @@ def decode_workspace(B: int, H: int, D: int, capacity: int, device, dtype=torch.
     return torch.zeros(max(n, 16), device=device, dtype=torch.uint8)
 
 
+def _f32_param(t: torch.Tensor, n: int, name: str, dev) -> torch.Tensor:
+    if not torch.is_tensor(t) or t.numel() != n or t.device != dev:
+        raise ValueError(f"{name} must be a tensor of {n} element(s) on the inputs' device")
+    return t.detach().to(torch.float32).reshape(n).contiguous()
+
+
 def relation_decode(p1: torch.Tensor, p2: torch.Tensor, info: torch.Tensor, S: torch.Tensor, cache_p2: torch.Tensor,
                     cache_info: torch.Tensor, lam: torch.Tensor, tau_s: float = 2.0,
                     inv_freq: Optional[torch.Tensor] = None, theta: Optional[torch.Tensor] = None, layer_idx: int = 0,
@@ -46,35 +52,60 @@ def relation_decode(p1: torch.Tensor, p2: torch.Tensor, info: torch.Tensor, S: t
         the kernel's last head of each sequence.
     Returns (y [B, H, dh] in the cache dtype, g [B, H] fp32 exchange mass = 1 - F_SS).
     """
+    if p1.dim() != 3:
+        raise ValueError("p1/p2/info must be [B, H, dh]")
     B, H, D = p1.shape
-    cap = cache_p2.shape[2]
+    dev = p1.device
     for t in (p1, p2, info):
-        if t.stride(-1) != 1 or t.stride(1) != D or t.stride(0) != p1.stride(0):
+        if t.shape != p1.shape or t.stride(-1) != 1 or t.stride(1) != D or t.stride(0) != p1.stride(0):
             raise ValueError("p1/p2/info must be [B, H, dh] with head stride dh and one batch stride")
-        if t.dtype != cache_p2.dtype:
-            raise TypeError("decode inputs must be in the cache dtype")
+        if t.dtype != cache_p2.dtype or t.device != dev:
+            raise TypeError("decode inputs must be in the cache dtype, on the cache's device")
+    if cache_p2.dim() != 4 or tuple(cache_p2.shape[:2]) != (B, H) or cache_p2.shape[3] != D:
+        raise ValueError(f"cache_p2 must be [B, H, capacity, dh] = [{B}, {H}, *, {D}], got {tuple(cache_p2.shape)}")
+    if cache_info.shape != cache_p2.shape or cache_info.dtype != cache_p2.dtype:
+        raise ValueError("cache_info must have cache_p2's shape and dtype")
+    for t in (cache_p2, cache_info):
+        if t.device != dev or t.stride(-1) != 1:
+            raise ValueError("the caches must be on the inputs' device with unit stride on dh")
+    cap = cache_p2.shape[2]
+    # S is read as int64 and, with advance, written back by the kernel: no conversion is possible
+    if S.dtype != torch.int64 or S.device != dev or S.numel() != B or not S.is_contiguous():
+        raise ValueError(f"S must be a contiguous int64 device tensor of B = {B} positions")
+    # fp32 device copies of the small parameters (no copy when they already are; the temporaries
+    # stay referenced until the launch is queued, and the caching allocator orders their reuse)
+    lam32 = _f32_param(lam, 1, "lam", dev)
+    inv32 = None if inv_freq is None else _f32_param(inv_freq, D // 2, "inv_freq", dev)
+    th32 = None if theta is None else _f32_param(theta, H // 2, "theta", dev)
+    if xm is not None and (xm.dtype != torch.float32 or xm.numel() != B or not xm.is_contiguous() or xm.device != dev):
+        raise ValueError("xm must be a contiguous fp32 tensor of B elements")
+    if workspace is not None and (workspace.device != dev or not workspace.is_contiguous()):
+        raise ValueError("workspace must be a contiguous tensor on the inputs' device")
+    if y is not None and (y.shape != (B, H, D) or y.dtype != p1.dtype or y.device != dev or y.stride(-1) != 1
+                          or y.stride(1) != D):
+        raise ValueError("y must be [B, H, dh] in the cache dtype with head stride dh")
+    if g is not None and (g.shape != (B, H) or g.dtype != torch.float32 or g.device != dev or not g.is_contiguous()):
+        raise ValueError("g must be a contiguous fp32 [B, H] tensor")
     if not p1.is_cuda:
         raise RuntimeError("relation_decode needs the HIP library and an MI355X")
     if workspace is None:
-        workspace = decode_workspace(B, H, D, cap, p1.device, p1.dtype)
+        workspace = decode_workspace(B, H, D, cap, dev, p1.dtype)
     if y is None:
-        y = torch.empty(B, H, D, device=p1.device, dtype=p1.dtype)
+        y = torch.empty(B, H, D, device=dev, dtype=p1.dtype)
     if g is None:
-        g = torch.empty(B, H, device=p1.device, dtype=torch.float32)
+        g = torch.empty(B, H, device=dev, dtype=torch.float32)
     a = L.DecodeArgs()
     a.dtype = L.dtype_code(p1)
     a.B, a.H, a.D, a.capacity = B, H, D, cap
     a.layer_parity, a.flags, a.tau_s = int(layer_idx) % 2, L.MOTE_DECODE_ADVANCE if advance else 0, float(tau_s)
-    a.lam = lam.data_ptr()
-    a.inv_freq, a.theta = L.ptr(inv_freq), L.ptr(theta)
+    a.lam = lam32.data_ptr()
+    a.inv_freq, a.theta = L.ptr(inv32), L.ptr(th32)
     a.S = S.data_ptr()
     a.p1, a.p2, a.info, a.in_sb = p1.data_ptr(), p2.data_ptr(), info.data_ptr(), p1.stride(0)
     a.cache_p2, a.cache_info = L.view(cache_p2), L.view(cache_info)
     a.y, a.y_sb, a.g = y.data_ptr(), y.stride(0), g.data_ptr()
-    a.workspace, a.workspace_bytes = workspace.data_ptr(), workspace.numel()
+    a.workspace, a.workspace_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     if xm is not None:
-        if xm.dtype != torch.float32 or xm.numel() != B or not xm.is_contiguous():
-            raise ValueError("xm must be a contiguous fp32 tensor of B elements")
         a.xm = xm.data_ptr()
     L.check(L.lib().mote_relation_decode(a, L.stream_of(p1)), "mote_relation_decode")
     return y, g

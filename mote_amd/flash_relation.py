@@ -17,10 +17,12 @@ Additions with no counterpart in the reference:
 
 from __future__ import annotations
 
+import math
 import os
 from typing import Tuple
 
 import torch
+import torch.nn.functional as F
 
 from . import _lib as L
 
@@ -183,6 +185,25 @@ def flash_relation(p1: torch.Tensor, p2: torch.Tensor, info: torch.Tensor, lam: 
         raise RuntimeError("flash_relation needs the HIP library (libmote_relation.so) and an MI355X")
     y, g, _ibar, _lse = _relation_fwd(p1, p2, info, lam, float(tau_s), int(q_start))
     return y, g.detach()
+
+
+def relation_reference(p1: torch.Tensor, p2: torch.Tensor, info: torch.Tensor, lam: torch.Tensor, tau_s: float = 2.0,
+                       q_start: int = 0) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The same function materialized in fp32, for callers' tests (flash_relation.py:666-682):
+    scores U = p1 P2^T / sqrt(D) over every (query, key) pair, Self sigmoid(U_ii / tau_s) on the
+    diagonal, SiLU(U_ij) - lam ln(i + 1) over the strict past, softmax, Y = F I~, g = the past's
+    share of F. O(TQ * TK) memory; nothing in this package calls it."""
+    TQ, D = p1.shape[-2], p1.shape[-1]
+    TK = p2.shape[-2]
+    q, k, v = p1.float(), p2.float(), info.float()
+    u = torch.matmul(q, k.transpose(-1, -2)) / math.sqrt(D)
+    pos = torch.arange(q_start, q_start + TQ, device=q.device).unsqueeze(-1)  # absolute query index
+    key = torch.arange(TK, device=q.device).unsqueeze(0)
+    count = torch.log((pos + 1).float())
+    scores = torch.where(key == pos, torch.sigmoid(u / tau_s), F.silu(u) - lam.float() * count)
+    scores = scores.masked_fill(key > pos, float("-inf"))
+    flow = torch.softmax(scores, dim=-1)
+    return torch.matmul(flow, v), (flow * (key < pos)).sum(-1)
 
 
 # ---- varlen prefill (forward only) -------------------------------------------------------------

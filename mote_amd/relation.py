@@ -41,6 +41,46 @@ def rope_inv_freq(dim: int, theta: float, device=None) -> torch.Tensor:
     return (1.0 / (theta ** (k2 / dim))).to(device)
 
 
+# ---- torch-level RoPE helpers (the names mote/model/relation.py:37-68 exports) ------------------
+# The module's own forward runs RoPE inside the HIP prologue kernels; these helpers are for callers
+# that rotate rows themselves (mote/infer/graph.py:39, 158-164). They round where the kernels round:
+# tables cast to the operand dtype, then every product and sum in that dtype.
+def _rope_cos_sin(positions: torch.Tensor, dim: int, theta: float, dtype: torch.dtype) -> Tuple[torch.Tensor, torch.Tensor]:
+    """positions [T] (integers) -> cos, sin [T, dim] in `dtype`: fp32 angles pos * inv_freq, the
+    half-table repeated for the rotate-half convention (relation.py:37-42)."""
+    inv = rope_inv_freq(dim, theta, positions.device)
+    ang = positions.to(torch.float32)[:, None] * inv[None, :]
+    ang = torch.cat([ang, ang], dim=-1)
+    return ang.cos().to(dtype), ang.sin().to(dtype)
+
+
+_ROPE_CPU_TABLES: "dict" = {}
+
+
+def rope_tables(S: int, T: int, dim: int, theta: float, dtype: torch.dtype, device=None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """cos / sin for absolute positions S .. S+T-1, memoised per (S, T, dim, theta, dtype, device),
+    at most 32 entries (relation.py:45-58)."""
+    key = (int(S), int(T), int(dim), float(theta), dtype, str(torch.device(device) if device is not None else "cpu"))
+    hit = _ROPE_CPU_TABLES.get(key)
+    if hit is None:
+        if len(_ROPE_CPU_TABLES) >= 32:
+            _ROPE_CPU_TABLES.clear()
+        hit = _rope_cos_sin(torch.arange(S, S + T, device=device), dim, theta, dtype)
+        _ROPE_CPU_TABLES[key] = hit
+    return hit
+
+
+def _rotate_half(x: torch.Tensor) -> torch.Tensor:
+    """(x1, x2) -> (-x2, x1) over the two halves of the last axis (relation.py:61-63)."""
+    half = x.shape[-1] // 2
+    return torch.cat([-x[..., half:], x[..., :half]], dim=-1)
+
+
+def _apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """x [B, H, T, dh] rotated by tables [T, dh]: x cos + rotate_half(x) sin (relation.py:66-68)."""
+    return x * cos[None, None] + _rotate_half(x) * sin[None, None]
+
+
 # ---- mote::rope_givens ---------------------------------------------------------------------------
 def _heads_out(B, T, H, D, like, dtype):
     return torch.empty(B, T, H, D, device=like.device, dtype=dtype).transpose(1, 2)
@@ -323,6 +363,32 @@ class FullRelation(nn.Module):
             self.register_buffer("pair_a", a, persistent=False)
             self.register_buffer("pair_b", b, persistent=False)
         self.register_buffer("inv_freq", rope_inv_freq(self.d_head, rope_theta, device), persistent=False)
+
+    def _apply(self, fn, recurse=True):
+        # `.to(dtype)`, `.half()`, `.bfloat16()` would round the RoPE frequencies (an angle error of
+        # radians at positions in the thousands); the reference recomputes them in fp32 on every call
+        # (relation.py:39). Keep the buffer fp32 on whatever device the parameters moved to.
+        super()._apply(fn, recurse)
+        self._buffers["inv_freq"] = rope_inv_freq(self.d_head, self.rope_theta, self.lam.device)
+        return self
+
+    def _givens(self, info: torch.Tensor) -> torch.Tensor:
+        """Givens mixing of head pairs for callers that rotate rows themselves (relation.py:160-174,
+        graph.py:165): info [B, H, T, dh]; pairs (0,1),(2,3),... on even layers, (1,2),...,(H-1,0) on
+        odd ones; (a, b) -> (c a - s b, s a + c b) with c, s = cos / sin(theta) in info's dtype. The
+        module's forward applies the same rotation inside its HIP prologue kernels."""
+        if not self.use_givens:
+            return info
+        H = info.shape[1]
+        c = torch.cos(self.theta).to(info.dtype)[None, :, None, None]
+        s = torch.sin(self.theta).to(info.dtype)[None, :, None, None]
+        first = torch.arange(self.layer_idx % 2, H, 2, device=info.device)
+        second = (first + 1) % H
+        ia, ib = info.index_select(1, first), info.index_select(1, second)
+        out = torch.empty_like(info)
+        out.index_copy_(1, first, c * ia - s * ib)
+        out.index_copy_(1, second, s * ia + c * ib)
+        return out
 
     # ------------------------------------------------------------------------------------------
     def heads(self, x: torch.Tensor, S: int):

@@ -19,8 +19,15 @@ How each function is pinned (tests/test_oracle.py holds the checks):
   -theta undoes it, odd layers pair (H-1, 0).
 * `FullRelationRef` / `decode_step_ref` — module == composition of the pinned parts; decode at
   position S == the last row of a full forward over S + 1 positions.
+* `decode_rows_ref` — bit for bit (bf16 and fp32) the pinned `rope_tables` + `apply_rope` and
+  `givens` applied at position S in the operand dtype; the rows `decode_step_ref` writes into the
+  cache; in float64 the last row of `FullRelationRef.heads` over S + 1 positions.
+* `HeadRMSNormRef` — `torch.nn.functional.rms_norm` in float64 (rows below and above eps), the
+  closed form of a constant row, bf16 within one rounding of the float64 value.
 * Planted mistakes (log i for log(i+1), the self term counted in g, a missing 1/tau, a Givens sign
-  flip, a RoPE sign flip) are injected through `_plant` and each must fail one of the pins above.
+  flip, a RoPE sign flip, RoPE tables not rounded to the operand dtype, one rounding instead of the
+  reference's one per op, odd layers paired like even ones, eps outside the root of QK-Norm) are
+  injected through `_plant` and each must fail one of the pins above.
 """
 
 from __future__ import annotations
@@ -267,9 +274,12 @@ class HeadRMSNormRef(nn.Module):
         self.eps = eps
         self.weight = nn.Parameter(torch.ones(dim, dtype=dtype))
 
-    def forward(self, x):
+    def forward(self, x, _plant: Optional[str] = None):
         xf = x.float()
-        yf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
+        if _plant == "eps_outside":  # planted mistake: eps added after the root
+            yf = xf / (xf.pow(2).mean(-1, keepdim=True).sqrt() + self.eps)
+        else:
+            yf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
         return (yf * self.weight.float()).to(x.dtype)
 
 
@@ -406,30 +416,48 @@ def relation_decode_ref(p1, p2buf, infobuf, S, lam, tau_s: float = 2.0, dtype=to
     return torch.stack(ys), torch.stack(gs)
 
 
-def decode_rows_ref(p1, p2, info, S, inv_freq, theta, layer_idx: int, dtype):
-    """The new chunk's rows as the graph decoder prepares them (mote/infer/graph.py:158-172):
-    RoPE at position S[b] on p1 and p2 (fp32 angle float(S) * inv_freq, cos/sin cast to the cache
-    dtype), Givens on I~, then the cast to the cache dtype. Inputs [B, H, dh] raw projections;
-    `inv_freq` / `theta` None skip RoPE / Givens. Returns three [B, H, dh] tensors in `dtype`."""
+def decode_rows_ref(p1, p2, info, S, inv_freq, theta, layer_idx: int, dtype, _plant: Optional[str] = None):
+    """The new chunk's rows as the graph decoder prepares them (mote/infer/graph.py:158-172).
+
+    Inputs are the raw projections [B, H, dh]; the arithmetic runs in `dtype` (the model dtype of
+    the projections, which is also the cache dtype here), one torch op at a time, so every product
+    and every sum is rounded to `dtype` exactly where the reference rounds it:
+    * RoPE at position S[b]: fp32 angles float(S) * inv_freq (graph.py:159), emb = cat(f, f),
+      cos / sin cast to `dtype` (:161), then p * cos + rotate_half(p) * sin (:163-164);
+    * Givens on I~ with c, s = cos / sin(theta) cast to `dtype`, pairs by layer parity
+      (relation.py:160-174): (a, b) -> (c a - s b, s a + c b);
+    * the cast to the cache dtype (graph.py:171-172), a no-op here.
+    `inv_freq` / `theta` None skip RoPE / Givens. Returns three [B, H, dh] tensors in `dtype`.
+    `_plant` injects a mistake for the pins: "cos_unrounded" (tables kept in fp32),
+    "single_rounding" (the rotation in float64, rounded once), "odd_pairs_shifted" (odd layers
+    pair (0,1),(2,3)... like even ones)."""
     B, H, dh = p1.shape
     outs = []
     for b in range(B):
         s = int(S[b])
-        q, k, v = (t[b : b + 1, :, None, :].double() for t in (p1, p2, info))
+        q, k, v = (t[b : b + 1, :, None, :].to(dtype) for t in (p1, p2, info))
         if inv_freq is not None:
-            ang = torch.tensor(float(s), dtype=torch.float32) * inv_freq.float().cpu()
-            full = torch.cat([ang, ang])
-            cos = full.cos().to(dtype).double()[None, None, None]
-            sin = full.sin().to(dtype).double()[None, None, None]
-            q = q * cos + rotate_half(q) * sin
-            k = k * cos + rotate_half(k) * sin
+            freqs = torch.tensor(float(s), dtype=torch.float32) * inv_freq.float().cpu()
+            emb = torch.cat([freqs, freqs])
+            cos, sin = emb.cos(), emb.sin()
+            if _plant == "single_rounding":
+                c64, s64 = cos.to(dtype).double(), sin.to(dtype).double()
+                q = (q.double() * c64 + rotate_half(q.double()) * s64).to(dtype)
+                k = (k.double() * c64 + rotate_half(k.double()) * s64).to(dtype)
+            else:
+                if _plant != "cos_unrounded":
+                    cos, sin = cos.to(dtype), sin.to(dtype)
+                q = (q * cos + rotate_half(q) * sin).to(dtype)
+                k = (k * cos + rotate_half(k) * sin).to(dtype)
         if theta is not None:
-            c = torch.cos(theta.float().cpu()).to(dtype).double()
-            sn = torch.sin(theta.float().cpu()).to(dtype).double()
-            a_idx, b_idx = givens_pairs(H, layer_idx)
-            ia, ib = v[:, a_idx].clone(), v[:, b_idx].clone()
+            c = torch.cos(theta.float().cpu()).to(dtype)[None, :, None, None]
+            sn = torch.sin(theta.float().cpu()).to(dtype)[None, :, None, None]
+            odd = layer_idx % 2 == 1 and _plant != "odd_pairs_shifted"
+            first = list(range(1, H, 2)) if odd else list(range(0, H, 2))
+            second = [(h + 1) % H for h in first]
+            ia, ib = v[:, first], v[:, second]
             v = v.clone()
-            v[:, a_idx] = c[None, :, None, None] * ia - sn[None, :, None, None] * ib
-            v[:, b_idx] = sn[None, :, None, None] * ia + c[None, :, None, None] * ib
+            v[:, first] = c * ia - sn * ib
+            v[:, second] = sn * ia + c * ib
         outs.append([t[0, :, 0].to(dtype) for t in (q, k, v)])
     return tuple(torch.stack([o[i] for o in outs]) for i in range(3))

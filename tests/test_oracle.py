@@ -11,6 +11,7 @@ import math
 import numpy as np
 import pytest
 import torch
+import torch.nn.functional as F
 
 from oracle import relation as O
 from oracle.brute import relation_brute
@@ -332,3 +333,123 @@ def test_dlam_terms_sum_to_dlam():
     terms = O.relation_dlam_terms(p1, p2, info, lam, dy, 2.0, 4)
     dlam = O.relation_grads_autograd(p1, p2, info, lam, dy, 2.0, 4, dtype=torch.float64)[3]
     assert abs(float(terms.sum()) - float(dlam)) < 1e-12
+
+
+# ------------------------------------------------------------------------------------------------
+# the decode step's new rows and QK-Norm
+# ------------------------------------------------------------------------------------------------
+def _decode_raw(B, H, D, seed, dtype):
+    g = torch.Generator().manual_seed(seed)
+    raw = [(torch.randn(B, H, D, generator=g) * 0.8).to(dtype) for _ in range(3)]
+    theta = torch.rand(H // 2, generator=g) * 0.6 - 0.3
+    return raw, theta
+
+
+def pin_decode_rows(_plant=None) -> bool:
+    """decode_rows_ref at positions S equals the separately pinned pieces applied one position at a
+    time in the same dtype: rope_tables(S, 1) + apply_rope on p1 / p2 and givens on I~ (torch
+    rounds every product and sum to the operand dtype, which is where the reference rounds).
+    bf16 must agree bit for bit; so must fp32. Both parities, with and without RoPE / Givens."""
+    ok = True
+    for dtype in (torch.bfloat16, torch.float32):
+        for layer in (0, 1):
+            B, H, D = 3, 8, 96
+            raw, theta = _decode_raw(B, H, D, 11 + layer, dtype)
+            S = torch.tensor([0, 517, 4351])
+            inv = O.rope_inv_freq(D, 10000.0)
+            got = O.decode_rows_ref(*raw, S, inv, theta, layer, dtype, _plant=_plant)
+            for b in range(B):
+                cos, sin = O.rope_tables(int(S[b]), 1, D, 10000.0, dtype)
+                q = O.apply_rope(raw[0][b][None, :, None, :], cos, sin)[0, :, 0]
+                k = O.apply_rope(raw[1][b][None, :, None, :], cos, sin)[0, :, 0]
+                v = O.givens(raw[2][b][None, :, None, :], theta, layer)[0, :, 0]
+                ok &= torch.equal(got[0][b], q) and torch.equal(got[1][b], k) and torch.equal(got[2][b], v)
+            # the switches: no RoPE leaves p1 / p2 as they are, no Givens leaves I~
+            off = O.decode_rows_ref(*raw, S, None, None, layer, dtype, _plant=_plant)
+            ok &= all(torch.equal(o, r) for o, r in zip(off, raw))
+    return bool(ok)
+
+
+def test_decode_rows_match_rope_and_givens_at_position_s():
+    assert pin_decode_rows()
+
+
+def test_decode_rows_are_the_rows_decode_step_writes():
+    """The rows decode_step_ref (the graph decoder's step, restated op by op) writes at S are
+    decode_rows_ref of the layer's raw projections, in bf16 and fp32."""
+    for dtype in (torch.bfloat16, torch.float32):
+        for layer in (0, 1):
+            torch.manual_seed(20 + layer)
+            m = O.FullRelationRef(64, 4, layer, dtype=dtype)
+            with torch.no_grad():
+                m.theta.uniform_(-0.3, 0.3)
+            S, cap = 23, 32
+            x = torch.randn(1, 1, 64).to(dtype)
+            p2buf = torch.zeros(1, 4, cap, 16, dtype=dtype)
+            ibuf = torch.zeros_like(p2buf)
+            O.decode_step_ref(m, x, p2buf, ibuf, S, Cb=cap)
+            with torch.no_grad():
+                raw = [lin(x).view(1, 4, 16) for lin in (m.w1, m.w2, m.wi)]
+            q, k, v = O.decode_rows_ref(*raw, torch.tensor([S]), O.rope_inv_freq(16, 10000.0), m.theta.detach(),
+                                        layer, dtype)
+            assert torch.equal(p2buf[0, :, S], k[0]) and torch.equal(ibuf[0, :, S], v[0])
+            assert float(p2buf[0, :, S + 1:].abs().sum()) == 0.0
+
+
+def test_decode_rows_match_the_module_heads_at_the_last_position():
+    """In float64 the rows at S are the last row of FullRelationRef.heads over S + 1 positions."""
+    torch.manual_seed(5)
+    m = O.FullRelationRef(64, 4, 1, dtype=torch.float64)
+    with torch.no_grad():
+        m.theta.uniform_(-0.3, 0.3)
+    S = 40
+    x = torch.randn(1, S + 1, 64, dtype=torch.float64)
+    p1, p2, info = m.heads(x, 0)
+    with torch.no_grad():
+        raw = [lin(x[:, S:]).view(1, 4, 16) for lin in (m.w1, m.w2, m.wi)]
+    q, k, v = O.decode_rows_ref(*raw, torch.tensor([S]), O.rope_inv_freq(16, 10000.0), m.theta.detach(), 1,
+                                torch.float64)
+    for got, want in ((q, p1), (k, p2), (v, info)):
+        assert torch.allclose(got[0], want[0, :, S], atol=1e-12)
+
+
+@pytest.mark.parametrize("plant", ["cos_unrounded", "single_rounding", "odd_pairs_shifted"])
+def test_planted_decode_row_mistakes_are_caught(plant):
+    assert not pin_decode_rows(_plant=plant), f"planted mistake {plant!r} passed"
+
+
+def pin_head_rms_norm(_plant=None) -> bool:
+    """QK-Norm (relation.py:71-94): float64 against torch.nn.functional.rms_norm with the gain, on
+    rows of very different scales (eps matters for the small ones); the closed form of a constant
+    row, c w / sqrt(c^2 + eps); bf16 within one bf16 rounding of the float64 value."""
+    g = torch.Generator().manual_seed(3)
+    dh = 96
+    norm = O.HeadRMSNormRef(dh, dtype=torch.float64)
+    with torch.no_grad():
+        norm.weight.copy_(torch.rand(dh, generator=g, dtype=torch.float64) + 0.5)
+    x = torch.randn(2, 4, 7, dh, generator=g, dtype=torch.float64)
+    x[:, :, :3] *= 1e-3  # mean square ~1e-6, below eps
+    ok = True
+    got = norm(x, _plant=_plant)
+    want = F.rms_norm(x, (dh,), norm.weight.detach(), eps=1e-5)
+    ok &= torch.allclose(got, want, rtol=1e-6, atol=1e-9)
+    c = 0.003
+    row = torch.full((1, 1, 1, dh), c, dtype=torch.float64)
+    closed = c * norm.weight.detach() / math.sqrt(c * c + 1e-5)
+    ok &= torch.allclose(norm(row, _plant=_plant)[0, 0, 0], closed, rtol=1e-6)
+    nb = O.HeadRMSNormRef(dh, dtype=torch.bfloat16)
+    with torch.no_grad():
+        nb.weight.copy_(norm.weight.detach().to(torch.bfloat16))
+    xb = x.to(torch.bfloat16)
+    gb = nb(xb, _plant=_plant)
+    wb = F.rms_norm(xb.double(), (dh,), nb.weight.detach().double(), eps=1e-5)
+    ok &= gb.dtype == torch.bfloat16 and bool(((gb.double() - wb).abs() <= wb.abs() * 2 ** -8 + 1e-30).all())
+    return bool(ok)
+
+
+def test_head_rms_norm():
+    assert pin_head_rms_norm()
+
+
+def test_planted_head_rms_norm_mistake_is_caught():
+    assert not pin_head_rms_norm(_plant="eps_outside")
