@@ -220,6 +220,22 @@ size_t mote_relation_decode_workspace(const mote_relation_decode_args* args);
 int mote_relation_decode(const mote_relation_decode_args* args, void* stream);
 
 /* ------------------------------------------------------------------------------------------------
+ * The decode step without a workspace. No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). Arguments and results are those of mote_relation_decode, whose `workspace` /
+ * `workspace_bytes` fields are ignored: the per-split partials and completion counters live in a
+ * static device array of MOTE_DECODE_STATIC_BYTES bytes per GPU, held until the process ends. A call
+ * takes at most 256 sequences and 1024 sequence-heads (B * H); anything beyond is refused with
+ * MOTE_ERR_WORKSPACE before any launch. Every call on one GPU shares the array:
+ * calls ordered on one stream are fine, calls that overlap on one GPU (unordered streams) race.
+ * The first call on a device clears its copy in the caller's stream order; the stream's device
+ * must be the current device. It allocates nothing.
+ * ------------------------------------------------------------------------------------------------ */
+#define MOTE_DECODE_STATIC_BYTES (1u << 20)
+
+int mote_relation_decode_static(const mote_relation_decode_args* args, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
  * Fused residual add + RMSNorm (the pre-norm of every H-Net block and the final norm).
  * Replaces: RMSNorm.forward(x, residual, prenorm, residual_in_fp32) (mote/model/norm.py:36-59), whose
  * CUDA path calls mamba_ssm's Triton rms_norm_fn with the same semantics (norm.py:17-23, 48-50).

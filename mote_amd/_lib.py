@@ -20,6 +20,7 @@ MOTE_OK = 0
 MOTE_F32 = 0
 MOTE_BF16 = 1
 MOTE_DECODE_ADVANCE = 1
+MOTE_DECODE_STATIC_BYTES = 1 << 20
 MOTE_BWD_ROWS, MOTE_BWD_KEYS, MOTE_BWD_FINISH, MOTE_BWD_QUERIES = 1, 2, 4, 8
 
 _DTYPES = {torch.float32: MOTE_F32, torch.bfloat16: MOTE_BF16}
@@ -199,6 +200,7 @@ EXPORTS = {
     "mote_rope_givens_bwd": ([C.POINTER(RopeBwdArgs), C.c_void_p], C.c_int),
     "mote_relation_decode_workspace": ([C.POINTER(DecodeArgs)], C.c_size_t),
     "mote_relation_decode": ([C.POINTER(DecodeArgs), C.c_void_p], C.c_int),
+    "mote_relation_decode_static": ([C.POINTER(DecodeArgs), C.c_void_p], C.c_int),
     "mote_add_rms_norm_fwd": ([C.POINTER(NormArgs), C.c_void_p], C.c_int),
     "mote_add_rms_norm_bwd_workspace": ([C.POINTER(NormBwdArgs)], C.c_size_t),
     "mote_add_rms_norm_bwd": ([C.POINTER(NormBwdArgs), C.c_void_p], C.c_int),

@@ -75,6 +75,11 @@ int mote_relation_decode(const mote_relation_decode_args* args, void* stream) {
   return mote::launch_decode(args, reinterpret_cast<hipStream_t>(stream));
 }
 
+int mote_relation_decode_static(const mote_relation_decode_args* args, void* stream) {
+  mote::g_err[0] = 0;
+  return mote::launch_decode_static(args, reinterpret_cast<hipStream_t>(stream));
+}
+
 int mote_add_rms_norm_fwd(const mote_add_rms_norm_args* args, void* stream) {
   mote::g_err[0] = 0;
   return mote::launch_add_rms_norm_fwd(args, reinterpret_cast<hipStream_t>(stream));

@@ -37,6 +37,7 @@ int launch_rope_givens_fwd(const mote_rope_givens_args* a, hipStream_t stream);
 int launch_rope_givens_bwd(const mote_rope_givens_bwd_args* a, hipStream_t stream);
 size_t rope_givens_bwd_workspace_bytes(const mote_rope_givens_bwd_args* a);
 int launch_decode(const mote_relation_decode_args* a, hipStream_t stream);
+int launch_decode_static(const mote_relation_decode_args* a, hipStream_t stream);
 size_t decode_workspace_bytes(const mote_relation_decode_args* a);
 int launch_add_rms_norm_fwd(const mote_add_rms_norm_args* a, hipStream_t stream);
 int launch_add_rms_norm_bwd(const mote_add_rms_norm_bwd_args* a, hipStream_t stream);

@@ -27,6 +27,7 @@
 // The new rows (graph.py:158-172) are computed by every workgroup in its prologue, under the
 // latency of the first loads: the query and the new P2 row RoPE'd at S, I~ Givens-rotated with its
 // partner head's raw row, all rounded to the cache dtype. Bandwidth-bound by design: no MFMA.
+#include <mutex>
 #include <type_traits>
 
 #include "common.hpp"
@@ -303,7 +304,16 @@ relation_decode_kernel(const DecParams p) {
       store_coherent(part + 1, L);
     }
   }
-  // publish: every wave's coherent stores complete, then one count per workgroup
+  // Publish, then count. The ordering comes from the gfx942-family memory model (LLVM AMDGPUUsage,
+  // "Memory Model GFX942", which gfx950 follows), not from a release / acquire pair: monotonic
+  // atomic stores and loads at agent scope are issued with sc1 (read off the ISA: global_store /
+  // global_load ... sc1), so the stores write through the XCD's L2 to the device-coherent level and
+  // the loads do not hit a stale L2 line; s_waitcnt vmcnt(0) returns once every store of the wave is
+  // acknowledged there. After the barrier all partials of the workgroup are visible device-wide,
+  // before the count's atomic add is even issued; the workgroup that sees the last count reads them
+  // with agent-scope atomic loads after its add has returned. A release add / acquire load would add
+  // an L2 writeback and invalidate per workgroup (buffer_wbl2 sc1 / buffer_inv sc1) for data that
+  // never sits in L2.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (tid == 0) {
@@ -429,17 +439,19 @@ static DecWs decode_ws(const mote_relation_decode_args* a) {
 
 size_t decode_workspace_bytes(const mote_relation_decode_args* a) { return decode_ws(a).total; }
 
-int launch_decode(const mote_relation_decode_args* a, hipStream_t stream) {
-  if (!a) return set_error(MOTE_ERR_ARGUMENT, "relation_decode: null args");
-  if (a->dtype != MOTE_F32 && a->dtype != MOTE_BF16) return set_error(MOTE_ERR_ARGUMENT, "relation_decode: bad dtype %d", a->dtype);
+static int check_decode_args(const mote_relation_decode_args* a, const char* what) {
+  if (!a) return set_error(MOTE_ERR_ARGUMENT, "%s: null args", what);
+  if (a->dtype != MOTE_F32 && a->dtype != MOTE_BF16) return set_error(MOTE_ERR_ARGUMENT, "%s: bad dtype %d", what, a->dtype);
   if (a->D <= 0 || a->D > 128 || a->D % 8 != 0)
-    return set_error(MOTE_ERR_SHAPE, "relation_decode: head dim %d unsupported (need 8 <= D <= 128, D %% 8 == 0)", a->D);
-  if (a->B <= 0 || a->H <= 0 || a->H % 2 || a->capacity <= 0) return set_error(MOTE_ERR_SHAPE, "relation_decode: bad sizes");
+    return set_error(MOTE_ERR_SHAPE, "%s: head dim %d unsupported (need 8 <= D <= 128, D %% 8 == 0)", what, a->D);
+  if (a->B <= 0 || a->H <= 0 || a->H % 2 || a->capacity <= 0) return set_error(MOTE_ERR_SHAPE, "%s: bad sizes", what);
   if (!a->lam || !a->S || !a->p1 || !a->p2 || !a->info || !a->cache_p2.data || !a->cache_info.data || !a->y || !a->g)
-    return set_error(MOTE_ERR_ARGUMENT, "relation_decode: null pointer");
-  if (!a->workspace || a->workspace_bytes < decode_workspace_bytes(a))
-    return set_error(MOTE_ERR_WORKSPACE, "relation_decode: workspace of %zu bytes, %zu needed", a->workspace_bytes,
-                     decode_workspace_bytes(a));
+    return set_error(MOTE_ERR_ARGUMENT, "%s: null pointer", what);
+  return MOTE_OK;
+}
+
+// The launch itself, with the partials and counters at base + the offsets of `w`.
+static int launch_decode_ws(const mote_relation_decode_args* a, void* ws_base, const DecWs& w, hipStream_t stream) {
   DecParams p;
   p.lam = a->lam; p.S = a->S;
   p.rope = a->inv_freq != nullptr;
@@ -452,8 +464,7 @@ int launch_decode(const mote_relation_decode_args* a, hipStream_t stream) {
   p.y = a->y; p.y_sb = a->y_sb; p.g = a->g;
   const size_t BH = size_t(a->B) * a->H;
   p.nsplit = decode_splits(a);
-  const DecWs w = decode_ws(a);
-  char* ws = reinterpret_cast<char*>(a->workspace);
+  char* ws = reinterpret_cast<char*>(ws_base);
   p.part = reinterpret_cast<float*>(ws + w.part);
   p.cnt = reinterpret_cast<int*>(ws + w.cnt);
   p.cnt_seq = reinterpret_cast<int*>(ws + w.cnt_seq);
@@ -484,6 +495,89 @@ int launch_decode(const mote_relation_decode_args* a, hipStream_t stream) {
   }
 #undef MOTE_DEC_LAUNCH
   return check_launch("relation_decode");
+}
+
+int launch_decode(const mote_relation_decode_args* a, hipStream_t stream) {
+  if (const int rc = check_decode_args(a, "relation_decode")) return rc;
+  if (!a->workspace || a->workspace_bytes < decode_workspace_bytes(a))
+    return set_error(MOTE_ERR_WORKSPACE, "relation_decode: workspace of %zu bytes, %zu needed", a->workspace_bytes,
+                     decode_workspace_bytes(a));
+  return launch_decode_ws(a, a->workspace, decode_ws(a), stream);
+}
+
+// ------------------------------------------------------------------------------------------------
+// The no-allocation entry point: the partials and counters live in `scratch`, a static device array
+// (one copy per GPU, alive until the process ends). In host code `scratch` names a host-side stand-in,
+// not device memory: its device address comes from hipGetSymbolAddress, once per device (with that
+// device current), and only that address is ever handed to a kernel. The first call on a device
+// clears its copy with a fill kernel in the caller's stream order. Calls on one GPU share the array.
+//
+// Layout. The completion counters must be zero when a call starts. A call leaves the counters it
+// used at zero, but the workspace layout (counters after the partials) moves them with the shape, so
+// in a shared array a smaller call's counters would land on a larger call's stale partials. Here the
+// counters have fixed slots at the front instead: sequence counter b in line b, head counter bh in
+// line kStaticSeqLines + bh, 256 bytes each; every slot is either untouched since the clear or
+// reset by its last user. The partials follow; their contents never need to start at zero.
+// ------------------------------------------------------------------------------------------------
+constexpr int kStaticSeqLines = 256;    // sequences per call
+constexpr int kStaticHeadLines = 1024;  // sequence-heads per call
+static DecWs decode_ws_static(const mote_relation_decode_args* a) {
+  const size_t line = kDecCntStride * sizeof(int);
+  DecWs w;
+  w.cnt_seq = 0;
+  w.cnt = size_t(kStaticSeqLines) * line;
+  w.part = w.cnt + size_t(kStaticHeadLines) * line;
+  w.total = w.part + size_t(a->B) * a->H * size_t(decode_splits(a)) * size_t(a->D + 2) * sizeof(float);
+  return w;
+}
+
+static __device__ __align__(256) unsigned char scratch[MOTE_DECODE_STATIC_BYTES];
+
+constexpr int kMaxScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxScratchDevices];  // device address of `scratch` per device, once known
+
+__global__ void __launch_bounds__(256) clear_scratch_kernel(uint4* p, int n16) {
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n16; i += gridDim.x * 256) p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+static int scratch_address(hipStream_t stream, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices)
+    return set_error(MOTE_ERR_LAUNCH, "relation_decode_static: no usable current device");
+  if (stream) {
+    int sdev = -1;
+    if (hipStreamGetDevice(stream, &sdev) != hipSuccess || sdev != dev)
+      return set_error(MOTE_ERR_ARGUMENT, "relation_decode_static: the stream's device (%d) must be the current one (%d)",
+                       sdev, dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return set_error(MOTE_ERR_LAUNCH, "relation_decode_static: hipGetSymbolAddress failed: %s", hipGetErrorString(e));
+    hipLaunchKernelGGL(clear_scratch_kernel, dim3(64), dim3(256), 0, stream, reinterpret_cast<uint4*>(ptr),
+                       int(MOTE_DECODE_STATIC_BYTES / 16));
+    if (const int rc = check_launch("relation_decode_static (scratch clear)")) return rc;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return MOTE_OK;
+}
+
+int launch_decode_static(const mote_relation_decode_args* a, hipStream_t stream) {
+  if (const int rc = check_decode_args(a, "relation_decode_static")) return rc;
+  const DecWs w = decode_ws_static(a);
+  if (a->B > kStaticSeqLines || int64_t(a->B) * a->H > kStaticHeadLines || w.total > MOTE_DECODE_STATIC_BYTES)
+    return set_error(MOTE_ERR_WORKSPACE,
+                     "relation_decode_static: B = %d sequences x H = %d heads need %zu bytes of scratch with at most "
+                     "%d sequences and %d sequence-heads; the static array holds %u (use mote_relation_decode with a "
+                     "workspace)", a->B, a->H, w.total, kStaticSeqLines, kStaticHeadLines,
+                     unsigned(MOTE_DECODE_STATIC_BYTES));
+  void* ws = nullptr;
+  if (const int rc = scratch_address(stream, &ws)) return rc;
+  return launch_decode_ws(a, ws, w, stream);
 }
 
 }  // namespace mote

@@ -76,3 +76,28 @@ def test_skinny_gemm_rejects_unsupported_shapes_without_a_gpu():
         assert _lib.lib().mote_skinny_gemm(a, None) == 2, (B, N, K)
     a.B, a.N, a.K = 0, 16, 128
     assert _lib.lib().mote_skinny_gemm(a, None) == 0  # nothing to do, nothing launched
+
+
+def test_static_decode_refuses_shapes_beyond_its_array_without_a_gpu():
+    """mote_relation_decode_static checks its arguments and the limits of its fixed scratch array
+    (256 sequences, 1024 sequence-heads) before it touches a device: a larger call is refused with
+    MOTE_ERR_WORKSPACE and a message naming the limits."""
+    from mote_amd import _lib
+
+    if not _lib.available():
+        pytest.skip("libmote_relation.so not built")
+    a = _lib.DecodeArgs()
+    a.dtype = _lib.MOTE_BF16
+    a.lam = a.S = a.p1 = a.p2 = a.info = a.y = a.g = 16
+    a.cache_p2.data = a.cache_info.data = 16
+    for B, H in ((257, 2), (130, 8), (64, 18)):  # too many sequences, sequence-heads
+        a.B, a.H, a.D, a.capacity = B, H, 128, 4096
+        assert _lib.lib().mote_relation_decode_static(a, None) == 3, (B, H)
+        msg = _lib.lib().mote_last_error()
+        assert f"B = {B} sequences x H = {H} heads".encode() in msg
+        assert str(_lib.MOTE_DECODE_STATIC_BYTES).encode() in msg
+    a.B, a.H = 128, 8
+    a.D = 100
+    assert _lib.lib().mote_relation_decode_static(a, None) == 2  # the shape checks come first
+    a.D, a.g = 128, None
+    assert _lib.lib().mote_relation_decode_static(a, None) == 1
