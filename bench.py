@@ -775,6 +775,26 @@ def bench_cpu(T: int):
                 cpu=cpu, seconds_per_layer=dt)
 
 
+def profile_kernels(which: str, dev, steps: int = 3) -> None:
+    """A short run of one configuration's kernels for rocprofv3 counter passes (no timing, no JSON):
+    c3 = the Mote-96M stack step, c2 = the Mote-32M stack step, c5 = the Mote-138M varlen prefill,
+    each `steps` times after one warm-up."""
+    if which == "c3":
+        inp = StackInputs(chunk_count(2, 16384), 2, dev)
+    elif which == "c2":
+        inp = StackInputs(chunk_count(1, 2048, 4), 1, dev, B=4, d_model=512, heads=8, layers=8)
+    elif which == "c5":
+        bench_c5(steps, 1, dev)
+        torch.cuda.synchronize()
+        return
+    else:
+        raise SystemExit(f"--kernels-only takes c2, c3 or c5, not {which!r}")
+    for _ in range(steps + 1):
+        stack_step(inp)
+    torch.cuda.synchronize()
+    log(f"[bench] profiled {which}: {steps + 1} stack steps")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -786,6 +806,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the C2 / C5 / add+RMSNorm / dechunk lines")
     ap.add_argument("--engine-only", action="store_true",
                     help="only the decode-engine lines (batch 1 and 16, --decode-steps tokens), for profiling")
+    ap.add_argument("--kernels-only", choices=("c2", "c3", "c5"), default=None,
+                    help="only run one configuration's kernels a few times, for rocprofv3 counter passes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the Relation path is built and measured on a single GPU "
@@ -797,6 +819,9 @@ def main():
     if not fr.HAS_HIP:
         raise SystemExit("bench.py needs libmote_relation.so and a GPU")
     dev = torch.device("cuda")
+    if args.kernels_only:
+        profile_kernels(args.kernels_only, dev)
+        return
     if args.engine_only:
         print(json.dumps({k: bench_decode_engine(b, args.decode_steps, dev) for k, b in (("b1", 1), ("b16", 16))}),
               flush=True)

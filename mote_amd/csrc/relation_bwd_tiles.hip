@@ -121,26 +121,41 @@ __device__ __forceinline__ void kv_block(const bf16_t* Qs, const bf16_t* Ds, con
       }
     }
   }
-  // rows 32 qh + 16 qt + 4 lg + r; key 16 kt + li of the wave's half
+  // rows 32 qh + 16 qt + 4 lg + r; key 16 kt + li of the wave's half. The elementwise chain runs
+  // phase by phase over the 8 elements of one key tile (two query tiles), so each transcendental's
+  // result is consumed 8 instructions later instead of by the next one.
   Frag aw[2], au[2];
   float wv[2][8], uv[2][8];
+  float lv[8], cv[8];
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
     const float4 l4 = *reinterpret_cast<const float4*>(Ss + 32 * qh + 16 * qt + 4 * lg);
     const float4 c4 = *reinterpret_cast<const float4*>(Ss + 64 + 32 * qh + 16 * qt + 4 * lg);
-    const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
-    const float cv[4] = {c4.x, c4.y, c4.z, c4.w};
+    lv[4 * qt] = l4.x; lv[4 * qt + 1] = l4.y; lv[4 * qt + 2] = l4.z; lv[4 * qt + 3] = l4.w;
+    cv[4 * qt] = c4.x; cv[4 * qt + 1] = c4.y; cv[4 * qt + 2] = c4.z; cv[4 * qt + 3] = c4.w;
+  }
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
+  for (int kt = 0; kt < 2; ++kt) {
+    float t[8], sg[8];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        bool keep = true;
-        if constexpr (MASKED) keep = key0 + 16 * kt + li < qa0 + 16 * qt + 4 * lg + r;
-        float w;
-        const float du = bwd_elem(sacc[qt][kt][r], wacc[qt][kt][r], lv[r], cv[r], nc2, scale, keep, w);
-        wv[kt][4 * qt + r] = w;
-        uv[kt][4 * qt + r] = du;
-      }
+    for (int e = 0; e < 8; ++e) t[e] = sacc[e >> 2][kt][e & 3] * nc2;  // -U log2e
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sg[e] = fexp2(t[e]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sg[e] = frcp(1.0f + sg[e]);             // sigmoid(U)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float w = fexp2(-fmaf(t[e], sg[e], lv[e]));                       // exp2(U log2e sg - lse2)
+      if constexpr (MASKED) w = key0 + 16 * kt + li < qa0 + 16 * (e >> 2) + 4 * lg + (e & 3) ? w : 0.f;
+      wv[kt][e] = w;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      // SiLU'(U) = sg (1 + U (1 - sg)) with U (1 - sg) ln2-scaled from t: a = t (sg - 1) = U log2e (1 - sg)
+      const float a = fmaf(t[e], sg[e], -t[e]);
+      const float sp = sg[e] * fmaf(a, kLn2, 1.0f);
+      uv[kt][e] = wv[kt][e] * (wacc[e >> 2][kt][e & 3] + cv[e]) * sp;
+    }
   }
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt) {
@@ -211,6 +226,9 @@ bwd_kv_kernel(const BwdParams p) {
 
   const float nc2 = -p.scale * kLog2e;
   const int qb_lo = max(0, k0 + 1 - p.q_start) / 64;
+  // PairTable::offset(qb) for the block in hand, advanced by qb + A per block (offset(qb + 1) - offset(qb))
+  const int pair_a = (p.q_start + 126) / 64;
+  int64_t pair_off = PairTable::offset(qb_lo, p.q_start);
   // dU^T fragments of this key block: pair (qb, kb) at PairTable::offset(qb) + kb, 8 fragments of
   // 64 lanes x 8 bf16 each, fragment kh * 4 + query tile; the wave writes fragments (kh, 2 qh + qt)
   bf16_t* dut_bh = reinterpret_cast<bf16_t*>(p.dut) + int64_t(bh) * p.npairs * 4096 + (kh * 4 + 2 * qh) * 512;
@@ -241,9 +259,8 @@ bwd_kv_kernel(const BwdParams p) {
     const float* Ss = reinterpret_cast<const float*>(Qs + 2 * TILE);
     const int i0 = qb * 64 + 32 * qh;   // the wave's first query row
     const int qa0 = p.q_start + i0;     // its position
-    bf16_t* dut_w = kb < PairTable::nkb(qb, p.TQ, p.q_start)
-                        ? dut_bh + (PairTable::offset(qb, p.q_start) + kb) * 4096
-                        : nullptr;
+    bf16_t* dut_w = kb < PairTable::nkb(qb, p.TQ, p.q_start) ? dut_bh + (pair_off + kb) * 4096 : nullptr;
+    pair_off += qb + pair_a;  // PairTable::offset(qb + 1)
     // quadrant visible at all (some key < some query position), and not wholly padding rows
     if (i0 < p.TQ && key0 < qa0 + 31)
       kv_block<DP, decltype(masked)::value>(Qs, Ds, Ss, kvs, kvs + TILE, dvacc, dkacc, dut_w, eye, qh, kh, li, lg,
@@ -251,9 +268,15 @@ bwd_kv_kernel(const BwdParams p) {
     else if (dut_w)
       store_dut_zero(dut_w, lane);
     MOTE_STAMP(2, qb - qb_lo);
-    __builtin_amdgcn_s_waitcnt(0);
+    // The next block's transfers were issued before this block's two dU^T stores, and vector-memory
+    // operations retire in issue order: waiting until at most the two stores are outstanding means the
+    // transfers have landed, while the stores stay in flight across the barrier.
+    if (dut_w)
+      __builtin_amdgcn_s_waitcnt(kVmWaitStage<2>());
+    else
+      __builtin_amdgcn_s_waitcnt(kVmWaitStage<0>());
     MOTE_STAMP(3, qb - qb_lo);
-    __syncthreads();
+    lds_barrier();
     MOTE_STAMP(4, qb - qb_lo);
   };
   // unmasked for every wave once the block's first query position exceeds the last key

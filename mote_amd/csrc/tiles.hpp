@@ -52,6 +52,17 @@ __device__ __forceinline__ void lds_dma16_s(const void* base, uint32_t voff, voi
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(la) : "memory", "m0");
 }
 
+// The same with the LDS destination as a 32-bit LDS address, and no memory clobber: the transfer
+// writes a stage slot that no instruction around it reads (the loops order slot reuse with their
+// barriers, which do clobber memory), so the compiler may keep addresses and values in registers
+// across it instead of reloading them after every transfer.
+__device__ __forceinline__ void lds_dma16_sa(const void* base, uint32_t voff, uint32_t la) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(la) : "m0");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* l) {
+  return uint32_t(reinterpret_cast<uintptr_t>((const void __attribute__((address_space(3)))*)l));
+}
+
 template <int DP>
 __device__ __forceinline__ int tile_swz(int row) {
   if constexpr (DP == 64) return (row >> 1) & 7;
@@ -108,6 +119,7 @@ struct TileStager {
   }
 
   __device__ __forceinline__ void init(int wave, int lane, const int64_t (&stride)[NT]) {
+    __builtin_assume(wave >= 0 && wave < NW);
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int ins = wave + NW * i;
@@ -120,14 +132,20 @@ struct TileStager {
   // copy of row rlast instead (the kernels mask them).
   __device__ __forceinline__ void issue(bf16_t* dst, const bf16_t* const (&src)[NT], const int64_t (&stride)[NT], int r0,
                                         int rlast, int wave, int lane) const {
+    // the wave index is below NW: each transfer's tile t is then a constant of the unrolled loop
+    __builtin_assume(wave >= 0 && wave < NW);
     if (__builtin_expect(r0 + 63 <= rlast, 1)) {
-      // whole block in range: scalar base + the precomputed lane offset
+      // whole block in range: one scalar base per tile + the precomputed lane offsets
+      const bf16_t* base[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) base[t] = src[t] + int64_t(r0) * stride[t];
+      const uint32_t la = lds_addr(dst);
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
         const int ins = wave + NW * i;
         if (NINS % NW == 0 || ins < NINS) {
           const int t = ins / CPR, n = ins % CPR;
-          lds_dma16_s(src[t] + int64_t(r0) * stride[t], voff[i], dst + t * 64 * DP + n * 512);
+          lds_dma16_sa(base[t], voff[i], la + uint32_t(t * 64 * DP + n * 512) * 2u);
         }
       }
     } else {
