@@ -296,8 +296,9 @@ int mote_add_rms_norm_bwd(const mote_add_rms_norm_bwd_args* args, void* stream);
  * Fused projection prologue (bf16): qkv = x [w1; w2; wi]^T, RoPE on p1 / p2 and the Givens rotation
  * on I~ in the product's epilogue, written into the three [B, H, T, D] head views; the same results as
  * the projection (x [w1; w2; wi]^T rounded to bf16) followed by mote_rope_givens_fwd.
- * Replaces: the three projections and the RoPE / Givens of FullRelation.forward
- * (mote/model/relation.py:199-215); the unfused path stays for QK-Norm, fp32 and other head dims.
+ * Replaces: the three projections, the optional QK-Norm and the RoPE / Givens of
+ * FullRelation.forward (mote/model/relation.py:199-215); the unfused path stays for fp32 and other
+ * head dims.
  * x: [B, T, H*D] bf16 with the batches back to back (x_sb == T x_sr); w: [3 H D, H D] bf16 rows
  * w1 | w2 | wi (row stride w_sr); D in {64, 96, 128}; H even; H D % 32 == 0. inv_freq NULL: no RoPE;
  * theta NULL: no Givens. info_raw (may be NULL) receives the I~ projections before the rotation,
@@ -319,10 +320,38 @@ typedef struct mote_qkv_rope_args {
   void* workspace;
   size_t workspace_bytes;
   int table_ready;
+  /* QK-Norm (relation.py:71-94, 208-210), applied to p1 / p2 before RoPE when both gains are given:
+     per token and head y = x rsqrt(mean(x^2) + eps) * gain (fp32 gains [D]), rounded to bf16.
+     qk_raw (may be NULL; only with the gains) receives the p1 | p2 projections before the norm,
+     [B, T, 2 H D] with batch / row strides qr_sb / qr_sr, for the backward. */
+  const float* norm_w1;
+  const float* norm_w2;
+  float norm_eps;
+  void* qk_raw; int64_t qr_sb, qr_sr;
 } mote_qkv_rope_args;
 
 size_t mote_qkv_rope_workspace(const mote_qkv_rope_args* args);
 int mote_qkv_rope_fwd(const mote_qkv_rope_args* args, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * Output gate of FullRelation._out (bf16): z = y * sigmoid(x wg^T) with the product rounded to bf16,
+ * the sigmoid rounded to bf16 and z rounded again (the reference's bf16 ops, relation.py:179-181),
+ * in one launch of the prologue's product kernel; s receives the sigmoid for the backward.
+ * Replaces: `y * torch.sigmoid(self.wg(x))` of mote/model/relation.py:179-181 (one GEMM and two
+ * elementwise passes); `wo` follows on the caller's GEMM library.
+ * x, y, z, s: [B * T, D] bf16 rows (the batches back to back); w: [D, D] bf16; D a multiple of 128.
+ * ------------------------------------------------------------------------------------------------ */
+typedef struct mote_gate_product_args {
+  int B, T, D;
+  const void* x; int64_t x_sr;
+  const void* w; int64_t w_sr;
+  const void* y; int64_t y_sr;
+  void* z;
+  void* s;
+  int64_t z_sr;             /* row stride of z and s */
+} mote_gate_product_args;
+
+int mote_gate_product(const mote_gate_product_args* args, void* stream);
 
 /* ------------------------------------------------------------------------------------------------
  * Skinny product for the decode engine's per-token projections (bf16, fp32 accumulation):

@@ -113,6 +113,16 @@ class QkvRopeArgs(C.Structure):
         ("inv_freq", C.c_void_p), ("theta", C.c_void_p), ("p1", View), ("p2", View), ("info", View),
         ("info_raw", C.c_void_p), ("ir_sb", C.c_int64), ("ir_sr", C.c_int64),
         ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t), ("table_ready", C.c_int),
+        ("norm_w1", C.c_void_p), ("norm_w2", C.c_void_p), ("norm_eps", C.c_float),
+        ("qk_raw", C.c_void_p), ("qr_sb", C.c_int64), ("qr_sr", C.c_int64),
+    ]
+
+
+class GateProductArgs(C.Structure):
+    _fields_ = [
+        ("B", C.c_int), ("T", C.c_int), ("D", C.c_int), ("x", C.c_void_p), ("x_sr", C.c_int64),
+        ("w", C.c_void_p), ("w_sr", C.c_int64), ("y", C.c_void_p), ("y_sr", C.c_int64),
+        ("z", C.c_void_p), ("s", C.c_void_p), ("z_sr", C.c_int64),
     ]
 
 
@@ -206,6 +216,7 @@ EXPORTS = {
     "mote_add_rms_norm_bwd": ([C.POINTER(NormBwdArgs), C.c_void_p], C.c_int),
     "mote_qkv_rope_workspace": ([C.POINTER(QkvRopeArgs)], C.c_size_t),
     "mote_qkv_rope_fwd": ([C.POINTER(QkvRopeArgs), C.c_void_p], C.c_int),
+    "mote_gate_product": ([C.POINTER(GateProductArgs), C.c_void_p], C.c_int),
     "mote_skinny_gemm": ([C.POINTER(SkinnyGemmArgs), C.c_void_p], C.c_int),
     "mote_chunk_route": ([C.POINTER(ChunkRouteArgs), C.c_void_p], C.c_int),
     "mote_chunk_gather": ([C.POINTER(ChunkGatherArgs), C.c_void_p], C.c_int),

@@ -103,6 +103,11 @@ int mote_qkv_rope_fwd(const mote_qkv_rope_args* args, void* stream) {
   return mote::launch_qkv_rope_fwd(args, reinterpret_cast<hipStream_t>(stream));
 }
 
+int mote_gate_product(const mote_gate_product_args* args, void* stream) {
+  mote::g_err[0] = 0;
+  return mote::launch_gate_product(args, reinterpret_cast<hipStream_t>(stream));
+}
+
 int mote_skinny_gemm(const mote_skinny_gemm_args* args, void* stream) {
   mote::g_err[0] = 0;
   return mote::launch_skinny_gemm(args, reinterpret_cast<hipStream_t>(stream));

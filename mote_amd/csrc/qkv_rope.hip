@@ -43,6 +43,12 @@ struct QkvParams {
   bf16_t* o2; int64_t o2_sb, o2_sh, o2_sr;
   bf16_t* o3; int64_t o3_sb, o3_sh, o3_sr;
   bf16_t* iraw; int64_t ir_sb, ir_sr;      // [B, T, H dh] pre-rotation I~, or null
+  const float* nw1;                        // QK-Norm gains [dh] of p1 / p2 (fp32), or null: no QK-Norm
+  const float* nw2;
+  float eps;
+  bf16_t* qkraw; int64_t qr_sb, qr_sr;     // [B, T, 2 H dh] p1 | p2 projections before QK-Norm, or null
+  const bf16_t* gy; int64_t gy_sr;         // gate mode: y [M, H dh] (the Relation output, token-major)
+  bf16_t* gz; bf16_t* gs; int64_t gz_sr;   // gate mode: z = y sigmoid(x wg^T) and the sigmoid, [M, H dh]
   int B, T, H, K, M, parity, nk;
   int ntok, ncol;                          // token tiles, column tiles (3 H / 2)
 };
@@ -75,7 +81,7 @@ __global__ void __launch_bounds__(256) rope_table_kernel(const float* inv_freq, 
   tab[i] = uint32_t(f2bf(cs)) | (uint32_t(f2bf(sn)) << 16);
 }
 
-template <int DH, int NW>
+template <int DH, int NW, bool GATE>
 __global__ void __launch_bounds__(64 * NW)
 qkv_rope_kernel(const QkvParams p) {
   using S = QkvShape<DH, NW>;
@@ -92,7 +98,7 @@ qkv_rope_kernel(const QkvParams p) {
   const int r0 = (seq / p.ncol) * kQkvTok;
   const int colt = seq % p.ncol;
   const int npair = p.H / 2;
-  const int part = colt / npair, hp = colt % npair;
+  const int part = GATE ? 0 : colt / npair, hp = GATE ? colt : colt % npair;
   int h0 = 2 * hp, h1 = 2 * hp + 1;
   if (part == 2 && p.parity) {
     h0 = 2 * hp + 1;
@@ -198,6 +204,77 @@ qkv_rope_kernel(const QkvParams p) {
       *reinterpret_cast<uint2*>(smem + tok * S::OUTW + col) = v;
     }
   __syncthreads();
+
+  if constexpr (GATE) {
+    // output gate (relation.py:179-181): z = y * sigmoid(g) with g the bf16 product, the sigmoid
+    // rounded to bf16 and the product rounded again, as the reference's bf16 ops round them; the
+    // sigmoid is also written for the backward. The pair's 2 dh columns are contiguous (h1 = h0 + 1).
+    constexpr int CH = 2 * DH / 8;
+    for (int q = threadIdx.x; q < kQkvTok * CH; q += 64 * NW) {
+      const int tok = q / CH, c = q % CH;
+      const int r = r0 + tok;
+      if (r >= p.M) break;  // tasks go token by token: every later one is past M too
+      const int64_t col = int64_t(h0) * DH + c * 8;
+      const uint4 gv = *reinterpret_cast<const uint4*>(smem + tok * S::OUTW + c * 8);
+      const uint4 yv = *reinterpret_cast<const uint4*>(p.gy + int64_t(r) * p.gy_sr + col);
+      const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, yw[4] = {yv.x, yv.y, yv.z, yv.w};
+      uint32_t zw[4], sw[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const bf16_t s0 = f2bf(sigmoid_acc(bf2f(gw[k] & 0xffffu))), s1 = f2bf(sigmoid_acc(bf2f(gw[k] >> 16)));
+        const bf16_t z0 = f2bf(bf2f(yw[k] & 0xffffu) * bf2f(s0)), z1 = f2bf(bf2f(yw[k] >> 16) * bf2f(s1));
+        sw[k] = uint32_t(s0) | (uint32_t(s1) << 16);
+        zw[k] = uint32_t(z0) | (uint32_t(z1) << 16);
+      }
+      *reinterpret_cast<uint4*>(p.gz + int64_t(r) * p.gz_sr + col) = make_uint4(zw[0], zw[1], zw[2], zw[3]);
+      *reinterpret_cast<uint4*>(p.gs + int64_t(r) * p.gz_sr + col) = make_uint4(sw[0], sw[1], sw[2], sw[3]);
+    }
+    return;
+  }
+
+  if (part < 2 && p.nw1) {
+    // QK-Norm of p1 / p2 before RoPE (relation.py:71-94, 208-210): per token and head, in fp32,
+    // y = x rsqrt(mean(x^2) + eps) times the gain, rounded to bf16 in place in the tile (the
+    // reference's HeadRMSNorm returns its input dtype); the pre-norm row is kept for the backward.
+    const float* nw = part == 0 ? p.nw1 : p.nw2;
+    for (int q = threadIdx.x; q < 2 * kQkvTok; q += 64 * NW) {
+      const int tok = q >> 1, hd = q & 1;
+      bf16_t* row = smem + tok * S::OUTW + hd * DH;
+      float ss = 0.f;
+#pragma unroll
+      for (int c = 0; c < DH / 8; ++c) {
+        const uint4 v = *reinterpret_cast<const uint4*>(row + c * 8);
+        const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float a = bf2f(vw[k] & 0xffffu), b = bf2f(vw[k] >> 16);
+          ss = fmaf(a, a, ss);
+          ss = fmaf(b, b, ss);
+        }
+      }
+      const float rr = rsqrtf(ss / float(DH) + p.eps);
+      const int r = r0 + tok;
+      const bool keep_raw = p.qkraw && r < p.M;
+      const int bb = p.B == 1 ? 0 : r / p.T, tt = r - bb * p.T;
+      bf16_t* raw = keep_raw ? p.qkraw + bb * p.qr_sb + int64_t(tt) * p.qr_sr + (part * p.H + (hd ? h1 : h0)) * DH
+                             : nullptr;
+#pragma unroll
+      for (int c = 0; c < DH / 8; ++c) {
+        const uint4 v = *reinterpret_cast<const uint4*>(row + c * 8);
+        if (keep_raw) *reinterpret_cast<uint4*>(raw + c * 8) = v;
+        const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+        uint32_t ow[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float a = (bf2f(vw[k] & 0xffffu) * rr) * nw[c * 8 + 2 * k];
+          const float b = (bf2f(vw[k] >> 16) * rr) * nw[c * 8 + 2 * k + 1];
+          ow[k] = uint32_t(f2bf(a)) | (uint32_t(f2bf(b)) << 16);
+        }
+        *reinterpret_cast<uint4*>(row + c * 8) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+      }
+    }
+    __syncthreads();
+  }
 
   // rotations and stores. The chunks of a token row pair up: RoPE pairs chunk cc of a head with
   // chunk cc + dh/16 of the same head (the two halves, one table entry for both), Givens pairs chunk
@@ -329,8 +406,11 @@ int launch_qkv_rope_fwd(const mote_qkv_rope_args* a, hipStream_t stream) {
       !al16v(a->p1.data, a->p1.stride_b, a->p1.stride_h, a->p1.stride_r) ||
       !al16v(a->p2.data, a->p2.stride_b, a->p2.stride_h, a->p2.stride_r) ||
       !al16v(a->info.data, a->info.stride_b, a->info.stride_h, a->info.stride_r) ||
-      (a->info_raw && !al16v(a->info_raw, a->ir_sb, a->ir_sr, 0)))
+      (a->info_raw && !al16v(a->info_raw, a->ir_sb, a->ir_sr, 0)) ||
+      (a->qk_raw && !al16v(a->qk_raw, a->qr_sb, a->qr_sr, 0)))
     return set_error(MOTE_ERR_ARGUMENT, "qkv_rope: rows must start on 16-byte boundaries");
+  if ((a->norm_w1 == nullptr) != (a->norm_w2 == nullptr) || (a->qk_raw && !a->norm_w1))
+    return set_error(MOTE_ERR_ARGUMENT, "qkv_rope: QK-Norm needs both gains (and qk_raw only with them)");
   if (a->inv_freq && (!a->workspace || a->workspace_bytes < qkv_rope_workspace_bytes(a) ||
                       reinterpret_cast<uintptr_t>(a->workspace) % 16))
     return set_error(MOTE_ERR_WORKSPACE, "qkv_rope: workspace too small or misaligned");
@@ -344,6 +424,9 @@ int launch_qkv_rope_fwd(const mote_qkv_rope_args* a, hipStream_t stream) {
   p.o3 = reinterpret_cast<bf16_t*>(a->info.data); p.o3_sb = a->info.stride_b; p.o3_sh = a->info.stride_h;
   p.o3_sr = a->info.stride_r;
   p.iraw = reinterpret_cast<bf16_t*>(a->info_raw); p.ir_sb = a->ir_sb; p.ir_sr = a->ir_sr;
+  p.nw1 = a->norm_w1; p.nw2 = a->norm_w2; p.eps = a->norm_eps;
+  p.qkraw = reinterpret_cast<bf16_t*>(a->qk_raw); p.qr_sb = a->qr_sb; p.qr_sr = a->qr_sr;
+  p.gy = nullptr; p.gy_sr = 0; p.gz = p.gs = nullptr; p.gz_sr = 0;
   p.B = a->B; p.T = a->T; p.H = a->H; p.K = K; p.M = int(M); p.parity = a->layer_parity & 1; p.nk = K / kQkvK;
   p.ntok = int((M + kQkvTok - 1) / kQkvTok);
   p.ncol = 3 * (a->H / 2);
@@ -357,11 +440,47 @@ int launch_qkv_rope_fwd(const mote_qkv_rope_args* a, hipStream_t stream) {
   const int nwg = p.ntok * p.ncol;
   const dim3 grid(unsigned((nwg + 7) / 8 * 8));  // whole rounds over the 8 XCDs; the extra ids return
   switch (a->D) {
-    case 64: hipLaunchKernelGGL((qkv_rope_kernel<64, kQkvWaves>), grid, dim3(64 * kQkvWaves), 0, stream, p); break;
-    case 96: hipLaunchKernelGGL((qkv_rope_kernel<96, kQkvWaves>), grid, dim3(64 * kQkvWaves), 0, stream, p); break;
-    default: hipLaunchKernelGGL((qkv_rope_kernel<128, kQkvWaves>), grid, dim3(64 * kQkvWaves), 0, stream, p); break;
+    case 64: hipLaunchKernelGGL((qkv_rope_kernel<64, kQkvWaves, false>), grid, dim3(64 * kQkvWaves), 0, stream, p); break;
+    case 96: hipLaunchKernelGGL((qkv_rope_kernel<96, kQkvWaves, false>), grid, dim3(64 * kQkvWaves), 0, stream, p); break;
+    default: hipLaunchKernelGGL((qkv_rope_kernel<128, kQkvWaves, false>), grid, dim3(64 * kQkvWaves), 0, stream, p); break;
   }
   return check_launch("qkv_rope");
+}
+
+// The output gate's product on the same kernel: the D columns of x wg^T are tiled as D / (2 dh)
+// "head pairs" of dh in {128, 96, 64}, the first that divides them.
+int launch_gate_product(const mote_gate_product_args* a, hipStream_t stream) {
+  if (!a) return set_error(MOTE_ERR_ARGUMENT, "gate_product: null args");
+  if (a->B < 0 || a->T < 0 || a->D <= 0) return set_error(MOTE_ERR_SHAPE, "gate_product: bad sizes");
+  int DH = 0;
+  for (const int c : {128, 96, 64})
+    if (a->D % (2 * c) == 0) { DH = c; break; }
+  if (!DH || a->D % kQkvK) return set_error(MOTE_ERR_SHAPE, "gate_product: width %d (needs a multiple of 128)", a->D);
+  const int64_t M = int64_t(a->B) * a->T;
+  if (M == 0) return MOTE_OK;
+  if (M > (int64_t(1) << 30)) return set_error(MOTE_ERR_SHAPE, "gate_product: %lld tokens", (long long)M);
+  if (!a->x || !a->w || !a->y || !a->z || !a->s) return set_error(MOTE_ERR_ARGUMENT, "gate_product: null pointer");
+  if (a->x_sr >= (int64_t(1) << 24) || a->w_sr >= (int64_t(1) << 24))
+    return set_error(MOTE_ERR_ARGUMENT, "gate_product: row strides must stay below 2^24 elements");
+  if (!al16v(a->x, a->x_sr, 0, 0) || !al16v(a->w, a->w_sr, 0, 0) || !al16v(a->y, a->y_sr, 0, 0) ||
+      !al16v(a->z, a->z_sr, 0, 0) || !al16v(a->s, a->z_sr, 0, 0))
+    return set_error(MOTE_ERR_ARGUMENT, "gate_product: rows must start on 16-byte boundaries");
+  QkvParams p = {};
+  p.x = reinterpret_cast<const bf16_t*>(a->x); p.x_sr = a->x_sr;
+  p.w = reinterpret_cast<const bf16_t*>(a->w); p.w_sr = a->w_sr;
+  p.gy = reinterpret_cast<const bf16_t*>(a->y); p.gy_sr = a->y_sr;
+  p.gz = reinterpret_cast<bf16_t*>(a->z); p.gs = reinterpret_cast<bf16_t*>(a->s); p.gz_sr = a->z_sr;
+  p.B = 1; p.T = int(M); p.H = a->D / DH; p.K = a->D; p.M = int(M); p.parity = 0; p.nk = a->D / kQkvK;
+  p.ntok = int((M + kQkvTok - 1) / kQkvTok);
+  p.ncol = p.H / 2;
+  const int nwg = p.ntok * p.ncol;
+  const dim3 grid(unsigned((nwg + 7) / 8 * 8));
+  switch (DH) {
+    case 64: hipLaunchKernelGGL((qkv_rope_kernel<64, kQkvWaves, true>), grid, dim3(64 * kQkvWaves), 0, stream, p); break;
+    case 96: hipLaunchKernelGGL((qkv_rope_kernel<96, kQkvWaves, true>), grid, dim3(64 * kQkvWaves), 0, stream, p); break;
+    default: hipLaunchKernelGGL((qkv_rope_kernel<128, kQkvWaves, true>), grid, dim3(64 * kQkvWaves), 0, stream, p); break;
+  }
+  return check_launch("gate_product");
 }
 
 }  // namespace mote

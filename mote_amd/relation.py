@@ -233,19 +233,25 @@ def _rope_table_ws(a, x: torch.Tensor, inv: Optional[torch.Tensor], cacheable: b
 
 @torch.library.custom_op("mote::qkv_rope", mutates_args=())
 def _qkv_rope(x: torch.Tensor, w: torch.Tensor, inv_freq: Optional[torch.Tensor], theta: Optional[torch.Tensor],
-              n_heads: int, parity: int, pos0: int, keep_info: bool
-              ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
-    """(p1, p2, I~) as [B, H, T, dh] views of x [w1; w2; wi]^T after RoPE / Givens, and (keep_info)
-    the I~ projections before the rotation ([B, T, H dh]; empty otherwise) for the backward."""
+              n_heads: int, parity: int, pos0: int, keep_info: bool, norm_w1: Optional[torch.Tensor] = None,
+              norm_w2: Optional[torch.Tensor] = None, norm_eps: float = 1e-5
+              ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(p1, p2, I~) as [B, H, T, dh] views of x [w1; w2; wi]^T after (QK-Norm,) RoPE / Givens, and for
+    the backward (keep_info): the I~ projections before the rotation ([B, T, H dh]) and, with QK-Norm,
+    the p1 | p2 projections before the norm ([B, T, 2 H dh]); empty otherwise."""
     if not x.is_cuda:
         raise RuntimeError("mote::qkv_rope needs the HIP library and an MI355X")
     B, T, K = x.shape
     H = n_heads
     D = K // H
+    norm = norm_w1 is not None
+    if norm != (norm_w2 is not None):
+        raise ValueError("mote::qkv_rope: QK-Norm needs both gains")
     x = x.contiguous()
     w = w.contiguous()
     p1, p2, info = (_heads_out(B, T, H, D, x, x.dtype) for _ in range(3))
     iraw = torch.empty(B, T, K, device=x.device, dtype=x.dtype) if keep_info else x.new_empty(0)
+    qkraw = torch.empty(B, T, 2 * K, device=x.device, dtype=x.dtype) if (keep_info and norm) else x.new_empty(0)
     a = L.QkvRopeArgs()
     a.B, a.T, a.H, a.D, a.pos0, a.layer_parity = B, T, H, D, int(pos0), int(parity)
     a.x, a.x_sb, a.x_sr = x.data_ptr(), x.stride(0), x.stride(1)
@@ -256,32 +262,55 @@ def _qkv_rope(x: torch.Tensor, w: torch.Tensor, inv_freq: Optional[torch.Tensor]
     a.p1, a.p2, a.info = L.view(p1), L.view(p2), L.view(info)
     if keep_info:
         a.info_raw, a.ir_sb, a.ir_sr = iraw.data_ptr(), iraw.stride(0), iraw.stride(1)
+    if norm:
+        nw1 = norm_w1.detach().to(device=x.device, dtype=torch.float32).contiguous()
+        nw2 = norm_w2.detach().to(device=x.device, dtype=torch.float32).contiguous()
+        if nw1.numel() != D or nw2.numel() != D:
+            raise ValueError("mote::qkv_rope: QK-Norm gains must have head-dim elements")
+        a.norm_w1, a.norm_w2, a.norm_eps = nw1.data_ptr(), nw2.data_ptr(), float(norm_eps)
+        if keep_info:
+            a.qk_raw, a.qr_sb, a.qr_sr = qkraw.data_ptr(), qkraw.stride(0), qkraw.stride(1)
     ws, a.table_ready = _rope_table_ws(a, x, inv, inv is inv_freq)
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
     L.check(L.lib().mote_qkv_rope_fwd(a, L.stream_of(x)), "mote_qkv_rope_fwd")
-    return p1, p2, info, iraw
+    return p1, p2, info, iraw, qkraw
 
 
 @_qkv_rope.register_fake
-def _qkv_rope_fake(x, w, inv_freq, theta, n_heads, parity, pos0, keep_info):
+def _qkv_rope_fake(x, w, inv_freq, theta, n_heads, parity, pos0, keep_info, norm_w1=None, norm_w2=None, norm_eps=1e-5):
     B, T, K = x.shape
     D = K // n_heads
     mk = lambda: x.new_empty((B, T, n_heads, D)).transpose(1, 2)
-    return mk(), mk(), mk(), (x.new_empty((B, T, K)) if keep_info else x.new_empty(0))
+    norm = norm_w1 is not None
+    return (mk(), mk(), mk(), (x.new_empty((B, T, K)) if keep_info else x.new_empty(0)),
+            (x.new_empty((B, T, 2 * K)) if (keep_info and norm) else x.new_empty(0)))
 
 
 def _qr_setup(ctx, inputs, output):
-    x, w, inv_freq, theta, n_heads, parity, pos0, keep_info = inputs
-    ctx.save_for_backward(x, w, inv_freq, theta, output[3])
+    x, w, inv_freq, theta, n_heads, parity, pos0, keep_info, norm_w1, norm_w2, norm_eps = inputs
+    ctx.save_for_backward(x, w, inv_freq, theta, output[3], norm_w1, norm_w2, output[4])
     ctx.has_theta = theta is not None
+    ctx.norm = norm_w1 is not None
     ctx.keep = keep_info
-    ctx.n_heads, ctx.parity, ctx.pos0 = n_heads, parity, pos0
+    ctx.n_heads, ctx.parity, ctx.pos0, ctx.eps = n_heads, parity, pos0, norm_eps
 
 
-def _qr_backward(ctx, dp1, dp2, dinfo, _diraw):
-    x, w, inv_freq, theta, iraw = ctx.saved_tensors
-    if ctx.has_theta and not ctx.keep:
-        raise RuntimeError("mote::qkv_rope: the backward needs keep_info=True when theta is given")
+def _head_rms_norm_bwd(raw: torch.Tensor, gain: torch.Tensor, dy: torch.Tensor, eps: float, H: int):
+    """Backward of y = x rsqrt(mean(x^2) + eps) * gain per head (relation.py:71-94), in fp32:
+    dx = r g - r^3 x mean(g x) with g = dy * gain; dgain = sum over tokens and heads of dy x r."""
+    B, T, K = raw.shape
+    x = raw.float().view(B, T, H, K // H)
+    d = dy.float().reshape(B, T, H, K // H)
+    r = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps)
+    g = d * gain.float()
+    dx = r * g - x * r.pow(3) * (g * x).mean(-1, keepdim=True)
+    return dx.view(B, T, K), (d * x * r).sum((0, 1, 2))
+
+
+def _qr_backward(ctx, dp1, dp2, dinfo, _diraw, _dqkraw):
+    x, w, inv_freq, theta, iraw, norm_w1, norm_w2, qkraw = ctx.saved_tensors
+    if (ctx.has_theta or ctx.norm) and not ctx.keep:
+        raise RuntimeError("mote::qkv_rope: the backward needs keep_info=True with theta or QK-Norm")
     B, T, K = x.shape
     H = ctx.n_heads
     D = K // H
@@ -291,21 +320,85 @@ def _qr_backward(ctx, dp1, dp2, dinfo, _diraw):
     dinfo = z() if dinfo is None else dinfo
     src = iraw if ctx.keep else x.new_empty(B, T, K)  # read only for dtheta
     dqkv, dtheta = _rope_givens_bwd(dp1, dp2, dinfo, src, inv_freq, theta, H, ctx.parity, ctx.pos0, True)
+    dn1 = dn2 = None
+    if ctx.norm:  # gradients of the normalised p1 / p2 back through QK-Norm
+        dq, dn1 = _head_rms_norm_bwd(qkraw[..., :K], norm_w1, dqkv[..., :K], ctx.eps, H)
+        dk, dn2 = _head_rms_norm_bwd(qkraw[..., K:], norm_w2, dqkv[..., K:2 * K], ctx.eps, H)
+        dqkv = torch.cat([dq.to(dqkv.dtype), dk.to(dqkv.dtype), dqkv[..., 2 * K:]], dim=-1)
+        dn1, dn2 = dn1.to(norm_w1.dtype), dn2.to(norm_w2.dtype)
     dx = torch.matmul(dqkv, w)                                        # [B, T, 3K] x [3K, K]
     dw = torch.matmul(dqkv.reshape(-1, 3 * K).t(), x.reshape(-1, K))  # [3K, K]
-    return dx, dw, None, (dtheta[: H // 2] if ctx.has_theta else None), None, None, None, None
+    return (dx, dw, None, (dtheta[: H // 2] if ctx.has_theta else None), None, None, None, None, dn1, dn2, None)
 
 
 _qkv_rope.register_autograd(_qr_backward, setup_context=_qr_setup)
 
 
 def qkv_rope(x: torch.Tensor, w: torch.Tensor, n_heads: int, inv_freq: Optional[torch.Tensor],
-             theta: Optional[torch.Tensor], layer_idx: int, pos0: int = 0):
+             theta: Optional[torch.Tensor], layer_idx: int, pos0: int = 0,
+             norm: Optional[Tuple[torch.Tensor, torch.Tensor, float]] = None):
     """The fused prologue: bf16 x [B, T, H dh] and w = [w1; w2; wi] [3 H dh, H dh] -> (p1, p2, I~),
-    the same as rope_givens(F.linear(x, w), ...) (relation.py:199-215). Differentiable in x, w, theta."""
-    keep = theta is not None and torch.is_grad_enabled()
-    p1, p2, info, _ = _qkv_rope(x, w, inv_freq, theta, int(n_heads), int(layer_idx) % 2, int(pos0), keep)
+    the same as rope_givens(F.linear(x, w), ...) (relation.py:199-215); `norm` = (p1 gain, p2 gain,
+    eps) applies QK-Norm to p1 / p2 first (relation.py:208-210). Differentiable in x, w, theta and
+    the gains."""
+    n1, n2, eps = norm if norm is not None else (None, None, 1e-5)
+    keep = torch.is_grad_enabled() and (theta is not None or norm is not None)
+    p1, p2, info, _, _ = _qkv_rope(x, w, inv_freq, theta, int(n_heads), int(layer_idx) % 2, int(pos0), keep,
+                                   n1, n2, float(eps))
     return p1, p2, info
+
+
+# ---- mote::out_gate (the output gate of _out) ----------------------------------------------------
+@torch.library.custom_op("mote::out_gate", mutates_args=())
+def _out_gate(x: torch.Tensor, wg: torch.Tensor, y: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """bf16 (z, s): z = y * sigmoid(x wg^T) and s = the sigmoid, [B, T, D] (relation.py:179-181)."""
+    if not x.is_cuda:
+        raise RuntimeError("mote::out_gate needs the HIP library and an MI355X")
+    B, T, D = x.shape
+    x2 = x.reshape(B * T, D).contiguous()
+    y2 = y.reshape(B * T, D).contiguous()
+    wc = wg.contiguous()
+    z = torch.empty(B, T, D, device=x.device, dtype=x.dtype)
+    s = torch.empty(B, T, D, device=x.device, dtype=x.dtype)
+    a = L.GateProductArgs()
+    a.B, a.T, a.D = 1, B * T, D
+    a.x, a.x_sr = x2.data_ptr(), x2.stride(0)
+    a.w, a.w_sr = wc.data_ptr(), wc.stride(0)
+    a.y, a.y_sr = y2.data_ptr(), y2.stride(0)
+    a.z, a.s, a.z_sr = z.data_ptr(), s.data_ptr(), D
+    L.check(L.lib().mote_gate_product(a, L.stream_of(x)), "mote_gate_product")
+    return z, s
+
+
+@_out_gate.register_fake
+def _out_gate_fake(x, wg, y):
+    return x.new_empty(x.shape), x.new_empty(x.shape)
+
+
+def _og_setup(ctx, inputs, output):
+    x, wg, y = inputs
+    ctx.save_for_backward(x, wg, y, output[1])
+
+
+def _og_backward(ctx, dz, _ds):
+    """z = y s, s = sigmoid(g), g = x wg^T: dy = dz s, dg = dz y s (1 - s), dx = dg wg, dwg = dg^T x."""
+    x, wg, y, s = ctx.saved_tensors
+    dzf, sf = dz.float(), s.float()
+    dy = (dzf * sf).to(y.dtype)
+    dg = (dzf * y.float() * sf * (1.0 - sf)).to(x.dtype)
+    D = x.shape[-1]
+    dx = torch.matmul(dg, wg)
+    dwg = torch.matmul(dg.reshape(-1, D).t(), x.reshape(-1, D))
+    return dx, dwg, dy
+
+
+_out_gate.register_autograd(_og_backward, setup_context=_og_setup)
+USE_FUSED_GATE = True  # bf16 and a width that is a multiple of 128: the gate product kernel
+
+
+def out_gate(x: torch.Tensor, wg: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
+    """y * sigmoid(x wg^T) in one launch (bf16 x, wg, y [B, T, D]); differentiable in all three."""
+    return _out_gate(x, wg, y)[0]
 
 
 class HeadRMSNorm(nn.Module):
@@ -400,8 +493,9 @@ class FullRelation(nn.Module):
         theta = self.theta if self.use_givens else None
         bf16 = x.dtype == torch.bfloat16 or (torch.is_autocast_enabled() and
                                              torch.get_autocast_dtype("cuda") == torch.bfloat16)
-        if USE_FUSED_PROLOGUE and bf16 and not self.qk_norm and dh in (64, 96, 128) and (H * dh) % 32 == 0:
-            return qkv_rope(x.to(torch.bfloat16), w.to(torch.bfloat16), H, inv, theta, self.layer_idx, S)
+        if USE_FUSED_PROLOGUE and bf16 and dh in (64, 96, 128) and (H * dh) % 32 == 0:
+            norm = (self.p1_norm.weight, self.p2_norm.weight, self.p1_norm.eps) if self.qk_norm else None
+            return qkv_rope(x.to(torch.bfloat16), w.to(torch.bfloat16), H, inv, theta, self.layer_idx, S, norm)
         qkv = F.linear(x, w)
         if self.qk_norm:
             q, k, v = qkv.split(D, dim=-1)
@@ -415,7 +509,11 @@ class FullRelation(nn.Module):
         B, H, T, dh = y.shape
         y = y.transpose(1, 2).reshape(B, T, H * dh)
         if self.out_gate:
-            y = y * torch.sigmoid(self.wg(x))
+            bf16 = y.dtype == torch.bfloat16 and (x.dtype == torch.bfloat16 or torch.is_autocast_enabled())
+            if USE_FUSED_GATE and bf16 and y.is_cuda and (H * dh) % 128 == 0:
+                y = out_gate(x.to(torch.bfloat16), self.wg.weight.to(torch.bfloat16), y)
+            else:
+                y = y * torch.sigmoid(self.wg(x))
         return self.wo(y)
 
     def forward(self, x: torch.Tensor, cache: Optional[RelationCache] = None, return_cache: bool = False,

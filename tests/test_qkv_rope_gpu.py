@@ -224,3 +224,83 @@ def test_fused_prologue_replays_in_a_hip_graph(cuda):
                 for o, r in zip(outs, ref):
                     assert torch.equal(o, r)
         del graph
+
+
+@pytest.mark.parametrize("H,D,T,parity", [(8, 96, 301, 1), (4, 64, 129, 0), (2, 128, 64, 1)])
+def test_fused_prologue_with_qk_norm_matches_oracle(cuda, H, D, T, parity):
+    """QK-Norm in the fused prologue (relation.py:208-210): the bf16 projections of p1 / p2 go through
+    the oracle's HeadRMSNormRef (fp32 math, bf16 result) before RoPE; outputs within 2e-2 of the
+    float64 composition, and the gradients of x, w, theta and both gains against its autograd."""
+    from mote_amd.relation import qkv_rope, rope_inv_freq
+
+    print(f"case qkv_rope qk-norm H={H} D={D} T={T} parity={parity}", flush=True)
+    g = torch.Generator().manual_seed(70 + H)
+    K = H * D
+    x = torch.randn(1, T, K, generator=g).bfloat16()
+    w = (torch.randn(3 * K, K, generator=g) / K ** 0.5).bfloat16()
+    theta = torch.rand(H // 2, generator=g) * 2 - 1
+    n1, n2 = torch.rand(D, generator=g) + 0.5, torch.rand(D, generator=g) + 0.5
+    inv = rope_inv_freq(D, 10000.0)
+    xg, wg, tg, n1g, n2g = (t.to(cuda).requires_grad_(True) for t in (x, w, theta, n1, n2))
+    p1, p2, info = qkv_rope(xg, wg, H, inv.to(cuda), tg, parity, 0, norm=(n1g, n2g, 1e-5))
+    # oracle: bf16 projection, QK-Norm (fp32 math, bf16 result), then RoPE / Givens in float64
+    xr, wr, tr, n1r, n2r = (t.double().requires_grad_(True) for t in (x.float(), w.float(), theta, n1, n2))
+    qkv = xr @ wr.t()
+    q, k, v = (t.reshape(1, T, H, D).transpose(1, 2) for t in qkv.split(K, dim=-1))
+    rms = lambda t, gain: t * torch.rsqrt(t.pow(2).mean(-1, keepdim=True) + 1e-5) * gain
+    q, k = rms(q, n1r), rms(k, n2r)
+    cos, sin = O.rope_tables(0, T, D, 10000.0, torch.bfloat16)
+    q, k = O.apply_rope(q, cos.double(), sin.double()), O.apply_rope(k, cos.double(), sin.double())
+    v = O.givens(v, tr, parity)
+    for got, want in ((p1, q), (p2, k), (info, v)):
+        assert rel_err(got, want.detach()) < 2e-2, rel_err(got, want.detach())
+    # the bf16 rounding points of the norm: against the oracle module's HeadRMSNormRef on the kernel's
+    # own projection is covered by the module tests; here the composition in float64
+    dys = [torch.randn(1, H, T, D, generator=g).bfloat16() for _ in range(3)]
+    sum((o.float() * d.to(cuda).float()).sum() for o, d in zip((p1, p2, info), dys)).backward()
+    sum((o * d.double()).sum() for o, d in zip((q, k, v), dys)).backward()
+    for name, a, b in (("x", xg, xr), ("w", wg, wr), ("theta", tg, tr), ("gain1", n1g, n1r), ("gain2", n2g, n2r)):
+        assert rel_err(a.grad, b.grad) < 2e-2, (name, rel_err(a.grad, b.grad))
+
+
+@pytest.mark.parametrize("B,T,D", [(1, 4964, 768), (2, 333, 512), (1, 1, 256)])
+def test_out_gate_product_matches_oracle(cuda, B, T, D):
+    """mote::out_gate: z = y * sigmoid(x wg^T) (relation.py:179-181) with the reference's bf16 rounding
+    points; z and the saved sigmoid against float64, gradients of x, wg and y against float64
+    autograd of y * sigmoid(bf16(x wg^T))."""
+    from mote_amd.relation import _out_gate, out_gate
+
+    print(f"case out_gate B={B} T={T} D={D}", flush=True)
+    g = torch.Generator().manual_seed(80 + T)
+    x = torch.randn(B, T, D, generator=g).bfloat16()
+    wg = (torch.randn(D, D, generator=g) / D ** 0.5).bfloat16()
+    y = torch.randn(B, T, D, generator=g).bfloat16()
+    xg, wgg, yg = (t.to(cuda).requires_grad_(True) for t in (x, wg, y))
+    z = out_gate(xg, wgg, yg)
+    _, s = _out_gate(xg.detach(), wgg.detach(), yg.detach())
+    xr, wr, yr = (t.double().requires_grad_(True) for t in (x.float(), wg.float(), y.float()))
+    sr = torch.sigmoid((xr @ wr.t()).to(torch.bfloat16).double())
+    zr = yr * sr
+    assert rel_err(z, zr.detach()) < 2e-2, rel_err(z, zr.detach())
+    assert rel_err(s, sr.detach()) < 1e-2, rel_err(s, sr.detach())
+    dz = torch.randn(B, T, D, generator=g).bfloat16()
+    (z.float() * dz.to(cuda).float()).sum().backward()
+    (zr * dz.double()).sum().backward()
+    for name, a, b in (("x", xg, xr), ("wg", wgg, wr), ("y", yg, yr)):
+        assert rel_err(a.grad, b.grad) < 2e-2, (name, rel_err(a.grad, b.grad))
+
+
+def test_out_gate_and_qk_norm_ops_pass_opcheck(cuda):
+    from mote_amd.relation import rope_inv_freq
+
+    g = torch.Generator().manual_seed(90)
+    x = torch.randn(1, 70, 256, generator=g).bfloat16().to(cuda).requires_grad_(True)
+    wg = (torch.randn(256, 256, generator=g) / 16).bfloat16().to(cuda).requires_grad_(True)
+    y = torch.randn(1, 70, 256, generator=g).bfloat16().to(cuda).requires_grad_(True)
+    torch.library.opcheck(torch.ops.mote.out_gate.default, (x, wg, y))
+    w = (torch.randn(768, 256, generator=g) / 16).bfloat16().to(cuda).requires_grad_(True)
+    n1 = (torch.rand(64, generator=g) + 0.5).to(cuda).requires_grad_(True)
+    n2 = (torch.rand(64, generator=g) + 0.5).to(cuda).requires_grad_(True)
+    th = torch.rand(2, generator=g).to(cuda).requires_grad_(True)
+    torch.library.opcheck(torch.ops.mote.qkv_rope.default,
+                          (x, w, rope_inv_freq(64, 10000.0).to(cuda), th, 4, 1, 3, True, n1, n2, 1e-5))
