@@ -214,6 +214,11 @@ typedef struct mote_relation_decode_args {
   void* workspace;
   size_t workspace_bytes;
   float* xm;               /* [B] mean over the heads of g (graph.py:186), or NULL */
+  /* Predicate, or NULL (always run): a device byte (a bool tensor, e.g. the router's boundary bit)
+     read by every workgroup; 0 makes the launch write nothing (no append, no advance, no outputs).
+     It stands in for the graph decoder's conditional node around the main step (graph.py:44-57,
+     224-226): one captured graph serves both branches. */
+  const unsigned char* run;
 } mote_relation_decode_args;
 
 size_t mote_relation_decode_workspace(const mote_relation_decode_args* args);
@@ -368,9 +373,29 @@ typedef struct mote_skinny_gemm_args {
   const void* x; int64_t x_sr;
   const void* w; int64_t w_sr;
   void* y; int64_t y_sr;
+  const unsigned char* run;  /* predicate as in mote_relation_decode_args, or NULL */
 } mote_skinny_gemm_args;
 
 int mote_skinny_gemm(const mote_skinny_gemm_args* args, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * Arena rows <-> a host page of the prefix store as strided DMA: one hipMemcpy2DAsync per (layer,
+ * kind) plane moves its H head rows of `rows` x D elements at their pitches; no staging copy, no
+ * kernel. Replaces: the row copies of the prefix store's _store_rows / hydrate
+ * (mote/infer/prefix_cache.py:144-165: `page[..., off:off+take].copy_(arena.rows(c, c+take))` and
+ * the reverse). to_page = 1: arena rows [arena_row0, +rows) -> page rows [page_row0, +rows);
+ * 0: page -> arena. arena: address of element (plane 0, head 0, row 0, 0) of one sequence; a_plane /
+ * a_head: elements between planes / heads (the batched arena: batch * H * capacity * D and
+ * capacity * D). page likewise (p_plane = H * page_rows * D, p_head = page_rows * D). elem_bytes: 2
+ * or 4. Asynchronous on `stream` (host pages pinned).
+ * ------------------------------------------------------------------------------------------------ */
+typedef struct mote_page_copy_args {
+  int to_page, planes, H, D, elem_bytes, rows;
+  void* arena; int64_t a_plane, a_head; int arena_row0;
+  void* page; int64_t p_plane, p_head; int page_row0;
+} mote_page_copy_args;
+
+int mote_arena_page_copy(const mote_page_copy_args* args, void* stream);
 
 /* ------------------------------------------------------------------------------------------------
  * Chunking either side of the main network (mote/model/dc.py:192-352).

@@ -81,7 +81,7 @@ class DecodeArgs(C.Structure):
         ("p1", C.c_void_p), ("p2", C.c_void_p), ("info", C.c_void_p), ("in_sb", C.c_int64),
         ("cache_p2", View), ("cache_info", View),
         ("y", C.c_void_p), ("y_sb", C.c_int64), ("g", C.c_void_p),
-        ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t), ("xm", C.c_void_p),
+        ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t), ("xm", C.c_void_p), ("run", C.c_void_p),
     ]
 
 
@@ -130,7 +130,16 @@ class SkinnyGemmArgs(C.Structure):
     _fields_ = [
         ("dtype", C.c_int), ("B", C.c_int), ("N", C.c_int), ("K", C.c_int),
         ("x", C.c_void_p), ("x_sr", C.c_int64), ("w", C.c_void_p), ("w_sr", C.c_int64),
-        ("y", C.c_void_p), ("y_sr", C.c_int64),
+        ("y", C.c_void_p), ("y_sr", C.c_int64), ("run", C.c_void_p),
+    ]
+
+
+class PageCopyArgs(C.Structure):
+    _fields_ = [
+        ("to_page", C.c_int), ("planes", C.c_int), ("H", C.c_int), ("D", C.c_int), ("elem_bytes", C.c_int),
+        ("rows", C.c_int), ("arena", C.c_void_p), ("a_plane", C.c_int64), ("a_head", C.c_int64),
+        ("arena_row0", C.c_int), ("page", C.c_void_p), ("p_plane", C.c_int64), ("p_head", C.c_int64),
+        ("page_row0", C.c_int),
     ]
 
 
@@ -218,6 +227,7 @@ EXPORTS = {
     "mote_qkv_rope_fwd": ([C.POINTER(QkvRopeArgs), C.c_void_p], C.c_int),
     "mote_gate_product": ([C.POINTER(GateProductArgs), C.c_void_p], C.c_int),
     "mote_skinny_gemm": ([C.POINTER(SkinnyGemmArgs), C.c_void_p], C.c_int),
+    "mote_arena_page_copy": ([C.POINTER(PageCopyArgs), C.c_void_p], C.c_int),
     "mote_chunk_route": ([C.POINTER(ChunkRouteArgs), C.c_void_p], C.c_int),
     "mote_chunk_gather": ([C.POINTER(ChunkGatherArgs), C.c_void_p], C.c_int),
     "mote_chunk_gather_bwd": ([C.POINTER(ChunkGatherBwdArgs), C.c_void_p], C.c_int),

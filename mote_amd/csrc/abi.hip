@@ -108,6 +108,11 @@ int mote_gate_product(const mote_gate_product_args* args, void* stream) {
   return mote::launch_gate_product(args, reinterpret_cast<hipStream_t>(stream));
 }
 
+int mote_arena_page_copy(const mote_page_copy_args* args, void* stream) {
+  mote::g_err[0] = 0;
+  return mote::launch_page_copy(args, reinterpret_cast<hipStream_t>(stream));
+}
+
 int mote_skinny_gemm(const mote_skinny_gemm_args* args, void* stream) {
   mote::g_err[0] = 0;
   return mote::launch_skinny_gemm(args, reinterpret_cast<hipStream_t>(stream));

@@ -46,6 +46,7 @@ int launch_chunk_route(const mote_chunk_route_args* a, hipStream_t stream);
 size_t qkv_rope_workspace_bytes(const mote_qkv_rope_args* a);
 int launch_qkv_rope_fwd(const mote_qkv_rope_args* a, hipStream_t stream);
 int launch_gate_product(const mote_gate_product_args* a, hipStream_t stream);
+int launch_page_copy(const mote_page_copy_args* a, hipStream_t stream);
 int launch_skinny_gemm(const mote_skinny_gemm_args* a, hipStream_t stream);
 int launch_chunk_gather(const mote_chunk_gather_args* a, hipStream_t stream);
 int launch_chunk_gather_bwd(const mote_chunk_gather_bwd_args* a, hipStream_t stream);

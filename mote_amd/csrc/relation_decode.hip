@@ -51,6 +51,7 @@ struct DecParams {
   int64_t y_sb;
   float* g;
   float* xm;          // [B] mean over heads of g, or null
+  const unsigned char* run;  // predicate: 0 -> the launch writes nothing (null: always run)
   float* part;        // [BH][nsplit][D + 2]  (max, l, z)
   int* cnt;           // [BH] splits published in this call, kDecCntStride ints apart (zero between calls)
   int* cnt_seq;       // [B] heads finished in this call, kDecCntStride ints apart (zero between calls)
@@ -161,6 +162,10 @@ relation_decode_kernel(const DecParams p) {
   fetch(2, I2{});
 
   const int64_t S64 = p.S[b];  // after the cache loads: their addresses do not depend on it
+  // The predicate (a device flag, e.g. the router's boundary bit): with 0 every workgroup leaves
+  // here, before any write, count or barrier, so a captured step costs one empty launch when the
+  // chunk is not a boundary (graph.py:224-226 skips the step with a conditional node instead).
+  if (p.run && p.run[0] == 0) return;
   const bool bad = S64 < 0 || S64 >= p.cap;
   const int S = bad ? 0 : int(S64);
 
@@ -469,6 +474,7 @@ static int launch_decode_ws(const mote_relation_decode_args* a, void* ws_base, c
   p.cnt = reinterpret_cast<int*>(ws + w.cnt);
   p.cnt_seq = reinterpret_cast<int*>(ws + w.cnt_seq);
   p.xm = a->xm;
+  p.run = a->run;
   p.B = a->B; p.H = a->H; p.D = a->D; p.cap = a->capacity; p.parity = a->layer_parity & 1; p.flags = a->flags;
   p.scale = 1.0f / sqrtf((float)a->D);
   p.tau_inv = 1.0f / a->tau_s;

@@ -22,6 +22,7 @@ struct SkinnyParams {
   const bf16_t* x; int64_t x_sr;
   const bf16_t* w; int64_t w_sr;
   bf16_t* y; int64_t y_sr;
+  const unsigned char* run;  // predicate: 0 -> the launch writes nothing (null: always run)
   int B, N, K;
 };
 
@@ -47,6 +48,9 @@ __global__ void __launch_bounds__(64 * kSkWaves) skinny_gemm_kernel(const Skinny
       bx[s] = E::load8(xrow + 32 * s);
     }
   }
+  // the predicate after the loads are issued (reads are harmless); uniform, so the whole
+  // workgroup leaves before its barrier
+  if (p.run && p.run[0] == 0) return;
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
@@ -89,6 +93,7 @@ int launch_skinny_gemm(const mote_skinny_gemm_args* a, hipStream_t stream) {
   p.x = reinterpret_cast<const bf16_t*>(a->x); p.x_sr = a->x_sr;
   p.w = reinterpret_cast<const bf16_t*>(a->w); p.w_sr = a->w_sr;
   p.y = reinterpret_cast<bf16_t*>(a->y); p.y_sr = a->y_sr;
+  p.run = a->run;
   p.B = a->B; p.N = a->N; p.K = a->K;
   const int nks = a->K / (32 * kSkWaves);
   const dim3 grid(unsigned(a->N / 16)), block(64 * kSkWaves);

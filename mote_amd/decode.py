@@ -30,6 +30,11 @@ def decode_workspace(B: int, H: int, D: int, capacity: int, device, dtype=torch.
     return torch.zeros(max(n, 16), device=device, dtype=torch.uint8)
 
 
+def _check_run(run: Optional[torch.Tensor], dev) -> None:
+    if run is not None and (run.dtype not in (torch.bool, torch.uint8) or run.numel() != 1 or run.device != dev):
+        raise ValueError("run must be a one-element bool or uint8 tensor on the inputs' device")
+
+
 def _f32_param(t: torch.Tensor, n: int, name: str, dev) -> torch.Tensor:
     if not torch.is_tensor(t) or t.numel() != n or t.device != dev:
         raise ValueError(f"{name} must be a tensor of {n} element(s) on the inputs' device")
@@ -40,7 +45,8 @@ def relation_decode(p1: torch.Tensor, p2: torch.Tensor, info: torch.Tensor, S: t
                     cache_info: torch.Tensor, lam: torch.Tensor, tau_s: float = 2.0,
                     inv_freq: Optional[torch.Tensor] = None, theta: Optional[torch.Tensor] = None, layer_idx: int = 0,
                     advance: bool = False, workspace: Optional[torch.Tensor] = None, y: Optional[torch.Tensor] = None,
-                    g: Optional[torch.Tensor] = None, xm: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+                    g: Optional[torch.Tensor] = None, xm: Optional[torch.Tensor] = None,
+                    run: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """One decode step for B sequences.
 
     p1, p2, info: raw projections of the new chunk, [B, H, dh] (head stride dh, any batch stride),
@@ -50,6 +56,9 @@ def relation_decode(p1: torch.Tensor, p2: torch.Tensor, info: torch.Tensor, S: t
     cache_p2, cache_info: [B, H, capacity, dh] views (RelationArena.p2(layer) / .info(layer)).
     xm: optional fp32 [B] that receives the mean of g over the heads (graph.py:186), worked out by
         the kernel's last head of each sequence.
+    run: optional one-element bool / uint8 device tensor (e.g. the router's boundary bit): when it
+        holds 0 the launch writes nothing at all (no append, no advance, no y / g / xm), so one
+        captured graph serves both branches of the graph decoder's conditional main step.
     Returns (y [B, H, dh] in the cache dtype, g [B, H] fp32 exchange mass = 1 - F_SS).
     """
     if p1.dim() != 3:
@@ -79,6 +88,7 @@ def relation_decode(p1: torch.Tensor, p2: torch.Tensor, info: torch.Tensor, S: t
     th32 = None if theta is None else _f32_param(theta, H // 2, "theta", dev)
     if xm is not None and (xm.dtype != torch.float32 or xm.numel() != B or not xm.is_contiguous() or xm.device != dev):
         raise ValueError("xm must be a contiguous fp32 tensor of B elements")
+    _check_run(run, dev)
     if workspace is not None and (workspace.device != dev or not workspace.is_contiguous()):
         raise ValueError("workspace must be a contiguous tensor on the inputs' device")
     if y is not None and (y.shape != (B, H, D) or y.dtype != p1.dtype or y.device != dev or y.stride(-1) != 1
@@ -107,19 +117,23 @@ def relation_decode(p1: torch.Tensor, p2: torch.Tensor, info: torch.Tensor, S: t
     a.workspace, a.workspace_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     if xm is not None:
         a.xm = xm.data_ptr()
+    a.run = L.ptr(run)
     L.check(L.lib().mote_relation_decode(a, L.stream_of(p1)), "mote_relation_decode")
     return y, g
 
 
-def skinny_linear(x: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+def skinny_linear(x: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] = None,
+                  run: Optional[torch.Tensor] = None) -> torch.Tensor:
     """y [B, N] = x [B, K] w[N, K]^T for the decode engine's per-token projections (bf16, B <= 16,
-    N % 16 == 0, K % 128 == 0, K <= 1024): one launch of mote_skinny_gemm."""
+    N % 16 == 0, K % 128 == 0, K <= 1024): one launch of mote_skinny_gemm. With `run` (a device
+    flag) the launch leaves `out` untouched when the flag is 0."""
     B, K = x.shape
     N = w.shape[0]
     if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
         raise TypeError("skinny_linear: bf16 x and w")
     if x.stride(-1) != 1 or w.stride(-1) != 1 or w.shape[1] != K:
         raise ValueError("skinny_linear: x [B, K] and w [N, K] with unit element stride")
+    _check_run(run, x.device)
     if out is None:
         out = torch.empty(B, N, device=x.device, dtype=x.dtype)
     a = L.SkinnyGemmArgs()
@@ -127,6 +141,7 @@ def skinny_linear(x: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] 
     a.x, a.x_sr = x.data_ptr(), x.stride(0)
     a.w, a.w_sr = w.data_ptr(), w.stride(0)
     a.y, a.y_sr = out.data_ptr(), out.stride(0)
+    a.run = L.ptr(run)
     L.check(L.lib().mote_skinny_gemm(a, L.stream_of(x)), "mote_skinny_gemm")
     return out
 
@@ -158,6 +173,7 @@ class RelationDecodeStep:
         self.theta = torch.empty(max(H // 2, 1), device=dev, dtype=torch.float32) if mixer.use_givens else None
         self.inv_freq = mixer.inv_freq.to(device=dev, dtype=torch.float32).clone() if mixer.use_rope else None
         self.w_qkv = None
+        self._bufs: dict = {}
         self.sync_params()
 
     @torch.no_grad()
@@ -174,14 +190,36 @@ class RelationDecodeStep:
         if self.theta is not None:
             self.theta.copy_(self.mixer.theta.detach().float())
 
+    def _static(self, name: str, shape, dtype) -> torch.Tensor:
+        """A persistent output buffer (a predicated launch that does not run leaves it as it was)."""
+        t = self._bufs.get(name)
+        if t is None or tuple(t.shape) != tuple(shape) or t.dtype != dtype:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("run the predicated decode step once outside the capture first (its "
+                                   "persistent outputs are allocated then)")
+            t = torch.zeros(shape, device=self.arena.device, dtype=dtype)
+            self._bufs[name] = t
+        return t
+
     @torch.no_grad()
-    def __call__(self, x: torch.Tensor, S: torch.Tensor, advance: bool = False):
+    def __call__(self, x: torch.Tensor, S: torch.Tensor, advance: bool = False, run: Optional[torch.Tensor] = None,
+                 xm: Optional[torch.Tensor] = None):
+        """One new chunk per sequence: x [B, 1, D] -> (out [B, 1, D], xm [B]).
+
+        run: optional device flag; with it every write of the step (arena append, S advance, the
+        outputs, xm) happens only when the flag is nonzero, and the outputs live in persistent
+        buffers that keep their last values otherwise (the bf16 skinny path: B <= 16, T = 1).
+        xm: optional fp32 [B] buffer for the exchange mass (default: the step's own)."""
         m = self.mixer
         B, T, Dm = x.shape
         H, dh = m.n_heads, m.d_head
         skinny = T == 1 and _skinny_ok(B, x, self.w_qkv, m.wo.weight, *([m.wg.weight] if m.out_gate else []))
+        if run is not None and not skinny:
+            raise ValueError("a predicated decode step needs the bf16 skinny path (B <= 16, one chunk)")
+        xm = self.xm if xm is None else xm
         if skinny:  # bf16 decode shapes: the skinny product instead of the general GEMM library
-            qkv = skinny_linear(x.reshape(B, Dm), self.w_qkv).view(B, 3, H, dh)
+            qbuf = self._static("qkv", (B, 3 * H * dh), x.dtype) if run is not None else None
+            qkv = skinny_linear(x.reshape(B, Dm), self.w_qkv, qbuf, run).view(B, 3, H, dh)
         else:
             qkv = F.linear(x, self.w_qkv).view(B, 3, H, dh)
         qkv = qkv.to(self.arena.dtype)
@@ -191,11 +229,13 @@ class RelationDecodeStep:
             qkv = torch.stack([q, k, qkv[:, 2]], dim=1)
         relation_decode(qkv[:, 0], qkv[:, 1], qkv[:, 2], S, self.arena.p2(self.layer), self.arena.info(self.layer),
                         self.lam, m.tau_s, self.inv_freq, self.theta, m.layer_idx, advance, self.workspace,
-                        self.y, self.g, self.xm)
+                        self.y, self.g, xm, run)
         if skinny:  # _out (relation.py:176-182) on the skinny product
             y = self.y.to(x.dtype).reshape(B, H * dh)
             if m.out_gate:
-                y = y * torch.sigmoid(skinny_linear(x.reshape(B, Dm), m.wg.weight))
-            return skinny_linear(y, m.wo.weight).view(B, 1, Dm), self.xm
+                gbuf = self._static("gate", (B, Dm), x.dtype) if run is not None else None
+                y = y * torch.sigmoid(skinny_linear(x.reshape(B, Dm), m.wg.weight, gbuf, run))
+            obuf = self._static("out", (B, Dm), x.dtype) if run is not None else None
+            return skinny_linear(y, m.wo.weight, obuf, run).view(B, 1, Dm), xm
         y = self.y.to(x.dtype).view(B, H, 1, dh)
-        return m._out(y, x), self.xm
+        return m._out(y, x), xm
