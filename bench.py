@@ -239,19 +239,136 @@ def copy_calibration(dev, mib: int = 1024):
     del a, b
 
 
-def measured_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` at this workload, as measured by the two counter passes and
-    recorded in profiles/hbm_traffic.txt (lines "<kernel> <bytes per launch>"); None if absent."""
-    path = os.path.join(ROOT, "profiles", "hbm_traffic.txt")
+# The device sources each recorded kernel figure depends on: a figure read from profiles/ counts only
+# while these files are unchanged since it was measured (their fingerprint is recorded beside it).
+_COMMON = ("common.hpp", "params.hpp")
+KERNEL_SOURCES = {
+    "bwd_kv_kernel": ("relation_bwd_tiles.hip", "tiles.hpp", "bwd.hpp") + _COMMON,
+    "bwd_dq_kernel": ("relation_bwd_tiles.hip", "tiles.hpp", "bwd.hpp") + _COMMON,
+    "relation_fwd_tile_kernel": ("relation_fwd.hip", "tiles.hpp") + _COMMON,
+    "bwd_rows_kernel": ("relation_bwd.hip", "bwd.hpp") + _COMMON,
+    "rope_givens_fwd_stream_kernel": ("rope_givens.hip",) + _COMMON,
+    "rope_givens_bwd_stream_kernel": ("rope_givens.hip",) + _COMMON,
+    "relation_decode_kernel": ("relation_decode.hip",) + _COMMON,
+    "qkv_rope_kernel": ("qkv_rope.hip", "tiles.hpp") + _COMMON,
+}
+
+
+def source_fingerprint(kernel: str) -> str:
+    """12 hex digits of sha256 over the kernel's device sources (decode figures share one entry)."""
+    import hashlib
+
+    base = kernel.split("@")[0]
+    base = "relation_decode_kernel" if base.startswith("relation_decode_kernel") else base
+    h = hashlib.sha256()
+    for f in KERNEL_SOURCES[base]:
+        with open(os.path.join(ROOT, "mote_amd", "csrc", f), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:12]
+
+
+def _recorded(fname: str, kernel: str):
+    """(fields after the kernel name, whether they were measured on the current sources) from a
+    profiles/ file of lines "<kernel> <fields...> src=<fingerprint>", or (None, None)."""
+    path = os.path.join(ROOT, "profiles", fname)
     try:
         with open(path) as f:
             for line in f:
                 parts = line.split()
-                if len(parts) == 2 and parts[0] == kernel:
-                    return int(float(parts[1]))
+                if len(parts) >= 3 and parts[0] == kernel and parts[-1].startswith("src="):
+                    return parts[1:-1], parts[-1][4:] == source_fingerprint(kernel)
     except OSError:
         pass
-    return None
+    return None, None
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` at this workload from the two counter passes recorded in
+    profiles/hbm_traffic.txt, with where it came from; the bytes are null when the kernel's sources
+    changed after the measurement (the record is then stale, not this build's)."""
+    fields, current = _recorded("hbm_traffic.txt", kernel)
+    if fields is None:
+        return None, {"recorded": None}
+    note = {"recorded": "profiles/hbm_traffic.txt", "sources_match": bool(current)}
+    return (int(float(fields[0])) if current else None), note
+
+
+def _traffic(kernel: str) -> dict:
+    b, note = measured_traffic(kernel)
+    return {"traffic": b, "traffic_source": note}
+
+
+def measured_counters(kernel: str):
+    """MFMA busy, VALU busy and MFMA/VALU co-execution (fractions) of `kernel` from the counter
+    passes recorded in profiles/kernel_counters.txt; null when the sources changed since."""
+    fields, current = _recorded("kernel_counters.txt", kernel)
+    if fields is None:
+        return {"recorded": None}
+    out = {"recorded": "profiles/kernel_counters.txt", "sources_match": bool(current)}
+    for f in fields:
+        k, _, v = f.partition("=")
+        out[k] = float(v) if current else None
+    return out
+
+
+def summarize_counters(base: str) -> None:
+    """Print profiles/ lines from rocprofv3 counter-collection CSVs under `base`: <cfg>_A / <cfg>_B
+    (SQ counter passes of `--kernels-only <cfg>`) -> kernel_counters.txt lines; fetch / write
+    (FETCH_SIZE / WRITE_SIZE passes over the default workload) -> hbm_traffic.txt lines. Each line
+    ends with the fingerprint of the sources it was measured on."""
+    import csv
+    import glob
+    import re
+
+    def load(d):
+        per, name = {}, {}
+        for f in glob.glob(os.path.join(base, d, "*counter_collection.csv")):
+            for r in csv.DictReader(open(f)):
+                k = int(r["Dispatch_Id"])
+                per.setdefault(k, {})[r["Counter_Name"]] = float(r["Counter_Value"])
+                name[k] = re.sub(r"^void |mote::|\(.*$", "", r["Kernel_Name"]).split("<")[0]
+        return per, name
+
+    known = tuple(KERNEL_SOURCES)
+    for cfg in ("c3", "c2", "c5"):
+        agg = {}
+        for pas in ("A", "B"):
+            per, name = load(f"{cfg}_{pas}")
+            for k, cs in per.items():
+                if name[k] not in known:
+                    continue
+                for c, v in cs.items():
+                    agg.setdefault(name[k], {}).setdefault(c, []).append(v)
+        for kern, cs in sorted(agg.items()):
+            av = {c: sum(v) / len(v) for c, v in cs.items()}
+            cyc = av.get("SQ_BUSY_CYCLES", 0.0) / 32.0  # summed over the 32 shader engines
+            if not cyc or "SQ_VALU_MFMA_BUSY_CYCLES" not in av:
+                continue
+            mfma = av["SQ_VALU_MFMA_BUSY_CYCLES"] / (cyc * 1024)          # per SIMD
+            valu = av.get("SQ_ACTIVE_INST_VALU", 0.0) / (cyc * 256)       # quad-cycles per CU
+            coex = av.get("SQ_VALU_MFMA_COEXEC_CYCLES", 0.0) / max(av["SQ_VALU_MFMA_BUSY_CYCLES"], 1.0)
+            print(f"{kern}@{cfg} mfma_busy={mfma:.4f} valu_busy={valu:.4f} mfma_valu_coexec={coex:.4f} "
+                  f"src={source_fingerprint(kern)}")
+    fetch, fname = load("fetch")
+    write, _ = load("write")
+    cal = [k for k, n in fname.items() if "copyBuffer" in n]
+    if fetch and cal:
+        big = max(cal, key=lambda k: fetch[k].get("FETCH_SIZE", 0))
+        sf = 1048576.0 / fetch[big]["FETCH_SIZE"]
+        sw = 1048576.0 / write[big]["WRITE_SIZE"] if big in write else 1.0
+        tot = {}
+        for k, cs in fetch.items():
+            if fname[k] in known and k in write:
+                b = (cs["FETCH_SIZE"] * sf + write[k]["WRITE_SIZE"] * sw) * 1024
+                tot.setdefault(fname[k], []).append(b)
+        for kern, v in sorted(tot.items()):
+            groups = {kern: v}
+            if kern == "relation_decode_kernel":  # batch 1 (~14 MB per launch) and batch 16 (~200 MB)
+                groups = {kern + "_b1": [b for b in v if b < 5e7], kern + "_b16": [b for b in v if b >= 5e7]}
+            for kn, vv in groups.items():
+                if vv:
+                    print(f"{kn} {sum(vv) / len(vv):.0f} src={source_fingerprint(kn)}   "
+                          f"# scale FETCH x{sf:.3f}, WRITE x{sw:.3f}")
 
 
 # ------------------------------------------------------------------------------------------------
@@ -745,20 +862,32 @@ def bench_dc(B: int, dev, copies: int, launches: int = 20):
 # ------------------------------------------------------------------------------------------------
 # CPU baseline: the oracle on the host cores
 # ------------------------------------------------------------------------------------------------
+def _cpu_times(fn, warmup: int = 1, reps: int = 3):
+    """Seconds of `reps` timed calls of fn after `warmup` untimed ones (time.perf_counter)."""
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return ts
+
+
 def bench_cpu(T: int):
+    """The CPU baselines of the build's own restatement of the reference (the test oracle: fp32,
+    materialized scores, autograd for the backward) on the host cores, each one warm-up and three
+    timed runs over a bounded sample of its workload:
+    c3: one Mote-96M layer fwd+bwd at T (the 12-layer step extrapolated), TFLOP/s;
+    c2: the Mote-32M stack, 8 layers fwd+bwd over the 4 sequences' real rows, TFLOP/s;
+    c5: one Mote-138M layer forward over the 8 ragged sequences, one at a time (18 layers
+        extrapolated), TFLOP/s;
+    decode_b1 / decode_b16: one 12-layer decode step at S = 4096 (the new rows' RoPE / Givens, the
+        append and the read of rows [0, S]), microseconds per step."""
     from oracle import relation as O
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    g = torch.Generator().manual_seed(2)
-    p1, p2, info = (torch.randn(1, N_HEADS, T, D_HEAD, generator=g).requires_grad_(True) for _ in range(3))
-    lam = torch.tensor(0.5, requires_grad=True)
-    dy = torch.randn(1, N_HEADS, T, D_HEAD, generator=g)
-    t0 = time.perf_counter()
-    y, _ = O.relation_reference(p1, p2, info, lam, 2.0, 0)
-    torch.autograd.grad((y * dy).sum(), [p1, p2, info, lam])
-    dt = time.perf_counter() - t0
-    flops = 7.0 * N_HEADS * D_HEAD * T * T
     cpu = platform.processor() or platform.machine()
     try:
         with open("/proc/cpuinfo") as f:
@@ -768,11 +897,89 @@ def bench_cpu(T: int):
                     break
     except OSError:
         pass
-    log(f"[bench] CPU oracle: one layer fwd+bwd {dt:.1f} s on {cores} threads ({cpu})")
-    return dict(value=flops / dt / 1e12, unit="TFLOP/s", cores=cores, kind="port",
-                sample=f"one Mote-96M Relation layer fwd+bwd (T={T}, H=8, dh=96, fp32, materialized oracle), "
-                       f"timed once: {dt:.2f} s; the 12-layer step would take {12 * dt:.1f} s",
-                cpu=cpu, seconds_per_layer=dt)
+    res = {}
+
+    def fwd_bwd(p1, p2, info, lam, dy):
+        y, _ = O.relation_reference(p1, p2, info, lam, 2.0, 0)
+        torch.autograd.grad((y * dy).sum(), [p1, p2, info, lam])
+
+    def leaves(g, B, H, Tn, D):
+        return [torch.randn(B, H, Tn, D, generator=g).requires_grad_(True) for _ in range(3)]
+
+    # C3: one layer fwd + bwd
+    g = torch.Generator().manual_seed(2)
+    p1, p2, info = leaves(g, 1, N_HEADS, T, D_HEAD)
+    lam = torch.tensor(0.5, requires_grad=True)
+    dy = torch.randn(1, N_HEADS, T, D_HEAD, generator=g)
+    ts = _cpu_times(lambda: fwd_bwd(p1, p2, info, lam, dy))
+    dt = sum(ts) / len(ts)
+    res["c3"] = dict(value=7.0 * N_HEADS * D_HEAD * T * T / dt / 1e12, unit="TFLOP/s", cores=cores, kind="port",
+                     sample=f"one Mote-96M Relation layer fwd+bwd (T={T}, H=8, dh=96, fp32, materialized oracle with "
+                            f"autograd), 1 warm-up + 3 timed: {', '.join(f'{t:.2f}' for t in ts)} s; the 12-layer "
+                            f"step would take {12 * dt:.1f} s", seconds=ts, cpu=cpu)
+    del p1, p2, info, dy
+    # C2: the Mote-32M stack, real rows of each sequence
+    gm = torch.Generator().manual_seed(1)
+    mask = torch.rand(4, 2048, generator=gm) < (1.0 / 3.3)
+    mask[:, 0] = True
+    M = mask.sum(-1).tolist()
+    layers = [[(leaves(g, 1, 8, m, 64), torch.randn(1, 8, m, 64, generator=g)) for m in M] for _ in range(8)]
+    lam2 = torch.tensor(0.5, requires_grad=True)
+
+    def c2_step():
+        for lay in layers:
+            for (q, k, v), d in lay:
+                fwd_bwd(q, k, v, lam2, d)
+    ts = _cpu_times(c2_step)
+    dt = sum(ts) / len(ts)
+    res["c2"] = dict(value=8 * 7.0 * 8 * 64 * sum(m * m for m in M) / dt / 1e12, unit="TFLOP/s", cores=cores,
+                     kind="port", sample=f"the Mote-32M stack (8 layers, B=4, chunks {M}, H=8, dh=64) fwd+bwd over "
+                     f"each sequence's real rows, 1 warm-up + 3 timed: {', '.join(f'{t:.2f}' for t in ts)} s per step",
+                     seconds=ts)
+    del layers
+    # C5: one layer forward over the 8 ragged sequences
+    lens = torch.randint(1000, 5001, (8,), generator=torch.Generator().manual_seed(4)).tolist()
+    seqs = [[torch.randn(1, N_HEADS, n, D_HEAD, generator=g) for _ in range(3)] for n in lens]
+
+    def c5_layer():
+        with torch.no_grad():
+            for q, k, v in seqs:
+                O.relation_reference(q, k, v, torch.tensor(0.5), 2.0, 0)
+    ts = _cpu_times(c5_layer)
+    dt = sum(ts) / len(ts)
+    res["c5"] = dict(value=2.0 * N_HEADS * D_HEAD * sum(n * n for n in lens) / dt / 1e12, unit="TFLOP/s", cores=cores,
+                     kind="port", sample=f"one Mote-138M Relation layer forward over 8 ragged sequences {lens} (one at a "
+                     f"time, fp32 materialized), 1 warm-up + 3 timed: {', '.join(f'{t:.2f}' for t in ts)} s; the "
+                     f"18-layer prefill would take {18 * dt:.1f} s", seconds=ts)
+    del seqs
+    # C4: one 12-layer decode step at S = 4096, batch 1 and 16 (bf16 caches as the GPU's)
+    S0, cap = 4096, 4097
+    inv = O.rope_inv_freq(D_HEAD, 10000.0)
+    for batch in (1, 16):
+        caches = [[(torch.randn(batch, N_HEADS, cap, D_HEAD, generator=g) * 0.7).to(torch.bfloat16) for _ in range(2)]
+                  for _ in range(N_LAYERS)]
+        raws = [[(torch.randn(batch, N_HEADS, D_HEAD, generator=g) * 0.7).to(torch.bfloat16) for _ in range(3)]
+                for _ in range(N_LAYERS)]
+        theta = torch.rand(N_HEADS // 2, generator=g) * 0.6 - 0.3
+        Sv = torch.full((batch,), S0, dtype=torch.int64)
+
+        def dec_step():
+            with torch.no_grad():
+                for li in range(N_LAYERS):
+                    kc, vc = caches[li]
+                    q, k, v = O.decode_rows_ref(*raws[li], Sv, inv, theta, li, torch.bfloat16)
+                    kc[:, :, S0], vc[:, :, S0] = k, v
+                    O.relation_decode_ref(q, kc, vc, Sv, torch.tensor(0.4), 2.0)
+        ts = _cpu_times(dec_step)
+        dt = sum(ts) / len(ts)
+        res[f"decode_b{batch}"] = dict(value=dt * 1e6, unit="us/step", cores=cores, kind="port",
+                                       sample=f"one 12-layer decode step, batch {batch}, S = 4096, bf16 caches (new rows, "
+                                       f"append, fp32 read of rows [0, S]), 1 warm-up + 3 timed: "
+                                       f"{', '.join(f'{t * 1e3:.1f}' for t in ts)} ms", seconds=ts)
+        del caches
+    log(f"[bench] CPU oracle on {cores} threads ({cpu}): " +
+        ", ".join(f"{k} {v['value']:.4g} {v['unit']}" for k, v in res.items()))
+    return res
 
 
 def profile_kernels(which: str, dev, steps: int = 3) -> None:
@@ -808,7 +1015,12 @@ def main():
                     help="only the decode-engine lines (batch 1 and 16, --decode-steps tokens), for profiling")
     ap.add_argument("--kernels-only", choices=("c2", "c3", "c5"), default=None,
                     help="only run one configuration's kernels a few times, for rocprofv3 counter passes")
+    ap.add_argument("--summarize-counters", metavar="DIR", default=None,
+                    help="print profiles/ lines from rocprofv3 counter CSVs under DIR and exit (no GPU)")
     args = ap.parse_args()
+    if args.summarize_counters:
+        summarize_counters(args.summarize_counters)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the Relation path is built and measured on a single GPU "
               "(run with --gpus 1)", file=sys.stderr)
@@ -860,17 +1072,19 @@ def main():
                    "flop_convention": "7*H*dh*T^2 per layer (causal; fwd 2x, bwd 5x)"},
         "roofline": {"kernel": "bwd_kv_kernel (key-stationary backward: U, dW, dV, dK)", "bound": "mfma",
                      "achieved": round(st["keys_tflops"], 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(st["keys_tflops"] / PEAK_BF16_TFLOPS, 4), "traffic": measured_traffic("bwd_kv_kernel"),
+                     "frac": round(st["keys_tflops"] / PEAK_BF16_TFLOPS, 4), **_traffic("bwd_kv_kernel"),
+                     "counters": measured_counters("bwd_kv_kernel@c3"),
                      "flop_per_launch": 4.0 * N_HEADS * D_HEAD * st["T"] ** 2, "avg_launch_ms": round(st["keys_ms"], 4)},
         "roofline_bwd_dq": {"kernel": "bwd_dq_kernel (query-stationary dQ from the stored dU^T tiles)", "bound": "hbm",
                             "achieved": round(st["queries_gbs"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                             "frac": round(st["queries_gbs"] / PEAK_HBM_GBS, 4),
-                            "traffic": measured_traffic("bwd_dq_kernel"),
+                            **_traffic("bwd_dq_kernel"), "counters": measured_counters("bwd_dq_kernel@c3"),
                             "bytes_per_launch": st["queries_bytes"], "avg_launch_ms": round(st["queries_ms"], 4)},
         "roofline_fwd": {"kernel": "relation_fwd_tile_kernel", "bound": "mfma", "achieved": round(st["fwd_tflops"], 2),
                          "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(st["fwd_tflops"] / PEAK_BF16_TFLOPS, 4),
-                         "traffic": measured_traffic("relation_fwd_tile_kernel"),
+                         **_traffic("relation_fwd_tile_kernel"),
+                         "counters": measured_counters("relation_fwd_tile_kernel@c3"),
                          "flop_per_launch": 2.0 * N_HEADS * D_HEAD * st["T"] ** 2, "avg_launch_ms": round(st["fwd_ms"], 4)},
         "stack_frac_of_peak": round(st["tflops"] / PEAK_BF16_TFLOPS, 4),
     }
@@ -881,7 +1095,7 @@ def main():
                 "step_frac_hbm": round(v["gbs"] / PEAK_HBM_GBS, 4), "kernel_us": round(v["kernel_us"], 2),
                 "kernel_GBs": round(v["kernel_gbs"], 1), "kernel_frac_hbm": round(v["kernel_gbs"] / PEAK_HBM_GBS, 4),
                 "eager_launch_us": round(v["eager_us"], 2),
-                "traffic": measured_traffic(f"relation_decode_kernel_{k}"),
+                **_traffic(f"relation_decode_kernel_{k}"),
                 "cache_copies_rotated": v["copies"]}
             for k, v in dec.items()}
     if dec:
@@ -895,7 +1109,8 @@ def main():
             "avg_launch_ms": round(q["fused"]["us_per_launch"] / 1e3, 5)}
     out.update(extra)
     if cpu is not None:
-        out["cpu_baseline"] = {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")}
+        out["cpu_baseline"] = {k: cpu["c3"][k] for k in ("value", "unit", "cores", "kind", "sample")}
+        out["cpu_baselines"] = cpu
     print(json.dumps(out), flush=True)
 
 
