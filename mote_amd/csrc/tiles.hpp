@@ -3,7 +3,10 @@
 // A tile is row-major (DP elements per row, no padding) with the 16-byte chunks of each row
 // XOR-swizzled against bank conflicts: logical chunk c of row r sits at physical chunk
 // c ^ tile_swz<DP>(r). For every read pattern of the kernels the swizzle value is a per-lane
-// constant.
+// constant. For DP = 96 the value is bits 1-2 of the row, chosen by measurement (rocprofv3
+// SQ_LDS_BANK_CONFLICT over the C3 kernels): bits 2-3 left the key kernel's LDS stalled on
+// conflicts 18 % of its busy cycles and the forward's 10 %; bits 1-2 leave 1 % and 0.1 %, and the
+// key kernel runs 9 % faster.
 //
 // Staging goes global -> LDS with global_load_lds_dwordx4: lane l of one wave instruction writes its
 // 16 bytes at M0 + 16 l, so instruction n of a tile fills physical chunks 64 n .. 64 n + 63 and no
@@ -67,7 +70,7 @@ template <int DP>
 __device__ __forceinline__ int tile_swz(int row) {
   if constexpr (DP == 64) return (row >> 1) & 7;
   else if constexpr (DP == 128) return row & 7;
-  else return (row >> 2) & 3;  // DP 32 (4 chunks) and 96 (12 chunks): stays inside aligned groups of 4
+  else return (row >> 1) & 3;  // DP 32 (4 chunks) and 96 (12 chunks): stays inside aligned groups of 4
 }
 
 typedef __attribute__((ext_vector_type(4))) short s16x4;
