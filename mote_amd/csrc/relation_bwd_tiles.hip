@@ -368,6 +368,8 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
   constexpr int SLOT = TILE + 4096; // bf16 per ring slot: the P2 tile, then the pair's 8 dU^T fragments
   constexpr int VMS = DP / 32 + 2;  // vector-memory instructions per block and wave (P2 staging + 2 fragments)
   constexpr int HALF = DP / 2;      // fp32 columns per half of the reduction buffer
+  constexpr int RS = HALF + 4;      // its row stride: an odd count of 16-byte chunks, so the 16 rows of
+                                    // a lane group's f32x4 accesses fall on distinct banks
   // one array per ring slot (each slot holds half of the final reduction buffer)
   __shared__ __align__(16) bf16_t ks0[SLOT];
   __shared__ __align__(16) bf16_t ks1[SLOT];
@@ -450,11 +452,12 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
   }
 
   // add the two key halves through LDS: head-dim columns [0, DP/2) in slot 0, the rest in slot 1,
-  // each [64 queries][DP/2] fp32 (exactly one slot)
+  // each [64 queries][RS] fp32
+  static_assert(64 * RS * 4 <= SLOT * 2, "a reduction half fits one ring slot");
   float* R0 = reinterpret_cast<float*>(ks0);
   float* R1 = reinterpret_cast<float*>(ks1);
   auto rptr = [&](int row, int col) -> float* {
-    return col < HALF ? R0 + row * HALF + col : R1 + row * HALF + (col - HALF);
+    return col < HALF ? R0 + row * RS + col : R1 + row * RS + (col - HALF);
   };
   __builtin_amdgcn_s_waitcnt(0);  // the last (past-the-end) prefetches into slots 0 and 1 have landed
   __syncthreads();

@@ -3,10 +3,12 @@
 // A tile is row-major (DP elements per row, no padding) with the 16-byte chunks of each row
 // XOR-swizzled against bank conflicts: logical chunk c of row r sits at physical chunk
 // c ^ tile_swz<DP>(r). For every read pattern of the kernels the swizzle value is a per-lane
-// constant. For DP = 96 the value is bits 1-2 of the row, chosen by measurement (rocprofv3
-// SQ_LDS_BANK_CONFLICT over the C3 kernels): bits 2-3 left the key kernel's LDS stalled on
-// conflicts 18 % of its busy cycles and the forward's 10 %; bits 1-2 leave 1 % and 0.1 %, and the
-// key kernel runs 9 % faster.
+// constant. The values were chosen by measurement (rocprofv3 SQ_LDS_BANK_CONFLICT): for DP = 96,
+// bits 1-2 of the row, where bits 2-3 left the key kernel's LDS stalled on conflicts 18 % of its
+// busy cycles and the forward's 10 % (bits 1-2: 1 % and 0.1 %, and a 9 % faster key kernel); for
+// DP = 64, bits 0-2, where bits 1-3 left the forward 1.6 % and the key kernel 4.7 % (now 0.3 % and
+// 2.7 %): a transposed read covers 8 rows x 2 chunks at once, and bits 0-2 give the four rows of
+// each bank half distinct chunk pairs.
 //
 // Staging goes global -> LDS with global_load_lds_dwordx4: lane l of one wave instruction writes its
 // 16 bytes at M0 + 16 l, so instruction n of a tile fills physical chunks 64 n .. 64 n + 63 and no
@@ -68,8 +70,7 @@ __device__ __forceinline__ uint32_t lds_addr(const void* l) {
 
 template <int DP>
 __device__ __forceinline__ int tile_swz(int row) {
-  if constexpr (DP == 64) return (row >> 1) & 7;
-  else if constexpr (DP == 128) return row & 7;
+  if constexpr (DP == 64 || DP == 128) return row & 7;
   else return (row >> 1) & 3;  // DP 32 (4 chunks) and 96 (12 chunks): stays inside aligned groups of 4
 }
 
