@@ -225,211 +225,242 @@ __global__ void __launch_bounds__(256) sum_partials_kernel(const float* partial,
 }
 
 // ------------------------------------------------------------------------------------------------
-// Streaming kernels (16-byte chunks), used when D/2 is a multiple of the chunk, every view is 16-byte
-// aligned and a [p1 | p2 | I~] row has at most 1024 chunks. A block takes up to kRopeR rows and has
-// one thread per chunk position of the row, so every index of a thread (tensor, head, chunk, partner
-// chunk, output address) is worked out once; per row the thread loads its own chunk and its partner
-// (the other RoPE half of its head, or the same chunk of the Givens partner head; the partner's
-// lines are the neighbouring threads', so they come from L2), and stores one output chunk. Every
-// load of the block is issued before any math (the table value first: loads complete in order), the
-// RoPE factors of the block's rows go through LDS, and the only barrier waits for them.
+// Streaming kernels (16-byte chunks), used when D/2 is a multiple of the chunk and every view is
+// 16-byte aligned. One thread per rotation unit of a row: a RoPE unit is a chunk of a head's first
+// half with the same chunk of its second half (in p1 or p2), a Givens unit the same chunk of the two
+// heads of a pair (in I~); the thread loads both chunks and stores both results, so every input
+// chunk is loaded once and the two rows of a rotation meet in one thread. A row has
+// U = 3 H cph / 2 units (cph chunks per head). A block has NS row slots of U threads and takes
+// kRopeNR rows per slot (rows row0 + NS r + slot), so each thread keeps 2 kRopeNR chunk loads in
+// flight; all of them are issued before any math (the table values first: loads complete in order),
+// the RoPE factors of the block's rows go through LDS, and the only barrier waits for them.
 // ------------------------------------------------------------------------------------------------
-constexpr int kRopeR = 4;       // rows per block, forward (two loads per row in flight)
-constexpr int kRopeRB = 2;      // rows per block, backward (four loads per row in flight)
-constexpr int kRopeMaxCh = 1024;
+constexpr int kRopeNR = 4;
+constexpr int kRopeMaxThreads = 1024;
 
-// The RoPE factors of a block's NR rows, [NR][D/2] cos then sin in LDS, rounded to the element type
-// as the reference casts its tables: thread k < D/2 computes column k for every row, from its
-// inverse frequency `invk`, loaded before the chunk loads so that the sincos runs while they arrive.
-template <typename T, int NR>
-__device__ __forceinline__ void rope_factors(float invk, int rope, int pos0, int row0, int nrow, int T_, int half,
-                                             float* tc, float* ts) {
-  const int k = threadIdx.x;
-  if (k >= half) return;
-#pragma unroll
-  for (int r = 0; r < NR; ++r) {
+// The RoPE factors of a block's nr rows, [nr][D/2] cos then sin in LDS, rounded to the element type
+// as the reference casts its tables. Entry i = r D/2 + k goes to thread i mod blockDim: a sincos of
+// a large angle (positions in the thousands) takes the long argument reduction, so the entries are
+// spread over the whole block rather than left to D/2 threads. The inverse frequencies of a thread's
+// first two entries (`inv2`) are loaded before the chunk loads, so the sincos runs while they arrive.
+struct RopeInv {
+  float v[2];
+};
+__device__ __forceinline__ RopeInv rope_inv(const float* inv_safe, int rope, int half) {
+  RopeInv R;
+  R.v[0] = inv_safe[(threadIdx.x % half) * rope];
+  R.v[1] = inv_safe[((threadIdx.x + blockDim.x) % half) * rope];
+  return R;
+}
+template <typename T>
+__device__ __forceinline__ void rope_factors(const RopeInv& inv2, const float* inv_safe, int rope, int pos0, int row0,
+                                             int nr, int nrow, int T_, int half, float* tc, float* ts) {
+  int j = 0;
+  for (int i = threadIdx.x; i < nr * half; i += blockDim.x, ++j) {
+    const int r = i / half, k = i - r * half;
     const int t = (row0 + min(r, nrow - 1)) % T_;
+    const float invk = j == 0 ? inv2.v[0] : j == 1 ? inv2.v[1] : inv_safe[k * rope];
     float sn, cs;
     sincosf((float)(pos0 + t) * invk, &sn, &cs);
-    tc[r * half + k] = rope ? rnd<T>(cs) : 1.f;
-    ts[r * half + k] = rope ? rnd<T>(sn) : 0.f;
+    tc[i] = rope ? rnd<T>(cs) : 1.f;
+    ts[i] = rope ? rnd<T>(sn) : 0.f;
   }
 }
 
-// The thread's place in the [p1 | p2 | I~] row: tensor, head, chunk in the head, partner chunk and
-// the Givens pairing (relation.py:150-174).
-struct RopeLane {
-  int which, hd, k, pc, pair, other, a0;
-  bool lo, first;
+// A thread's rotation unit: tensor (0: p1, 1: p2, 2: I~), the two heads (one head for RoPE), the
+// chunk k (RoPE: k < cph / 2, its partner k + cph / 2; Givens: the same chunk k < cph of both
+// heads), the Givens pair, and the two chunks' positions in the [p1 | p2 | I~] row. Givens pairs
+// (relation.py:150-174): even layers (0,1),(2,3)..., odd layers (1,2),...,(H-1,0); the first head of a
+// pair gets c a - s b, the second s a + c b.
+struct RopeUnit {
+  int which, ha, hb, k, pair, ca, cb;
 };
-__device__ __forceinline__ RopeLane rope_lane(int c, int H, int D, int EPC, int parity) {
-  RopeLane L;
-  const int cph = D / EPC, hch = cph / 2, cpt = H * cph;
-  L.which = c / cpt;
-  const int cc = c - L.which * cpt;
-  L.hd = cc / cph;
-  L.k = cc - L.hd * cph;
-  L.lo = L.k < hch;
-  L.a0 = (L.lo ? L.k : L.k - hch) * EPC;  // RoPE factor index of the chunk's first element
-  givens_pair(L.hd, H, parity, L.pair, L.other, L.first);
-  L.pc = L.which < 2 ? c + (L.lo ? hch : -hch) : 2 * cpt + L.other * cph + L.k;
-  return L;
+__device__ __forceinline__ RopeUnit rope_unit(int u, int H, int cph, int parity) {
+  RopeUnit R;
+  const int hch = cph / 2, ur = 2 * H * hch, cpt = H * cph;
+  if (u < ur) {
+    R.which = u / (H * hch);
+    const int rem = u - R.which * H * hch;
+    R.ha = R.hb = rem / hch;
+    R.k = rem - R.ha * hch;
+    R.pair = 0;
+    R.ca = R.which * cpt + R.ha * cph + R.k;
+    R.cb = R.ca + hch;
+  } else {
+    const int g = u - ur;
+    R.which = 2;
+    R.pair = g / cph;
+    R.k = g - R.pair * cph;
+    R.ha = parity == 0 ? 2 * R.pair : 2 * R.pair + 1;
+    R.hb = parity == 0 ? 2 * R.pair + 1 : (2 * R.pair + 2) % H;
+    R.ca = 2 * cpt + R.ha * cph + R.k;
+    R.cb = 2 * cpt + R.hb * cph + R.k;
+  }
+  return R;
 }
 
 template <typename T>
-__global__ void __launch_bounds__(kRopeMaxCh) rope_givens_fwd_stream_kernel(const RopeParams p) {
+__global__ void __launch_bounds__(kRopeMaxThreads) rope_givens_fwd_stream_kernel(const RopeParams p, int NS) {
   using E = Elem<T>;
   constexpr int EPC = 16 / sizeof(T);
-  extern __shared__ float rope_tab[];  // [kRopeR][D/2] cos, then [kRopeR][D/2] sin
+  extern __shared__ float rope_tab[];  // [NS kRopeNR][D/2] cos, then sin
   const int tid = threadIdx.x;
-  const int H = p.H, D = p.D, half = D / 2, npair = H / 2;
-  const int nch = 3 * H * D / EPC;
+  const int H = p.H, D = p.D, half = D / 2, npair = H / 2, cph = D / EPC, hch = cph / 2;
+  const int U = 3 * H * cph / 2, rpb = NS * kRopeNR;
   const int rows = p.B * p.T;
-  const int row0 = blockIdx.x * kRopeR;
-  const int nrow = min(kRopeR, rows - row0);
-  const int ntab = kRopeR * half;
+  const int row0 = blockIdx.x * rpb;
+  const int nrow = min(rpb, rows - row0);
   float* tc = rope_tab;
-  float* ts = rope_tab + ntab;
-  const RopeLane L = rope_lane(min(tid, nch - 1), H, D, EPC, p.parity);
+  float* ts = rope_tab + rpb * half;
+  const bool act = tid < NS * U;
+  const int slot = act ? tid / U : 0;
+  const RopeUnit R = rope_unit(act ? tid - slot * U : 0, H, cph, p.parity);
 
   // table values first (indices by multiplication with the 0/1 flags: a select becomes a branch)
-  const float invk = p.inv_safe[min(tid, half - 1) * p.rope];
-  const float th = p.theta_safe[min(L.pair, npair - 1) * p.givens];
-  Chunk xv[kRopeR], pv[kRopeR];
+  const RopeInv inv2 = rope_inv(p.inv_safe, p.rope, half);
+  const float th = p.theta_safe[min(R.pair, npair - 1) * p.givens];
+  Chunk xa[kRopeNR], xb[kRopeNR];
   const T* q = reinterpret_cast<const T*>(p.qkv);
 #pragma unroll
-  for (int r = 0; r < kRopeR; ++r) {
-    const int row = row0 + min(r, nrow - 1), b = row / p.T, t = row - b * p.T;
+  for (int r = 0; r < kRopeNR; ++r) {
+    const int row = row0 + min(NS * r + slot, nrow - 1), b = row / p.T, t = row - b * p.T;
     const T* base = q + int64_t(b) * p.qkv_sb + int64_t(t) * p.qkv_sr;
-    xv[r] = load_chunk(base + min(tid, nch - 1) * EPC);
-    pv[r] = load_chunk(base + L.pc * EPC);
+    xa[r] = load_chunk(base + R.ca * EPC);
+    xb[r] = load_chunk(base + R.cb * EPC);
   }
-  // the RoPE factors of the block's rows and the Givens factor of the thread's pair
-  rope_factors<T, kRopeR>(invk, p.rope, p.pos0, row0, nrow, p.T, half, tc, ts);
+  rope_factors<T>(inv2, p.inv_safe, p.rope, p.pos0, row0, rpb, nrow, p.T, half, tc, ts);
   float gsn, gcs;
   sincosf(th, &gsn, &gcs);
   const float gc = p.givens ? rnd<T>(gcs) : 1.f, gs = p.givens ? rnd<T>(gsn) : 0.f;
   __syncthreads();
-  if (tid >= nch) return;
+  if (!act) return;
 
-  // out = x C + y S with, per element: RoPE first half C = c, S = -s; second half C = c, S = s;
-  // Givens first member C = c, S = -s (out_a = c a - s b); second C = c, S = s (out_b = s a + c b)
-  const bool rope_part = L.which < 2;
-  const float sgn = rope_part ? (L.lo ? -1.f : 1.f) : (L.first ? -1.f : 1.f);
+  // RoPE: out_k = x_k c - x_{k+D/2} s, out_{k+D/2} = x_{k+D/2} c + x_k s; Givens: out_a = c a - s b,
+  // out_b = s a + c b
+  const bool rope_part = R.which < 2;
   T* obase;
-  int64_t osb, osr;
-  if (L.which == 0) {
-    obase = reinterpret_cast<T*>(p.o1) + int64_t(L.hd) * p.o1_sh;
-    osb = p.o1_sb;
-    osr = p.o1_sr;
-  } else if (L.which == 1) {
-    obase = reinterpret_cast<T*>(p.o2) + int64_t(L.hd) * p.o2_sh;
-    osb = p.o2_sb;
-    osr = p.o2_sr;
+  int64_t osb, osh, osr;
+  if (R.which == 0) {
+    obase = reinterpret_cast<T*>(p.o1); osb = p.o1_sb; osh = p.o1_sh; osr = p.o1_sr;
+  } else if (R.which == 1) {
+    obase = reinterpret_cast<T*>(p.o2); osb = p.o2_sb; osh = p.o2_sh; osr = p.o2_sr;
   } else {
-    obase = reinterpret_cast<T*>(p.o3) + int64_t(L.hd) * p.o3_sh;
-    osb = p.o3_sb;
-    osr = p.o3_sr;
+    obase = reinterpret_cast<T*>(p.o3); osb = p.o3_sb; osh = p.o3_sh; osr = p.o3_sr;
   }
-  obase += L.k * EPC;
+  T* oa = obase + int64_t(R.ha) * osh + R.k * EPC;
+  T* ob = rope_part ? oa + hch * EPC : obase + int64_t(R.hb) * osh + R.k * EPC;
+  const int a0 = R.k * EPC;  // RoPE factor index of the chunk's first element
 #pragma unroll
-  for (int r = 0; r < kRopeR; ++r) {
-    if (r >= nrow) break;
-    const int row = row0 + r, b = row / p.T, t = row - b * p.T;
-    const T* ex = reinterpret_cast<const T*>(&xv[r]);
-    const T* ey = reinterpret_cast<const T*>(&pv[r]);
-    Chunk out;
-    T* eo = reinterpret_cast<T*>(&out);
+  for (int r = 0; r < kRopeNR; ++r) {
+    const int rr = NS * r + slot;
+    if (rr >= nrow) break;
+    const int row = row0 + rr, b = row / p.T, t = row - b * p.T;
+    const T* ea = reinterpret_cast<const T*>(&xa[r]);
+    const T* eb = reinterpret_cast<const T*>(&xb[r]);
+    Chunk outa, outb;
+    T* ya = reinterpret_cast<T*>(&outa);
+    T* yb = reinterpret_cast<T*>(&outb);
 #pragma unroll
     for (int e = 0; e < EPC; ++e) {
-      const float C = rope_part ? tc[r * half + L.a0 + e] : gc;
-      const float S = sgn * (rope_part ? ts[r * half + L.a0 + e] : gs);
-      eo[e] = E::from_f(rot_round<T>(E::to_f(ex[e]), C, E::to_f(ey[e]), S));
+      const float C = rope_part ? tc[rr * half + a0 + e] : gc;
+      const float S = rope_part ? ts[rr * half + a0 + e] : gs;
+      const float va = E::to_f(ea[e]), vb = E::to_f(eb[e]);
+      ya[e] = E::from_f(rot_round<T>(va, C, vb, -S));
+      yb[e] = E::from_f(rot_round<T>(vb, C, va, S));
     }
-    store_chunk(obase + int64_t(b) * osb + int64_t(t) * osr, out);
+    const int64_t off = int64_t(b) * osb + int64_t(t) * osr;
+    store_chunk(oa + off, outa);
+    store_chunk(ob + off, outb);
   }
 }
 
 template <typename T>
-__global__ void __launch_bounds__(kRopeMaxCh) rope_givens_bwd_stream_kernel(const RopeBwdParams p) {
+__global__ void __launch_bounds__(kRopeMaxThreads) rope_givens_bwd_stream_kernel(const RopeBwdParams p, int NS) {
   using E = Elem<T>;
   constexpr int EPC = 16 / sizeof(T);
-  extern __shared__ float rope_tab[];  // [kRopeRB][D/2] cos, [kRopeRB][D/2] sin, [chunks] d theta
+  extern __shared__ float rope_tab[];  // [NS kRopeNR][D/2] cos, sin, then [threads] d theta
   const int tid = threadIdx.x;
-  const int H = p.H, D = p.D, half = D / 2, npair = H / 2;
-  const int cph = D / EPC, cpt = H * cph, nch = 3 * cpt;
+  const int H = p.H, D = p.D, half = D / 2, npair = H / 2, cph = D / EPC, hch = cph / 2;
+  const int U = 3 * H * cph / 2, rpb = NS * kRopeNR, ur = 2 * H * hch;
   const int rows = p.B * p.T;
-  const int row0 = blockIdx.x * kRopeRB;
-  const int nrow = min(kRopeRB, rows - row0);
-  const int ntab = kRopeRB * half;
+  const int row0 = blockIdx.x * rpb;
+  const int nrow = min(rpb, rows - row0);
   float* tc = rope_tab;
-  float* ts = rope_tab + ntab;
-  float* red = rope_tab + 2 * ntab;
-  const RopeLane L = rope_lane(min(tid, nch - 1), H, D, EPC, p.parity);
+  float* ts = rope_tab + rpb * half;
+  float* red = rope_tab + 2 * rpb * half;
+  const bool act = tid < NS * U;
+  const int slot = act ? tid / U : 0;
+  const int u = act ? tid - slot * U : 0;
+  const RopeUnit R = rope_unit(u, H, cph, p.parity);
 
-  const float invk = p.inv_safe[min(tid, half - 1) * p.rope];
-  const float th = p.theta_safe[min(L.pair, npair - 1) * p.givens];
-  // gradient chunks: the thread's own and its partner's, from the view of its tensor
+  const RopeInv inv2 = rope_inv(p.inv_safe, p.rope, half);
+  const float th = p.theta_safe[min(R.pair, npair - 1) * p.givens];
+  // gradient chunks of the unit, from the view of its tensor
   const T* gb;
   int64_t gsb, gsh, gsr;
-  if (L.which == 0) {
+  if (R.which == 0) {
     gb = reinterpret_cast<const T*>(p.g1); gsb = p.g1_sb; gsh = p.g1_sh; gsr = p.g1_sr;
-  } else if (L.which == 1) {
+  } else if (R.which == 1) {
     gb = reinterpret_cast<const T*>(p.g2); gsb = p.g2_sb; gsh = p.g2_sh; gsr = p.g2_sr;
   } else {
     gb = reinterpret_cast<const T*>(p.g3); gsb = p.g3_sb; gsh = p.g3_sh; gsr = p.g3_sr;
   }
-  const int hch = cph / 2;
-  const T* gself = gb + int64_t(L.hd) * gsh + L.k * EPC;
-  const T* gpart = L.which < 2 ? gself + (L.lo ? hch : -hch) * EPC : gb + int64_t(L.other) * gsh + L.k * EPC;
-  // I~ inputs of the pair (for d theta): every thread loads two chunks of the I~ part of qkv (those
-  // of p1 / p2 threads repeat an I~ thread's lines), so no load sits under a condition
-  const int xa = L.which == 2 ? L.hd : L.hd % H, xb = L.which == 2 ? L.other : L.hd % H;
-  const T* xq = reinterpret_cast<const T*>(p.qkv) + p.ioff + L.k * EPC;
-  Chunk g0[kRopeRB], g1[kRopeRB], x0[kRopeRB], x1[kRopeRB];
+  const T* gpa = gb + int64_t(R.ha) * gsh + R.k * EPC;
+  const T* gpb = R.which < 2 ? gpa + hch * EPC : gb + int64_t(R.hb) * gsh + R.k * EPC;
+  // the pair's I~ inputs (for d theta); RoPE units load their head's I~ chunk instead, so that no
+  // load sits under a lane condition
+  const T* xq = reinterpret_cast<const T*>(p.qkv) + p.ioff + (R.k % cph) * EPC;
+  Chunk g0[kRopeNR], g1[kRopeNR], x0[kRopeNR], x1[kRopeNR];
 #pragma unroll
-  for (int r = 0; r < kRopeRB; ++r) {
-    const int row = row0 + min(r, nrow - 1), b = row / p.T, t = row - b * p.T;
+  for (int r = 0; r < kRopeNR; ++r) {
+    const int row = row0 + min(NS * r + slot, nrow - 1), b = row / p.T, t = row - b * p.T;
     const int64_t go = int64_t(b) * gsb + int64_t(t) * gsr;
-    g0[r] = load_chunk(gself + go);
-    g1[r] = load_chunk(gpart + go);
+    g0[r] = load_chunk(gpa + go);
+    g1[r] = load_chunk(gpb + go);
     const T* xr = xq + int64_t(b) * p.qkv_sb + int64_t(t) * p.qkv_sr;
-    x0[r] = load_chunk(xr + xa * D);
-    x1[r] = load_chunk(xr + xb * D);
+    x0[r] = load_chunk(xr + R.ha * D);
+    x1[r] = load_chunk(xr + R.hb * D);
   }
-  rope_factors<T, kRopeRB>(invk, p.rope, p.pos0, row0, nrow, p.T, half, tc, ts);
+  rope_factors<T>(inv2, p.inv_safe, p.rope, p.pos0, row0, rpb, nrow, p.T, half, tc, ts);
   float gsn, gcs;
   sincosf(th, &gsn, &gcs);
-  const float ce = p.givens ? gcs : 1.f, se = p.givens ? gsn : 0.f;     // exact: the derivative
+  const float ce = p.givens ? gcs : 1.f, se = p.givens ? gsn : 0.f;                  // exact: the derivative
   const float cr = p.givens ? rnd<T>(gcs) : 1.f, sr = p.givens ? rnd<T>(gsn) : 0.f;  // applied rotation
   __syncthreads();
 
-  // dx = g C + g' S: RoPE^T first half C = c, S = s (dx_k = d_k c + d_{k+h} s), second half
-  // C = c, S = -s (dx_{k+h} = d_{k+h} c - d_k s); Givens^T first member C = c, S = s
-  // (da = c ga + s gb), second C = c, S = -s (db = c gb - s ga)
-  const bool act = tid < nch;
-  const bool rope_part = L.which < 2;
-  const float sgn = rope_part ? (L.lo ? 1.f : -1.f) : (L.first ? 1.f : -1.f);
-  const bool dth_lane = act && !rope_part && L.first && p.givens;
-  T* dbase = reinterpret_cast<T*>(p.dqkv) + min(tid, nch - 1) * EPC;
+  // RoPE^T: dx_k = d_k c + d_{k+D/2} s, dx_{k+D/2} = d_{k+D/2} c - d_k s; Givens^T: da = c ga + s gb,
+  // db = c gb - s ga
+  const bool rope_part = R.which < 2;
+  const bool dth_unit = act && !rope_part && p.givens;
+  T* da_out = reinterpret_cast<T*>(p.dqkv) + R.ca * EPC;
+  T* db_out = reinterpret_cast<T*>(p.dqkv) + R.cb * EPC;
+  const int a0 = R.k * EPC;
   float acc = 0.f;
 #pragma unroll
-  for (int r = 0; r < kRopeRB; ++r) {
-    if (r >= nrow) break;
-    const int row = row0 + r, b = row / p.T, t = row - b * p.T;
+  for (int r = 0; r < kRopeNR; ++r) {
+    const int rr = NS * r + slot;
+    if (rr >= nrow) break;
+    const int row = row0 + rr, b = row / p.T, t = row - b * p.T;
     const T* e0 = reinterpret_cast<const T*>(&g0[r]);
     const T* e1 = reinterpret_cast<const T*>(&g1[r]);
-    Chunk out;
-    T* eo = reinterpret_cast<T*>(&out);
+    Chunk outa, outb;
+    T* ya = reinterpret_cast<T*>(&outa);
+    T* yb = reinterpret_cast<T*>(&outb);
 #pragma unroll
     for (int e = 0; e < EPC; ++e) {
-      const float C = rope_part ? tc[r * half + L.a0 + e] : cr;
-      const float S = sgn * (rope_part ? ts[r * half + L.a0 + e] : sr);
-      eo[e] = E::from_f(E::to_f(e0[e]) * C + E::to_f(e1[e]) * S);
+      const float C = rope_part ? tc[rr * half + a0 + e] : cr;
+      const float S = rope_part ? ts[rr * half + a0 + e] : sr;
+      const float ga = E::to_f(e0[e]), gbv = E::to_f(e1[e]);
+      ya[e] = E::from_f(ga * C + gbv * S);
+      yb[e] = E::from_f(gbv * C + ga * -S);
     }
-    if (act) store_chunk(dbase + int64_t(b) * p.dq_sb + int64_t(t) * p.dq_sr, out);
-    if (dth_lane) {
-      // d theta of the pair from its first member: ga (-s a - c b) + gb (c a - s b), exact s, c
+    if (act) {
+      const int64_t off = int64_t(b) * p.dq_sb + int64_t(t) * p.dq_sr;
+      store_chunk(da_out + off, outa);
+      store_chunk(db_out + off, outb);
+    }
+    if (dth_unit) {
+      // d theta of the pair: ga (-s a - c b) + gb (c a - s b), exact s, c
       const T* ea = reinterpret_cast<const T*>(&x0[r]);
       const T* eb = reinterpret_cast<const T*>(&x1[r]);
 #pragma unroll
@@ -441,13 +472,13 @@ __global__ void __launch_bounds__(kRopeMaxCh) rope_givens_bwd_stream_kernel(cons
     }
   }
   if (!p.givens) return;
-  // per pair: the first member's chunks in a fixed order (one partial per block)
-  if (act) red[tid] = acc;
+  // one partial per block and pair: the pair's units in a fixed order (slot, then chunk)
+  red[tid] = dth_unit ? acc : 0.f;
   __syncthreads();
   for (int pr = tid; pr < npair; pr += blockDim.x) {
-    const int ha = p.parity == 0 ? 2 * pr : 2 * pr + 1;
     float s2 = 0.f;
-    for (int k = 0; k < cph; ++k) s2 += red[2 * cpt + ha * cph + k];
+    for (int sl = 0; sl < NS; ++sl)
+      for (int k = 0; k < cph; ++k) s2 += red[sl * U + ur + pr * cph + k];
     p.partial[int64_t(blockIdx.x) * npair + pr] = s2;
   }
 }
@@ -470,6 +501,17 @@ static bool aligned16_bwd(const mote_rope_givens_bwd_args* a) {
          al16(a->dp1.data, a->dp1.stride_b, a->dp1.stride_h, a->dp1.stride_r, es) &&
          al16(a->dp2.data, a->dp2.stride_b, a->dp2.stride_h, a->dp2.stride_r, es) &&
          al16(a->dinfo.data, a->dinfo.stride_b, a->dinfo.stride_h, a->dinfo.stride_r, es);
+}
+
+// Streaming kernels' shape: chunks of EPC elements that split each head in halves, units per row
+// (3 H cph / 2) and row slots per block. One slot: measured at the Mote-96M shape (bf16, 144 units),
+// two slots of four rows ran the forward 4 % and the backward 40 % slower than one (more RoPE
+// factors per block, fewer blocks in flight).
+static bool stream_shape(int H, int D, int epc, int& units, int& NS) {
+  if (D % (2 * epc) != 0) return false;
+  units = 3 * H * (D / epc) / 2;
+  NS = 1;
+  return units <= kRopeMaxThreads;
 }
 
 static int check_rope_common(int dtype, int B, int T, int H, int D, const void* qkv) {
@@ -498,16 +540,16 @@ int launch_rope_givens_fwd(const mote_rope_givens_args* a, hipStream_t stream) {
   p.B = a->B; p.T = a->T; p.H = a->H; p.D = a->D; p.pos0 = a->pos0; p.parity = a->layer_parity & 1;
   const int rows = a->B * a->T;
   const int epc = a->dtype == MOTE_BF16 ? 8 : 4;
-  const int nch = 3 * a->H * a->D / epc;
-  const bool vec = (a->D / 2) % epc == 0 && a->D % epc == 0 && nch <= kRopeMaxCh && aligned16(a);
+  int units, NS;
+  const bool vec = stream_shape(a->H, a->D, epc, units, NS) && aligned16(a);
   if (vec) {
-    const int blocks = (rows + kRopeR - 1) / kRopeR;
-    const int threads = (nch + 63) / 64 * 64;
-    const size_t lds = size_t(2) * kRopeR * (a->D / 2) * sizeof(float);
+    const int blocks = (rows + NS * kRopeNR - 1) / (NS * kRopeNR);
+    const int threads = (NS * units + 63) / 64 * 64;
+    const size_t lds = size_t(2) * NS * kRopeNR * (a->D / 2) * sizeof(float);
     if (a->dtype == MOTE_BF16)
-      hipLaunchKernelGGL(rope_givens_fwd_stream_kernel<bf16_t>, dim3(blocks), dim3(threads), lds, stream, p);
+      hipLaunchKernelGGL(rope_givens_fwd_stream_kernel<bf16_t>, dim3(blocks), dim3(threads), lds, stream, p, NS);
     else
-      hipLaunchKernelGGL(rope_givens_fwd_stream_kernel<float>, dim3(blocks), dim3(threads), lds, stream, p);
+      hipLaunchKernelGGL(rope_givens_fwd_stream_kernel<float>, dim3(blocks), dim3(threads), lds, stream, p, NS);
   } else if (a->dtype == MOTE_BF16) {
     hipLaunchKernelGGL(rope_givens_fwd_kernel<bf16_t>, dim3(rows), dim3(256), 0, stream, p);
   } else {
@@ -545,16 +587,16 @@ int launch_rope_givens_bwd(const mote_rope_givens_bwd_args* a, hipStream_t strea
   p.B = a->B; p.T = a->T; p.H = a->H; p.D = a->D; p.pos0 = a->pos0; p.parity = a->layer_parity & 1;
   const int rows = a->B * a->T;
   const int epc = a->dtype == MOTE_BF16 ? 8 : 4;
-  const int nch = 3 * a->H * a->D / epc;
-  const bool vec = (a->D / 2) % epc == 0 && a->D % epc == 0 && nch <= kRopeMaxCh && aligned16_bwd(a);
-  const int blocks = vec ? (rows + kRopeRB - 1) / kRopeRB : rows;
+  int units, NS;
+  const bool vec = stream_shape(a->H, a->D, epc, units, NS) && aligned16_bwd(a);
+  const int blocks = vec ? (rows + NS * kRopeNR - 1) / (NS * kRopeNR) : rows;
   if (vec) {
-    const int threads = (nch + 63) / 64 * 64;
-    const size_t lds = (size_t(2) * kRopeRB * (a->D / 2) + size_t(nch)) * sizeof(float);
+    const int threads = (NS * units + 63) / 64 * 64;
+    const size_t lds = (size_t(2) * NS * kRopeNR * (a->D / 2) + size_t(threads)) * sizeof(float);
     if (a->dtype == MOTE_BF16)
-      hipLaunchKernelGGL(rope_givens_bwd_stream_kernel<bf16_t>, dim3(blocks), dim3(threads), lds, stream, p);
+      hipLaunchKernelGGL(rope_givens_bwd_stream_kernel<bf16_t>, dim3(blocks), dim3(threads), lds, stream, p, NS);
     else
-      hipLaunchKernelGGL(rope_givens_bwd_stream_kernel<float>, dim3(blocks), dim3(threads), lds, stream, p);
+      hipLaunchKernelGGL(rope_givens_bwd_stream_kernel<float>, dim3(blocks), dim3(threads), lds, stream, p, NS);
   } else if (a->dtype == MOTE_BF16) {
     hipLaunchKernelGGL(rope_givens_bwd_kernel<bf16_t>, dim3(rows), dim3(256), 0, stream, p);
   } else {
