@@ -404,13 +404,28 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
 #pragma unroll
     for (int s = 0; s < 2; ++s) dqacc[dt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // The Self term's inputs, dU_ii and the P2 row of each of the thread's (query, 8-column chunk)
+  // items, loaded before the key loop: their latency passes under it instead of after it. Rows past
+  // TQ load row TQ - 1 (not stored).
+  constexpr int NIT = 64 * CPR / 256;
+  static_assert(64 * CPR % 256 == 0, "whole (query, chunk) items per thread");
+  float us_pre[NIT];
+  Frag k8_pre[NIT];
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int item = tid + 256 * it;
+    const int i = min(i0 + item / CPR, p.TQ - 1);
+    us_pre[it] = p.duii[int64_t(bh) * p.TQp + i];
+    k8_pre[it] = E::load8(kbase + int64_t(p.q_start + i) * p.k_sr + (item % CPR) * 8);
+  }
+
   const bf16_t* srcs[1] = {kbase};
   const int64_t strides[1] = {p.k_sr};
   TileStager<DP, 4, 1> st;
   st.init(wave, lane, strides);
-  // Block kb: P2 rows and the wave's fragments into ring slot kb % NS. Every step issues one block
-  // and waits for one, the same count each time (blocks past the end reload the last block's
-  // addresses), so the wait before a read is always "all but the two newest blocks".
+  // Block kb: P2 rows and the wave's fragments into ring slot kb % NS, issued NS - 1 steps ahead;
+  // blocks past the end are not issued. The wait before block kb's reads leaves in flight the later
+  // blocks already issued: NS - 2 of them, fewer in the last steps.
   auto issue = [&](int kb, auto u) {
     const int kc = min(kb, nkb - 1);
     bf16_t* dst = slot(u);
@@ -421,26 +436,29 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
   static_assert(NS == 4, "four ring slots");
   auto step = [&](int kb, auto u) {
     constexpr int U = decltype(u)::value;
-    __builtin_amdgcn_s_waitcnt(kVmWaitStage<(NS - 2) * VMS>());  // this wave's part of block kb is in
+    if (kb >= nkb) return;  // uniform over the workgroup: every wave skips the same steps
+    // this wave's part of block kb is in (blocks issued after it may still be in flight)
+    const int later = nkb - 1 - kb;
+    if (later >= NS - 2) __builtin_amdgcn_s_waitcnt(kVmWaitStage<(NS - 2) * VMS>());
+    else if (later == 1) __builtin_amdgcn_s_waitcnt(kVmWaitStage<VMS>());
+    else __builtin_amdgcn_s_waitcnt(kVmWaitStage<0>());
     lds_barrier();  // every wave's part of block kb is in; every wave is done with block kb - 1's slot
-    issue(kb + NS - 1, std::integral_constant<int, (U + NS - 1) % NS>{});
-    if (kb < nkb) {
-      const bf16_t* Ks = slot(u);
-      Frag bf[2];
+    if (kb + NS - 1 < nkb) issue(kb + NS - 1, std::integral_constant<int, (U + NS - 1) % NS>{});
+    const bf16_t* Ks = slot(u);
+    Frag bf[2];
 #pragma unroll
-      for (int s = 0; s < 2; ++s) bf[s] = E::load8(Ks + TILE + fo + s * 512 + lane * 8);
+    for (int s = 0; s < 2; ++s) bf[s] = E::load8(Ks + TILE + fo + s * 512 + lane * 8);
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const Frag ak = tile_tr_frag<DP>(Ks, 32 * kh, dt, li, lg);
+    for (int dt = 0; dt < DT; ++dt) {
+      const Frag ak = tile_tr_frag<DP>(Ks, 32 * kh, dt, li, lg);
 #pragma unroll
-        for (int s = 0; s < 2; ++s) dqacc[dt][s] = E::mma(ak, bf[s], dqacc[dt][s]);
-      }
+      for (int s = 0; s < 2; ++s) dqacc[dt][s] = E::mma(ak, bf[s], dqacc[dt][s]);
     }
   };
   if (nkb > 0) {
     issue(0, std::integral_constant<int, 0>{});
-    issue(1, std::integral_constant<int, 1>{});
-    issue(2, std::integral_constant<int, 2>{});
+    if (nkb > 1) issue(1, std::integral_constant<int, 1>{});
+    if (nkb > 2) issue(2, std::integral_constant<int, 2>{});
     for (int kb0 = 0; kb0 < nkb; kb0 += NS) {
       step(kb0, std::integral_constant<int, 0>{});
       step(kb0 + 1, std::integral_constant<int, 1>{});
@@ -457,8 +475,7 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
   auto rptr = [&](int row, int col) -> float* {
     return col < HALF ? R0 + row * RS + col : R1 + row * RS + (col - HALF);
   };
-  __builtin_amdgcn_s_waitcnt(0);  // the last (past-the-end) prefetches into slots 0 and 1 have landed
-  __syncthreads();
+  __syncthreads();  // every wave is done reading slots 0 and 1 (the last step waited for every transfer)
   if (kh == 1) {
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
@@ -482,12 +499,14 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
   __syncthreads();
   // Self part dU_ii P2_i, scale, 16-byte stores
   bf16_t* dqout = reinterpret_cast<bf16_t*>(p.dp1) + b * p.dq_sb + h * p.dq_sh;
-  for (int item = tid; item < 64 * CPR; item += 256) {
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int item = tid + 256 * it;
     const int row = item / CPR, d0 = (item % CPR) * 8;
     const int i = i0 + row;
     if (i >= p.TQ) continue;
-    const float us = p.duii[int64_t(bh) * p.TQp + i];
-    const Frag k8 = E::load8(kbase + int64_t(p.q_start + i) * p.k_sr + d0);
+    const float us = us_pre[it];
+    const Frag k8 = k8_pre[it];
     float o[8];
 #pragma unroll
     for (int e = 0; e < 8; e += 4) {
