@@ -233,7 +233,9 @@ __global__ void __launch_bounds__(256) sum_partials_kernel(const float* partial,
 // U = 3 H cph / 2 units (cph chunks per head). A block has NS row slots of U threads and takes
 // kRopeNR rows per slot (rows row0 + NS r + slot), so each thread keeps 2 kRopeNR chunk loads in
 // flight; all of them are issued before any math (the table values first: loads complete in order),
-// the RoPE factors of the block's rows go through LDS, and the only barrier waits for them.
+// the RoPE factors of the block's rows and the Givens factors go through LDS, and the only barrier
+// waits for them. Every unit reads its factors the same way (16-byte LDS reads, a per-lane base and
+// row stride), so waves that hold both RoPE and Givens units run one instruction stream.
 // ------------------------------------------------------------------------------------------------
 constexpr int kRopeNR = 4;
 constexpr int kRopeMaxThreads = 1024;
@@ -243,22 +245,32 @@ constexpr int kRopeMaxThreads = 1024;
 // a large angle (positions in the thousands) takes the long argument reduction, so the entries are
 // spread over the whole block rather than left to D/2 threads. The inverse frequencies of a thread's
 // first two entries (`inv2`) are loaded before the chunk loads, so the sincos runs while they arrive.
+// n / d for 0 <= n < 2^21 and d >= 1, given rd = rcp(d) (within 1 ulp): (n + 1/2) / d lies at least
+// 1 / (2 d) from every integer, farther than the relative error (under 2^-22) moves it, so the
+// truncation is floor(n / d). A few instructions where an integer division by a runtime value takes
+// about twenty.
+__device__ __forceinline__ int small_div(int n, float rd) { return int((float(n) + 0.5f) * rd); }
+
 struct RopeInv {
   float v[2];
 };
 __device__ __forceinline__ RopeInv rope_inv(const float* inv_safe, int rope, int half) {
+  const float rh = frcp(float(half));
+  const int i0 = threadIdx.x, i1 = threadIdx.x + blockDim.x;
   RopeInv R;
-  R.v[0] = inv_safe[(threadIdx.x % half) * rope];
-  R.v[1] = inv_safe[((threadIdx.x + blockDim.x) % half) * rope];
+  R.v[0] = inv_safe[(i0 - small_div(i0, rh) * half) * rope];
+  R.v[1] = inv_safe[(i1 - small_div(i1, rh) * half) * rope];
   return R;
 }
+// Factors of positions pos0 + t0 + r, r < nr (rows past nrow repeat the last one).
 template <typename T>
-__device__ __forceinline__ void rope_factors(const RopeInv& inv2, const float* inv_safe, int rope, int pos0, int row0,
-                                             int nr, int nrow, int T_, int half, float* tc, float* ts) {
+__device__ __forceinline__ void rope_factors(const RopeInv& inv2, const float* inv_safe, int rope, int pos0, int t0,
+                                             int nr, int nrow, int half, float* tc, float* ts) {
+  const float rh = frcp(float(half));
   int j = 0;
   for (int i = threadIdx.x; i < nr * half; i += blockDim.x, ++j) {
-    const int r = i / half, k = i - r * half;
-    const int t = (row0 + min(r, nrow - 1)) % T_;
+    const int r = small_div(i, rh), k = i - r * half;
+    const int t = t0 + min(r, nrow - 1);
     const float invk = j == 0 ? inv2.v[0] : j == 1 ? inv2.v[1] : inv_safe[k * rope];
     float sn, cs;
     sincosf((float)(pos0 + t) * invk, &sn, &cs);
@@ -275,63 +287,173 @@ __device__ __forceinline__ void rope_factors(const RopeInv& inv2, const float* i
 struct RopeUnit {
   int which, ha, hb, k, pair, ca, cb;
 };
+// Without branches: a wave can hold units of both kinds.
 __device__ __forceinline__ RopeUnit rope_unit(int u, int H, int cph, int parity) {
   RopeUnit R;
   const int hch = cph / 2, ur = 2 * H * hch, cpt = H * cph;
-  if (u < ur) {
-    R.which = u / (H * hch);
-    const int rem = u - R.which * H * hch;
-    R.ha = R.hb = rem / hch;
-    R.k = rem - R.ha * hch;
-    R.pair = 0;
-    R.ca = R.which * cpt + R.ha * cph + R.k;
-    R.cb = R.ca + hch;
-  } else {
-    const int g = u - ur;
-    R.which = 2;
-    R.pair = g / cph;
-    R.k = g - R.pair * cph;
-    R.ha = parity == 0 ? 2 * R.pair : 2 * R.pair + 1;
-    R.hb = parity == 0 ? 2 * R.pair + 1 : (2 * R.pair + 2) % H;
-    R.ca = 2 * cpt + R.ha * cph + R.k;
-    R.cb = 2 * cpt + R.hb * cph + R.k;
-  }
+  const bool rope_part = u < ur;
+  // RoPE: u = (which H + head) hch + k; Givens: u - ur = pair cph + k
+  const int v = rope_part ? u : u - ur;
+  const int dv = rope_part ? hch : cph;
+  const int hu = small_div(v, frcp(float(dv)));
+  R.k = v - hu * dv;
+  const int which = hu >= H ? 1 : 0;
+  const int head = hu - which * H;
+  R.which = rope_part ? which : 2;
+  R.pair = rope_part ? 0 : hu;
+  const int ga = parity == 0 ? 2 * hu : 2 * hu + 1;
+  const int gb = parity == 0 ? 2 * hu + 1 : (2 * hu + 2 == H ? 0 : 2 * hu + 2);
+  R.ha = rope_part ? head : ga;
+  R.hb = rope_part ? head : gb;
+  R.ca = rope_part ? which * cpt + head * cph + R.k : 2 * cpt + ga * cph + R.k;
+  R.cb = rope_part ? R.ca + hch : 2 * cpt + gb * cph + R.k;
   return R;
+}
+
+// The Givens factors of the block's layer, EPC copies per pair, so that a Givens unit reads its chunk's
+// factors the way a RoPE unit does (a factor row of stride 0): rounded cos, rounded sin, and for the
+// backward the exact values [npair] cos, [npair] sin (d theta). `th` is the thread's theta, loaded
+// before the chunk loads; the launcher keeps npair * EPC within the block.
+template <typename T, int EPC>
+__device__ __forceinline__ void givens_factors(float th, int givens, int npair, float* gc, float* gs, float* ge) {
+  const int i = threadIdx.x;
+  if (i < npair * EPC) {
+    float sn, cs;
+    sincosf(th, &sn, &cs);
+    gc[i] = givens ? rnd<T>(cs) : 1.f;
+    gs[i] = givens ? rnd<T>(sn) : 0.f;
+    if (ge && i % EPC == 0) {
+      ge[i / EPC] = givens ? cs : 1.f;
+      ge[npair + i / EPC] = givens ? sn : 0.f;
+    }
+  }
+}
+
+// A unit's rotation factors: RoPE units read row rr of the block's table at their chunk, Givens units
+// their pair's copies (row stride 0). Offsets in floats from the table's start; sin at + soff.
+struct UnitFactors {
+  int c0, stride, soff;
+};
+__device__ __forceinline__ UnitFactors unit_factors(const RopeUnit& R, int rpb, int half, int npair, int epc) {
+  UnitFactors F;
+  const bool rope_part = R.which < 2;
+  const int gbase = 2 * rpb * half;  // the Givens copies follow the RoPE table
+  F.c0 = rope_part ? R.k * epc : gbase + min(R.pair, npair - 1) * epc;
+  F.stride = rope_part ? half : 0;
+  F.soff = rope_part ? rpb * half : npair * epc;
+  return F;
+}
+
+template <int EPC>
+__device__ __forceinline__ void read_factors(const float* tab, const UnitFactors& F, int rr, float (&C)[EPC], float (&S)[EPC]) {
+  const float* c = tab + F.c0 + rr * F.stride;
+#pragma unroll
+  for (int q = 0; q < EPC / 4; ++q) {
+    const float4 cv = *reinterpret_cast<const float4*>(c + 4 * q);
+    const float4 sv = *reinterpret_cast<const float4*>(c + F.soff + 4 * q);
+    C[4 * q] = cv.x; C[4 * q + 1] = cv.y; C[4 * q + 2] = cv.z; C[4 * q + 3] = cv.w;
+    S[4 * q] = sv.x; S[4 * q + 1] = sv.y; S[4 * q + 2] = sv.z; S[4 * q + 3] = sv.w;
+  }
+}
+
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+
+// Two fp32 values as two bf16 in one word (lo = a), one v_cvt_pk_bf16_f32 for both.
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
+__device__ __forceinline__ float bf_lo(uint32_t u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
+
+// Forward rotation of a chunk pair with the element type's rounding points (rot_round):
+// out_a = x_a C - x_b S, out_b = x_b C + x_a S, every product and the sum rounded to T. For bf16 the
+// roundings of element pairs share one conversion.
+template <typename T, int EPC>
+__device__ __forceinline__ void rot_chunks(const Chunk& xa, const Chunk& xb, const float (&C)[EPC], const float (&S)[EPC],
+                                           Chunk& oa, Chunk& ob) {
+#pragma clang fp contract(off)
+  if constexpr (sizeof(T) == 2) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float a0 = bf_lo(xa.w[w]), a1 = bf_hi(xa.w[w]), b0 = bf_lo(xb.w[w]), b1 = bf_hi(xb.w[w]);
+      const float c0 = C[2 * w], c1 = C[2 * w + 1], s0 = S[2 * w], s1 = S[2 * w + 1];
+      const uint32_t ac = pack_bf16(a0 * c0, a1 * c1), bs = pack_bf16(b0 * -s0, b1 * -s1);
+      const uint32_t bc = pack_bf16(b0 * c0, b1 * c1), as = pack_bf16(a0 * s0, a1 * s1);
+      oa.w[w] = pack_bf16(bf_lo(ac) + bf_lo(bs), bf_hi(ac) + bf_hi(bs));
+      ob.w[w] = pack_bf16(bf_lo(bc) + bf_lo(as), bf_hi(bc) + bf_hi(as));
+    }
+  } else {
+    const float* ea = reinterpret_cast<const float*>(&xa);
+    const float* eb = reinterpret_cast<const float*>(&xb);
+    float* ya = reinterpret_cast<float*>(&oa);
+    float* yb = reinterpret_cast<float*>(&ob);
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) {
+      ya[e] = rot_round<T>(ea[e], C[e], eb[e], -S[e]);
+      yb[e] = rot_round<T>(eb[e], C[e], ea[e], S[e]);
+    }
+  }
+}
+
+// Backward rotation (the transpose, fp32 arithmetic, one rounding at the end):
+// d_a = g_a C + g_b S, d_b = g_b C - g_a S.
+template <typename T, int EPC>
+__device__ __forceinline__ void rot_chunks_t(const Chunk& ga, const Chunk& gb, const float (&C)[EPC], const float (&S)[EPC],
+                                             Chunk& oa, Chunk& ob) {
+  if constexpr (sizeof(T) == 2) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float a0 = bf_lo(ga.w[w]), a1 = bf_hi(ga.w[w]), b0 = bf_lo(gb.w[w]), b1 = bf_hi(gb.w[w]);
+      const float c0 = C[2 * w], c1 = C[2 * w + 1], s0 = S[2 * w], s1 = S[2 * w + 1];
+      oa.w[w] = pack_bf16(a0 * c0 + b0 * s0, a1 * c1 + b1 * s1);
+      ob.w[w] = pack_bf16(b0 * c0 + a0 * -s0, b1 * c1 + a1 * -s1);
+    }
+  } else {
+    const float* ea = reinterpret_cast<const float*>(&ga);
+    const float* eb = reinterpret_cast<const float*>(&gb);
+    float* ya = reinterpret_cast<float*>(&oa);
+    float* yb = reinterpret_cast<float*>(&ob);
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) {
+      ya[e] = ea[e] * C[e] + eb[e] * S[e];
+      yb[e] = eb[e] * C[e] + ea[e] * -S[e];
+    }
+  }
 }
 
 template <typename T>
 __global__ void __launch_bounds__(kRopeMaxThreads) rope_givens_fwd_stream_kernel(const RopeParams p, int NS) {
-  using E = Elem<T>;
   constexpr int EPC = 16 / sizeof(T);
-  extern __shared__ float rope_tab[];  // [NS kRopeNR][D/2] cos, then sin
+  // RoPE factors [rpb][D/2] cos, then sin; the Givens copies [npair][EPC] cos, then sin
+  extern __shared__ float rope_tab[];
   const int tid = threadIdx.x;
   const int H = p.H, D = p.D, half = D / 2, npair = H / 2, cph = D / EPC, hch = cph / 2;
   const int U = 3 * H * cph / 2, rpb = NS * kRopeNR;
-  const int rows = p.B * p.T;
-  const int row0 = blockIdx.x * rpb;
-  const int nrow = min(rpb, rows - row0);
-  float* tc = rope_tab;
-  float* ts = rope_tab + rpb * half;
+  const int b = blockIdx.y, t0 = blockIdx.x * rpb;  // positions t0 .. t0 + nrow - 1 of sequence b
+  const int nrow = min(rpb, p.T - t0);
   const bool act = tid < NS * U;
-  const int slot = act ? tid / U : 0;
+  const int slot = act ? small_div(tid, frcp(float(U))) : 0;
   const RopeUnit R = rope_unit(act ? tid - slot * U : 0, H, cph, p.parity);
 
   // table values first (indices by multiplication with the 0/1 flags: a select becomes a branch)
   const RopeInv inv2 = rope_inv(p.inv_safe, p.rope, half);
-  const float th = p.theta_safe[min(R.pair, npair - 1) * p.givens];
+  const float th = p.theta_safe[min(tid / EPC, npair - 1) * p.givens];
+  // the unit's rows (clamped to the block's last row)
+  int rt[kRopeNR];
   Chunk xa[kRopeNR], xb[kRopeNR];
-  const T* q = reinterpret_cast<const T*>(p.qkv);
+  const T* q = reinterpret_cast<const T*>(p.qkv) + int64_t(b) * p.qkv_sb;
 #pragma unroll
   for (int r = 0; r < kRopeNR; ++r) {
-    const int row = row0 + min(NS * r + slot, nrow - 1), b = row / p.T, t = row - b * p.T;
-    const T* base = q + int64_t(b) * p.qkv_sb + int64_t(t) * p.qkv_sr;
+    rt[r] = t0 + min(NS * r + slot, nrow - 1);
+    const T* base = q + int64_t(rt[r]) * p.qkv_sr;
     xa[r] = load_chunk(base + R.ca * EPC);
     xb[r] = load_chunk(base + R.cb * EPC);
   }
-  rope_factors<T>(inv2, p.inv_safe, p.rope, p.pos0, row0, rpb, nrow, p.T, half, tc, ts);
-  float gsn, gcs;
-  sincosf(th, &gsn, &gcs);
-  const float gc = p.givens ? rnd<T>(gcs) : 1.f, gs = p.givens ? rnd<T>(gsn) : 0.f;
+  float* tc = rope_tab;
+  float* ts = tc + rpb * half;
+  rope_factors<T>(inv2, p.inv_safe, p.rope, p.pos0, t0, rpb, nrow, half, tc, ts);
+  givens_factors<T, EPC>(th, p.givens, npair, ts + rpb * half, ts + rpb * half + npair * EPC, nullptr);
   __syncthreads();
   if (!act) return;
 
@@ -347,28 +469,18 @@ __global__ void __launch_bounds__(kRopeMaxThreads) rope_givens_fwd_stream_kernel
   } else {
     obase = reinterpret_cast<T*>(p.o3); osb = p.o3_sb; osh = p.o3_sh; osr = p.o3_sr;
   }
-  T* oa = obase + int64_t(R.ha) * osh + R.k * EPC;
-  T* ob = rope_part ? oa + hch * EPC : obase + int64_t(R.hb) * osh + R.k * EPC;
-  const int a0 = R.k * EPC;  // RoPE factor index of the chunk's first element
+  T* oa = obase + int64_t(b) * osb + int64_t(R.ha) * osh + R.k * EPC;
+  T* ob = rope_part ? oa + hch * EPC : obase + int64_t(b) * osb + int64_t(R.hb) * osh + R.k * EPC;
+  const UnitFactors F = unit_factors(R, rpb, half, npair, EPC);
 #pragma unroll
   for (int r = 0; r < kRopeNR; ++r) {
     const int rr = NS * r + slot;
     if (rr >= nrow) break;
-    const int row = row0 + rr, b = row / p.T, t = row - b * p.T;
-    const T* ea = reinterpret_cast<const T*>(&xa[r]);
-    const T* eb = reinterpret_cast<const T*>(&xb[r]);
+    float C[EPC], S[EPC];
+    read_factors<EPC>(rope_tab, F, rr, C, S);
     Chunk outa, outb;
-    T* ya = reinterpret_cast<T*>(&outa);
-    T* yb = reinterpret_cast<T*>(&outb);
-#pragma unroll
-    for (int e = 0; e < EPC; ++e) {
-      const float C = rope_part ? tc[rr * half + a0 + e] : gc;
-      const float S = rope_part ? ts[rr * half + a0 + e] : gs;
-      const float va = E::to_f(ea[e]), vb = E::to_f(eb[e]);
-      ya[e] = E::from_f(rot_round<T>(va, C, vb, -S));
-      yb[e] = E::from_f(rot_round<T>(vb, C, va, S));
-    }
-    const int64_t off = int64_t(b) * osb + int64_t(t) * osr;
+    rot_chunks<T, EPC>(xa[r], xb[r], C, S, outa, outb);
+    const int64_t off = int64_t(rt[r]) * osr;
     store_chunk(oa + off, outa);
     store_chunk(ob + off, outb);
   }
@@ -378,23 +490,26 @@ template <typename T>
 __global__ void __launch_bounds__(kRopeMaxThreads) rope_givens_bwd_stream_kernel(const RopeBwdParams p, int NS) {
   using E = Elem<T>;
   constexpr int EPC = 16 / sizeof(T);
-  extern __shared__ float rope_tab[];  // [NS kRopeNR][D/2] cos, sin, then [threads] d theta
+  // RoPE factors [rpb][D/2] cos, then sin; the Givens copies [npair][EPC] cos, then sin; the exact
+  // Givens cos, sin [npair] each; then [threads] d theta
+  extern __shared__ float rope_tab[];
   const int tid = threadIdx.x;
   const int H = p.H, D = p.D, half = D / 2, npair = H / 2, cph = D / EPC, hch = cph / 2;
   const int U = 3 * H * cph / 2, rpb = NS * kRopeNR, ur = 2 * H * hch;
-  const int rows = p.B * p.T;
-  const int row0 = blockIdx.x * rpb;
-  const int nrow = min(rpb, rows - row0);
+  const int b = blockIdx.y, t0 = blockIdx.x * rpb;  // positions t0 .. t0 + nrow - 1 of sequence b
+  const int nrow = min(rpb, p.T - t0);
   float* tc = rope_tab;
-  float* ts = rope_tab + rpb * half;
-  float* red = rope_tab + 2 * rpb * half;
+  float* ts = tc + rpb * half;
+  float* gtab = ts + rpb * half;
+  float* gexact = gtab + 2 * npair * EPC;
+  float* red = gexact + 2 * npair;
   const bool act = tid < NS * U;
-  const int slot = act ? tid / U : 0;
+  const int slot = act ? small_div(tid, frcp(float(U))) : 0;
   const int u = act ? tid - slot * U : 0;
   const RopeUnit R = rope_unit(u, H, cph, p.parity);
 
   const RopeInv inv2 = rope_inv(p.inv_safe, p.rope, half);
-  const float th = p.theta_safe[min(R.pair, npair - 1) * p.givens];
+  const float th = p.theta_safe[min(tid / EPC, npair - 1) * p.givens];
   // gradient chunks of the unit, from the view of its tensor
   const T* gb;
   int64_t gsb, gsh, gsr;
@@ -405,57 +520,47 @@ __global__ void __launch_bounds__(kRopeMaxThreads) rope_givens_bwd_stream_kernel
   } else {
     gb = reinterpret_cast<const T*>(p.g3); gsb = p.g3_sb; gsh = p.g3_sh; gsr = p.g3_sr;
   }
-  const T* gpa = gb + int64_t(R.ha) * gsh + R.k * EPC;
-  const T* gpb = R.which < 2 ? gpa + hch * EPC : gb + int64_t(R.hb) * gsh + R.k * EPC;
+  const T* gpa = gb + int64_t(b) * gsb + int64_t(R.ha) * gsh + R.k * EPC;
+  const T* gpb = R.which < 2 ? gpa + hch * EPC : gb + int64_t(b) * gsb + int64_t(R.hb) * gsh + R.k * EPC;
   // the pair's I~ inputs (for d theta); RoPE units load their head's I~ chunk instead, so that no
   // load sits under a lane condition
-  const T* xq = reinterpret_cast<const T*>(p.qkv) + p.ioff + (R.k % cph) * EPC;
+  const T* xq = reinterpret_cast<const T*>(p.qkv) + int64_t(b) * p.qkv_sb + p.ioff + R.k * EPC;
+  int rt[kRopeNR];
   Chunk g0[kRopeNR], g1[kRopeNR], x0[kRopeNR], x1[kRopeNR];
 #pragma unroll
   for (int r = 0; r < kRopeNR; ++r) {
-    const int row = row0 + min(NS * r + slot, nrow - 1), b = row / p.T, t = row - b * p.T;
-    const int64_t go = int64_t(b) * gsb + int64_t(t) * gsr;
+    rt[r] = t0 + min(NS * r + slot, nrow - 1);
+    const int64_t go = int64_t(rt[r]) * gsr;
     g0[r] = load_chunk(gpa + go);
     g1[r] = load_chunk(gpb + go);
-    const T* xr = xq + int64_t(b) * p.qkv_sb + int64_t(t) * p.qkv_sr;
+    const T* xr = xq + int64_t(rt[r]) * p.qkv_sr;
     x0[r] = load_chunk(xr + R.ha * D);
     x1[r] = load_chunk(xr + R.hb * D);
   }
-  rope_factors<T>(inv2, p.inv_safe, p.rope, p.pos0, row0, rpb, nrow, p.T, half, tc, ts);
-  float gsn, gcs;
-  sincosf(th, &gsn, &gcs);
-  const float ce = p.givens ? gcs : 1.f, se = p.givens ? gsn : 0.f;                  // exact: the derivative
-  const float cr = p.givens ? rnd<T>(gcs) : 1.f, sr = p.givens ? rnd<T>(gsn) : 0.f;  // applied rotation
+  rope_factors<T>(inv2, p.inv_safe, p.rope, p.pos0, t0, rpb, nrow, half, tc, ts);
+  givens_factors<T, EPC>(th, p.givens, npair, gtab, gtab + npair * EPC, gexact);
   __syncthreads();
 
   // RoPE^T: dx_k = d_k c + d_{k+D/2} s, dx_{k+D/2} = d_{k+D/2} c - d_k s; Givens^T: da = c ga + s gb,
   // db = c gb - s ga
   const bool rope_part = R.which < 2;
   const bool dth_unit = act && !rope_part && p.givens;
-  T* da_out = reinterpret_cast<T*>(p.dqkv) + R.ca * EPC;
-  T* db_out = reinterpret_cast<T*>(p.dqkv) + R.cb * EPC;
-  const int a0 = R.k * EPC;
+  const int pr = min(R.pair, npair - 1);
+  const float ce = gexact[pr], se = gexact[npair + pr];  // exact: the derivative
+  T* da_out = reinterpret_cast<T*>(p.dqkv) + int64_t(b) * p.dq_sb + R.ca * EPC;
+  T* db_out = reinterpret_cast<T*>(p.dqkv) + int64_t(b) * p.dq_sb + R.cb * EPC;
+  const UnitFactors F = unit_factors(R, rpb, half, npair, EPC);
   float acc = 0.f;
 #pragma unroll
   for (int r = 0; r < kRopeNR; ++r) {
     const int rr = NS * r + slot;
     if (rr >= nrow) break;
-    const int row = row0 + rr, b = row / p.T, t = row - b * p.T;
-    const T* e0 = reinterpret_cast<const T*>(&g0[r]);
-    const T* e1 = reinterpret_cast<const T*>(&g1[r]);
+    float C[EPC], S[EPC];
+    read_factors<EPC>(rope_tab, F, rr, C, S);
     Chunk outa, outb;
-    T* ya = reinterpret_cast<T*>(&outa);
-    T* yb = reinterpret_cast<T*>(&outb);
-#pragma unroll
-    for (int e = 0; e < EPC; ++e) {
-      const float C = rope_part ? tc[rr * half + a0 + e] : cr;
-      const float S = rope_part ? ts[rr * half + a0 + e] : sr;
-      const float ga = E::to_f(e0[e]), gbv = E::to_f(e1[e]);
-      ya[e] = E::from_f(ga * C + gbv * S);
-      yb[e] = E::from_f(gbv * C + ga * -S);
-    }
+    rot_chunks_t<T, EPC>(g0[r], g1[r], C, S, outa, outb);
     if (act) {
-      const int64_t off = int64_t(b) * p.dq_sb + int64_t(t) * p.dq_sr;
+      const int64_t off = int64_t(rt[r]) * p.dq_sr;
       store_chunk(da_out + off, outa);
       store_chunk(db_out + off, outb);
     }
@@ -463,6 +568,8 @@ __global__ void __launch_bounds__(kRopeMaxThreads) rope_givens_bwd_stream_kernel
       // d theta of the pair: ga (-s a - c b) + gb (c a - s b), exact s, c
       const T* ea = reinterpret_cast<const T*>(&x0[r]);
       const T* eb = reinterpret_cast<const T*>(&x1[r]);
+      const T* e0 = reinterpret_cast<const T*>(&g0[r]);
+      const T* e1 = reinterpret_cast<const T*>(&g1[r]);
 #pragma unroll
       for (int e = 0; e < EPC; ++e) {
         const float a = E::to_f(ea[e]), bb = E::to_f(eb[e]);
@@ -475,11 +582,11 @@ __global__ void __launch_bounds__(kRopeMaxThreads) rope_givens_bwd_stream_kernel
   // one partial per block and pair: the pair's units in a fixed order (slot, then chunk)
   red[tid] = dth_unit ? acc : 0.f;
   __syncthreads();
-  for (int pr = tid; pr < npair; pr += blockDim.x) {
+  for (int q = tid; q < npair; q += blockDim.x) {
     float s2 = 0.f;
     for (int sl = 0; sl < NS; ++sl)
-      for (int k = 0; k < cph; ++k) s2 += red[sl * U + ur + pr * cph + k];
-    p.partial[int64_t(blockIdx.x) * npair + pr] = s2;
+      for (int k = 0; k < cph; ++k) s2 += red[sl * U + ur + q * cph + k];
+    p.partial[(int64_t(b) * gridDim.x + blockIdx.x) * npair + q] = s2;
   }
 }
 
@@ -511,7 +618,7 @@ static bool stream_shape(int H, int D, int epc, int& units, int& NS) {
   if (D % (2 * epc) != 0) return false;
   units = 3 * H * (D / epc) / 2;
   NS = 1;
-  return units <= kRopeMaxThreads;
+  return units <= kRopeMaxThreads && units >= (H / 2) * epc;  // the block writes the Givens copies
 }
 
 static int check_rope_common(int dtype, int B, int T, int H, int D, const void* qkv) {
@@ -543,13 +650,13 @@ int launch_rope_givens_fwd(const mote_rope_givens_args* a, hipStream_t stream) {
   int units, NS;
   const bool vec = stream_shape(a->H, a->D, epc, units, NS) && aligned16(a);
   if (vec) {
-    const int blocks = (rows + NS * kRopeNR - 1) / (NS * kRopeNR);
+    const dim3 blocks((a->T + NS * kRopeNR - 1) / (NS * kRopeNR), a->B);  // row groups of each sequence
     const int threads = (NS * units + 63) / 64 * 64;
-    const size_t lds = size_t(2) * NS * kRopeNR * (a->D / 2) * sizeof(float);
+    const size_t lds = (size_t(2) * NS * kRopeNR * (a->D / 2) + size_t(2) * (a->H / 2) * epc) * sizeof(float);
     if (a->dtype == MOTE_BF16)
-      hipLaunchKernelGGL(rope_givens_fwd_stream_kernel<bf16_t>, dim3(blocks), dim3(threads), lds, stream, p, NS);
+      hipLaunchKernelGGL(rope_givens_fwd_stream_kernel<bf16_t>, blocks, dim3(threads), lds, stream, p, NS);
     else
-      hipLaunchKernelGGL(rope_givens_fwd_stream_kernel<float>, dim3(blocks), dim3(threads), lds, stream, p, NS);
+      hipLaunchKernelGGL(rope_givens_fwd_stream_kernel<float>, blocks, dim3(threads), lds, stream, p, NS);
   } else if (a->dtype == MOTE_BF16) {
     hipLaunchKernelGGL(rope_givens_fwd_kernel<bf16_t>, dim3(rows), dim3(256), 0, stream, p);
   } else {
@@ -589,14 +696,16 @@ int launch_rope_givens_bwd(const mote_rope_givens_bwd_args* a, hipStream_t strea
   const int epc = a->dtype == MOTE_BF16 ? 8 : 4;
   int units, NS;
   const bool vec = stream_shape(a->H, a->D, epc, units, NS) && aligned16_bwd(a);
-  const int blocks = vec ? (rows + NS * kRopeNR - 1) / (NS * kRopeNR) : rows;
+  const int groups = (a->T + NS * kRopeNR - 1) / (NS * kRopeNR);  // row groups of each sequence
+  const dim3 blocks = vec ? dim3(groups, a->B) : dim3(rows);
   if (vec) {
     const int threads = (NS * units + 63) / 64 * 64;
-    const size_t lds = (size_t(2) * NS * kRopeNR * (a->D / 2) + size_t(threads)) * sizeof(float);
+    const size_t lds = (size_t(2) * NS * kRopeNR * (a->D / 2) + size_t(2) * (a->H / 2) * (epc + 1) + size_t(threads)) *
+                       sizeof(float);
     if (a->dtype == MOTE_BF16)
-      hipLaunchKernelGGL(rope_givens_bwd_stream_kernel<bf16_t>, dim3(blocks), dim3(threads), lds, stream, p, NS);
+      hipLaunchKernelGGL(rope_givens_bwd_stream_kernel<bf16_t>, blocks, dim3(threads), lds, stream, p, NS);
     else
-      hipLaunchKernelGGL(rope_givens_bwd_stream_kernel<float>, dim3(blocks), dim3(threads), lds, stream, p, NS);
+      hipLaunchKernelGGL(rope_givens_bwd_stream_kernel<float>, blocks, dim3(threads), lds, stream, p, NS);
   } else if (a->dtype == MOTE_BF16) {
     hipLaunchKernelGGL(rope_givens_bwd_kernel<bf16_t>, dim3(rows), dim3(256), 0, stream, p);
   } else {
@@ -604,7 +713,7 @@ int launch_rope_givens_bwd(const mote_rope_givens_bwd_args* a, hipStream_t strea
   }
   rc = check_launch("rope_givens_bwd");
   if (rc || !a->theta) return rc;
-  const int nparts = blocks;  // one partial per block (the per-row kernel: one per row)
+  const int nparts = int(blocks.x * blocks.y);  // one partial per block (the per-row kernel: one per row)
   hipLaunchKernelGGL(sum_partials_kernel, dim3(a->H / 2), dim3(256), 0, stream, p.partial, nparts, a->H / 2, a->dtheta);
   return check_launch("rope_givens_bwd/sum");
 }
