@@ -267,16 +267,21 @@ template <typename T>
 __device__ __forceinline__ void rope_factors(const RopeInv& inv2, const float* inv_safe, int rope, int pos0, int t0,
                                              int nr, int nrow, int half, float* tc, float* ts) {
   const float rh = frcp(float(half));
-  int j = 0;
-  for (int i = threadIdx.x; i < nr * half; i += blockDim.x, ++j) {
-    const int r = small_div(i, rh), k = i - r * half;
+  const int n = nr * half;
+  auto entry = [&](int i, float invk) {
+    const int r = small_div(i, rh);
     const int t = t0 + min(r, nrow - 1);
-    const float invk = j == 0 ? inv2.v[0] : j == 1 ? inv2.v[1] : inv_safe[k * rope];
     float sn, cs;
     sincosf((float)(pos0 + t) * invk, &sn, &cs);
     tc[i] = rope ? rnd<T>(cs) : 1.f;
     ts[i] = rope ? rnd<T>(sn) : 0.f;
-  }
+  };
+  // the first two entries take the preloaded frequencies; a value merged from a later load would make
+  // the compiler wait for that load, the youngest, and so for every chunk load before it
+  const int i0 = threadIdx.x, i1 = threadIdx.x + blockDim.x;
+  if (i0 < n) entry(i0, inv2.v[0]);
+  if (i1 < n) entry(i1, inv2.v[1]);
+  for (int i = i1 + blockDim.x; i < n; i += blockDim.x) entry(i, inv_safe[(i - small_div(i, rh) * half) * rope]);
 }
 
 // A thread's rotation unit: tensor (0: p1, 1: p2, 2: I~), the two heads (one head for RoPE), the
@@ -439,6 +444,10 @@ __global__ void __launch_bounds__(kRopeMaxThreads) rope_givens_fwd_stream_kernel
   // table values first (indices by multiplication with the 0/1 flags: a select becomes a branch)
   const RopeInv inv2 = rope_inv(p.inv_safe, p.rope, half);
   const float th = p.theta_safe[min(tid / EPC, npair - 1) * p.givens];
+  // Keeps these table loads ahead of the chunk loads: left alone, the compiler sinks them to their
+  // use (the factor loop, after every chunk load) and, loads completing in order, the sincos then
+  // waits for all the chunks.
+  asm volatile("" ::: "memory");
   // the unit's rows (clamped to the block's last row)
   int rt[kRopeNR];
   Chunk xa[kRopeNR], xb[kRopeNR];
@@ -486,8 +495,14 @@ __global__ void __launch_bounds__(kRopeMaxThreads) rope_givens_fwd_stream_kernel
   }
 }
 
+// The backward's block: the RoPE units fill the first waves, the Givens units start at a wave boundary
+// (rope_bwd_threads), so a wave holds units of one kind and only the Givens waves load the I~ inputs
+// that d theta needs. One row slot of kRopeNR rows.
+__host__ __device__ inline int rope_bwd_givens_lane0(int H, int cph) { return (H * cph + 63) / 64 * 64; }
+static inline int rope_bwd_threads(int H, int cph) { return rope_bwd_givens_lane0(H, cph) + ((H / 2) * cph + 63) / 64 * 64; }
+
 template <typename T>
-__global__ void __launch_bounds__(kRopeMaxThreads) rope_givens_bwd_stream_kernel(const RopeBwdParams p, int NS) {
+__global__ void __launch_bounds__(kRopeMaxThreads) rope_givens_bwd_stream_kernel(const RopeBwdParams p) {
   using E = Elem<T>;
   constexpr int EPC = 16 / sizeof(T);
   // RoPE factors [rpb][D/2] cos, then sin; the Givens copies [npair][EPC] cos, then sin; the exact
@@ -495,7 +510,7 @@ __global__ void __launch_bounds__(kRopeMaxThreads) rope_givens_bwd_stream_kernel
   extern __shared__ float rope_tab[];
   const int tid = threadIdx.x;
   const int H = p.H, D = p.D, half = D / 2, npair = H / 2, cph = D / EPC, hch = cph / 2;
-  const int U = 3 * H * cph / 2, rpb = NS * kRopeNR, ur = 2 * H * hch;
+  const int rpb = kRopeNR, ur = 2 * H * hch, ug = npair * cph;
   const int b = blockIdx.y, t0 = blockIdx.x * rpb;  // positions t0 .. t0 + nrow - 1 of sequence b
   const int nrow = min(rpb, p.T - t0);
   float* tc = rope_tab;
@@ -503,13 +518,19 @@ __global__ void __launch_bounds__(kRopeMaxThreads) rope_givens_bwd_stream_kernel
   float* gtab = ts + rpb * half;
   float* gexact = gtab + 2 * npair * EPC;
   float* red = gexact + 2 * npair;
-  const bool act = tid < NS * U;
-  const int slot = act ? small_div(tid, frcp(float(U))) : 0;
-  const int u = act ? tid - slot * U : 0;
+  const int g0lane = rope_bwd_givens_lane0(H, cph);
+  const bool gwave = __builtin_amdgcn_readfirstlane(tid >> 6) * 64 >= g0lane;  // wave-uniform
+  const bool act = gwave ? tid - g0lane < ug : tid < ur;
+  // idle lanes take a unit of their wave's kind, so their addresses stay valid
+  const int u = gwave ? ur + min(tid - g0lane, ug - 1) : min(tid, ur - 1);
   const RopeUnit R = rope_unit(u, H, cph, p.parity);
 
   const RopeInv inv2 = rope_inv(p.inv_safe, p.rope, half);
   const float th = p.theta_safe[min(tid / EPC, npair - 1) * p.givens];
+  // Keeps these table loads ahead of the chunk loads: left alone, the compiler sinks them to their
+  // use (the factor loop, after every chunk load) and, loads completing in order, the sincos then
+  // waits for all the chunks.
+  asm volatile("" ::: "memory");
   // gradient chunks of the unit, from the view of its tensor
   const T* gb;
   int64_t gsb, gsh, gsr;
@@ -522,20 +543,25 @@ __global__ void __launch_bounds__(kRopeMaxThreads) rope_givens_bwd_stream_kernel
   }
   const T* gpa = gb + int64_t(b) * gsb + int64_t(R.ha) * gsh + R.k * EPC;
   const T* gpb = R.which < 2 ? gpa + hch * EPC : gb + int64_t(b) * gsb + int64_t(R.hb) * gsh + R.k * EPC;
-  // the pair's I~ inputs (for d theta); RoPE units load their head's I~ chunk instead, so that no
-  // load sits under a lane condition
-  const T* xq = reinterpret_cast<const T*>(p.qkv) + int64_t(b) * p.qkv_sb + p.ioff + R.k * EPC;
   int rt[kRopeNR];
+#pragma unroll
+  for (int r = 0; r < kRopeNR; ++r) rt[r] = t0 + min(r, nrow - 1);
+  // the pair's I~ inputs (d theta), loaded by the Givens waves only, ahead of the gradients
   Chunk g0[kRopeNR], g1[kRopeNR], x0[kRopeNR], x1[kRopeNR];
+  if (gwave && p.givens) {
+    const T* xq = reinterpret_cast<const T*>(p.qkv) + int64_t(b) * p.qkv_sb + p.ioff + R.k * EPC;
+#pragma unroll
+    for (int r = 0; r < kRopeNR; ++r) {
+      const T* xr = xq + int64_t(rt[r]) * p.qkv_sr;
+      x0[r] = load_chunk(xr + R.ha * D);
+      x1[r] = load_chunk(xr + R.hb * D);
+    }
+  }
 #pragma unroll
   for (int r = 0; r < kRopeNR; ++r) {
-    rt[r] = t0 + min(NS * r + slot, nrow - 1);
     const int64_t go = int64_t(rt[r]) * gsr;
     g0[r] = load_chunk(gpa + go);
     g1[r] = load_chunk(gpb + go);
-    const T* xr = xq + int64_t(rt[r]) * p.qkv_sr;
-    x0[r] = load_chunk(xr + R.ha * D);
-    x1[r] = load_chunk(xr + R.hb * D);
   }
   rope_factors<T>(inv2, p.inv_safe, p.rope, p.pos0, t0, rpb, nrow, half, tc, ts);
   givens_factors<T, EPC>(th, p.givens, npair, gtab, gtab + npair * EPC, gexact);
@@ -553,10 +579,9 @@ __global__ void __launch_bounds__(kRopeMaxThreads) rope_givens_bwd_stream_kernel
   float acc = 0.f;
 #pragma unroll
   for (int r = 0; r < kRopeNR; ++r) {
-    const int rr = NS * r + slot;
-    if (rr >= nrow) break;
+    if (r >= nrow) break;
     float C[EPC], S[EPC];
-    read_factors<EPC>(rope_tab, F, rr, C, S);
+    read_factors<EPC>(rope_tab, F, r, C, S);
     Chunk outa, outb;
     rot_chunks_t<T, EPC>(g0[r], g1[r], C, S, outa, outb);
     if (act) {
@@ -579,13 +604,12 @@ __global__ void __launch_bounds__(kRopeMaxThreads) rope_givens_bwd_stream_kernel
     }
   }
   if (!p.givens) return;
-  // one partial per block and pair: the pair's units in a fixed order (slot, then chunk)
+  // one partial per block and pair: the pair's units in a fixed order (chunk)
   red[tid] = dth_unit ? acc : 0.f;
   __syncthreads();
   for (int q = tid; q < npair; q += blockDim.x) {
     float s2 = 0.f;
-    for (int sl = 0; sl < NS; ++sl)
-      for (int k = 0; k < cph; ++k) s2 += red[sl * U + ur + q * cph + k];
+    for (int k = 0; k < cph; ++k) s2 += red[g0lane + q * cph + k];
     p.partial[(int64_t(b) * gridDim.x + blockIdx.x) * npair + q] = s2;
   }
 }
@@ -695,17 +719,17 @@ int launch_rope_givens_bwd(const mote_rope_givens_bwd_args* a, hipStream_t strea
   const int rows = a->B * a->T;
   const int epc = a->dtype == MOTE_BF16 ? 8 : 4;
   int units, NS;
-  const bool vec = stream_shape(a->H, a->D, epc, units, NS) && aligned16_bwd(a);
-  const int groups = (a->T + NS * kRopeNR - 1) / (NS * kRopeNR);  // row groups of each sequence
+  const int threads = rope_bwd_threads(a->H, a->D / epc);
+  const bool vec = stream_shape(a->H, a->D, epc, units, NS) && threads <= kRopeMaxThreads && aligned16_bwd(a);
+  const int groups = (a->T + kRopeNR - 1) / kRopeNR;  // row groups of each sequence
   const dim3 blocks = vec ? dim3(groups, a->B) : dim3(rows);
   if (vec) {
-    const int threads = (NS * units + 63) / 64 * 64;
-    const size_t lds = (size_t(2) * NS * kRopeNR * (a->D / 2) + size_t(2) * (a->H / 2) * (epc + 1) + size_t(threads)) *
+    const size_t lds = (size_t(2) * kRopeNR * (a->D / 2) + size_t(2) * (a->H / 2) * (epc + 1) + size_t(threads)) *
                        sizeof(float);
     if (a->dtype == MOTE_BF16)
-      hipLaunchKernelGGL(rope_givens_bwd_stream_kernel<bf16_t>, blocks, dim3(threads), lds, stream, p, NS);
+      hipLaunchKernelGGL(rope_givens_bwd_stream_kernel<bf16_t>, blocks, dim3(threads), lds, stream, p);
     else
-      hipLaunchKernelGGL(rope_givens_bwd_stream_kernel<float>, blocks, dim3(threads), lds, stream, p, NS);
+      hipLaunchKernelGGL(rope_givens_bwd_stream_kernel<float>, blocks, dim3(threads), lds, stream, p);
   } else if (a->dtype == MOTE_BF16) {
     hipLaunchKernelGGL(rope_givens_bwd_kernel<bf16_t>, dim3(rows), dim3(256), 0, stream, p);
   } else {
