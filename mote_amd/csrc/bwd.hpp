@@ -56,14 +56,15 @@ struct PairTable {
   }
 };
 
-// dlam = the fixed-order sum of the n row-block partials (the rows stage writes them), by the 256
-// threads of one workgroup through `red` (256 floats of LDS); every thread must call it.
+// dlam = the fixed-order sum of the n row-block partials (the rows stage writes them), by the NT
+// threads of one workgroup through `red` (NT floats of LDS); every thread must call it.
+template <int NT = 256>
 __device__ __forceinline__ void dlam_sum(const float* part, int n, float* out, float* red) {
   float acc = 0.f;
-  for (int i = threadIdx.x; i < n; i += 256) acc += part[i];
+  for (int i = threadIdx.x; i < n; i += NT) acc += part[i];
   red[threadIdx.x] = acc;
   __syncthreads();
-  for (int w = 128; w >= 1; w >>= 1) {
+  for (int w = NT / 2; w >= 1; w >>= 1) {
     if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
     __syncthreads();
   }

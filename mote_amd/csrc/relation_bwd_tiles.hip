@@ -26,12 +26,24 @@
 // B operand of dQ^T += K^T dU^T, and K^T comes from transposed reads of the K tile. The key-half
 // waves add through LDS; the Self part dU_ii P2_i joins before the store.
 #include <type_traits>
+#include <utility>
 
 #include "common.hpp"
 #include "bwd.hpp"
 #include "tiles.hpp"
 
 namespace mote {
+
+// f(integral_constant<int, 0>), ..., f(integral_constant<int, N - 1>): a loop whose index is a
+// compile-time constant in every iteration.
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 // Elementwise core shared by both kernels: raw dot u, raw dW, row terms (lse2 = L log2e,
 // c = dA - Delta). Returns dU; w through the reference.
@@ -352,51 +364,53 @@ bwd_kv_kernel(const BwdParams p) {
 // query-stationary kernel: dP1 = (dU P2 + dU_ii P2_i) / sqrt(D) from the stored dU^T fragments
 // ------------------------------------------------------------------------------------------------
 // One workgroup per 64 queries of one (batch, head), longest first. Wave w = (qh, kh) accumulates
-// dQ^T of queries 32 qh .. +31 over key half kh of every key block: A = K^T by transposed LDS reads
-// of the staged P2 tile, B = the key kernel's dU^T fragments straight from global memory (16 bytes per
-// lane). No elementwise work: the kernel streams the fragments, with NS key blocks in flight (P2 tiles
-// in an NS-deep LDS ring, fragments in NS register sets; the loop is unrolled by NS so that every
-// buffer index is a constant). The key halves add through LDS before the Self term and the stores.
+// dQ^T of two query blocks per workgroup of eight waves: wave w takes key half kh = w % 2 and the
+// 32 queries qq = w / 2 of the pair (qq / 2 = 0: the later block, 1: the earlier one). Per key block:
+// A = K^T by transposed LDS reads of the staged P2 tile, B = the key kernel's dU^T fragments of the
+// wave's query block (16 bytes per lane, through the same ring slot). Both query blocks read one
+// staged P2 tile: staging it is the kernel's largest cost (the L2 -> LDS path, shared by the CU),
+// and 128 queries per workgroup stage it half as often as 64. No elementwise work: NS key blocks in
+// flight (P2 tiles and fragments in an NS-deep LDS ring; the loop is unrolled by NS so every slot
+// index is a constant). Query blocks pair from the top (the two longest together, longest pairs
+// first); the earlier block of a pair sees at most one key block fewer, and with an odd count the
+// lowest pair has one block. The key halves add through LDS before the Self term and the stores.
 template <int DP>
-__global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
+__global__ void __launch_bounds__(512) bwd_dq_kernel(const BwdParams p) {
   using E = Elem<bf16_t>;
   using Frag = E::Frag;
+  constexpr int NW = 8;
   constexpr int DT = DP / 16, CPR = DP / 8, TILE = 64 * DP;
-  constexpr int NS = 4;             // key blocks in flight
-  constexpr int SLOT = TILE + 4096; // bf16 per ring slot: the P2 tile, then the pair's 8 dU^T fragments
-  constexpr int VMS = DP / 32 + 2;  // vector-memory instructions per block and wave (P2 staging + 2 fragments)
-  constexpr int HALF = DP / 2;      // fp32 columns per half of the reduction buffer
-  constexpr int RS = HALF + 4;      // its row stride: an odd count of 16-byte chunks, so the 16 rows of
-                                    // a lane group's f32x4 accesses fall on distinct banks
-  // one array per ring slot (each slot holds half of the final reduction buffer)
-  __shared__ __align__(16) bf16_t ks0[SLOT];
-  __shared__ __align__(16) bf16_t ks1[SLOT];
-  __shared__ __align__(16) bf16_t ks2[SLOT];
-  __shared__ __align__(16) bf16_t ks3[SLOT];
+  constexpr int SLOT = TILE + 2 * 4096;   // bf16 per ring slot: the P2 tile, then each query block's 8 fragments
+  constexpr int NS = 4;                   // ring slots: key blocks issued ahead + 1 (five measured slower)
+  using Stager = TileStager<DP, NW, 1>;
+  constexpr int PER = Stager::PER;        // P2 transfers per block of the busiest waves
+  constexpr int RSF = DP + 4;             // fp32 row stride of the reduction buffer: an odd count of
+                                          // 16-byte chunks, so a lane group's rows fall on distinct banks
+  static_assert(128 * RSF * 4 <= NS * SLOT * 2, "the reduction buffer fits the ring");
+  __shared__ __align__(16) bf16_t ring[NS * SLOT];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15, lg = lane >> 4;
-  const int kh = wave & 1, qh = wave >> 1;
+  const int kh = wave & 1, qq = wave >> 1;
+  const int sub = qq >> 1, qh = qq & 1;
   const int BH = p.B * p.H;
   const int bh = blockIdx.x % BH;
   const int nqb = p.TQp / 64;
-  const int qb = nqb - 1 - blockIdx.x / BH;  // the last query block sees the most keys: longest first
+  const int qtop = nqb - 1 - 2 * (blockIdx.x / BH);  // the pair's later query block
+  const bool wq = qtop - sub >= 0;                   // the wave has a query block (wave-uniform)
+  const int qbw = wq ? qtop - sub : qtop;            // a wave without one mirrors the other's addresses
   const int b = bh / p.H, h = bh % p.H;
-  const int i0 = qb * 64;
+  const int ibase = (qtop - 1) * 64;                 // query of reduction row 0 (the earlier block)
   const bf16_t* kbase = reinterpret_cast<const bf16_t*>(p.p2) + b * p.k_sb + h * p.k_sh;
-  const int nkb = PairTable::nkb(qb, p.TQ, p.q_start);
+  const int nkb = PairTable::nkb(qtop, p.TQ, p.q_start);                   // the workgroup's key blocks
+  const int nkb_w = PairTable::nkb(qbw, p.TQ, p.q_start);                  // the wave's (addresses)
+  const int nkb_c = wq ? nkb_w : 0;                                        // the wave's (products)
   // the wave's two fragments (kh, 2 qh) and (kh, 2 qh + 1) of each pair: 2 KB contiguous
   const int fo = (kh * 4 + 2 * qh) * 512;
   const bf16_t* fr = reinterpret_cast<const bf16_t*>(p.dut) +
-                     (int64_t(bh) * p.npairs + PairTable::offset(qb, p.q_start)) * 4096 + fo + lane * 8;
-  auto slot = [&](auto u) -> bf16_t* {
-    constexpr int U = decltype(u)::value;
-    if constexpr (U == 0) return ks0;
-    else if constexpr (U == 1) return ks1;
-    else if constexpr (U == 2) return ks2;
-    else return ks3;
-  };
+                     (int64_t(bh) * p.npairs + PairTable::offset(qbw, p.q_start)) * 4096 + fo + lane * 8;
+  const int fslot = TILE + sub * 4096 + fo;  // the wave's fragments within a slot
 
   f32x4 dqacc[DT][2];
 #pragma unroll
@@ -405,49 +419,63 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
     for (int s = 0; s < 2; ++s) dqacc[dt][s] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // The Self term's inputs, dU_ii and the P2 row of each of the thread's (query, 8-column chunk)
-  // items, loaded before the key loop: their latency passes under it instead of after it. Rows past
-  // TQ load row TQ - 1 (not stored).
-  constexpr int NIT = 64 * CPR / 256;
-  static_assert(64 * CPR % 256 == 0, "whole (query, chunk) items per thread");
+  // items, loaded before the key loop: their latency passes under it instead of after it. Rows
+  // outside [0, TQ) load a row inside (not stored).
+  constexpr int NIT = 128 * CPR / (64 * NW);
+  static_assert(128 * CPR % (64 * NW) == 0, "whole (query, chunk) items per thread");
   float us_pre[NIT];
   Frag k8_pre[NIT];
 #pragma unroll
   for (int it = 0; it < NIT; ++it) {
-    const int item = tid + 256 * it;
-    const int i = min(i0 + item / CPR, p.TQ - 1);
+    const int item = tid + 64 * NW * it;
+    const int i = min(max(ibase + item / CPR, 0), p.TQ - 1);
     us_pre[it] = p.duii[int64_t(bh) * p.TQp + i];
     k8_pre[it] = E::load8(kbase + int64_t(p.q_start + i) * p.k_sr + (item % CPR) * 8);
   }
 
   const bf16_t* srcs[1] = {kbase};
   const int64_t strides[1] = {p.k_sr};
-  TileStager<DP, 4, 1> st;
+  Stager st;
   st.init(wave, lane, strides);
-  // Block kb: P2 rows and the wave's fragments into ring slot kb % NS, issued NS - 1 steps ahead;
-  // blocks past the end are not issued. The wait before block kb's reads leaves in flight the later
-  // blocks already issued: NS - 2 of them, fewer in the last steps.
+  // Block kb: P2 rows (the staging instructions dealt over the waves) and the wave's fragments into
+  // ring slot kb % NS, issued NS - 1 steps ahead; blocks past the end are not issued. A wave past its
+  // own block's last key block reloads that block's last fragments (valid addresses, no products).
+  // The wait before block kb's reads leaves in flight the later blocks already issued: NS - 2 of
+  // them, fewer in the last steps; each wave counts its own transfers per block.
   auto issue = [&](int kb, auto u) {
-    const int kc = min(kb, nkb - 1);
-    bf16_t* dst = slot(u);
-    st.issue(dst, srcs, strides, kc * 64, p.TK - 1, wave, lane);
+    constexpr int U = decltype(u)::value;
+    bf16_t* dst = ring + U * SLOT;
+    st.issue(dst, srcs, strides, kb * 64, p.TK - 1, wave, lane);
+    const int kc = min(kb, nkb_w - 1);
 #pragma unroll
-    for (int s = 0; s < 2; ++s) TileStager<DP, 4, 1>::load(fr + int64_t(kc) * 4096 + s * 512, dst + TILE + fo + s * 512);
+    for (int s = 0; s < 2; ++s) Stager::load(fr + int64_t(kc) * 4096 + s * 512, dst + fslot + s * 512);
   };
-  static_assert(NS == 4, "four ring slots");
+  const bool busy = wave + NW * (PER - 1) < Stager::NINS;  // this wave issues PER staging transfers, else PER - 1
+  // wait until at most min(later, NS - 2) blocks of this wave's transfers are outstanding
+  auto wait_blocks = [&](int later, auto vms) {
+    constexpr int V = decltype(vms)::value;
+    static_assert(NS >= 3 && NS <= 6, "ring depth");
+    if (later >= NS - 2) __builtin_amdgcn_s_waitcnt(kVmWaitStage<(NS - 2) * V>());
+    else if (NS > 5 && later == 3) __builtin_amdgcn_s_waitcnt(kVmWaitStage<(NS > 5 ? 3 : 0) * V>());
+    else if (NS > 4 && later == 2) __builtin_amdgcn_s_waitcnt(kVmWaitStage<(NS > 4 ? 2 : 0) * V>());
+    else if (NS > 3 && later == 1) __builtin_amdgcn_s_waitcnt(kVmWaitStage<(NS > 3 ? 1 : 0) * V>());
+    else __builtin_amdgcn_s_waitcnt(kVmWaitStage<0>());
+  };
+  auto wait_for = [&](int later) {
+    if (busy) wait_blocks(later, std::integral_constant<int, PER + 2>{});
+    else wait_blocks(later, std::integral_constant<int, PER + 1>{});
+  };
   auto step = [&](int kb, auto u) {
     constexpr int U = decltype(u)::value;
     if (kb >= nkb) return;  // uniform over the workgroup: every wave skips the same steps
-    // this wave's part of block kb is in (blocks issued after it may still be in flight)
-    const int later = nkb - 1 - kb;
-    if (later >= NS - 2) __builtin_amdgcn_s_waitcnt(kVmWaitStage<(NS - 2) * VMS>());
-    else if (later == 1) __builtin_amdgcn_s_waitcnt(kVmWaitStage<VMS>());
-    else __builtin_amdgcn_s_waitcnt(kVmWaitStage<0>());
+    wait_for(nkb - 1 - kb);  // this wave's part of block kb is in
     lds_barrier();  // every wave's part of block kb is in; every wave is done with block kb - 1's slot
     if (kb + NS - 1 < nkb) issue(kb + NS - 1, std::integral_constant<int, (U + NS - 1) % NS>{});
-    const bf16_t* Ks = slot(u);
+    if (kb >= nkb_c) return;  // wave-uniform: the earlier block has no pair with this key block
+    const bf16_t* Ks = ring + U * SLOT;
     Frag bf[2];
 #pragma unroll
-    for (int s = 0; s < 2; ++s) bf[s] = E::load8(Ks + TILE + fo + s * 512 + lane * 8);
+    for (int s = 0; s < 2; ++s) bf[s] = E::load8(Ks + fslot + s * 512 + lane * 8);
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
       const Frag ak = tile_tr_frag<DP>(Ks, 32 * kh, dt, li, lg);
@@ -456,34 +484,23 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
     }
   };
   if (nkb > 0) {
-    issue(0, std::integral_constant<int, 0>{});
-    if (nkb > 1) issue(1, std::integral_constant<int, 1>{});
-    if (nkb > 2) issue(2, std::integral_constant<int, 2>{});
-    for (int kb0 = 0; kb0 < nkb; kb0 += NS) {
-      step(kb0, std::integral_constant<int, 0>{});
-      step(kb0 + 1, std::integral_constant<int, 1>{});
-      step(kb0 + 2, std::integral_constant<int, 2>{});
-      step(kb0 + 3, std::integral_constant<int, 3>{});
-    }
+    static_for<NS - 1>([&](auto u) {
+      if (decltype(u)::value < nkb) issue(decltype(u)::value, u);
+    });
+    for (int kb0 = 0; kb0 < nkb; kb0 += NS) static_for<NS>([&](auto u) { step(kb0 + decltype(u)::value, u); });
   }
 
-  // add the two key halves through LDS: head-dim columns [0, DP/2) in slot 0, the rest in slot 1,
-  // each [64 queries][RS] fp32
-  static_assert(64 * RS * 4 <= SLOT * 2, "a reduction half fits one ring slot");
-  float* R0 = reinterpret_cast<float*>(ks0);
-  float* R1 = reinterpret_cast<float*>(ks1);
-  auto rptr = [&](int row, int col) -> float* {
-    return col < HALF ? R0 + row * RS + col : R1 + row * RS + (col - HALF);
-  };
-  __syncthreads();  // every wave is done reading slots 0 and 1 (the last step waited for every transfer)
+  // add the two key halves through LDS: [128 queries][RSF] fp32 over the ring, rows 0..63 the
+  // earlier block, 64..127 the later one
+  float* R = reinterpret_cast<float*>(ring);
+  const int rbase = (1 - sub) * 64 + 32 * qh;
+  __syncthreads();  // every wave is done reading the ring (the last step waited for every transfer)
   if (kh == 1) {
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const int row = 32 * qh + 16 * s + li;
-        *reinterpret_cast<f32x4*>(rptr(row, 16 * dt + 4 * lg)) = dqacc[dt][s];
-      }
+      for (int s = 0; s < 2; ++s)
+        *reinterpret_cast<f32x4*>(R + (rbase + 16 * s + li) * RSF + 16 * dt + 4 * lg) = dqacc[dt][s];
   }
   __syncthreads();
   if (kh == 0) {
@@ -491,8 +508,7 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        const int row = 32 * qh + 16 * s + li;
-        f32x4* q = reinterpret_cast<f32x4*>(rptr(row, 16 * dt + 4 * lg));
+        f32x4* q = reinterpret_cast<f32x4*>(R + (rbase + 16 * s + li) * RSF + 16 * dt + 4 * lg);
         *q = *q + dqacc[dt][s];
       }
   }
@@ -501,16 +517,16 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
   bf16_t* dqout = reinterpret_cast<bf16_t*>(p.dp1) + b * p.dq_sb + h * p.dq_sh;
 #pragma unroll
   for (int it = 0; it < NIT; ++it) {
-    const int item = tid + 256 * it;
+    const int item = tid + 64 * NW * it;
     const int row = item / CPR, d0 = (item % CPR) * 8;
-    const int i = i0 + row;
-    if (i >= p.TQ) continue;
+    const int i = ibase + row;
+    if (i < 0 || i >= p.TQ) continue;
     const float us = us_pre[it];
     const Frag k8 = k8_pre[it];
     float o[8];
 #pragma unroll
     for (int e = 0; e < 8; e += 4) {
-      const float4 a = *reinterpret_cast<const float4*>(rptr(row, d0 + e));
+      const float4 a = *reinterpret_cast<const float4*>(R + row * RSF + d0 + e);
       o[e] = a.x; o[e + 1] = a.y; o[e + 2] = a.z; o[e + 3] = a.w;
     }
 #pragma unroll
@@ -518,10 +534,12 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
     const Frag ov = E::from_f32(o);
     *reinterpret_cast<bf16x8*>(dqout + int64_t(i) * p.dq_sr + d0) = ov.v;
   }
-  // the last workgroup (query block 0, the shortest) also sums dlam: the rows stage has written
+  // the last workgroup (the lowest pair, the shortest) also sums dlam: the rows stage has written
   // every partial before this launch
-  if (blockIdx.x == gridDim.x - 1)
-    dlam_sum(p.dlam_part, BH * nqb, p.dlam, reinterpret_cast<float*>(ks2));
+  if (blockIdx.x == gridDim.x - 1) {
+    __syncthreads();  // the Self-term reads of R are done before dlam_sum reuses the memory
+    dlam_sum<64 * NW>(p.dlam_part, BH * nqb, p.dlam, R);
+  }
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -535,8 +553,8 @@ static void launch_tiles_dp(const BwdParams& p, int stages, hipStream_t stream) 
     hipLaunchKernelGGL((bwd_kv_kernel<DP>), dim3(nkb * BH), dim3(256), 0, stream, p);
   }
   if (stages & MOTE_BWD_QUERIES) {
-    const int nqb = p.TQp / 64;
-    hipLaunchKernelGGL((bwd_dq_kernel<DP>), dim3(nqb * BH), dim3(256), 0, stream, p);
+    const int npq = (p.TQp / 64 + 1) / 2;  // query-block pairs
+    hipLaunchKernelGGL((bwd_dq_kernel<DP>), dim3(npq * BH), dim3(512), 0, stream, p);
   }
 }
 
