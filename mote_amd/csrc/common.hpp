@@ -52,13 +52,34 @@ __device__ __forceinline__ float wave_xor(float v, int mask) { return __shfl_xor
 // with the gfx950 row swaps: v_permlane16_swap / v_permlane32_swap of a register with itself put
 // the partner row's value in one of the two results and the lane's own value in the other.
 typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
+// The max of two lanes' values without fmaxf's canonicalisation: the operands come back from the swap
+// as integers, so the compiler quiets each one (a v_max of the value with itself) before the max. The
+// inputs here are MFMA dot products or -inf, never signalling NaNs.
+__device__ __forceinline__ float vmax_raw(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
 __device__ __forceinline__ float lanegroup_max(float x) {
   const unsigned u = __float_as_uint(x);
   const u32x2 a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  x = vmax_raw(__uint_as_float(a[0]), __uint_as_float(a[1]));
   const unsigned v = __float_as_uint(x);
   const u32x2 b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  return vmax_raw(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+// Two independent lanegroup_max chains interleaved (each one's swap fills the other's hazard wait).
+__device__ __forceinline__ void lanegroup_max2(float& x, float& y) {
+  const unsigned ux = __float_as_uint(x), uy = __float_as_uint(y);
+  const u32x2 ax = __builtin_amdgcn_permlane16_swap(ux, ux, false, false);
+  const u32x2 ay = __builtin_amdgcn_permlane16_swap(uy, uy, false, false);
+  const float mx = vmax_raw(__uint_as_float(ax[0]), __uint_as_float(ax[1]));
+  const float my = vmax_raw(__uint_as_float(ay[0]), __uint_as_float(ay[1]));
+  const unsigned vx = __float_as_uint(mx), vy = __float_as_uint(my);
+  const u32x2 bx = __builtin_amdgcn_permlane32_swap(vx, vx, false, false);
+  const u32x2 by = __builtin_amdgcn_permlane32_swap(vy, vy, false, false);
+  x = vmax_raw(__uint_as_float(bx[0]), __uint_as_float(bx[1]));
+  y = vmax_raw(__uint_as_float(by[0]), __uint_as_float(by[1]));
 }
 __device__ __forceinline__ float lanegroup_sum(float x) {
   const unsigned u = __float_as_uint(x);

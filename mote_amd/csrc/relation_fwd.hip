@@ -446,8 +446,11 @@ __device__ __forceinline__ void fwd_softmax_pv(const bf16_t* Vs, const f32x4 (&s
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) mx = fmaxf(mx, keep[s][kt][r] ? sacc[kt][s][r] : kNegInf);
-    bnd[s] = fmaxf(lanegroup_max(mx) * c2, 0.f);
+    bnd[s] = mx;
   }
+  lanegroup_max2(bnd[0], bnd[1]);
+#pragma unroll
+  for (int s = 0; s < 2; ++s) bnd[s] = fmaxf(bnd[s] * c2, 0.f);
   const bool need = (bnd[0] > m_run[0] + kRescale) || (bnd[1] > m_run[1] + kRescale);
   if (__ballot(need) != 0ull) {
     asm volatile("" ::: "memory");  // a real branch: the rescale is rare
