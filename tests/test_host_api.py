@@ -215,3 +215,20 @@ def test_head_rms_norm_module_matches_the_oracle():
     x = torch.randn(2, 8, 11, 96).bfloat16()
     assert torch.equal(n(x), r(x))
     assert math.isfinite(float(n(x).float().sum()))
+
+
+@pytest.mark.parametrize("T,qk_norm,fused", [(64, False, True), (40000, False, False), (40000, True, True)])
+def test_fused_prologue_row_threshold(monkeypatch, T, qk_norm, fused):
+    """FullRelation.heads takes the fused prologue up to FUSED_PROLOGUE_MAX_ROWS rows without QK-Norm
+    (beyond it the product + RoPE kernel path measured faster), and at every size with QK-Norm. The
+    launches are replaced by recorders, so this runs on the CPU."""
+    from mote_amd import relation as R
+
+    calls = []
+    monkeypatch.setattr(R, "qkv_rope", lambda *a, **k: calls.append("fused") or ("p1", "p2", "info"))
+    monkeypatch.setattr(R, "rope_givens", lambda *a, **k: calls.append("unfused") or ("p1", "p2", "info"))
+    m = R.FullRelation(128, 2, 1, qk_norm=qk_norm, dtype=torch.bfloat16)
+    assert R.FUSED_PROLOGUE_MAX_ROWS < 40000 <= 2 * R.FUSED_PROLOGUE_MAX_ROWS
+    x = torch.zeros(1, T, 128, dtype=torch.bfloat16)
+    m.heads(x, 0)
+    assert calls == ["fused" if fused else "unfused"]
