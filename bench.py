@@ -254,16 +254,42 @@ KERNEL_SOURCES = {
 }
 
 
+def _code_only(text: str) -> str:
+    """C++ source without its comments and blank space at line ends (string literals kept whole), so
+    that an edit of comments alone leaves a kernel's fingerprint unchanged."""
+    out, i, n = [], 0, len(text)
+    while i < n:
+        c = text[i]
+        if c == '"':  # string literal, escapes included
+            j = i + 1
+            while j < n and text[j] != '"':
+                j += 2 if text[j] == "\\" else 1
+            out.append(text[i:j + 1])
+            i = j + 1
+        elif text.startswith("//", i):
+            j = text.find("\n", i)
+            i = n if j < 0 else j
+        elif text.startswith("/*", i):
+            j = text.find("*/", i + 2)
+            i = n if j < 0 else j + 2
+        else:
+            out.append(c)
+            i += 1
+    lines = [ln.rstrip() for ln in "".join(out).split("\n")]
+    return "\n".join(ln for ln in lines if ln)
+
+
 def source_fingerprint(kernel: str) -> str:
-    """12 hex digits of sha256 over the kernel's device sources (decode figures share one entry)."""
+    """12 hex digits of sha256 over the code of the kernel's device sources, comments excluded
+    (decode figures share one entry)."""
     import hashlib
 
     base = kernel.split("@")[0]
     base = "relation_decode_kernel" if base.startswith("relation_decode_kernel") else base
     h = hashlib.sha256()
     for f in KERNEL_SOURCES[base]:
-        with open(os.path.join(ROOT, "mote_amd", "csrc", f), "rb") as fh:
-            h.update(fh.read())
+        with open(os.path.join(ROOT, "mote_amd", "csrc", f), encoding="utf-8") as fh:
+            h.update(_code_only(fh.read()).encode())
     return h.hexdigest()[:12]
 
 

@@ -2,11 +2,10 @@
 // for the algebra; the reference's two-pass `_bwd_kv_kernel` / `_bwd_q_kernel`, :370-460, has the
 // same split of the work).
 //
-// Both kernels walk 64 x 64 blocks of the (query, key) plane with four waves per workgroup; wave w
-// owns the 32 x 32 quadrant (query half qh = w / 2, key half kh = w % 2) of every block, so a block
-// costs a quarter of the latency it would on one wave and fully masked quadrants of the diagonal
-// blocks are skipped. Operand tiles of 64 rows are staged global -> LDS with global_load_lds
-// (tiles.hpp), double-buffered.
+// Both kernels walk 64 x 64 blocks of the (query, key) plane; a wave owns a 32 x 32 quadrant (query
+// half qh, key half kh) of every block of its workgroup, so a block costs a quarter of the latency it
+// would on one wave and fully masked quadrants of the diagonal blocks are skipped. Operand tiles of
+// 64 rows are staged global -> LDS with global_load_lds (tiles.hpp).
 //
 // Per element (query i, key j < i) with U = <P1_i, P2_j> / sqrt(D), sg = sigmoid(U), L = LSE_i:
 //   w = exp(SiLU(U) - L)  (computed as exp2(U log2e sg - L log2e)),
@@ -21,10 +20,11 @@
 // LDS at the end, then the Self terms of keys that are also queries ((1 - g) dY into dI~ and
 // dU_ii P1 into dP2) and 16-byte stores.
 //
-// Query kernel (one workgroup per 64 queries, longest first): per key block S^T = K Q^T and
-// dW^T = V dI-bar^T (keys in the accumulator rows), dU^T in the accumulator layout is the permuted-k
-// B operand of dQ^T += K^T dU^T, and K^T comes from transposed reads of the K tile. The key-half
-// waves add through LDS; the Self part dU_ii P2_i joins before the store.
+// The key kernel also stores dU^T, for every visible (query block, key block) pair, in the register
+// layout of the B operand of dQ^T += K^T dU^T. Query kernel (one workgroup of eight waves per two
+// query blocks, longest first): per key block, that product with K^T from transposed reads of the
+// staged P2 tile and the stored fragments; no elementwise work and no recomputed products. The
+// key-half waves add through LDS; the Self part dU_ii P2_i joins before the store.
 #include <type_traits>
 #include <utility>
 
@@ -363,8 +363,7 @@ bwd_kv_kernel(const BwdParams p) {
 // ------------------------------------------------------------------------------------------------
 // query-stationary kernel: dP1 = (dU P2 + dU_ii P2_i) / sqrt(D) from the stored dU^T fragments
 // ------------------------------------------------------------------------------------------------
-// One workgroup per 64 queries of one (batch, head), longest first. Wave w = (qh, kh) accumulates
-// dQ^T of two query blocks per workgroup of eight waves: wave w takes key half kh = w % 2 and the
+// dQ^T of two query blocks of one (batch, head) per workgroup of eight waves: wave w takes key half kh = w % 2 and the
 // 32 queries qq = w / 2 of the pair (qq / 2 = 0: the later block, 1: the earlier one). Per key block:
 // A = K^T by transposed LDS reads of the staged P2 tile, B = the key kernel's dU^T fragments of the
 // wave's query block (16 bytes per lane, through the same ring slot). Both query blocks read one
