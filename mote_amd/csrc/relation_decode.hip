@@ -19,10 +19,10 @@
 // split counts, rows or not, so the count never depends on S. The workgroup that brings the count
 // to nsplit reads all partials back with agent-coherent loads (one batch) and finishes the head:
 // merge in a fixed order, the Self score from the new row, g = sigmoid(LSE - lam ln(S+1) - S_self),
-// Y = (1-g) I~_S + g z/l, the append of the new P2 / I~ row at S and the reset of the counter. A
-// second counter per sequence picks the last head to finish; with MOTE_DECODE_ADVANCE it adds 1 to
-// S[b]: by then every workgroup of the sequence has read S[b]. Counters start at zero (the
-// workspace is zeroed once) and every call leaves them zero.
+// Y = (1-g) I~_S + g z/l, the append of the new P2 / I~ row at S and the reset of the counter. With
+// MOTE_DECODE_ADVANCE or an xm output, a second counter per sequence picks the last head to finish:
+// it adds 1 to S[b] (by then every workgroup of the sequence has read S[b]) and writes xm. Counters start at zero (the workspace is zeroed once) and every call
+// leaves them zero.
 //
 // The new rows (graph.py:158-172) are computed by every workgroup in its prologue, under the
 // latency of the first loads: the query and the new P2 row RoPE'd at S, I~ Givens-rotated with its
@@ -386,22 +386,28 @@ relation_decode_kernel(const DecParams p) {
     }
   }
   if (tid == 0) {
-    p.g[bh] = bad ? __builtin_nanf("") : gate;
+    const float gv = bad ? __builtin_nanf("") : gate;
     __hip_atomic_store(p.cnt + bh * kDecCntStride, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // the last head of the sequence: every workgroup of the sequence has read S[b] by now. With xm
-    // the count is acquire-release, so the last head also sees every other head's g.
-    int before;
-    if (p.xm)
-      before = __hip_atomic_fetch_add(p.cnt_seq + b * kDecCntStride, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    else
-      before = __hip_atomic_fetch_add(p.cnt_seq + b * kDecCntStride, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (before == p.H - 1) {
-      __hip_atomic_store(p.cnt_seq + b * kDecCntStride, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (p.flags & MOTE_DECODE_ADVANCE) p.S[b] = S64 + 1;
-      if (p.xm) {
-        float sum = 0.f;  // fixed head order
-        for (int hh = 0; hh < p.H; ++hh) sum += p.g[b * p.H + hh];
-        p.xm[b] = sum / float(p.H);
+    // The per-sequence count only serves the advance of S and xm; without either there is nothing
+    // to count, and the last workgroup ends without waiting for an atomic's return.
+    p.g[bh] = gv;
+    if ((p.flags & MOTE_DECODE_ADVANCE) || p.xm) {
+      // the last head of the sequence: every workgroup of the sequence has read S[b] by now. With xm
+      // the count is acquire-release, so the last head also sees every other head's g (measured
+      // against g published with coherent stores and a relaxed count: 1 % slower per engine token).
+      int before;
+      if (p.xm)
+        before = __hip_atomic_fetch_add(p.cnt_seq + b * kDecCntStride, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+      else
+        before = __hip_atomic_fetch_add(p.cnt_seq + b * kDecCntStride, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (before == p.H - 1) {
+        __hip_atomic_store(p.cnt_seq + b * kDecCntStride, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (p.flags & MOTE_DECODE_ADVANCE) p.S[b] = S64 + 1;
+        if (p.xm) {
+          float sum = 0.f;  // fixed head order
+          for (int hh = 0; hh < p.H; ++hh) sum += p.g[b * p.H + hh];
+          p.xm[b] = sum / float(p.H);
+        }
       }
     }
   }
