@@ -167,6 +167,33 @@ def test_decode_exchange_mass_mean_over_heads(cuda):
         assert torch.equal(Sd.cpu(), Sv + call + 1)
 
 
+def test_decode_counts_across_mixed_calls(cuda):
+    """Calls that neither advance S nor ask for xm skip the per-sequence count; interleaved with calls
+    that do, on one workspace, every call still sees zeroed counters: S moves exactly on the advancing
+    calls, xm equals the mean of that call's g, and y / g match the oracle at the position in hand."""
+    from mote_amd.decode import decode_workspace, relation_decode
+
+    print("case decode mixed counts b4", flush=True)
+    S = [100, 4000, 1, 2049]
+    kc, vc, raw, th, inv, Sv = _setup(4, 8, 96, 4352, S, torch.bfloat16, seed=11)
+    kd, vd, Sd = kc.cuda(), vc.cuda(), Sv.cuda()
+    ws = decode_workspace(4, 8, 96, 4352, "cuda")
+    kref, vref, Sref = kc.clone(), vc.clone(), Sv.clone()
+    for call, (adv, want_xm) in enumerate([(False, False), (True, False), (False, True), (False, False),
+                                           (True, True), (False, False)]):
+        xm = torch.full((4,), float("nan"), device="cuda") if want_xm else None
+        y, gg = relation_decode(*(t.cuda() for t in raw), Sd, kd, vd, torch.tensor(0.4, device="cuda"), 2.0,
+                                inv.cuda(), th.cuda(), 0, advance=adv, workspace=ws, xm=xm)
+        torch.cuda.synchronize()
+        yr, gr, kref, vref = _oracle(kref, vref, raw, th, inv, Sref, 0, 0.4, torch.bfloat16)
+        assert rel_err(y, yr) < 2e-2 and float((gg.cpu().double() - gr).abs().max()) < 2e-2, call
+        if want_xm:
+            assert float((xm - gg.mean(-1)).abs().max()) < 1e-6, call
+        Sref = Sref + int(adv)
+        assert torch.equal(Sd.cpu(), Sref), call
+    _check_append(kd, vd, kref, vref, torch.bfloat16)
+
+
 @pytest.mark.parametrize("B,N,K,xpad", [(1, 2304, 768, 0), (16, 2304, 768, 0), (5, 768, 768, 64), (3, 48, 128, 0),
                                         (16, 64, 1024, 8)])
 def test_skinny_linear_matches_float64(cuda, B, N, K, xpad):
