@@ -28,7 +28,7 @@ struct BwdParams {
   float* duii;   // [BH][TQp]
   float* dp1acc; // [BH][TQ][D]                                 (register-staged kernels)
   float* dlam_part;  // [BH][TQp / 64]
-  void* dut;     // [BH][npairs][8][64 lanes][8] bf16: dU^T as dQ-product B fragments (tile kernels)
+  void* dut;     // [BH][npairs][4 waves][2 query tiles][64 lanes][8] bf16: dU as the key kernel's waves hold it (tile kernels)
   int64_t npairs;    // (query block, key block) pairs per (batch, head), PairTable::total
   int B, H, TQ, TK, D, q_start, TQp;
   float scale, tau_inv;

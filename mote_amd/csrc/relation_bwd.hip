@@ -735,7 +735,7 @@ static WsLayout ws_layout(const mote_relation_bwd_args* a) {
   w.wdib = o; o = align256(o + BH * TQp * DP * es);
   if (tiles) {
     w.stat = o; o = align256(o + BH * (TQp / kRowBlock) * 128 * 4);
-    // dU^T fragments: 8 KB per visible (query block, key block) pair
+    // dU fragments: 8 KB per visible (query block, key block) pair
     w.dut = o; o = align256(o + BH * size_t(PairTable::total(a->TQ, a->q_start)) * 8192);
   } else {
     w.wq = o; o = align256(o + BH * TQp * DP * es);

@@ -20,10 +20,11 @@
 // LDS at the end, then the Self terms of keys that are also queries ((1 - g) dY into dI~ and
 // dU_ii P1 into dP2) and 16-byte stores.
 //
-// The key kernel also stores dU^T, for every visible (query block, key block) pair, in the register
-// layout of the B operand of dQ^T += K^T dU^T. Query kernel (one workgroup of eight waves per two
-// query blocks, longest first): per key block, that product with K^T from transposed reads of the
-// staged P2 tile and the stored fragments; no elementwise work and no recomputed products. The
+// The key kernel also stores dU, for every visible (query block, key block) pair, in the register
+// layout its waves hold it in (keys in lanes). Query kernel (one workgroup of eight waves per two
+// query blocks, longest first): per key block, dQ^T += K^T dU^T with both operands from transposed
+// LDS reads, of the staged P2 tile and of the staged dU fragments; no elementwise work and no
+// recomputed products. The
 // key-half waves add through LDS; the Self part dU_ii P2_i joins before the store.
 #include <type_traits>
 #include <utility>
@@ -62,31 +63,32 @@ __device__ __forceinline__ float bwd_elem(float u, float dw, float lse2, float c
 
 __device__ __forceinline__ int lane_of(int li, int lg) { return 16 * lg + li; }
 
-// dU^T of the wave's quadrant as the B fragments of dQ^T += K^T dU^T (bwd_dq_kernel). au[kt] holds
-// key 16 kt + li and, in slots 4 qt + r, query 16 qt + 4 lg + r; a 16x16x16 product with the identity
-// (eye: slot r is 1 where li == 4 lg + r) moves the queries of one query tile into the accumulator
-// columns, exactly (one bf16 term per sum). Fragment qt then holds, for query 16 qt + li, keys
-// 4 lg + r (slots 0..3, kt = 0) and 16 + 4 lg + r (slots 4..7, kt = 1): the k order of tile_tr_frag.
-// One 16-byte store per lane and fragment: the wave writes 1 KB contiguous.
-__device__ __forceinline__ void store_dut(const Elem<bf16_t>::Frag (&au)[2], s16x4 eye, bf16_t* dst, int lane) {
-#pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    f32x4 t[2];
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      const bf16x8 v = au[kt].v;
-      const bf16x4 h = qt ? bf16x4{v[4], v[5], v[6], v[7]} : bf16x4{v[0], v[1], v[2], v[3]};
-      t[kt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, h), eye,
-                                                        f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-    }
-    bf16x8 o;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      o[r] = (__bf16)t[0][r];
-      o[4 + r] = (__bf16)t[1][r];
-    }
-    *reinterpret_cast<bf16x8*>(dst + qt * 512 + lane * 8) = o;
-  }
+// dU of the wave's quadrant for the dQ kernel, stored as the wave holds it: au[kt] has key 16 kt + li
+// and, in slots 4 qt + r, query 16 qt + 4 lg + r. Lane L writes two 16-byte chunks, one per query
+// tile qt: {au[0] slots 4 qt .. 4 qt + 3, au[1] slots 4 qt .. 4 qt + 3}, chunk qt at position
+// dut_pos(L) of a 1 KB region. The dQ kernel reads the transpose (queries in lanes) with
+// ds_read_b64_tr_b16 (dut_frag); dut_pos spreads the sixteen 8-byte pieces of one transposed read
+// over the banks.
+__device__ __forceinline__ int dut_pos(int L) { return L ^ (((L >> 4) & 3) << 2); }
+
+__device__ __forceinline__ void store_dut(const Elem<bf16_t>::Frag (&au)[2], bf16_t* dst, int lane) {
+  const bf16x8 v0 = au[0].v, v1 = au[1].v;
+  const int off = dut_pos(lane) * 8;
+  *reinterpret_cast<bf16x8*>(dst + off) = bf16x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+  *reinterpret_cast<bf16x8*>(dst + 512 + off) = bf16x8{v0[4], v0[5], v0[6], v0[7], v1[4], v1[5], v1[6], v1[7]};
+}
+
+// The dQ product's B fragment of query tile qt from the 2 KB that one key-kernel wave stored (staged
+// in LDS at `reg`): lane (li = 4 k + m, lg) points at key 4 lg + k of each key tile, queries
+// 16 qt + 4 m .. + 3, and receives query 16 qt + li of keys 4 lg .. 4 lg + 3 (slots 0..3, key tile 0)
+// and 16 + 4 lg .. + 3 (slots 4..7, key tile 1): the k order of tile_tr_frag.
+__device__ __forceinline__ Elem<bf16_t>::Frag dut_frag(const bf16_t* reg, int qt, int li, int lg) {
+  const int k = li >> 2, m = li & 3;
+  const bf16_t* p = reg + qt * 512 + dut_pos(16 * m + 4 * lg + k) * 8;
+  const bf16x4 lo = lds_tr4(p), hi = lds_tr4(p + 4);
+  Elem<bf16_t>::Frag f;
+  f.v = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return f;
 }
 
 __device__ __forceinline__ void store_dut_zero(bf16_t* dst, int lane) {
@@ -100,7 +102,7 @@ __device__ __forceinline__ void store_dut_zero(bf16_t* dst, int lane) {
 template <int DP, bool MASKED>
 __device__ __forceinline__ void kv_block(const bf16_t* Qs, const bf16_t* Ds, const float* Ss, const bf16_t* Ks,
                                          const bf16_t* Vs, f32x4 (&dvacc)[2][DP / 16], f32x4 (&dkacc)[2][DP / 16],
-                                         bf16_t* dut_w, s16x4 eye, int qh, int kh, int li, int lg, int key0, int qa0,
+                                         bf16_t* dut_w, int qh, int kh, int li, int lg, int key0, int qa0,
                                          float nc2, float scale) {
   using E = Elem<bf16_t>;
   using Frag = E::Frag;
@@ -181,9 +183,10 @@ __device__ __forceinline__ void kv_block(const bf16_t* Qs, const bf16_t* Ds, con
       dkacc[kt][dt] = E::mma(au[kt], bq, dkacc[kt][dt]);
     }
   }
-  // both key tiles' dU^T in one 16-byte store per fragment (two 8-byte stores per key tile, made as
-  // each tile finishes, ran the key kernel 20 % slower)
-  if (dut_w) store_dut(au, eye, dut_w, lane_of(li, lg));
+  // both key tiles' dU in two 16-byte stores per lane (two 8-byte stores per key tile, made as each
+  // tile finishes, ran the key kernel 20 % slower; the transpose into the dQ product's B layout by
+  // identity products here, 1.5 % slower than the transposed reads in the dQ kernel)
+  if (dut_w) store_dut(au, dut_w, lane_of(li, lg));
 }
 
 template <int DP>
@@ -239,12 +242,9 @@ bwd_kv_kernel(const BwdParams p) {
   // PairTable::offset(qb) for the block in hand, advanced by qb + A per block (offset(qb + 1) - offset(qb))
   const int pair_a = (p.q_start + 126) / 64;
   int64_t pair_off = PairTable::offset(qb_lo, p.q_start);
-  // dU^T fragments of this key block: pair (qb, kb) at PairTable::offset(qb) + kb, 8 fragments of
-  // 64 lanes x 8 bf16 each, fragment kh * 4 + query tile; the wave writes fragments (kh, 2 qh + qt)
+  // dU of this key block: pair (qb, kb) at PairTable::offset(qb) + kb, 8 KB per pair; wave (kh, qh)
+  // writes its 2 KB at (kh * 4 + 2 qh) * 512 elements (store_dut)
   bf16_t* dut_bh = reinterpret_cast<bf16_t*>(p.dut) + int64_t(bh) * p.npairs * 4096 + (kh * 4 + 2 * qh) * 512;
-  s16x4 eye;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) eye[r] = li == 4 * lg + r ? short(0x3F80) : short(0);
   {
     // the key rows once (rows past the keys: finite copies whose results are never stored)
     const bf16_t* ksrc[2] = {kbase, vbase};
@@ -273,7 +273,7 @@ bwd_kv_kernel(const BwdParams p) {
     pair_off += qb + pair_a;  // PairTable::offset(qb + 1)
     // quadrant visible at all (some key < some query position), and not wholly padding rows
     if (i0 < p.TQ && key0 < qa0 + 31)
-      kv_block<DP, decltype(masked)::value>(Qs, Ds, Ss, kvs, kvs + TILE, dvacc, dkacc, dut_w, eye, qh, kh, li, lg,
+      kv_block<DP, decltype(masked)::value>(Qs, Ds, Ss, kvs, kvs + TILE, dvacc, dkacc, dut_w, qh, kh, li, lg,
                                             key0, qa0, nc2, p.scale);
     else if (dut_w)
       store_dut_zero(dut_w, lane);
@@ -361,12 +361,12 @@ bwd_kv_kernel(const BwdParams p) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// query-stationary kernel: dP1 = (dU P2 + dU_ii P2_i) / sqrt(D) from the stored dU^T fragments
+// query-stationary kernel: dP1 = (dU P2 + dU_ii P2_i) / sqrt(D) from the stored dU fragments
 // ------------------------------------------------------------------------------------------------
 // dQ^T of two query blocks of one (batch, head) per workgroup of eight waves: wave w takes key half kh = w % 2 and the
 // 32 queries qq = w / 2 of the pair (qq / 2 = 0: the later block, 1: the earlier one). Per key block:
-// A = K^T by transposed LDS reads of the staged P2 tile, B = the key kernel's dU^T fragments of the
-// wave's query block (16 bytes per lane, through the same ring slot). Both query blocks read one
+// A = K^T by transposed LDS reads of the staged P2 tile, B = dU^T by transposed LDS reads of the 2 KB
+// the key kernel's wave (kh, qh) stored for the wave's query block (through the same ring slot). Both query blocks read one
 // staged P2 tile: staging it is the kernel's largest cost (the L2 -> LDS path, shared by the CU),
 // and 128 queries per workgroup stage it half as often as 64. No elementwise work: NS key blocks in
 // flight (P2 tiles and fragments in an NS-deep LDS ring; the loop is unrolled by NS so every slot
@@ -405,7 +405,7 @@ __global__ void __launch_bounds__(512) bwd_dq_kernel(const BwdParams p) {
   const int nkb = PairTable::nkb(qtop, p.TQ, p.q_start);                   // the workgroup's key blocks
   const int nkb_w = PairTable::nkb(qbw, p.TQ, p.q_start);                  // the wave's (addresses)
   const int nkb_c = wq ? nkb_w : 0;                                        // the wave's (products)
-  // the wave's two fragments (kh, 2 qh) and (kh, 2 qh + 1) of each pair: 2 KB contiguous
+  // the 2 KB of each pair that the key kernel's wave (kh, qh) stored
   const int fo = (kh * 4 + 2 * qh) * 512;
   const bf16_t* fr = reinterpret_cast<const bf16_t*>(p.dut) +
                      (int64_t(bh) * p.npairs + PairTable::offset(qbw, p.q_start)) * 4096 + fo + lane * 8;
@@ -474,7 +474,7 @@ __global__ void __launch_bounds__(512) bwd_dq_kernel(const BwdParams p) {
     const bf16_t* Ks = ring + U * SLOT;
     Frag bf[2];
 #pragma unroll
-    for (int s = 0; s < 2; ++s) bf[s] = E::load8(Ks + fslot + s * 512 + lane * 8);
+    for (int s = 0; s < 2; ++s) bf[s] = dut_frag(Ks + fslot, s, li, lg);
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
       const Frag ak = tile_tr_frag<DP>(Ks, 32 * kh, dt, li, lg);
