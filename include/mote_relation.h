@@ -374,6 +374,11 @@ typedef struct mote_skinny_gemm_args {
   const void* w; int64_t w_sr;
   void* y; int64_t y_sr;
   const unsigned char* run;  /* predicate as in mote_relation_decode_args, or NULL */
+  /* Optional side job for the decode step that precedes this launch: xm[b] = the mean of
+   * g[b * heads .. b * heads + heads - 1] in head order, b < B (graph.py:186), when xm is not NULL.
+   * The decode step's g is complete by then (stream order), so the decode launch needs no count of
+   * finished heads for xm. Written only when the launch runs (run). */
+  const float* g; float* xm; int heads;
 } mote_skinny_gemm_args;
 
 int mote_skinny_gemm(const mote_skinny_gemm_args* args, void* stream);

@@ -131,6 +131,7 @@ class SkinnyGemmArgs(C.Structure):
         ("dtype", C.c_int), ("B", C.c_int), ("N", C.c_int), ("K", C.c_int),
         ("x", C.c_void_p), ("x_sr", C.c_int64), ("w", C.c_void_p), ("w_sr", C.c_int64),
         ("y", C.c_void_p), ("y_sr", C.c_int64), ("run", C.c_void_p),
+        ("g", C.c_void_p), ("xm", C.c_void_p), ("heads", C.c_int),
     ]
 
 

@@ -9,7 +9,9 @@
 //   its W rows and x rows issued before the first product (A fragment: lane (r = l % 16, q = l / 16)
 //   holds W[n0 + r][k + 8q .. +8], 64-byte runs per row; B fragment: x[b = l % 16][k + 8q .. +8],
 //   zero for b >= B); the four partial tiles add through LDS in a fixed order and wave 0 rounds and
-//   stores y[b][n0 + r] for b < B.
+//   stores y[b][n0 + r] for b < B. Optionally workgroup 0 also writes the decode step's exchange mass
+//   xm[b], the mean of g[b] over the heads (the decode launch then needs no count of its finished
+//   heads for it).
 #include "common.hpp"
 #include "params.hpp"
 
@@ -23,7 +25,8 @@ struct SkinnyParams {
   const bf16_t* w; int64_t w_sr;
   bf16_t* y; int64_t y_sr;
   const unsigned char* run;  // predicate: 0 -> the launch writes nothing (null: always run)
-  int B, N, K;
+  const float* g; float* xm;  // optional: xm[b] = mean of g[b][0 .. heads) (the decode step's exchange mass)
+  int B, N, K, heads;
 };
 
 template <int KS>
@@ -48,9 +51,17 @@ __global__ void __launch_bounds__(64 * kSkWaves) skinny_gemm_kernel(const Skinny
       bx[s] = E::load8(xrow + 32 * s);
     }
   }
+  // the decode step's exchange mass (graph.py:186) on the side: workgroup 0, wave 1, lane b < B
+  // sums g[b][0 .. heads) in head order
+  const int xb = int(threadIdx.x) - 64;
+  const bool xm_lane = p.xm != nullptr && blockIdx.x == 0 && xb >= 0 && xb < p.B;
+  float gsum = 0.f;
+  if (xm_lane)
+    for (int h = 0; h < p.heads; ++h) gsum += p.g[int64_t(xb) * p.heads + h];
   // the predicate after the loads are issued (reads are harmless); uniform, so the whole
   // workgroup leaves before its barrier
   if (p.run && p.run[0] == 0) return;
+  if (xm_lane) p.xm[xb] = gsum / float(p.heads);
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
@@ -84,6 +95,8 @@ int launch_skinny_gemm(const mote_skinny_gemm_args* a, hipStream_t stream) {
                      a->N, a->K, 32 * kSkWaves * kSkMaxKs);
   if (a->B == 0) return MOTE_OK;
   if (!a->x || !a->w || !a->y) return set_error(MOTE_ERR_ARGUMENT, "skinny_gemm: null pointer");
+  if (a->xm && (!a->g || a->heads <= 0))
+    return set_error(MOTE_ERR_ARGUMENT, "skinny_gemm: xm needs g and heads > 0");
   if (reinterpret_cast<uintptr_t>(a->x) % 16 || reinterpret_cast<uintptr_t>(a->w) % 16 || (a->x_sr * 2) % 16 ||
       (a->w_sr * 2) % 16 || reinterpret_cast<uintptr_t>(a->y) % 2)
     return set_error(MOTE_ERR_ARGUMENT, "skinny_gemm: x and W rows must start on 16-byte boundaries");
@@ -94,6 +107,7 @@ int launch_skinny_gemm(const mote_skinny_gemm_args* a, hipStream_t stream) {
   p.w = reinterpret_cast<const bf16_t*>(a->w); p.w_sr = a->w_sr;
   p.y = reinterpret_cast<bf16_t*>(a->y); p.y_sr = a->y_sr;
   p.run = a->run;
+  p.g = a->xm ? a->g : nullptr; p.xm = a->xm; p.heads = a->xm ? a->heads : 0;
   p.B = a->B; p.N = a->N; p.K = a->K;
   const int nks = a->K / (32 * kSkWaves);
   const dim3 grid(unsigned(a->N / 16)), block(64 * kSkWaves);

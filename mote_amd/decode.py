@@ -123,10 +123,12 @@ def relation_decode(p1: torch.Tensor, p2: torch.Tensor, info: torch.Tensor, S: t
 
 
 def skinny_linear(x: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] = None,
-                  run: Optional[torch.Tensor] = None) -> torch.Tensor:
+                  run: Optional[torch.Tensor] = None, g: Optional[torch.Tensor] = None,
+                  xm: Optional[torch.Tensor] = None) -> torch.Tensor:
     """y [B, N] = x [B, K] w[N, K]^T for the decode engine's per-token projections (bf16, B <= 16,
     N % 16 == 0, K % 128 == 0, K <= 1024): one launch of mote_skinny_gemm. With `run` (a device
-    flag) the launch leaves `out` untouched when the flag is 0."""
+    flag) the launch leaves `out` untouched when the flag is 0. With g (fp32 [B, H], contiguous) and
+    xm (fp32 [B]) the same launch writes xm[b] = mean of g[b] in head order (graph.py:186)."""
     B, K = x.shape
     N = w.shape[0]
     if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
@@ -142,6 +144,12 @@ def skinny_linear(x: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] 
     a.w, a.w_sr = w.data_ptr(), w.stride(0)
     a.y, a.y_sr = out.data_ptr(), out.stride(0)
     a.run = L.ptr(run)
+    if xm is not None:
+        if (g is None or g.dtype != torch.float32 or xm.dtype != torch.float32 or not g.is_contiguous()
+                or not xm.is_contiguous() or g.dim() != 2 or g.shape[0] != B or xm.numel() != B
+                or g.device != x.device or xm.device != x.device):
+            raise ValueError("skinny_linear: xm needs fp32 contiguous g [B, H] and xm [B] on x's device")
+        a.g, a.xm, a.heads = g.data_ptr(), xm.data_ptr(), g.shape[1]
     L.check(L.lib().mote_skinny_gemm(a, L.stream_of(x)), "mote_skinny_gemm")
     return out
 
@@ -227,15 +235,17 @@ class RelationDecodeStep:
             q = m.p1_norm(qkv[:, 0])
             k = m.p2_norm(qkv[:, 1])
             qkv = torch.stack([q, k, qkv[:, 2]], dim=1)
+        # on the skinny path the wo launch writes xm (its mean of g needs no count of finished heads
+        # in the decode launch)
         relation_decode(qkv[:, 0], qkv[:, 1], qkv[:, 2], S, self.arena.p2(self.layer), self.arena.info(self.layer),
                         self.lam, m.tau_s, self.inv_freq, self.theta, m.layer_idx, advance, self.workspace,
-                        self.y, self.g, xm, run)
+                        self.y, self.g, None if skinny else xm, run)
         if skinny:  # _out (relation.py:176-182) on the skinny product
             y = self.y.to(x.dtype).reshape(B, H * dh)
             if m.out_gate:
                 gbuf = self._static("gate", (B, Dm), x.dtype) if run is not None else None
                 y = y * torch.sigmoid(skinny_linear(x.reshape(B, Dm), m.wg.weight, gbuf, run))
             obuf = self._static("out", (B, Dm), x.dtype) if run is not None else None
-            return skinny_linear(y, m.wo.weight, obuf, run).view(B, 1, Dm), xm
+            return skinny_linear(y, m.wo.weight, obuf, run, g=self.g, xm=xm).view(B, 1, Dm), xm
         y = self.y.to(x.dtype).view(B, H, 1, dh)
         return m._out(y, x), xm

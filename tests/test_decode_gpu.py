@@ -246,3 +246,30 @@ def test_decode_step_skinny_path_matches_library_path(cuda):
     assert rel_err(o1, o2) < 2e-2, rel_err(o1, o2)
     assert float((x1 - x2).abs().max()) < 2e-2
     assert rel_err(b1, b2) < 2e-2 and torch.equal(s1, s2)
+
+
+def test_skinny_linear_writes_the_exchange_mass(cuda):
+    """The skinny product's side job: xm[b] = mean of g[b] over the heads in head order, the same
+    arithmetic as the decode launch's own xm; nothing written when the predicate is 0."""
+    from mote_amd.decode import skinny_linear
+
+    print("case skinny xm", flush=True)
+    g0 = torch.Generator().manual_seed(3)
+    x = torch.randn(5, 768, generator=g0).bfloat16().cuda()
+    w = torch.randn(768, 768, generator=g0).bfloat16().cuda()
+    g = torch.rand(5, 8, generator=g0).cuda()
+    xm = torch.full((5,), float("nan"), device="cuda")
+    y = skinny_linear(x, w, g=g, xm=xm)
+    torch.cuda.synchronize()
+    want = torch.zeros(5)
+    for h in range(8):
+        want = want + g.cpu()[:, h]
+    assert torch.equal(xm.cpu(), want / 8.0)
+    assert torch.equal(y, skinny_linear(x, w))
+    run = torch.zeros(1, dtype=torch.uint8, device="cuda")
+    xm2 = torch.full((5,), 7.0, device="cuda")
+    skinny_linear(x, w, torch.empty_like(y), run, g=g, xm=xm2)
+    torch.cuda.synchronize()
+    assert bool((xm2 == 7.0).all())
+    with pytest.raises(ValueError):
+        skinny_linear(x, w, g=None, xm=xm)
