@@ -185,7 +185,7 @@ __device__ __forceinline__ void kv_block(const bf16_t* Qs, const bf16_t* Ds, con
   }
   // both key tiles' dU in two 16-byte stores per lane (two 8-byte stores per key tile, made as each
   // tile finishes, ran the key kernel 20 % slower; the transpose into the dQ product's B layout by
-  // identity products here, 1.5 % slower than the transposed reads in the dQ kernel)
+  // identity products here ran the key kernel 2 % slower than the transposed reads in the dQ kernel)
   if (dut_w) store_dut(au, dut_w, lane_of(li, lg));
 }
 
