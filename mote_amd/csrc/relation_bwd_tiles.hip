@@ -64,18 +64,16 @@ __device__ __forceinline__ float bwd_elem(float u, float dw, float lse2, float c
 __device__ __forceinline__ int lane_of(int li, int lg) { return 16 * lg + li; }
 
 // dU of the wave's quadrant for the dQ kernel, stored as the wave holds it: au[kt] has key 16 kt + li
-// and, in slots 4 qt + r, query 16 qt + 4 lg + r. Lane L writes two 16-byte chunks, one per query
-// tile qt: {au[0] slots 4 qt .. 4 qt + 3, au[1] slots 4 qt .. 4 qt + 3}, chunk qt at position
-// dut_pos(L) of a 1 KB region. The dQ kernel reads the transpose (queries in lanes) with
-// ds_read_b64_tr_b16 (dut_frag); dut_pos spreads the sixteen 8-byte pieces of one transposed read
-// over the banks.
+// and, in slots 4 qt + r, query 16 qt + 4 lg + r. Lane L writes au[kt] whole, one 16-byte chunk per
+// key tile at position dut_pos(L) of the tile's 1 KB region. The dQ kernel reads the transpose
+// (queries in lanes) with ds_read_b64_tr_b16 (dut_frag); dut_pos spreads the sixteen 8-byte pieces
+// of one transposed read over the banks.
 __device__ __forceinline__ int dut_pos(int L) { return L ^ (((L >> 4) & 3) << 2); }
 
 __device__ __forceinline__ void store_dut(const Elem<bf16_t>::Frag (&au)[2], bf16_t* dst, int lane) {
-  const bf16x8 v0 = au[0].v, v1 = au[1].v;
   const int off = dut_pos(lane) * 8;
-  *reinterpret_cast<bf16x8*>(dst + off) = bf16x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-  *reinterpret_cast<bf16x8*>(dst + 512 + off) = bf16x8{v0[4], v0[5], v0[6], v0[7], v1[4], v1[5], v1[6], v1[7]};
+  *reinterpret_cast<bf16x8*>(dst + off) = au[0].v;
+  *reinterpret_cast<bf16x8*>(dst + 512 + off) = au[1].v;
 }
 
 // The dQ product's B fragment of query tile qt from the 2 KB that one key-kernel wave stored (staged
@@ -84,8 +82,8 @@ __device__ __forceinline__ void store_dut(const Elem<bf16_t>::Frag (&au)[2], bf1
 // and 16 + 4 lg .. + 3 (slots 4..7, key tile 1): the k order of tile_tr_frag.
 __device__ __forceinline__ Elem<bf16_t>::Frag dut_frag(const bf16_t* reg, int qt, int li, int lg) {
   const int k = li >> 2, m = li & 3;
-  const bf16_t* p = reg + qt * 512 + dut_pos(16 * m + 4 * lg + k) * 8;
-  const bf16x4 lo = lds_tr4(p), hi = lds_tr4(p + 4);
+  const bf16_t* p = reg + dut_pos(16 * m + 4 * lg + k) * 8 + qt * 4;
+  const bf16x4 lo = lds_tr4(p), hi = lds_tr4(p + 512);
   Elem<bf16_t>::Frag f;
   f.v = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   return f;
@@ -93,7 +91,7 @@ __device__ __forceinline__ Elem<bf16_t>::Frag dut_frag(const bf16_t* reg, int qt
 
 __device__ __forceinline__ void store_dut_zero(bf16_t* dst, int lane) {
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) *reinterpret_cast<bf16x8*>(dst + qt * 512 + lane * 8) = bf16x8{};
+  for (int kt = 0; kt < 2; ++kt) *reinterpret_cast<bf16x8*>(dst + kt * 512 + lane * 8) = bf16x8{};
 }
 
 // ------------------------------------------------------------------------------------------------
