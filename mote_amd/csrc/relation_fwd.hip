@@ -448,12 +448,15 @@ __device__ __forceinline__ void fwd_softmax_pv(const bf16_t* Vs, const f32x4 (&s
       for (int r = 0; r < 4; ++r) mx = fmaxf(mx, keep[s][kt][r] ? sacc[kt][s][r] : kNegInf);
     bnd[s] = mx;
   }
-  lanegroup_max2(bnd[0], bnd[1]);
-#pragma unroll
-  for (int s = 0; s < 2; ++s) bnd[s] = fmaxf(bnd[s] * c2, 0.f);
-  const bool need = (bnd[0] > m_run[0] + kRescale) || (bnd[1] > m_run[1] + kRescale);
+  // Whether any query's bound exceeds its reference by the slack needs no reduction over the lane
+  // groups: some lane's own maximum exceeds it exactly when the query's maximum does (c2 > 0 and the
+  // reference is at least 0). The query's maximum is formed only in the rare rescale branch.
+  const bool need = (bnd[0] * c2 > m_run[0] + kRescale) || (bnd[1] * c2 > m_run[1] + kRescale);
   if (__ballot(need) != 0ull) {
     asm volatile("" ::: "memory");  // a real branch: the rescale is rare
+    lanegroup_max2(bnd[0], bnd[1]);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) bnd[s] = fmaxf(bnd[s] * c2, 0.f);
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       const float mn = bnd[s] > m_run[s] + kRescale ? bnd[s] : m_run[s];
