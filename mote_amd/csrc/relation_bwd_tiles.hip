@@ -35,17 +35,6 @@
 
 namespace mote {
 
-// f(integral_constant<int, 0>), ..., f(integral_constant<int, N - 1>): a loop whose index is a
-// compile-time constant in every iteration.
-template <typename F, int... I>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
-  (f(std::integral_constant<int, I>{}), ...);
-}
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-  static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-
 // Elementwise core shared by both kernels: raw dot u, raw dW, row terms (lse2 = L log2e,
 // c = dA - Delta). Returns dU; w through the reference.
 __device__ __forceinline__ float bwd_elem(float u, float dw, float lse2, float c, float nc2, float scale, bool keep,

@@ -600,8 +600,10 @@ relation_fwd_tile_kernel(const FwdParams p) {
   if (kb_lo < kb_hi && NSTG > 2) issue_kb(kb_lo + 1, 1);
   // key blocks wholly before the workgroup's first query position first (unmasked block math), then
   // the diagonal ones (masked): two loops keep one register assignment of the accumulators each
-  int slot = 0;
-  auto step = [&](int kb, auto masked) {
+  // slotv: the block's ring slot, (kb - kb_lo) % NSTG, a constant in the unmasked loop's rounds of
+  // NSTG blocks (the LDS offsets of the block's reads then fold into the read instructions)
+  auto step = [&](int kb, auto masked, auto slotv) {
+    const int slot = slotv;
     MOTE_STAMP(0, kb);
     __builtin_amdgcn_s_waitcnt(kVmWaitStage<(NSTG - 2) * PER>());  // this wave's part of block kb is in
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0) only (vmcnt and expcnt at their maxima)
@@ -618,12 +620,20 @@ relation_fwd_tile_kernel(const FwdParams p) {
                                                   lg);
     }
     MOTE_STAMP(2, kb);
-    slot = slot + 1 == NSTG ? 0 : slot + 1;
   };
   const int kb_m = min(kb_hi, (qs + qb * 64) / 64);
   int kb = kb_lo;
-  for (; kb < kb_m; ++kb) step(kb, std::false_type{});
-  for (; kb < kb_hi; ++kb) step(kb, std::true_type{});
+  for (; kb + NSTG <= kb_m; kb += NSTG)
+    static_for<NSTG>([&](auto u) { step(kb + decltype(u)::value, std::false_type{}, u); });
+  int slot = 0;  // (kb - kb_lo) % NSTG after whole rounds
+  for (; kb < kb_m; ++kb) {
+    step(kb, std::false_type{}, slot);
+    slot = slot + 1 == NSTG ? 0 : slot + 1;
+  }
+  for (; kb < kb_hi; ++kb) {
+    step(kb, std::true_type{}, slot);
+    slot = slot + 1 == NSTG ? 0 : slot + 1;
+  }
 
   // row sums: row 0 of lacc, held by lanes 0..15 (query li); broadcast to the other lane groups
   float l_run[2];

@@ -18,9 +18,23 @@
 // row r0+k, columns [d0+4m, d0+4m+4) hands lane i the column d0+i of rows r0..r0+3.
 #pragma once
 
+#include <type_traits>
+#include <utility>
+
 #include "common.hpp"
 
 namespace mote {
+
+// f(integral_constant<int, 0>), ..., f(integral_constant<int, N - 1>): a loop whose index is a
+// compile-time constant in every iteration.
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 // s_waitcnt immediate (gfx9 encoding) that waits until at most N vector-memory operations of the
 // wave are outstanding, leaving the export and LDS/scalar counters unconstrained. Vector loads
