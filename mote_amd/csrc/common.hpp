@@ -90,6 +90,42 @@ __device__ __forceinline__ float lanegroup_sum(float x) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// DPP lane moves (gfx9 dpp_ctrl encodings), cheaper than a ds_bpermute shuffle: quad_perm [1,0,3,2]
+// and [2,3,0,1] read lane ^ 1 and lane ^ 2; within a row of 16 lanes, row_ror:8 reads lane ^ 8 and
+// row_ror:12 (a rotation by 12 to higher lanes) reads lane + 4 mod 16, which is lane ^ 4 for the
+// lanes whose bit 2 is clear.
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppNext4 = 0x12C, kDppRor8 = 0x128;
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+// Sum / max over the 64 lanes in the order of the xor butterfly 32, 16, 8, 4, 2, 1. The max reaches
+// every lane; the sum is the butterfly's in lanes 0-3 (the others hold other partial sums).
+__device__ __forceinline__ float wave_sum_lane0(float x) {
+  unsigned u = __float_as_uint(x);
+  u32x2 a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  u = __float_as_uint(x);
+  a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  x += dpp<kDppRor8>(x);
+  x += dpp<kDppNext4>(x);
+  x += dpp<kDppXor2>(x);
+  return x + dpp<kDppXor1>(x);
+}
+__device__ __forceinline__ float wave_max(float x) {
+  unsigned u = __float_as_uint(x);
+  u32x2 a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  u = __float_as_uint(x);
+  a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  x = fmaxf(x, dpp<kDppRor8>(x));
+  x = fmaxf(x, dpp<kDppNext4>(x));
+  x = fmaxf(x, dpp<kDppXor2>(x));
+  return fmaxf(x, dpp<kDppXor1>(x));
+}
+
 // ------------------------------------------------------------------------------------------------
 // Element traits: fragments and the K32 matrix step
 // ------------------------------------------------------------------------------------------------

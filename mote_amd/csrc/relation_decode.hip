@@ -116,6 +116,11 @@ relation_decode_kernel(const DecParams p) {
   int vzero;
   asm volatile("v_mov_b32 %0, 0" : "=v"(vzero));
   const float lam = p.lam[vzero];
+  // S and the predicate byte also go before the cache loads (whose addresses do not depend on
+  // them): the new rows and the predicate's test then wait for none of the cache loads. Without a
+  // predicate any valid byte is read.
+  const int64_t S64 = p.S[b + vzero];
+  const int run_v = (p.run ? p.run : reinterpret_cast<const unsigned char*>(p.lam))[vzero];
   // Written as integer arithmetic: the compiler turns selects here into branches, and a branch
   // would split the kernel-argument loads over two waits.
   const int odd = h & 1, par = p.parity;
@@ -160,12 +165,12 @@ relation_decode_kernel(const DecParams p) {
   fetch(0, I0{});
   fetch(1, I1{});
   fetch(2, I2{});
+  asm volatile("" ::: "memory");  // keeps the predicate's test (an early exit) after the cache loads
 
-  const int64_t S64 = p.S[b];  // after the cache loads: their addresses do not depend on it
   // The predicate (a device flag, e.g. the router's boundary bit): with 0 every workgroup leaves
   // here, before any write, count or barrier, so a captured step costs one empty launch when the
   // chunk is not a boundary (graph.py:224-226 skips the step with a conditional node instead).
-  if (p.run && p.run[0] == 0) return;
+  if (p.run && run_v == 0) return;
   const bool bad = S64 < 0 || S64 >= p.cap;
   const int S = bad ? 0 : int(S64);
 
@@ -225,8 +230,8 @@ relation_decode_kernel(const DecParams p) {
       for (int j = 0; j < EPC; ++j) dot2[j & 1] = fmaf(E::to_f(e[j]), qv[k][j], dot2[j & 1]);
     }
     float dot = dot2[0] + dot2[1];
-    dot += __shfl_xor(dot, 1, 64);
-    dot += __shfl_xor(dot, 2, 64);
+    dot += dpp<kDppXor1>(dot);  // the row's four lanes: the sum of xor 1 then xor 2 in every lane
+    dot += dpp<kDppXor2>(dot);
     const int row = (split + jstep * nsp) * kDecRows + roff;
     if (row < S) {
       const float u2 = dot * c2;
@@ -262,9 +267,11 @@ relation_decode_kernel(const DecParams p) {
   }
 
   // ---- merge of the 64 row groups (lanes of one row group hold the same m and l) ----
-  float mw = m;
-#pragma unroll
-  for (int msk = 4; msk <= 32; msk <<= 1) mw = fmaxf(mw, __shfl_xor(mw, msk, 64));
+  // over the wave's 16 row groups (lanes with equal lane & 3), in lane 0 the xor butterfly 4, 8, 16,
+  // 32: lane + 4 and lane ^ 8 within the row give lane 0 the partners xor 4 / 8 would, then the row
+  // swaps
+  float mw = fmaxf(m, dpp<kDppNext4>(m));
+  mw = lanegroup_max(fmaxf(mw, dpp<kDppRor8>(mw)));
   if (lane == 0) sm[wave] = mw;
   __syncthreads();
   float M = sm[0];
@@ -272,8 +279,8 @@ relation_decode_kernel(const DecParams p) {
   for (int w = 1; w < kDecWaves; ++w) M = fmaxf(M, sm[w]);
   const float a = fexp2(m - (M == kNegInf ? 0.f : M));  // 0 for a row group without rows
   float lw = l * a;
-#pragma unroll
-  for (int msk = 4; msk <= 32; msk <<= 1) lw += __shfl_xor(lw, msk, 64);
+  lw += dpp<kDppNext4>(lw);
+  lw = lanegroup_sum(lw + dpp<kDppRor8>(lw));
   if (lane == 0) sl[wave] = lw;
   float* zg = zred + roff * ZS;
 #pragma unroll
@@ -343,15 +350,11 @@ relation_decode_kernel(const DecParams p) {
   if (wave == 0) {
     // split weights 2^(m_s - Mh) and L = sum_s l_s 2^(m_s - Mh), one split per lane
     const float ms = lane < nsp ? zred[lane * stride] : kNegInf;
-    float mx = ms;
-#pragma unroll
-    for (int msk = 32; msk >= 1; msk >>= 1) mx = fmaxf(mx, __shfl_xor(mx, msk, 64));
+    const float mx = wave_max(ms);
     const float Mh = mx == kNegInf ? 0.f : mx;
     const float w = fexp2(ms - Mh);
     if (lane < nsp) wsp[lane] = w;
-    float ls = lane < nsp ? zred[lane * stride + 1] * w : 0.f;
-#pragma unroll
-    for (int msk = 32; msk >= 1; msk >>= 1) ls += __shfl_xor(ls, msk, 64);
+    const float ls = wave_sum_lane0(lane < nsp ? zred[lane * stride + 1] * w : 0.f);
     if (lane == 0) {
       sML[0] = Mh;
       sML[1] = ls;
@@ -360,8 +363,7 @@ relation_decode_kernel(const DecParams p) {
     // Self score U_SS = <q, P2_S> / sqrt(D)
     float u = 0.f;
     for (int d = lane; d < D; d += 64) u = fmaf(sq[d], knew[d], u);
-#pragma unroll
-    for (int msk = 32; msk >= 1; msk >>= 1) u += __shfl_xor(u, msk, 64);
+    u = wave_sum_lane0(u);
     if (lane == 0) sML[2] = u;
   }
   __syncthreads();
