@@ -202,9 +202,10 @@ __global__ void __launch_bounds__(256) rope_givens_bwd_kernel(const RopeBwdParam
 }
 
 // d theta: one block per pair; thread j sums partials j, j + 256, ... (eight loads in flight per
-// batch), then a fixed tree over the block: the order is fixed, so the result is reproducible.
+// batch), then each wave's lanes in a fixed butterfly (row swaps and DPP moves) and the four waves in
+// order: the order is fixed, so the result is reproducible.
 __global__ void __launch_bounds__(256) sum_partials_kernel(const float* partial, int rows, int npair, float* out) {
-  __shared__ float red[256];
+  __shared__ float red[4];
   const int tid = threadIdx.x, pr = blockIdx.x;
   float acc = 0.f;
   for (int base = 0; base < rows; base += 256 * 8) {
@@ -215,13 +216,10 @@ __global__ void __launch_bounds__(256) sum_partials_kernel(const float* partial,
     for (int m = 0; m < 8; ++m)
       if (base + m * 256 + tid < rows) acc += v[m];
   }
-  red[tid] = acc;
+  acc = wave_sum_lane0(acc);
+  if ((tid & 63) == 0) red[tid >> 6] = acc;
   __syncthreads();
-  for (int w = 128; w >= 1; w >>= 1) {
-    if (tid < w) red[tid] += red[tid + w];
-    __syncthreads();
-  }
-  if (tid == 0) out[pr] = red[0];
+  if (tid == 0) out[pr] = (red[0] + red[1]) + (red[2] + red[3]);
 }
 
 // ------------------------------------------------------------------------------------------------
