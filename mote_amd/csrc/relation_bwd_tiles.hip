@@ -35,21 +35,6 @@
 
 namespace mote {
 
-// Elementwise core shared by both kernels: raw dot u, raw dW, row terms (lse2 = L log2e,
-// c = dA - Delta). Returns dU; w through the reference.
-__device__ __forceinline__ float bwd_elem(float u, float dw, float lse2, float c, float nc2, float scale, bool keep,
-                                          float& w) {
-  const float t = u * nc2;                 // -U log2e
-  const float sg = frcp(1.0f + fexp2(t));  // sigmoid(U)
-  float wv = fexp2(-fmaf(t, sg, lse2));    // exp2(U log2e sg - lse2)
-  wv = keep ? wv : 0.f;
-  const float de = wv * (dw + c);
-  const float e = (u * scale) * sg;        // SiLU(U)
-  const float sp = fmaf(e, 1.0f - sg, sg); // SiLU'(U)
-  w = wv;
-  return de * sp;
-}
-
 __device__ __forceinline__ int lane_of(int li, int lg) { return 16 * lg + li; }
 
 // dU of the wave's quadrant for the dQ kernel, stored as the wave holds it: au[kt] has key 16 kt + li
@@ -90,7 +75,7 @@ template <int DP, bool MASKED>
 __device__ __forceinline__ void kv_block(const bf16_t* Qs, const bf16_t* Ds, const float* Ss, const bf16_t* Ks,
                                          const bf16_t* Vs, f32x4 (&dvacc)[2][DP / 16], f32x4 (&dkacc)[2][DP / 16],
                                          bf16_t* dut_w, int qh, int kh, int li, int lg, int key0, int qa0,
-                                         float nc2, float scale) {
+                                         float nc2) {
   using E = Elem<bf16_t>;
   using Frag = E::Frag;
   constexpr int KS = DP / 32, DT = DP / 16;
@@ -261,7 +246,7 @@ bwd_kv_kernel(const BwdParams p) {
     // quadrant visible at all (some key < some query position), and not wholly padding rows
     if (i0 < p.TQ && key0 < qa0 + 31)
       kv_block<DP, decltype(masked)::value>(Qs, Ds, Ss, kvs, kvs + TILE, dvacc, dkacc, dut_w, qh, kh, li, lg,
-                                            key0, qa0, nc2, p.scale);
+                                            key0, qa0, nc2);
     else if (dut_w)
       store_dut_zero(dut_w, lane);
     MOTE_STAMP(2, qb - qb_lo);
