@@ -44,6 +44,12 @@ const char* mote_last_error(void);
 /* Library version and the GPU architecture its kernels were built for ("gfx950"). */
 const char* mote_version(void);
 
+/* The layout of every argument struct below as this library was compiled: one line per struct,
+ * "name size;field offset size;..." (bytes, fields in declaration order), so a binding that mirrors
+ * the structs by hand (ctypes, cgo, JNI) can check itself against the library it loads. No
+ * counterpart in the reference, whose kernels take Python arguments. */
+const char* mote_abi_layout(void);
+
 /* ------------------------------------------------------------------------------------------------
  * Fused Relation forward.
  * Replaces: the Triton `_fwd_kernel` and its launcher `_launch_fwd`

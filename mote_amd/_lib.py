@@ -237,7 +237,31 @@ EXPORTS = {
     "mote_dechunk_bwd_workspace": ([C.POINTER(DechunkBwdArgs)], C.c_size_t),
     "mote_dechunk_bwd": ([C.POINTER(DechunkBwdArgs), C.c_void_p], C.c_int),
     "mote_dechunk_step": ([C.POINTER(DechunkStepArgs), C.c_void_p], C.c_int),
+    "mote_abi_layout": ([], C.c_char_p),
 }
+
+# the header's struct behind each ctypes mirror (checked against mote_abi_layout() by the tests)
+STRUCTS = {
+    "mote_view": View, "mote_relation_fwd_args": FwdArgs, "mote_relation_bwd_args": BwdArgs,
+    "mote_rope_givens_args": RopeArgs, "mote_rope_givens_bwd_args": RopeBwdArgs,
+    "mote_relation_decode_args": DecodeArgs, "mote_add_rms_norm_args": NormArgs,
+    "mote_add_rms_norm_bwd_args": NormBwdArgs, "mote_qkv_rope_args": QkvRopeArgs,
+    "mote_gate_product_args": GateProductArgs, "mote_skinny_gemm_args": SkinnyGemmArgs,
+    "mote_page_copy_args": PageCopyArgs, "mote_chunk_route_args": ChunkRouteArgs,
+    "mote_chunk_gather_args": ChunkGatherArgs, "mote_chunk_gather_bwd_args": ChunkGatherBwdArgs,
+    "mote_dechunk_args": DechunkArgs, "mote_dechunk_bwd_args": DechunkBwdArgs,
+    "mote_dechunk_step_args": DechunkStepArgs,
+}
+
+
+def abi_layout() -> dict:
+    """{struct: (size, {field: (offset, size)})} as the library's compiler laid the header out."""
+    out = {}
+    for line in lib().mote_abi_layout().decode().splitlines():
+        head, *fields = line.split(";")
+        name, size = head.split()
+        out[name] = (int(size), {f.split()[0]: (int(f.split()[1]), int(f.split()[2])) for f in fields})
+    return out
 
 _lock = threading.Lock()
 _lib = None

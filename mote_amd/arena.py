@@ -15,14 +15,19 @@ that read a whole bucket width and mask (mote/infer/graph.py:176-184) multiply m
 them, so the store is created and grown zeroed: stale values there are finite, never garbage.
 
 Growth. `ensure(rows)` reallocates to the next power-of-two multiple of the current capacity and
-bumps `generation` (captured graphs hold the old addresses and must be recaptured). Rows are carried
-over only when a prefix store has declared them live with `claim(owner, rows)`; otherwise the old
-store is released before the new one is allocated, so the peak is the new size alone.
+bumps `generation` (captured graphs hold the old addresses and must be recaptured). In a batch-1
+arena, rows are carried over only when a prefix store has declared them live (`owner` set, rows
+[0, n_valid)); otherwise the old store is released before the new one is allocated, so the peak is
+the new size alone. A batched arena has no per-slot residency record (decode advances each slot's
+fill on the device), so its growth carries every slot's rows up to the old capacity. With `pool`
+set (a `torch.cuda.MemPool`), the new store is allocated inside that pool.
 """
 
 from __future__ import annotations
 
-from typing import Iterator, Optional, Tuple
+import contextlib
+import dataclasses
+from typing import Any, Callable, Iterator, Optional, Tuple
 
 import torch
 
@@ -39,6 +44,7 @@ class RelationArena:
         self.dtype = dtype
         self.generation = 0
         self._resident: Tuple[Optional[int], int] = (None, 0)  # (prefix-store owner, live rows)
+        self.pool = None  # a serving MemPool: growth allocates inside it (engine.py:327)
         self.store = self._zeros(int(capacity))
 
     # ---- sizing ---------------------------------------------------------------------------------
@@ -89,11 +95,24 @@ class RelationArena:
     # ---- residency (which prefix-store branch's rows are live) ----------------------------------
     @property
     def owner(self) -> Optional[int]:
+        """The prefix-store branch whose rows [0, n_valid) the arena holds (None: nothing live).
+        Assignable, as the prefix store does (prefix_cache.py:158, 167, 216)."""
         return self._resident[0]
+
+    @owner.setter
+    def owner(self, owner: Optional[int]) -> None:
+        self._resident = (owner, self._resident[1])
 
     @property
     def n_valid(self) -> int:
         return self._resident[1]
+
+    @n_valid.setter
+    def n_valid(self, rows: int) -> None:
+        rows = int(rows)
+        if not 0 <= rows <= self.capacity:
+            raise ValueError(f"n_valid of {rows} rows in an arena of {self.capacity}")
+        self._resident = (self._resident[0], rows)
 
     def claim(self, owner: int, rows: int) -> None:
         """Declare rows [0, rows) live for prefix-store branch `owner` (kept across growth)."""
@@ -114,15 +133,25 @@ class RelationArena:
         self._reallocate(self.capacity * factor)
         return True
 
+    def _allocation_scope(self):
+        if self.pool is not None and self.device.type == "cuda":
+            return torch.cuda.use_mem_pool(self.pool)
+        return contextlib.nullcontext()
+
     def _reallocate(self, capacity: int) -> None:
         owner, live = self._resident
-        live = live if owner is not None else 0
+        if self.batch > 1:
+            live = self.capacity  # no per-slot record: every slot's rows travel
+        elif owner is None:
+            live = 0
         if live == 0:
             self.store = None  # drop the old rows before the new allocation: the peak is the new size
-            self.store = self._zeros(capacity)
+            with self._allocation_scope():
+                self.store = self._zeros(capacity)
             self._resident = (None, 0)
         else:
-            fresh = self._zeros(capacity)
+            with self._allocation_scope():
+                fresh = self._zeros(capacity)
             fresh[..., :live, :].copy_(self.store[..., :live, :])
             self.store = fresh
         self.generation += 1
@@ -155,30 +184,66 @@ class ArenaLayer:
         return self.arena.p2(self.layer)[:, :, :upto], self.arena.info(self.layer)[:, :, :upto]
 
 
+def _map_tensors(o: Any, fn: Callable[[torch.Tensor], Any]) -> Any:
+    """`o` rebuilt with `fn` applied to every tensor inside it (lists, tuples, named tuples and
+    dataclasses are walked; None, numbers and strings kept; anything else deep-copied), the walk a
+    recurrent layer's state needs when a whole inference state is moved or cloned
+    (mote/model/tree.py:17-32 is the reference's)."""
+    if isinstance(o, torch.Tensor):
+        return fn(o)
+    if isinstance(o, (list, tuple)):
+        items = [_map_tensors(x, fn) for x in o]
+        if isinstance(o, list):
+            return items
+        return type(o)(*items) if hasattr(o, "_fields") else tuple(items)
+    if o is None or isinstance(o, (bool, int, float, str)):
+        return o
+    if dataclasses.is_dataclass(o) and not isinstance(o, type):
+        return type(o)(**{f.name: _map_tensors(getattr(o, f.name), fn) for f in dataclasses.fields(o)})
+    import copy
+
+    return copy.deepcopy(o)
+
+
 class ArenaState:
-    """The Relation part of an inference state (arena.py:146-186): the shared arena and the number
-    of rows `n` this state has written. Copies share the arena and copy `n` only. (The reference
-    also carries recurrent states of non-Relation main layers here; those layers are not part of
-    this package.)"""
+    """The main-network part of an inference state (arena.py:146-186): the shared arena, the number
+    of rows `n` this state has written, and `mamba`, the recurrent states of a hybrid main network's
+    non-Relation layers (layer index -> state; empty for a pure Relation main network). Indexing a
+    Relation layer gives its ArenaLayer, a recurrent layer its stored state; `set` writes a recurrent
+    layer's new state back. Copies share the arena and copy `n`; `map` / `copy` apply a function to /
+    clone every tensor of the recurrent states."""
 
-    __slots__ = ("arena", "n")
+    __slots__ = ("arena", "n", "mamba")
 
-    def __init__(self, arena: RelationArena, n: int = 0):
+    def __init__(self, arena: RelationArena, n: int = 0, mamba: Optional[dict] = None):
         self.arena, self.n = arena, int(n)
+        self.mamba = dict(mamba) if mamba else {}
 
     def __len__(self) -> int:
         return self.arena.n_layers
 
-    def __getitem__(self, layer: int) -> ArenaLayer:
+    def __getitem__(self, layer: int):
+        if layer in self.mamba:
+            return self.mamba[layer]
         if not 0 <= layer < self.arena.n_layers:
             raise IndexError(layer)
         return ArenaLayer(self.arena, layer, self)
 
-    def __iter__(self) -> Iterator[ArenaLayer]:
-        return (ArenaLayer(self.arena, i, self) for i in range(self.arena.n_layers))
+    def __iter__(self) -> Iterator[Any]:
+        return (self[i] for i in range(self.arena.n_layers))
+
+    def set(self, layer: int, state) -> None:
+        """Store a recurrent layer's new state; Relation layers keep theirs in the arena, so a layer
+        that is not in `mamba` is left alone."""
+        if layer in self.mamba:
+            self.mamba[layer] = state
+
+    def map(self, fn: Callable[[torch.Tensor], Any]) -> "ArenaState":
+        """A state sharing the arena, with `fn` applied to every tensor of the recurrent states."""
+        return ArenaState(self.arena, self.n, {k: _map_tensors(v, fn) for k, v in self.mamba.items()})
 
     def copy(self) -> "ArenaState":
-        return ArenaState(self.arena, self.n)
+        return self.map(lambda t: t.clone())
 
     def advance(self, T: int) -> None:
         self.n += int(T)

@@ -102,9 +102,10 @@ class ArenaPages:
         return min(rows, PAGE)
 
     def hydrate(self, branch: Branch, n_chunks: int, arena: RelationArena, seq: int = 0) -> None:
-        """Make arena rows [0, n_chunks) of sequence `seq` hold the branch's chunks (stream-ordered
-        before later work on the arena's stream). A batch-1 arena that already holds the branch is
-        left alone (the hot case: no copy)."""
+        """Make arena rows [0, n_chunks) of sequence `seq` hold the branch's chunks; returns once
+        the rows are in the arena, so the branch's pages may be freed or reused right after. A
+        batch-1 arena that already holds the branch is left alone (the hot case: no copy). Growing
+        a batched arena keeps every other slot's rows (the arena carries them across growth)."""
         if n_chunks > branch.n_chunks:
             raise ValueError(f"the branch holds {branch.n_chunks} rows, not {n_chunks}")
         if arena.batch == 1 and arena.owner == branch.id and arena.n_valid >= n_chunks:
@@ -119,6 +120,10 @@ class ArenaPages:
             take = min(PAGE - off, n_chunks - c)
             _copy_rows(arena, seq, c, branch.pages[pi], off, take, to_page=False)
             c += take
+        if arena.device.type == "cuda" and n_chunks > 0:
+            # the DMA reads pinned pages that torch's caching host allocator does not know are in
+            # use: wait for it, so a page freed after return cannot be handed out while still read
+            torch.cuda.current_stream(arena.device).synchronize()
         if arena.batch == 1:
             arena.claim(branch.id, n_chunks)
         self.rows_copied_in += n_chunks

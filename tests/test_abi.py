@@ -19,6 +19,19 @@ def _declared():
     return sorted(set(re.findall(r"^\s*(?:const\s+)?(?:int|size_t|char\s*\*|const char\s*\*)\s*\*?\s*(mote_\w+)\s*\(", text, re.M)))
 
 
+def _header_structs():
+    """{struct: [field, ...]} in declaration order, read from the header text."""
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"typedef struct (\w+) \{(.*?)\} \1;", text, re.S):
+        fields = []
+        for decl in filter(None, (d.strip() for d in m.group(2).split(";"))):
+            first, *rest = decl.split(",")
+            fields += [first.split()[-1].lstrip("*")] + [r.strip().lstrip("*") for r in rest]
+        out[m.group(1)] = fields
+    return out
+
+
 def test_header_declares_the_entry_points():
     names = _declared()
     for n in ["mote_relation_fwd", "mote_relation_bwd", "mote_relation_bwd_workspace", "mote_relation_decode",
@@ -101,3 +114,24 @@ def test_static_decode_refuses_shapes_beyond_its_array_without_a_gpu():
     assert _lib.lib().mote_relation_decode_static(a, None) == 2  # the shape checks come first
     a.D, a.g = 128, None
     assert _lib.lib().mote_relation_decode_static(a, None) == 1
+
+
+def test_ctypes_mirrors_match_the_compiled_struct_layout():
+    """Every struct of the header: the library's table names the header's fields in order, and the
+    ctypes mirror in mote_amd/_lib.py has the same size and the same offset and size per field."""
+    from mote_amd import _lib
+
+    if not _lib.available():
+        pytest.skip("libmote_relation.so not built")
+    layout = _lib.abi_layout()
+    header = _header_structs()
+    assert set(layout) == set(header) == set(_lib.STRUCTS)
+    for name, fields in header.items():
+        size, table = layout[name]
+        assert list(table) == fields, name
+        cls = _lib.STRUCTS[name]
+        assert ctypes.sizeof(cls) == size, (name, ctypes.sizeof(cls), size)
+        assert [f[0] for f in cls._fields_] == fields, name
+        for f, (off, fsize) in table.items():
+            desc = getattr(cls, f)
+            assert (desc.offset, desc.size) == (off, fsize), (name, f, desc.offset, desc.size, off, fsize)

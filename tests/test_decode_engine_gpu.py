@@ -11,6 +11,24 @@ import torch
 pytestmark = pytest.mark.gpu
 
 
+def test_arena_growth_allocates_inside_the_serving_pool(cuda):
+    """engine.py:327 hands the arena its MemPool; growth (arena.py:101) allocates the new store there."""
+    from mote_amd.arena import RelationArena
+
+    print("case arena pool growth", flush=True)
+    arena = RelationArena(2, 4, 256, 64, "cuda", torch.bfloat16, batch=2)
+    arena.store[:, :, 1, :, :10] = 3.0
+    pool = torch.cuda.MemPool()
+    arena.pool = pool
+    assert arena.ensure(300) and arena.capacity == 512
+    ptr = arena.store.data_ptr()
+    segs = pool.snapshot()
+    assert any(s["address"] <= ptr < s["address"] + s["total_size"] for s in segs)
+    assert bool((arena.store[:, :, 1, :, :10] == 3.0).all())  # the other slot's rows travelled
+    assert float(arena.store[:, :, :, :, 256:].float().abs().sum()) == 0.0
+    torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("batch,dtype", [(1, torch.bfloat16), (3, torch.bfloat16), (1, torch.float32)])
 def test_pages_round_trip_through_dma(cuda, batch, dtype):
     from mote_amd.arena import RelationArena
