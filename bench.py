@@ -23,6 +23,7 @@ import json
 import math
 import os
 import platform
+import socket
 import sys
 import time
 
@@ -133,9 +134,9 @@ def check_replays(gr, outs, ref, n: int = 3):
                 raise RuntimeError(f"graph replay {r} differs from the eager step")
 
 
-def staged_bwd(p1, p2, info, ibar, lse, g, dy, timers):
-    """The one-pass backward with the key-block kernel bracketed by events (its three launches
-    issued separately through the ABI's `stages` field)."""
+def bwd_stage_args(p1, p2, info, ibar, lse, g, dy):
+    """The backward's argument block with its outputs and workspace allocated, for a caller that
+    issues the stages (rows, keys, queries, finish) one launch at a time; returns (args, keep-alive)."""
     from mote_amd import _lib as Lb
     from mote_amd.flash_relation import _token_major
 
@@ -152,6 +153,22 @@ def staged_bwd(p1, p2, info, ibar, lse, g, dy, timers):
     a.dp1, a.dp2, a.dinfo, a.dlam = Lb.view(dp1), Lb.view(dp2), Lb.view(dinfo), dlam.data_ptr()
     ws = torch.empty(int(Lb.lib().mote_relation_bwd_workspace(a)), device=p1.device, dtype=torch.uint8)
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    return a, (dp1, dp2, dinfo, dlam, ws)
+
+
+def run_stage(a, stage: int, stream) -> None:
+    from mote_amd import _lib as Lb
+
+    a.stages = stage
+    Lb.check(Lb.lib().mote_relation_bwd(a, stream), f"bwd stage {stage}")
+
+
+def staged_bwd(p1, p2, info, ibar, lse, g, dy, timers):
+    """The one-pass backward with the key-block kernel bracketed by events (its three launches
+    issued separately through the ABI's `stages` field)."""
+    from mote_amd import _lib as Lb
+
+    a, (dp1, dp2, dinfo, dlam, ws) = bwd_stage_args(p1, p2, info, ibar, lse, g, dy)
     st = Lb.stream_of(p1)
     a.stages = Lb.MOTE_BWD_ROWS
     Lb.check(Lb.lib().mote_relation_bwd(a, st), "bwd rows")
@@ -194,6 +211,7 @@ def bench_stack(steps: int, warmup: int, dev):
     for _ in range(max(1, min(steps, 3))):
         stack_step(inp, timers)
     torch.cuda.synchronize()
+    clock = stack_clock(inp, ms)
     avg = {k: sum(a.elapsed_time(b) for a, b in zip(*v)) / len(v[0]) for k, v in timers.items()}
     # per-kernel work (units of H*dh*T^2, one per causal product): forward U and P I~ (2); key kernel
     # U, dW, dV, dK (4); query kernel dQ (1), which reads the key kernel's dU^T tiles and is HBM-bound
@@ -204,11 +222,137 @@ def bench_stack(steps: int, warmup: int, dev):
                keys_tflops=4.0 * unit / (avg["bwd_keys"] * 1e-3) / 1e12,
                queries_tflops=1.0 * unit / (avg["bwd_queries"] * 1e-3) / 1e12,
                queries_bytes=dq_bytes, queries_gbs=dq_bytes / (avg["bwd_queries"] * 1e-3) / 1e9,
-               fwd_tflops=2.0 * unit / (avg["fwd"] * 1e-3) / 1e12)
+               fwd_tflops=2.0 * unit / (avg["fwd"] * 1e-3) / 1e12, clock=clock, dut=dut_residency(inp))
     log(f"[bench] stack: {ms:.3f} ms/step = {res['tflops']:.1f} TFLOP/s; fwd kernel {avg['fwd']*1e3:.1f} us "
         f"({res['fwd_tflops']:.1f} TF/s), bwd key kernel {avg['bwd_keys']*1e3:.1f} us ({res['keys_tflops']:.1f} TF/s), "
-        f"bwd dQ kernel {avg['bwd_queries']*1e3:.1f} us ({res['queries_gbs']:.0f} GB/s of dU^T tiles + P2 + dP1)")
+        f"bwd dQ kernel {avg['bwd_queries']*1e3:.1f} us ({res['queries_gbs']:.0f} GB/s of dU^T tiles + P2 + dP1); "
+        f"shader clock during a step {clock['sclk_mhz']} MHz {clock['sclk_mhz_runs']}; dQ kernel {res['dut']['dq_us_hot']} us right after the key kernel, "
+        f"{res['dut']['dq_us_after_sweep']} us after a {res['dut']['sweep_MiB']} MiB sweep")
     return res
+
+
+def gpu_identity(dev) -> dict:
+    """Which GPU and host the line was measured on."""
+    p = torch.cuda.get_device_properties(dev)
+    ident = {"name": p.name, "arch": getattr(p, "gcnArchName", ""), "cus": p.multi_processor_count,
+             "host": socket.gethostname()}
+    for k in ("uuid", "pci_bus_id", "pci_device_id", "pci_domain_id"):
+        v = getattr(p, k, None)
+        if v is not None:
+            ident[k] = str(v)
+    return ident
+
+
+class ClockProbe:
+    """mote_clock_probe launches on the current stream: each workgroup counts shader-clock ticks
+    (s_memtime) against the constant 100 MHz clock (s_memrealtime) over a short loop, so the shader
+    clock at that moment is 100 MHz x the ratio, with no host timing involved."""
+
+    def __init__(self, dev, max_workgroups: int = 256):
+        self.out = torch.zeros(3 * max_workgroups, dtype=torch.int64, device=dev)
+        self.max_workgroups = max_workgroups
+        self.samples = []  # (workgroups, snapshot of out) per launch
+
+    def launch(self, workgroups: int = 8, iters: int = 512, keep: bool = True) -> None:
+        from mote_amd import _lib as Lb
+
+        assert workgroups <= self.max_workgroups
+        Lb.check(Lb.lib().mote_clock_probe(self.out.data_ptr(), workgroups, iters, Lb.stream_of(self.out)),
+                 "mote_clock_probe")
+        if keep:
+            self.samples.append(self.out[: 3 * workgroups].clone())
+
+    def mhz(self) -> list:
+        """Shader clock of every kept launch (the mean over its workgroups)."""
+        out = []
+        for o in self.samples:
+            o = o.view(-1, 3).double().cpu()
+            out.append(float((100.0 * o[:, 0] / o[:, 1].clamp(min=1)).mean()))
+        return out
+
+
+def stack_clock(inp: "StackInputs", step_ms: float, reps: int = 3) -> dict:
+    """The shader clock the stack's kernels run at: while a stack step runs on the current stream, 8
+    probe workgroups on a second stream (one per XCD, a few wave slots of the chip) count shader-clock
+    ticks against the 100 MHz clock over a loop sized to end inside the step. The clock reacts to the
+    load within microseconds, so a probe run between kernels or alone reads a different clock than
+    the kernels see; this pass runs after the timed steps and its step time is not reported."""
+    dev = inp.layers[0]["qkv"].device
+    probe = ClockProbe(dev, 8)
+    side = torch.cuda.Stream()
+    iters = 1000
+    res = []
+    for r in range(reps + 1):
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            probe.launch(8, iters)
+        stack_step(inp)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        o = probe.samples[-1].view(-1, 3).double().cpu()
+        span_ms = float(o[:, 1].max()) / 1e5
+        if r == 0:  # size the loop to about 70 % of a step from the first probe's pace
+            iters = max(1000, int(iters * 0.7 * step_ms / max(span_ms, 1e-3)))
+            continue
+        res.append((float((100.0 * o[:, 0] / o[:, 1].clamp(min=1)).mean()), span_ms))
+    mhz = [m for m, _ in res]
+    return {"sclk_mhz": round(sum(mhz) / len(mhz), 1), "sclk_mhz_runs": [round(m, 1) for m in mhz],
+            "probe_span_ms": [round(t, 3) for _, t in res], "step_ms": round(step_ms, 3),
+            "method": "8 workgroups of mote_clock_probe on a second stream beside a stack step: s_memtime "
+                      "ticks over s_memrealtime (100 MHz) ticks", **shader_clock_check(dev)}
+
+
+def shader_clock_check(dev) -> dict:
+    """The probe's constant counter against HIP event time over a longer launch: both must advance
+    at 100 MHz for the probe's clock figures to mean what they say."""
+    pr = ClockProbe(dev)
+    pr.launch(256, 20000, keep=False)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    pr.launch(256, 20000)
+    e1.record()
+    torch.cuda.synchronize()
+    o = pr.samples[0].view(-1, 3).double().cpu()
+    real_ms = float(o[:, 1].max()) / 1e5
+    return {"probe_event_ms": round(e0.elapsed_time(e1), 3), "probe_realtime_ms": round(real_ms, 3),
+            "sclk_mhz_probe_alone": round(pr.mhz()[0], 1)}
+
+
+def dut_residency(inp: "StackInputs", reps: int = 5, sweep_mib: int = 1024) -> dict:
+    """Where the dQ kernel finds the dU^T tiles the key kernel wrote just before it: the dQ launch
+    timed right after the key kernel (tiles possibly still in the 256 MB Infinity Cache) and after a
+    read of `sweep_mib` MiB in between (which leaves none of them there). Both issue the same launch
+    on the same data; the difference is what the round trip through HBM costs."""
+    from mote_amd import _lib as Lb
+
+    ops = torch.ops.mote
+    L = inp.layers[0]
+    p1, p2, info = ops.rope_givens(L["qkv"], L["inv"], L["theta"], L["heads"], L["parity"], 0)
+    y, g, ibar, lse = ops.relation_fwd(p1, p2, info, L["lam"], 2.0, 0)
+    a, keep = bwd_stage_args(p1, p2, info, ibar, lse, g, L["dy"])
+    st = Lb.stream_of(p1)
+    sweep = torch.ones(sweep_mib << 18, dtype=torch.float32, device=p1.device)
+    times = {"hot": [], "after_sweep": []}
+    for r in range(2 * reps + 2):
+        kind = "hot" if r % 2 == 0 else "after_sweep"
+        run_stage(a, Lb.MOTE_BWD_ROWS, st)
+        run_stage(a, Lb.MOTE_BWD_KEYS, st)
+        if kind == "after_sweep":
+            sweep.sum()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        run_stage(a, Lb.MOTE_BWD_QUERIES, st)
+        e1.record()
+        torch.cuda.synchronize()
+        if r >= 2:
+            times[kind].append(e0.elapsed_time(e1) * 1e3)
+    hot, cold = (sum(v) / len(v) for v in (times["hot"], times["after_sweep"]))
+    tile_bytes = N_HEADS * pair_total(inp.T) * 8192
+    del sweep, keep
+    return {"dq_us_hot": round(hot, 2), "dq_us_after_sweep": round(cold, 2), "sweep_MiB": sweep_mib,
+            "dut_tile_bytes": tile_bytes, "reps": reps,
+            "note": "dQ launch right after the key kernel vs after a read of sweep_MiB in between"}
 
 
 def pair_total(TQ: int, q_start: int = 0) -> int:
@@ -308,14 +452,19 @@ def _recorded(fname: str, kernel: str):
     return None, None
 
 
+TRAFFIC_KIND = ("bytes between L2 and the memory fabric per launch (FETCH_SIZE + WRITE_SIZE, scaled by a copy of known "
+                "size); Infinity Cache hits are included, so this is an upper bound on the bytes that reach HBM")
+
+
 def measured_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` at this workload from the two counter passes recorded in
-    profiles/hbm_traffic.txt, with where it came from; the bytes are null when the kernel's sources
-    changed after the measurement (the record is then stale, not this build's)."""
+    """Bytes per launch of `kernel` between L2 and the memory fabric at this workload, from the two
+    counter passes recorded in profiles/hbm_traffic.txt, with where it came from; the bytes are null
+    when the kernel's sources changed after the measurement (the record is then stale, not this
+    build's). The counters see requests leaving L2, hits in the Infinity Cache included."""
     fields, current = _recorded("hbm_traffic.txt", kernel)
     if fields is None:
         return None, {"recorded": None}
-    note = {"recorded": "profiles/hbm_traffic.txt", "sources_match": bool(current)}
+    note = {"recorded": "profiles/hbm_traffic.txt", "sources_match": bool(current), "kind": TRAFFIC_KIND}
     return (int(float(fields[0])) if current else None), note
 
 
@@ -490,12 +639,45 @@ def bench_decode(batch: int, steps: int, dev, copies: int):
     kern_bytes = (S0 + 1) * 2 * N_HEADS * D_HEAD * 2 * batch  # the eager launches ran at S = S0
     # one launch inside the replayed graph: the step's time over its 12 launches (gaps included)
     launch_us = us / N_LAYERS
+    floor_us = launch_floor(dev, N_LAYERS, 256, steps)
     res = dict(batch=batch, us_per_step=us, gbs=bytes_per_step / (us * 1e-6) / 1e9, bytes_per_step=bytes_per_step,
                avg_S=s_avg, kernel_us=launch_us, kernel_gbs=bytes_per_step / N_LAYERS / (launch_us * 1e-6) / 1e9,
-               eager_us=kern_ms * 1e3, eager_gbs=kern_bytes / (kern_ms * 1e-3) / 1e9, copies=copies)
+               eager_us=kern_ms * 1e3, eager_gbs=kern_bytes / (kern_ms * 1e-3) / 1e9, copies=copies,
+               launch_floor_us=floor_us)
     log(f"[bench] decode b{batch}: {us:.1f} us/step ({res['gbs']:.0f} GB/s over the step), "
-        f"{launch_us:.2f} us per launch in the graph, one eager launch {res['eager_us']:.1f} us")
+        f"{launch_us:.2f} us per launch in the graph (launch floor {floor_us:.2f} us), "
+        f"one eager launch {res['eager_us']:.1f} us")
     return res
+
+
+def launch_floor(dev, launches: int, workgroups: int, replays: int) -> float:
+    """The per-launch cost of a chain of `launches` dependent near-empty launches of `workgroups`
+    workgroups (mote_clock_probe with one loop step: the decode kernel's grid, no memory traffic)
+    captured in one HIP graph and replayed like the decode step: the floor under a decode launch."""
+    probe = ClockProbe(dev, workgroups)
+
+    def chain():
+        for _ in range(launches):
+            probe.launch(workgroups, 1, keep=False)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        chain()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr, stream=side):
+            chain()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    for _ in range(8):
+        gr.replay()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(replays):
+        gr.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) * 1e3 / replays / launches
 
 
 # ------------------------------------------------------------------------------------------------
@@ -1113,6 +1295,8 @@ def main():
                          "counters": measured_counters("relation_fwd_tile_kernel@c3"),
                          "flop_per_launch": 2.0 * N_HEADS * D_HEAD * st["T"] ** 2, "avg_launch_ms": round(st["fwd_ms"], 4)},
         "stack_frac_of_peak": round(st["tflops"] / PEAK_BF16_TFLOPS, 4),
+        "gpu": {**gpu_identity(dev), **st["clock"]},
+        "dut_residency": st["dut"],
     }
     if dec:
         out["decode"] = {
@@ -1120,7 +1304,7 @@ def main():
                 "avg_S": round(v["avg_S"], 1), "step_GBs": round(v["gbs"], 1),
                 "step_frac_hbm": round(v["gbs"] / PEAK_HBM_GBS, 4), "kernel_us": round(v["kernel_us"], 2),
                 "kernel_GBs": round(v["kernel_gbs"], 1), "kernel_frac_hbm": round(v["kernel_gbs"] / PEAK_HBM_GBS, 4),
-                "eager_launch_us": round(v["eager_us"], 2),
+                "eager_launch_us": round(v["eager_us"], 2), "launch_floor_us": round(v["launch_floor_us"], 2),
                 **_traffic(f"relation_decode_kernel_{k}"),
                 "cache_copies_rotated": v["copies"]}
             for k, v in dec.items()}

@@ -50,6 +50,14 @@ const char* mote_version(void);
  * counterpart in the reference, whose kernels take Python arguments. */
 const char* mote_abi_layout(void);
 
+/* Measurement helper, no counterpart in the reference: the shader clock at the moment of the call.
+ * One launch of `workgroups` workgroups (256 threads) that each run `iters` steps of matrix-core
+ * products and exponentials; out (device, int64, 3 per workgroup) receives workgroup i's count of
+ * the shader clock (s_memtime) over its loop, the count of the constant 100 MHz clock
+ * (s_memrealtime) over the same span, and a value that keeps the work alive. Shader clock in MHz =
+ * 100 * out[3 i] / out[3 i + 1]. */
+int mote_clock_probe(int64_t* out, int workgroups, int iters, void* stream);
+
 /* ------------------------------------------------------------------------------------------------
  * Fused Relation forward.
  * Replaces: the Triton `_fwd_kernel` and its launcher `_launch_fwd`

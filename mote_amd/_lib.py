@@ -238,6 +238,7 @@ EXPORTS = {
     "mote_dechunk_bwd": ([C.POINTER(DechunkBwdArgs), C.c_void_p], C.c_int),
     "mote_dechunk_step": ([C.POINTER(DechunkStepArgs), C.c_void_p], C.c_int),
     "mote_abi_layout": ([], C.c_char_p),
+    "mote_clock_probe": ([C.c_void_p, C.c_int, C.c_int, C.c_void_p], C.c_int),
 }
 
 # the header's struct behind each ctypes mirror (checked against mote_abi_layout() by the tests)
