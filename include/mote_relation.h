@@ -353,6 +353,37 @@ size_t mote_qkv_rope_workspace(const mote_qkv_rope_args* args);
 int mote_qkv_rope_fwd(const mote_qkv_rope_args* args, void* stream);
 
 /* ------------------------------------------------------------------------------------------------
+ * Backward of QK-Norm for the fused prologue (bf16).
+ * Replaces: the autograd of HeadRMSNorm (mote/model/relation.py:71-94) applied to p1 / p2
+ * (:208-210), i.e. the two norms' backward in the prologue's backward. Per token row and head of
+ * part p (p1 = part 0, p2 = part 1; part p holds columns [p H D, (p + 1) H D) of a row), with x the
+ * raw projection before the norm, g = dy * gain_p and r = (mean(x^2) + eps)^(-1/2):
+ *   dx = r g - r^3 x mean(g x)   (fp32 math, rounded to bf16),
+ *   dgain_p = sum over rows and heads of dy x r (fp32, overwritten).
+ * x (e.g. mote_qkv_rope_fwd's qk_raw), dy and dx are [rows, parts H D] bf16 with row strides in
+ * elements; dx may be dy (in place). D in {32, 64, 96, 128}; rows on 16-byte boundaries.
+ * Workspace: mote_head_rms_norm_bwd_workspace() bytes (per-workgroup dgain partials, added in a
+ * fixed order: dgain is bitwise reproducible); its contents on entry do not matter.
+ * ------------------------------------------------------------------------------------------------ */
+typedef struct mote_head_norm_bwd_args {
+  int dtype;             /* MOTE_BF16 */
+  int rows, parts, H, D;
+  float eps;
+  const void* x; int64_t x_sr;
+  const void* dy; int64_t dy_sr;
+  void* dx; int64_t dx_sr;
+  const float* gain0;
+  const float* gain1;    /* parts == 2 */
+  float* dgain0;
+  float* dgain1;         /* parts == 2 */
+  void* workspace;
+  size_t workspace_bytes;
+} mote_head_norm_bwd_args;
+
+size_t mote_head_rms_norm_bwd_workspace(const mote_head_norm_bwd_args* args);
+int mote_head_rms_norm_bwd(const mote_head_norm_bwd_args* args, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
  * Output gate of FullRelation._out (bf16): z = y * sigmoid(x wg^T) with the product rounded to bf16,
  * the sigmoid rounded to bf16 and z rounded again (the reference's bf16 ops, relation.py:179-181),
  * in one launch of the prologue's product kernel; s receives the sigmoid for the backward.

@@ -118,6 +118,15 @@ class QkvRopeArgs(C.Structure):
     ]
 
 
+class HeadNormBwdArgs(C.Structure):
+    _fields_ = [
+        ("dtype", C.c_int), ("rows", C.c_int), ("parts", C.c_int), ("H", C.c_int), ("D", C.c_int), ("eps", C.c_float),
+        ("x", C.c_void_p), ("x_sr", C.c_int64), ("dy", C.c_void_p), ("dy_sr", C.c_int64),
+        ("dx", C.c_void_p), ("dx_sr", C.c_int64), ("gain0", C.c_void_p), ("gain1", C.c_void_p),
+        ("dgain0", C.c_void_p), ("dgain1", C.c_void_p), ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
+    ]
+
+
 class GateProductArgs(C.Structure):
     _fields_ = [
         ("B", C.c_int), ("T", C.c_int), ("D", C.c_int), ("x", C.c_void_p), ("x_sr", C.c_int64),
@@ -227,6 +236,8 @@ EXPORTS = {
     "mote_qkv_rope_workspace": ([C.POINTER(QkvRopeArgs)], C.c_size_t),
     "mote_qkv_rope_fwd": ([C.POINTER(QkvRopeArgs), C.c_void_p], C.c_int),
     "mote_gate_product": ([C.POINTER(GateProductArgs), C.c_void_p], C.c_int),
+    "mote_head_rms_norm_bwd_workspace": ([C.POINTER(HeadNormBwdArgs)], C.c_size_t),
+    "mote_head_rms_norm_bwd": ([C.POINTER(HeadNormBwdArgs), C.c_void_p], C.c_int),
     "mote_skinny_gemm": ([C.POINTER(SkinnyGemmArgs), C.c_void_p], C.c_int),
     "mote_arena_page_copy": ([C.POINTER(PageCopyArgs), C.c_void_p], C.c_int),
     "mote_chunk_route": ([C.POINTER(ChunkRouteArgs), C.c_void_p], C.c_int),
@@ -247,7 +258,7 @@ STRUCTS = {
     "mote_rope_givens_args": RopeArgs, "mote_rope_givens_bwd_args": RopeBwdArgs,
     "mote_relation_decode_args": DecodeArgs, "mote_add_rms_norm_args": NormArgs,
     "mote_add_rms_norm_bwd_args": NormBwdArgs, "mote_qkv_rope_args": QkvRopeArgs,
-    "mote_gate_product_args": GateProductArgs, "mote_skinny_gemm_args": SkinnyGemmArgs,
+    "mote_gate_product_args": GateProductArgs, "mote_head_norm_bwd_args": HeadNormBwdArgs, "mote_skinny_gemm_args": SkinnyGemmArgs,
     "mote_page_copy_args": PageCopyArgs, "mote_chunk_route_args": ChunkRouteArgs,
     "mote_chunk_gather_args": ChunkGatherArgs, "mote_chunk_gather_bwd_args": ChunkGatherBwdArgs,
     "mote_dechunk_args": DechunkArgs, "mote_dechunk_bwd_args": DechunkBwdArgs,

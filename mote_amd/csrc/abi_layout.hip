@@ -102,6 +102,14 @@ const Entry kLayout[] = {
     F(mote_qkv_rope_args, table_ready), F(mote_qkv_rope_args, norm_w1), F(mote_qkv_rope_args, norm_w2),
     F(mote_qkv_rope_args, norm_eps), F(mote_qkv_rope_args, qk_raw), F(mote_qkv_rope_args, qr_sb),
     F(mote_qkv_rope_args, qr_sr),
+    MOTE_STRUCT(mote_head_norm_bwd_args),
+    F(mote_head_norm_bwd_args, dtype), F(mote_head_norm_bwd_args, rows), F(mote_head_norm_bwd_args, parts),
+    F(mote_head_norm_bwd_args, H), F(mote_head_norm_bwd_args, D), F(mote_head_norm_bwd_args, eps),
+    F(mote_head_norm_bwd_args, x), F(mote_head_norm_bwd_args, x_sr), F(mote_head_norm_bwd_args, dy),
+    F(mote_head_norm_bwd_args, dy_sr), F(mote_head_norm_bwd_args, dx), F(mote_head_norm_bwd_args, dx_sr),
+    F(mote_head_norm_bwd_args, gain0), F(mote_head_norm_bwd_args, gain1), F(mote_head_norm_bwd_args, dgain0),
+    F(mote_head_norm_bwd_args, dgain1), F(mote_head_norm_bwd_args, workspace),
+    F(mote_head_norm_bwd_args, workspace_bytes),
     MOTE_STRUCT(mote_gate_product_args),
     F(mote_gate_product_args, B), F(mote_gate_product_args, T), F(mote_gate_product_args, D),
     F(mote_gate_product_args, x), F(mote_gate_product_args, x_sr), F(mote_gate_product_args, w),

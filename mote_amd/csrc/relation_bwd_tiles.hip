@@ -79,13 +79,24 @@ __device__ __forceinline__ void kv_block(const bf16_t* Qs, const bf16_t* Ds, con
   using E = Elem<bf16_t>;
   using Frag = E::Frag;
   constexpr int KS = DP / 32, DT = DP / 16;
+  // the query rows' statistics: lse2 (LSE in log2 units) and c = dA - Delta, which seeds the dW
+  // accumulator so the product yields dW + c with no add per element
+  float lv[8];
+  f32x4 c4[2];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const float4 l4 = *reinterpret_cast<const float4*>(Ss + 32 * qh + 16 * qt + 4 * lg);
+    const float4 cq = *reinterpret_cast<const float4*>(Ss + 64 + 32 * qh + 16 * qt + 4 * lg);
+    lv[4 * qt] = l4.x; lv[4 * qt + 1] = l4.y; lv[4 * qt + 2] = l4.z; lv[4 * qt + 3] = l4.w;
+    c4[qt] = f32x4{cq.x, cq.y, cq.z, cq.w};
+  }
   f32x4 sacc[2][2], wacc[2][2];  // [query tile][key tile]
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
       sacc[qt][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      wacc[qt][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      wacc[qt][kt] = c4[qt];
     }
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
@@ -112,14 +123,6 @@ __device__ __forceinline__ void kv_block(const bf16_t* Qs, const bf16_t* Ds, con
   // result is consumed 8 instructions later instead of by the next one.
   Frag aw[2], au[2];
   float wv[2][8], uv[2][8];
-  float lv[8], cv[8];
-#pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    const float4 l4 = *reinterpret_cast<const float4*>(Ss + 32 * qh + 16 * qt + 4 * lg);
-    const float4 c4 = *reinterpret_cast<const float4*>(Ss + 64 + 32 * qh + 16 * qt + 4 * lg);
-    lv[4 * qt] = l4.x; lv[4 * qt + 1] = l4.y; lv[4 * qt + 2] = l4.z; lv[4 * qt + 3] = l4.w;
-    cv[4 * qt] = c4.x; cv[4 * qt + 1] = c4.y; cv[4 * qt + 2] = c4.z; cv[4 * qt + 3] = c4.w;
-  }
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt) {
     float t[8], sg[8];
@@ -140,7 +143,7 @@ __device__ __forceinline__ void kv_block(const bf16_t* Qs, const bf16_t* Ds, con
       // SiLU'(U) = sg (1 + U (1 - sg)) with U (1 - sg) ln2-scaled from t: a = t (sg - 1) = U log2e (1 - sg)
       const float a = fmaf(t[e], sg[e], -t[e]);
       const float sp = sg[e] * fmaf(a, kLn2, 1.0f);
-      uv[kt][e] = wv[kt][e] * (wacc[e >> 2][kt][e & 3] + cv[e]) * sp;
+      uv[kt][e] = wv[kt][e] * wacc[e >> 2][kt][e & 3] * sp;  // wacc = dW + c
     }
     // dV += W^T dI-bar, dK += dU^T Q of key tile kt over the wave's 32 queries (k in permuted
     // order), right after kt's elementwise: tile 0's products then run beside tile 1's exponentials

@@ -300,16 +300,45 @@ def _qr_setup(ctx, inputs, output):
     ctx.n_heads, ctx.parity, ctx.pos0, ctx.eps = n_heads, parity, pos0, norm_eps
 
 
-def _head_rms_norm_bwd(raw: torch.Tensor, gain: torch.Tensor, dy: torch.Tensor, eps: float, H: int):
-    """Backward of y = x rsqrt(mean(x^2) + eps) * gain per head (relation.py:71-94), in fp32:
-    dx = r g - r^3 x mean(g x) with g = dy * gain; dgain = sum over tokens and heads of dy x r."""
-    B, T, K = raw.shape
-    x = raw.float().view(B, T, H, K // H)
-    d = dy.float().reshape(B, T, H, K // H)
-    r = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps)
-    g = d * gain.float()
-    dx = r * g - x * r.pow(3) * (g * x).mean(-1, keepdim=True)
-    return dx.view(B, T, K), (d * x * r).sum((0, 1, 2))
+@torch.library.custom_op("mote::head_rms_norm_bwd_", mutates_args=("dqkv",))
+def _head_norm_bwd_(dqkv: torch.Tensor, qkraw: torch.Tensor, gain1: torch.Tensor, gain2: torch.Tensor, eps: float,
+                    n_heads: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Backward of QK-Norm (relation.py:71-94) on p1 | p2 of the prologue, in place: the first 2 H dh
+    columns of dqkv [B, T, 3 H dh] (gradients of the normalised projections) become the gradients
+    of the raw projections qkraw [B, T, 2 H dh]; returns the two gains' gradients (fp32). One launch
+    of mote_head_rms_norm_bwd (per head row g = dy gain, r = rsqrt(mean(x^2) + eps):
+    dx = r g - r^3 x mean(g x), dgain = sum of dy x r)."""
+    if not dqkv.is_cuda:
+        raise RuntimeError("mote::head_rms_norm_bwd_ needs the HIP library and an MI355X")
+    B, T, K3 = dqkv.shape
+    K = K3 // 3
+    D = K // n_heads
+    if B * T == 0:
+        z = torch.zeros(D, device=dqkv.device, dtype=torch.float32)
+        return z, z.clone()
+    if dqkv.stride(2) != 1 or qkraw.stride(2) != 1 or (B > 1 and (dqkv.stride(0) != T * dqkv.stride(1) or
+                                                               qkraw.stride(0) != T * qkraw.stride(1))):
+        raise ValueError("mote::head_rms_norm_bwd_: token rows must be back to back with unit column stride")
+    g1 = gain1.detach().to(device=dqkv.device, dtype=torch.float32).contiguous()
+    g2 = gain2.detach().to(device=dqkv.device, dtype=torch.float32).contiguous()
+    dg1 = torch.empty(D, device=dqkv.device, dtype=torch.float32)
+    dg2 = torch.empty(D, device=dqkv.device, dtype=torch.float32)
+    a = L.HeadNormBwdArgs()
+    a.dtype, a.rows, a.parts, a.H, a.D, a.eps = L.dtype_code(dqkv), B * T, 2, int(n_heads), D, float(eps)
+    a.x, a.x_sr = qkraw.data_ptr(), qkraw.stride(1)
+    a.dy, a.dy_sr = dqkv.data_ptr(), dqkv.stride(1)
+    a.dx, a.dx_sr = dqkv.data_ptr(), dqkv.stride(1)
+    a.gain0, a.gain1, a.dgain0, a.dgain1 = g1.data_ptr(), g2.data_ptr(), dg1.data_ptr(), dg2.data_ptr()
+    ws = torch.empty(max(int(L.lib().mote_head_rms_norm_bwd_workspace(a)), 16), device=dqkv.device, dtype=torch.uint8)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    L.check(L.lib().mote_head_rms_norm_bwd(a, L.stream_of(dqkv)), "mote_head_rms_norm_bwd")
+    return dg1, dg2
+
+
+@_head_norm_bwd_.register_fake
+def _head_norm_bwd_fake(dqkv, qkraw, gain1, gain2, eps, n_heads):
+    D = dqkv.shape[-1] // 3 // n_heads
+    return dqkv.new_empty(D, dtype=torch.float32), dqkv.new_empty(D, dtype=torch.float32)
 
 
 def _qr_backward(ctx, dp1, dp2, dinfo, _diraw, _dqkraw):
@@ -326,10 +355,8 @@ def _qr_backward(ctx, dp1, dp2, dinfo, _diraw, _dqkraw):
     src = iraw if ctx.keep else x.new_empty(B, T, K)  # read only for dtheta
     dqkv, dtheta = _rope_givens_bwd(dp1, dp2, dinfo, src, inv_freq, theta, H, ctx.parity, ctx.pos0, True)
     dn1 = dn2 = None
-    if ctx.norm:  # gradients of the normalised p1 / p2 back through QK-Norm
-        dq, dn1 = _head_rms_norm_bwd(qkraw[..., :K], norm_w1, dqkv[..., :K], ctx.eps, H)
-        dk, dn2 = _head_rms_norm_bwd(qkraw[..., K:], norm_w2, dqkv[..., K:2 * K], ctx.eps, H)
-        dqkv = torch.cat([dq.to(dqkv.dtype), dk.to(dqkv.dtype), dqkv[..., 2 * K:]], dim=-1)
+    if ctx.norm:  # gradients of the normalised p1 / p2 back through QK-Norm, in place in dqkv
+        dn1, dn2 = _head_norm_bwd_(dqkv, qkraw, norm_w1, norm_w2, ctx.eps, H)
         dn1, dn2 = dn1.to(norm_w1.dtype), dn2.to(norm_w2.dtype)
     dx = torch.matmul(dqkv, w)                                        # [B, T, 3K] x [3K, K]
     dw = torch.matmul(dqkv.reshape(-1, 3 * K).t(), x.reshape(-1, K))  # [3K, K]

@@ -226,17 +226,20 @@ def test_fused_prologue_replays_in_a_hip_graph(cuda):
         del graph
 
 
-@pytest.mark.parametrize("H,D,T,parity", [(8, 96, 301, 1), (4, 64, 129, 0), (2, 128, 64, 1)])
-def test_fused_prologue_with_qk_norm_matches_oracle(cuda, H, D, T, parity):
+@pytest.mark.parametrize("B,H,D,T,parity", [(1, 8, 96, 301, 1), (1, 4, 64, 129, 0), (1, 2, 128, 64, 1),
+                                             (2, 8, 96, 300, 0), (3, 2, 64, 257, 1)])
+def test_fused_prologue_with_qk_norm_matches_oracle(cuda, B, H, D, T, parity):
     """QK-Norm in the fused prologue (relation.py:208-210): the bf16 projections of p1 / p2 go through
     the oracle's HeadRMSNormRef (fp32 math, bf16 result) before RoPE; outputs within 2e-2 of the
-    float64 composition, and the gradients of x, w, theta and both gains against its autograd."""
+    float64 composition, and the gradients of x, w, theta and both gains (the QK-Norm backward
+    kernel) against its autograd. Several batches with T not a multiple of the 256-token tile put
+    token tiles across two sequences."""
     from mote_amd.relation import qkv_rope, rope_inv_freq
 
-    print(f"case qkv_rope qk-norm H={H} D={D} T={T} parity={parity}", flush=True)
-    g = torch.Generator().manual_seed(70 + H)
+    print(f"case qkv_rope qk-norm B={B} H={H} D={D} T={T} parity={parity}", flush=True)
+    g = torch.Generator().manual_seed(70 + H + B)
     K = H * D
-    x = torch.randn(1, T, K, generator=g).bfloat16()
+    x = torch.randn(B, T, K, generator=g).bfloat16()
     w = (torch.randn(3 * K, K, generator=g) / K ** 0.5).bfloat16()
     theta = torch.rand(H // 2, generator=g) * 2 - 1
     n1, n2 = torch.rand(D, generator=g) + 0.5, torch.rand(D, generator=g) + 0.5
@@ -246,7 +249,7 @@ def test_fused_prologue_with_qk_norm_matches_oracle(cuda, H, D, T, parity):
     # oracle: bf16 projection, QK-Norm (fp32 math, bf16 result), then RoPE / Givens in float64
     xr, wr, tr, n1r, n2r = (t.double().requires_grad_(True) for t in (x.float(), w.float(), theta, n1, n2))
     qkv = xr @ wr.t()
-    q, k, v = (t.reshape(1, T, H, D).transpose(1, 2) for t in qkv.split(K, dim=-1))
+    q, k, v = (t.reshape(B, T, H, D).transpose(1, 2) for t in qkv.split(K, dim=-1))
     rms = lambda t, gain: t * torch.rsqrt(t.pow(2).mean(-1, keepdim=True) + 1e-5) * gain
     q, k = rms(q, n1r), rms(k, n2r)
     cos, sin = O.rope_tables(0, T, D, 10000.0, torch.bfloat16)
@@ -256,11 +259,58 @@ def test_fused_prologue_with_qk_norm_matches_oracle(cuda, H, D, T, parity):
         assert rel_err(got, want.detach()) < 2e-2, rel_err(got, want.detach())
     # the bf16 rounding points of the norm: against the oracle module's HeadRMSNormRef on the kernel's
     # own projection is covered by the module tests; here the composition in float64
-    dys = [torch.randn(1, H, T, D, generator=g).bfloat16() for _ in range(3)]
+    dys = [torch.randn(B, H, T, D, generator=g).bfloat16() for _ in range(3)]
     sum((o.float() * d.to(cuda).float()).sum() for o, d in zip((p1, p2, info), dys)).backward()
     sum((o * d.double()).sum() for o, d in zip((q, k, v), dys)).backward()
     for name, a, b in (("x", xg, xr), ("w", wg, wr), ("theta", tg, tr), ("gain1", n1g, n1r), ("gain2", n2g, n2r)):
         assert rel_err(a.grad, b.grad) < 2e-2, (name, rel_err(a.grad, b.grad))
+
+
+@pytest.mark.parametrize("B,T,H,D", [(1, 4964, 8, 96), (2, 301, 4, 64), (3, 17, 2, 128), (1, 5, 6, 32), (1, 0, 2, 64)])
+def test_head_norm_backward_kernel_matches_float64(cuda, B, T, H, D):
+    """mote::head_rms_norm_bwd_ (QK-Norm backward, relation.py:71-94) against the float64 formula of
+    the norm's derivative: dx = r g - r^3 x mean(g x) per head row with g = dy gain, dgain = sum dy x r;
+    the I~ columns are left alone, dx within 2e-2 (one bf16 rounding), dgain within 1e-4; two calls
+    give the same bits."""
+    from mote_amd.relation import _head_norm_bwd_
+
+    print(f"case head norm bwd B={B} T={T} H={H} D={D}", flush=True)
+    g = torch.Generator().manual_seed(300 + D + T)
+    K = H * D
+    raw = (torch.randn(B, T, 2 * K, generator=g) * 2).bfloat16()
+    d = torch.randn(B, T, 3 * K, generator=g).bfloat16()
+    n1, n2 = torch.rand(D, generator=g) + 0.5, torch.rand(D, generator=g) + 0.5
+    want_dx, want_dg = [], []
+    for part, gain in ((0, n1), (1, n2)):
+        x = raw[..., part * K:(part + 1) * K].double().reshape(B, T, H, D)
+        dy = d[..., part * K:(part + 1) * K].double().reshape(B, T, H, D)
+        r = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-5)
+        gg = dy * gain.double()
+        want_dx.append((r * gg - r.pow(3) * x * (gg * x).mean(-1, keepdim=True)).reshape(B, T, K))
+        want_dg.append((dy * x * r).sum((0, 1, 2)))
+    outs = []
+    for _ in range(2):
+        dq = d.to(cuda)
+        dg1, dg2 = _head_norm_bwd_(dq, raw.to(cuda), n1.to(cuda), n2.to(cuda), 1e-5, H)
+        torch.cuda.synchronize()
+        outs.append((dq.cpu(), dg1.cpu(), dg2.cpu()))
+    dq, dg1, dg2 = outs[0]
+    assert all(torch.equal(a, b) for a, b in zip(outs[0], outs[1]))
+    assert torch.equal(dq[..., 2 * K:], d[..., 2 * K:])
+    if T == 0:
+        assert float(dg1.abs().sum() + dg2.abs().sum()) == 0.0
+        return
+    assert rel_err(dq[..., :K], want_dx[0]) < 2e-2 and rel_err(dq[..., K:2 * K], want_dx[1]) < 2e-2
+    assert rel_err(dg1, want_dg[0]) < 1e-4 and rel_err(dg2, want_dg[1]) < 1e-4
+
+
+def test_head_norm_backward_op_passes_opcheck(cuda):
+    g = torch.Generator().manual_seed(91)
+    dq = torch.randn(2, 40, 3 * 256, generator=g).bfloat16().to(cuda)
+    raw = torch.randn(2, 40, 2 * 256, generator=g).bfloat16().to(cuda)
+    n1, n2 = (torch.rand(64, generator=g) + 0.5).to(cuda), (torch.rand(64, generator=g) + 0.5).to(cuda)
+    torch.library.opcheck(torch.ops.mote.head_rms_norm_bwd_.default, (dq, raw, n1, n2, 1e-5, 4),
+                          test_utils=("test_schema", "test_faketensor"))
 
 
 @pytest.mark.parametrize("B,T,D", [(1, 4964, 768), (2, 333, 512), (1, 1, 256)])

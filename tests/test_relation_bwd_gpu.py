@@ -88,6 +88,23 @@ def test_rescale_branch_grads(cuda):
     _check(got, ref, 1e-5, p1, p2, info, lam, dy, 0)
 
 
+@pytest.mark.parametrize("D", [64, 96, 128])
+def test_bf16_scale3_stress_grads(cuda, D):
+    """Scores of scale 3 (|U| up to ~30, the reference's rescale stress, tests/test_flash_relation.py:54-57)
+    in bf16 through the tile kernels: outputs and gradients within 2e-2 of the float64 oracle."""
+    import mote_amd.flash_relation as fr
+
+    print(f"case bf16 scale-3 grads D={D}", flush=True)
+    p1, p2, info, lam, dy = _inputs(1, 4, 333, 0, D, torch.bfloat16, seed=11, scale=3.0)
+    y, g = fr.flash_relation(p1, p2, info, lam, 2.0)
+    yr, gr = O.relation_reference(p1.detach().cpu(), p2.detach().cpu(), info.detach().cpu(), lam.detach().cpu(), 2.0, 0,
+                                  dtype=torch.float64)
+    assert rel_err(y, yr) < 2e-2 and rel_err(g, gr) < 2e-2
+    got = _grads(p1, p2, info, lam, dy, 0)
+    ref = _oracle_grads(p1, p2, info, lam, dy, 0)
+    _check(got, ref, 2e-2, p1, p2, info, lam, dy, 0)
+
+
 @pytest.mark.parametrize("det", [False, True])
 @pytest.mark.parametrize("D", [32, 48, 64, 96, 128])
 @pytest.mark.parametrize("TQ", [33, 257])
