@@ -202,12 +202,18 @@ int mote_rope_givens_bwd(const mote_rope_givens_bwd_args* args, void* stream);
  * never read. S[b] >= capacity writes NaN into y[b] and skips the append.
  * flags bit 0 (MOTE_DECODE_ADVANCE): add 1 to every S[b] once the step has read it (graph.py's
  * S += 1, :189-190), so a captured step needs no separate kernel for it.
+ * flags bit 1 (MOTE_DECODE_ROPE_F32): RoPE with fp32 cos / sin and fp32 arithmetic, the rotated p1 /
+ * p2 rounded once into `dtype`: the graph decoder's convention when its input x is fp32 under serving
+ * autocast (graph.py:158-164 builds the tables at x.dtype, :171-172 casts into the arena). Without it
+ * the tables are rounded to `dtype` and every product and sum of the rotation is rounded to `dtype`
+ * (x in the cache dtype, relation.py:211-214). Givens is in `dtype` either way (relation.py:165-166).
  * One launch on `stream`: a split-S sweep whose last workgroup per (sequence, head) merges the
  * partials. The workspace (mote_relation_decode_workspace() bytes) holds the per-split partials and
  * completion counters: zero-fill it once before its first call (every call leaves the counters at
  * zero again). Calls that share a workspace must not overlap.
  * ------------------------------------------------------------------------------------------------ */
 #define MOTE_DECODE_ADVANCE 1
+#define MOTE_DECODE_ROPE_F32 2
 
 typedef struct mote_relation_decode_args {
   int dtype;
@@ -246,9 +252,13 @@ int mote_relation_decode(const mote_relation_decode_args* args, void* stream);
  * static device array of MOTE_DECODE_STATIC_BYTES bytes per GPU, held until the process ends. A call
  * takes at most 256 sequences and 1024 sequence-heads (B * H); anything beyond is refused with
  * MOTE_ERR_WORKSPACE before any launch. Every call on one GPU shares the array:
- * calls ordered on one stream are fine, calls that overlap on one GPU (unordered streams) race.
- * The first call on a device clears its copy in the caller's stream order; the stream's device
- * must be the current device. It allocates nothing.
+ * calls ordered on one stream are fine, calls that overlap on one GPU (unordered streams) race. So
+ * a process that decodes on two streams at once (the reference's daemon serves on a stream of its
+ * own beside the trainer's, mote/infer/engine.py:150-162) must give this entry point to at most
+ * one of them and use mote_relation_decode with a workspace on the other.
+ * The first call on a device clears its copy in the caller's stream order and is refused under
+ * graph capture (the clear would be captured and rerun on every replay): make it once outside.
+ * The stream's device must be the current device. It allocates nothing.
  * ------------------------------------------------------------------------------------------------ */
 #define MOTE_DECODE_STATIC_BYTES (1u << 20)
 

@@ -20,6 +20,7 @@ MOTE_OK = 0
 MOTE_F32 = 0
 MOTE_BF16 = 1
 MOTE_DECODE_ADVANCE = 1
+MOTE_DECODE_ROPE_F32 = 2
 MOTE_DECODE_STATIC_BYTES = 1 << 20
 MOTE_BWD_ROWS, MOTE_BWD_KEYS, MOTE_BWD_FINISH, MOTE_BWD_QUERIES = 1, 2, 4, 8
 

@@ -178,10 +178,16 @@ relation_decode_kernel(const DecParams p) {
   // sink the small loads behind the cache loads); only the owning lanes write them to LDS
   float cs, sn;
   sincosf((float)S * invf, &sn, &cs);
+  // MOTE_DECODE_ROPE_F32: fp32 tables and fp32 arithmetic, one rounding at the end (the rows are
+  // computed both ways and selected, so the flag adds no branch ahead of the cache loads)
+  const bool rope32 = (p.flags & MOTE_DECODE_ROPE_F32) != 0;
+  const float cs32 = p.rope ? cs : 1.f, sn32 = p.rope ? sn : 0.f;
   cs = p.rope ? round_to<T>(cs) : 1.f;
   sn = p.rope ? round_to<T>(sn) : 0.f;
-  const float rq0 = rot_round<T>(q0, cs, q1, -sn), rq1 = rot_round<T>(q1, cs, q0, sn);
-  const float rk0 = rot_round<T>(k0, cs, k1, -sn), rk1 = rot_round<T>(k1, cs, k0, sn);
+  const float rq0 = rope32 ? round_to<T>(rot_round<float>(q0, cs32, q1, -sn32)) : rot_round<T>(q0, cs, q1, -sn);
+  const float rq1 = rope32 ? round_to<T>(rot_round<float>(q1, cs32, q0, sn32)) : rot_round<T>(q1, cs, q0, sn);
+  const float rk0 = rope32 ? round_to<T>(rot_round<float>(k0, cs32, k1, -sn32)) : rot_round<T>(k0, cs, k1, -sn);
+  const float rk1 = rope32 ? round_to<T>(rot_round<float>(k1, cs32, k0, sn32)) : rot_round<T>(k1, cs, k0, sn);
   float gc, gs;
   sincosf(th, &gs, &gc);
   gc = p.givens ? round_to<T>(gc) : 1.f;
@@ -567,6 +573,11 @@ static int scratch_address(hipStream_t stream, void** out) {
   }
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
+    // the clear must run once, not on every replay of a graph: refuse a first call under capture
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (stream && hipStreamIsCapturing(stream, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone)
+      return set_error(MOTE_ERR_ARGUMENT, "relation_decode_static: the first call on a device clears the static array "
+                                          "and must not be captured; call it once outside the capture first");
     void* ptr = nullptr;
     const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !ptr)

@@ -46,7 +46,7 @@ def relation_decode(p1: torch.Tensor, p2: torch.Tensor, info: torch.Tensor, S: t
                     inv_freq: Optional[torch.Tensor] = None, theta: Optional[torch.Tensor] = None, layer_idx: int = 0,
                     advance: bool = False, workspace: Optional[torch.Tensor] = None, y: Optional[torch.Tensor] = None,
                     g: Optional[torch.Tensor] = None, xm: Optional[torch.Tensor] = None,
-                    run: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+                    run: Optional[torch.Tensor] = None, rope_f32: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
     """One decode step for B sequences.
 
     p1, p2, info: raw projections of the new chunk, [B, H, dh] (head stride dh, any batch stride),
@@ -59,6 +59,9 @@ def relation_decode(p1: torch.Tensor, p2: torch.Tensor, info: torch.Tensor, S: t
     run: optional one-element bool / uint8 device tensor (e.g. the router's boundary bit): when it
         holds 0 the launch writes nothing at all (no append, no advance, no y / g / xm), so one
         captured graph serves both branches of the graph decoder's conditional main step.
+    rope_f32: RoPE with fp32 tables and arithmetic, rounded once into the cache dtype (the graph
+        decoder's rows when its x is fp32 under serving autocast, graph.py:158-172); otherwise the
+        tables and every operation of the rotation round to the cache dtype (x in that dtype).
     Returns (y [B, H, dh] in the cache dtype, g [B, H] fp32 exchange mass = 1 - F_SS).
     """
     if p1.dim() != 3:
@@ -107,7 +110,8 @@ def relation_decode(p1: torch.Tensor, p2: torch.Tensor, info: torch.Tensor, S: t
     a = L.DecodeArgs()
     a.dtype = L.dtype_code(p1)
     a.B, a.H, a.D, a.capacity = B, H, D, cap
-    a.layer_parity, a.flags, a.tau_s = int(layer_idx) % 2, L.MOTE_DECODE_ADVANCE if advance else 0, float(tau_s)
+    flags = (L.MOTE_DECODE_ADVANCE if advance else 0) | (L.MOTE_DECODE_ROPE_F32 if rope_f32 else 0)
+    a.layer_parity, a.flags, a.tau_s = int(layer_idx) % 2, flags, float(tau_s)
     a.lam = lam32.data_ptr()
     a.inv_freq, a.theta = L.ptr(inv32), L.ptr(th32)
     a.S = S.data_ptr()
@@ -237,9 +241,11 @@ class RelationDecodeStep:
             qkv = torch.stack([q, k, qkv[:, 2]], dim=1)
         # on the skinny path the wo launch writes xm (its mean of g needs no count of finished heads
         # in the decode launch)
+        # RoPE tables at x's dtype (graph.py:161): an fp32 x (serving autocast) rotates in fp32
+        rope_f32 = x.dtype == torch.float32 and self.arena.dtype != torch.float32
         relation_decode(qkv[:, 0], qkv[:, 1], qkv[:, 2], S, self.arena.p2(self.layer), self.arena.info(self.layer),
                         self.lam, m.tau_s, self.inv_freq, self.theta, m.layer_idx, advance, self.workspace,
-                        self.y, self.g, None if skinny else xm, run)
+                        self.y, self.g, None if skinny else xm, run, rope_f32)
         if skinny:  # _out (relation.py:176-182) on the skinny product
             y = self.y.to(x.dtype).reshape(B, H * dh)
             if m.out_gate:

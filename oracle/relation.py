@@ -416,7 +416,8 @@ def relation_decode_ref(p1, p2buf, infobuf, S, lam, tau_s: float = 2.0, dtype=to
     return torch.stack(ys), torch.stack(gs)
 
 
-def decode_rows_ref(p1, p2, info, S, inv_freq, theta, layer_idx: int, dtype, _plant: Optional[str] = None):
+def decode_rows_ref(p1, p2, info, S, inv_freq, theta, layer_idx: int, dtype, _plant: Optional[str] = None,
+                    rope_dtype=None):
     """The new chunk's rows as the graph decoder prepares them (mote/infer/graph.py:158-172).
 
     Inputs are the raw projections [B, H, dh]; the arithmetic runs in `dtype` (the model dtype of
@@ -427,6 +428,9 @@ def decode_rows_ref(p1, p2, info, S, inv_freq, theta, layer_idx: int, dtype, _pl
     * Givens on I~ with c, s = cos / sin(theta) cast to `dtype`, pairs by layer parity
       (relation.py:160-174): (a, b) -> (c a - s b, s a + c b);
     * the cast to the cache dtype (graph.py:171-172), a no-op here.
+    `rope_dtype` (default `dtype`) is x's dtype, the dtype of the RoPE tables (graph.py:161): with
+    float32 (the graph decoder under serving autocast, x fp32 and bf16 projections) the rotation runs
+    in fp32 and the cast of graph.py:171-172 rounds it once into `dtype`; Givens stays in `dtype`.
     `inv_freq` / `theta` None skip RoPE / Givens. Returns three [B, H, dh] tensors in `dtype`.
     `_plant` injects a mistake for the pins: "cos_unrounded" (tables kept in fp32),
     "single_rounding" (the rotation in float64, rounded once), "odd_pairs_shifted" (odd layers
@@ -445,10 +449,11 @@ def decode_rows_ref(p1, p2, info, S, inv_freq, theta, layer_idx: int, dtype, _pl
                 q = (q.double() * c64 + rotate_half(q.double()) * s64).to(dtype)
                 k = (k.double() * c64 + rotate_half(k.double()) * s64).to(dtype)
             else:
+                rd = dtype if rope_dtype is None else rope_dtype
                 if _plant != "cos_unrounded":
-                    cos, sin = cos.to(dtype), sin.to(dtype)
-                q = (q * cos + rotate_half(q) * sin).to(dtype)
-                k = (k * cos + rotate_half(k) * sin).to(dtype)
+                    cos, sin = cos.to(rd), sin.to(rd)
+                q = (q.to(rd) * cos + rotate_half(q.to(rd)) * sin).to(dtype)
+                k = (k.to(rd) * cos + rotate_half(k.to(rd)) * sin).to(dtype)
         if theta is not None:
             c = torch.cos(theta.float().cpu()).to(dtype)[None, :, None, None]
             sn = torch.sin(theta.float().cpu()).to(dtype)[None, :, None, None]

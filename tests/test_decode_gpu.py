@@ -77,6 +77,39 @@ def test_decode_batch16_mixed_positions(cuda):
     assert torch.equal(kd.cpu(), kc2) and torch.equal(vd.cpu(), vc2)
 
 
+@pytest.mark.parametrize("layer_idx", [0, 1])
+def test_decode_rope_f32_convention(cuda, layer_idx):
+    """MOTE_DECODE_ROPE_F32 (the graph decoder with fp32 x under serving autocast, graph.py:158-172):
+    the appended rows against decode_rows_ref with fp32 tables and one rounding: bit for bit except
+    where the kernel's fp32 sincos and the host's differ across a rounding tie (at most 0.5 % of the
+    elements, never more than one bf16 ulp); y and g within 2e-2 of the oracle step on those rows."""
+    from mote_amd.decode import relation_decode
+
+    print(f"case decode rope_f32 layer={layer_idx}", flush=True)
+    S = [4096, 3, 777, 4351]
+    kc, vc, raw, th, inv, Sv = _setup(4, 8, 96, 4352, S, torch.bfloat16, seed=41 + layer_idx)
+    kd, vd, Sd = kc.cuda(), vc.cuda(), Sv.cuda()
+    y, gg = relation_decode(*(t.cuda() for t in raw), Sd, kd, vd, torch.tensor(0.4, device="cuda"), 2.0, inv.cuda(),
+                            th.cuda(), layer_idx, rope_f32=True)
+    torch.cuda.synchronize()
+    q, k, v = O.decode_rows_ref(*raw, Sv, inv, th, layer_idx, torch.bfloat16, rope_dtype=torch.float32)
+    kc2, vc2 = kc.clone(), vc.clone()
+    for b in range(4):
+        kc2[b, :, S[b]] = k[b]
+        vc2[b, :, S[b]] = v[b]
+    assert torch.equal(vd.cpu(), vc2)  # Givens: the same convention either way
+    kg = kd.cpu()
+    assert torch.equal(kg[:, :, :4096][:, :, [s for s in range(4096) if s not in S]],
+                       kc[:, :, [s for s in range(4096) if s not in S]])
+    rows_got = torch.stack([kg[b, :, S[b]] for b in range(4)]).double()
+    rows_want = k.double()
+    diff = (rows_got - rows_want).abs()
+    ulp = (rows_want.abs().clamp(min=1e-30).log2().floor() - 7).exp2()
+    assert bool((diff <= ulp * 1.0001).all()) and float((diff == 0).double().mean()) >= 0.995
+    yr, gr = O.relation_decode_ref(q, kc2, vc2, Sv, torch.tensor(0.4), 2.0, dtype=torch.float64)
+    assert rel_err(y, yr) < 2e-2 and float((gg.cpu().double() - gr).abs().max()) < 2e-2
+
+
 def test_decode_position_zero_is_pure_self(cuda):
     kc, vc, raw, th, inv, Sv = _setup(2, 4, 64, 512, [0, 0], torch.float32)
     y, gg, kd, vd, _ = _run(kc, vc, raw, th, inv, Sv, 0, 0.5)

@@ -418,6 +418,44 @@ def test_planted_decode_row_mistakes_are_caught(plant):
     assert not pin_decode_rows(_plant=plant), f"planted mistake {plant!r} passed"
 
 
+def pin_decode_rows_rope_f32(_plant=None) -> bool:
+    """The graph decoder under serving autocast (graph.py:158-172 with x fp32): bf16 projections
+    rotated with fp32 tables in fp32 and rounded once into the bf16 arena. Pinned by what one
+    rounding means: fp32 arithmetic reproduces the exact rotation of the same bf16 inputs and fp32
+    table values to within a few fp32 ulps, so nearly every element is the bf16 rounding of the
+    float64 rotation (the rest sit on a rounding tie) and none is off by more than one bf16 ulp.
+    The per-op bf16 convention (`_plant="per_op"`: tables and every operation rounded to bf16)
+    misses the first count by far; Givens on I~ is the same in both conventions."""
+    B, H, D = 4, 8, 96
+    raw, theta = _decode_raw(B, H, D, 31, torch.bfloat16)
+    S = torch.tensor([0, 9, 1234, 4351])
+    inv = O.rope_inv_freq(D, 10000.0)
+    rd = None if _plant == "per_op" else torch.float32
+    got = O.decode_rows_ref(*raw, S, inv, theta, 1, torch.bfloat16, rope_dtype=rd)
+    plain = O.decode_rows_ref(*raw, S, inv, theta, 1, torch.bfloat16)
+    ok = torch.equal(got[2], plain[2])
+    same = total = 0
+    for b in range(B):
+        cos, sin = O.rope_tables(int(S[b]), 1, D, 10000.0, torch.float32)  # fp32 tables: angles in fp32
+        for t in range(2):
+            x = raw[t][b][None, :, None, :].double()
+            exact = (x * cos.double() + O.rotate_half(x) * sin.double())[0, :, 0]
+            want = exact.to(torch.bfloat16)
+            same += int((got[t][b] == want).sum())
+            total += want.numel()
+            ulp = (exact.abs().clamp(min=1e-30).log2().floor() - 7).exp2()
+            ok &= bool(((got[t][b].double() - exact).abs() <= ulp * 1.0001).all())
+    return bool(ok and same >= 0.995 * total)
+
+
+def test_decode_rows_rope_f32_is_one_rounding_of_the_exact_rotation():
+    assert pin_decode_rows_rope_f32()
+
+
+def test_planted_per_op_rounding_fails_the_rope_f32_pin():
+    assert not pin_decode_rows_rope_f32(_plant="per_op")
+
+
 def pin_head_rms_norm(_plant=None) -> bool:
     """QK-Norm (relation.py:71-94): float64 against torch.nn.functional.rms_norm with the gain, on
     rows of very different scales (eps matters for the small ones); the closed form of a constant
