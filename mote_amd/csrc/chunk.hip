@@ -9,15 +9,18 @@
 //
 // EMA (z_m = p_m x_m + (1 - p_m) z_{m-1} over the chunks of a row; p clamped to [eps, 1 - eps]).
 // The chunk axis is cut into segments of 64 chunks; a wave owns 128 channels (2 per lane, fp32
-// arithmetic) of one segment. Phase 1 runs each segment from zero and keeps its end value e_s and decay
-// A_s = prod (1 - p). Phase 2 folds the earlier segments' (A, e) into the carry in order, runs the
-// segment again from it, keeps z (fp32, for the backward) and writes z_m to every byte of chunk m, i.e. bytes
+// arithmetic) of one segment, a workgroup four consecutive segments. Phase 1 runs each segment from
+// zero (its end value e_s and decay A_s = prod (1 - p)) and the workgroup composes its four in order
+// through LDS into one aggregate. Phase 2 folds the earlier workgroups' aggregates into the carry in
+// order, then the workgroup's earlier segments, runs the segment again from it, keeps
+// w_m = x_m - z_{m-1} (fp32, for the backward) and writes z_m to every byte of chunk m, i.e. bytes
 // [perm[m], perm[m + 1]) (the last chunk to L): out[t] = z[cum[t] - 1] as dc.py:329-335 gathers it.
-// The segment size is fixed, so the arithmetic that produces z_m depends on chunks <= m only: the
-// result is causal bit for bit, as the reference keeps its own (dc.py:265-268).
+// The segments and workgroups are fixed, so the arithmetic that produces z_m depends on chunks <= m
+// only: the result is causal bit for bit, as the reference keeps its own (dc.py:265-268).
 // The backward mirrors this with a reverse scan g_m = ds_m + (1 - p_{m+1}) g_{m+1}, ds_m the sum of
-// the output gradient over chunk m's bytes; dx_m = p_m g_m, dp_m = sum_d g_m (x_m - z_{m-1}) (a
-// fixed-order sum over channel strips), scattered to boundary_prob[..., 1] through the clamp.
+// the output gradient over chunk m's bytes (workgroup aggregates composed from the last segment down,
+// folded from the row's end); dx_m = p_m g_m, dp_m = sum_d g_m (x_m - z_{m-1}) (a fixed-order sum over
+// channel strips), scattered to boundary_prob[..., 1] through the clamp.
 #include "common.hpp"
 #include "params.hpp"
 
@@ -33,7 +36,7 @@ struct RouteParams {
   const uint8_t* mask; int64_t mask_sr;
   int32_t* cum; int32_t* perm; int32_t* num;
   int32_t* cu;                     // cu_seqlens, written here when there is one row (else null)
-  int L, vec, vec4;                // vec: mask rows on 16-byte boundaries; vec4: cum rows too
+  int L, vec, vec4, vecp;          // vec: mask rows on 16-byte boundaries; vec4: cum rows too; vecp: perm rows
 };
 
 // exclusive prefix of v over the workgroup (in thread order) and the workgroup's total
@@ -60,6 +63,7 @@ __device__ __forceinline__ int block_excl_scan(int v, int* sh, int& total) {
 
 __global__ void __launch_bounds__(kRouteThreads) chunk_route_kernel(const RouteParams p) {
   __shared__ int sh[kRouteThreads / 64];
+  __shared__ __align__(16) int sperm[kRouteThreads * kRoutePer];  // one tile's permutation, by destination
   const int b = blockIdx.x;
   const uint8_t* mk = p.mask + int64_t(b) * p.mask_sr;
   int32_t* cum = p.cum + int64_t(b) * p.L;
@@ -88,7 +92,7 @@ __global__ void __launch_bounds__(kRouteThreads) chunk_route_kernel(const RouteP
       const int t = s + k;
       run += f[k];
       cv[k] = run;
-      if (t < p.L) perm[f[k] ? run - 1 : n + t - run] = t;
+      if (t < p.L) sperm[f[k] ? run - 1 : n + t - run] = t;  // scattered in LDS, not in memory
     }
     if (p.vec4 && s + kRoutePer <= p.L) {
 #pragma unroll
@@ -102,6 +106,14 @@ __global__ void __launch_bounds__(kRouteThreads) chunk_route_kernel(const RouteP
     if (threadIdx.x == 0) {
       p.num[b] = n;
       if (p.cu) { p.cu[0] = 0; p.cu[1] = n; }   // one row: cu_seqlens here, no second launch
+    }
+    __syncthreads();
+    // the permutation out in order: 16-byte stores of consecutive entries when the row allows
+    if (p.vecp) {
+      for (int i = threadIdx.x; i < p.L / 4; i += kRouteThreads)
+        reinterpret_cast<int4*>(perm)[i] = reinterpret_cast<const int4*>(sperm)[i];
+    } else {
+      for (int i = threadIdx.x; i < p.L; i += kRouteThreads) perm[i] = sperm[i];
     }
     return;
   }
@@ -214,6 +226,8 @@ __global__ void __launch_bounds__(256) chunk_gather_bwd_kernel(const GatherParam
 // ------------------------------------------------------------------------------------------------
 constexpr int kDcCh = 128;        // channels per wave (2 per lane)
 constexpr int kDcSeg = 64;        // chunks per segment (one lane per chunk for the per-chunk values)
+constexpr int kDcGrp = 4;         // segments (waves) per workgroup: their carries combine through LDS, so
+                                  // only the workgroups' aggregates cross workgroups
 
 struct DechunkParams {
   const void* x; int64_t x_sb, x_sr;        // hidden [B, M, D] (elements)
@@ -225,10 +239,11 @@ struct DechunkParams {
   const void* dout; int64_t g_sb, g_sr;     // [B, L, D] (backward)
   void* dx; int64_t dx_sb, dx_sr;           // [B, M, D] (backward)
   float* ds;                                // [B, M, D] fp32: dout summed over each chunk's bytes (backward)
-  void* zc;                                 // [B, M + 1, D] hidden's dtype: carried value, then z_m (forward)
-  float* segv; float* segd;                 // [B, nseg, D] segment values, [B, nseg] segment decays
+  float* segv; float* segd;                 // [B, nseg, D] segment values, [B, nseg] decays (backward)
+  float* grpv; float* grpd;                 // [B, ngrp, D] workgroup aggregates' values, [B, ngrp] decays
+  float* pc;                                // [B, M] clamped p of every chunk (vector path, kept by phase 1)
   float* part;                              // [B, nstrips, M] dp partials (backward)
-  int B, L, M, D, nseg, nstrips, p_f32;
+  int B, L, M, D, nseg, ngrp, nstrips, p_f32;
   float eps;
 };
 
@@ -291,161 +306,156 @@ __device__ __forceinline__ int dc_lo(const DechunkParams& p, int b, int m, int n
   return p.perm[int64_t(b) * p.L + m];
 }
 
-// phase 1 (forward): segment run from zero -> end value and decay. The segment's x rows are loaded
-// up front (clamped, unconditional), so one memory latency covers the 64 steps.
-template <bool F32>
-__global__ void __launch_bounds__(64) dechunk_seg_kernel(const DechunkParams p) {
-  typedef Pair<F32> P;
-  const int lane = threadIdx.x, strip = blockIdx.x, s = blockIdx.y, b = blockIdx.z;
-  const int d = min(strip * kDcCh + 2 * lane, p.D - 2);
-  const int n = dc_used(p, b);
-  const int m0 = min(s * kDcSeg, n), cnt = min(kDcSeg, n - m0);
-  float2 z = make_float2(0.f, 0.f);
-  float A = 1.f;
-  if (cnt > 0) {
-    const float pv = dc_p(p, b, m0 + min(lane, cnt - 1));
-    typename P::T xr[kDcSeg];
-    const int64_t xb = b * p.x_sb + d;
-#pragma unroll
-    for (int i = 0; i < kDcSeg; ++i) xr[i] = P::ld(p.x, xb + int64_t(m0 + min(i, cnt - 1)) * p.x_sr);
-#pragma unroll
-    for (int i = 0; i < kDcSeg; ++i) {
-      const float pc = i < cnt ? rdl(pv, i) : 0.f;  // past the segment: p = 0 leaves z and A as they are
-      const float a = 1.f - pc;
-      const float2 x = P::cvt(xr[i]);
-      z.x = fmaf(a, z.x, pc * x.x);
-      z.y = fmaf(a, z.y, pc * x.y);
-      A *= a;
-    }
-  }
-  const int64_t si = int64_t(b) * p.nseg + s;
-  if (strip * kDcCh + 2 * lane < p.D) stf2(p.segv, si * p.D + d, z);
-  if (strip == 0 && lane == 0) p.segd[si] = A;
-}
-
-// c <- A_j c + e_j for j = 0 .. s-1 (in order), in batches of 16 segments, the next batch loading while
-// the current one folds
-__device__ __forceinline__ void dc_fold_fwd(const DechunkParams& p, int b, int d, int s, float2& c) {
-  const int64_t sb0 = int64_t(b) * p.nseg;
+// c <- A_j c + e_j over the aggregates j = j0, j0 + step, ... (cnt of them) at gv (value rows of D
+// floats) / gd (decays), in batches of 16, the next batch loading while the current one folds
+__device__ __forceinline__ void dc_fold(const float* gv, const float* gd, int D, int d, int j0, int step, int cnt,
+                                        float2& c) {
   float2 ea[16], eb[16];
   float Aa[16], Ab[16];
-  auto load = [&](float2 (&e)[16], float (&A)[16], int j0) {
+  auto load = [&](float2 (&e)[16], float (&A)[16], int k0) {
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
-      const int j = max(min(j0 + k, s - 1), 0);
-      e[k] = ldf2(p.segv, (sb0 + j) * p.D + d);
-      A[k] = p.segd[sb0 + j];
+      const int j = j0 + step * min(k0 + k, cnt - 1);
+      e[k] = ldf2(gv, int64_t(j) * D + d);
+      A[k] = gd[j];
     }
   };
-  auto fold = [&](float2 (&e)[16], float (&A)[16], int j0) {
+  auto fold = [&](float2 (&e)[16], float (&A)[16], int k0) {
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
-      if (j0 + k < s) {
+      if (k0 + k < cnt) {
         c.x = fmaf(A[k], c.x, e[k].x);
         c.y = fmaf(A[k], c.y, e[k].y);
       }
     }
   };
-  if (s <= 0) return;
+  if (cnt <= 0) return;
   load(ea, Aa, 0);
-  for (int j0 = 0; j0 < s; j0 += 32) {
-    load(eb, Ab, j0 + 16);
-    fold(ea, Aa, j0);
-    if (j0 + 16 >= s) break;
-    load(ea, Aa, j0 + 32);
-    fold(eb, Ab, j0 + 16);
+  for (int k0 = 0; k0 < cnt; k0 += 32) {
+    load(eb, Ab, k0 + 16);
+    fold(ea, Aa, k0);
+    if (k0 + 16 >= cnt) break;
+    load(ea, Aa, k0 + 32);
+    fold(eb, Ab, k0 + 16);
   }
 }
 
-// G <- f_j + A'_j G for j = last .. s+1 (from the row's last segment down), batched as dc_fold_fwd
-__device__ __forceinline__ void dc_fold_bwd(const DechunkParams& p, int b, int d, int s, int last, float2& G) {
-  const int64_t sb0 = int64_t(b) * p.nseg;
-  float2 fa[16], fb[16];
-  float Aa[16], Ab[16];
-  auto load = [&](float2 (&f)[16], float (&A)[16], int j1) {
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const int j = min(max(j1 - k, s + 1), last);
-      f[k] = ldf2(p.segv, (sb0 + j) * p.D + d);
-      A[k] = p.segd[sb0 + j];
-    }
-  };
-  auto fold = [&](float2 (&f)[16], float (&A)[16], int j1) {
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      if (j1 - k > s) {
-        G.x = fmaf(A[k], G.x, f[k].x);
-        G.y = fmaf(A[k], G.y, f[k].y);
-      }
-    }
-  };
-  if (last <= s) return;
-  load(fa, Aa, last);
-  for (int j1 = last; j1 > s; j1 -= 32) {
-    load(fb, Ab, j1 - 16);
-    fold(fa, Aa, j1);
-    if (j1 - 16 <= s) break;
-    load(fa, Aa, j1 - 32);
-    fold(fb, Ab, j1 - 16);
-  }
-}
-
-// phase 2 (forward): carry in, run again; keep w_m = x_m - z_{m-1} (fp32) and the compact values
-// zc[b, 1 + m] = z_m in hidden's dtype, with zc[b, 0] = the carried value (or 0)
+// A wave's segment of the forward EMA: its chunks, their p (lane i holds chunk m0 + i) and x rows
+// (loaded up front, clamped, unconditional), run from zero to its end value e and decay A.
 template <bool F32>
-__global__ void __launch_bounds__(64) dechunk_scan_kernel(const DechunkParams p) {
+struct DcFwdSeg {
   typedef Pair<F32> P;
-  const int lane = threadIdx.x, strip = blockIdx.x, s = blockIdx.y, b = blockIdx.z;
+  int m0, cnt;
+  float pv;
+  typename P::T xr[kDcSeg];
+  float2 e;
+  float A;
+  __device__ __forceinline__ void run(const DechunkParams& p, int b, int d, int s, int n) {
+    m0 = min(s * kDcSeg, n);
+    cnt = min(kDcSeg, n - m0);
+    e = make_float2(0.f, 0.f);
+    A = 1.f;
+    pv = 0.f;
+    if (cnt <= 0) return;
+    pv = dc_p(p, b, m0 + min(threadIdx.x & 63, cnt - 1));
+    const int64_t xb = b * p.x_sb + d;
+#pragma unroll
+    for (int i = 0; i < kDcSeg; ++i) xr[i] = P::ld(p.x, xb + int64_t(m0 + min(i, cnt - 1)) * p.x_sr);
+#pragma unroll
+    for (int i = 0; i < kDcSeg; ++i) {
+      const float pc = i < cnt ? rdl(pv, i) : 0.f;  // past the segment: p = 0 leaves e and A as they are
+      const float a = 1.f - pc;
+      const float2 x = P::cvt(xr[i]);
+      e.x = fmaf(a, e.x, pc * x.x);
+      e.y = fmaf(a, e.y, pc * x.y);
+      A *= a;
+    }
+  }
+};
+
+// phase 1 (forward): every wave runs its segment from zero; the workgroup composes its kDcGrp
+// segments in order (through LDS) into one aggregate (value, decay) for the later workgroups
+template <bool F32>
+__global__ void __launch_bounds__(64 * kDcGrp) dechunk_grp_kernel(const DechunkParams p) {
+  __shared__ float2 se[kDcGrp][64];
+  __shared__ float sa[kDcGrp];
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int strip = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+  const int d = min(strip * kDcCh + 2 * lane, p.D - 2);
+  DcFwdSeg<F32> sg;
+  sg.run(p, b, d, g * kDcGrp + w, dc_used(p, b));
+  se[w][lane] = sg.e;
+  if (lane == 0) sa[w] = sg.A;
+  __syncthreads();
+  if (w == 0) {
+    float2 e = make_float2(0.f, 0.f);
+    float A = 1.f;
+#pragma unroll
+    for (int i = 0; i < kDcGrp; ++i) {
+      const float a = sa[i];
+      e.x = fmaf(a, e.x, se[i][lane].x);
+      e.y = fmaf(a, e.y, se[i][lane].y);
+      A *= a;
+    }
+    const int64_t gi = int64_t(b) * p.ngrp + g;
+    if (strip * kDcCh + 2 * lane < p.D) stf2(p.grpv, gi * p.D + d, e);
+    if (strip == 0 && lane == 0) p.grpd[gi] = A;
+  }
+}
+
+// phase 2 (forward): the carry into the workgroup (the row's carried value, then the earlier
+// workgroups' aggregates in order), into the wave (its workgroup's earlier segments, from LDS), then
+// the segment again from it: w_m = x_m - z_{m-1} (fp32, for the backward) and z_m written to every
+// byte of chunk m (bytes [first byte of m, first byte of m + 1); dc.py:329-335 gathers the same
+// values by the boundary count); bytes before the first boundary hold the carried value with one.
+template <bool F32>
+__global__ void __launch_bounds__(64 * kDcGrp) dechunk_out_kernel(const DechunkParams p) {
+  typedef Pair<F32> P;
+  __shared__ float2 se[kDcGrp][64];
+  __shared__ float sa[kDcGrp];
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int strip = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+  const int s = g * kDcGrp + w;
   const bool live = strip * kDcCh + 2 * lane < p.D;
   const int d = min(strip * kDcCh + 2 * lane, p.D - 2);
   const int n = dc_used(p, b);
-  const int m0 = min(s * kDcSeg, n), cnt = min(kDcSeg, n - m0);
+  DcFwdSeg<F32> sg;
+  sg.run(p, b, d, s, n);
+  // the lane's chunk's byte range (lanes past the segment: empty)
+  const int t0l = sg.cnt > 0 ? dc_lo(p, b, sg.m0 + lane, n) : p.L;
+  const int t1l = sg.cnt > 0 ? dc_lo(p, b, sg.m0 + lane + 1, n) : p.L;
+  se[w][lane] = sg.e;
+  if (lane == 0) sa[w] = sg.A;
   float2 c = make_float2(0.f, 0.f);
   if (p.init) c = ldf2(p.init, int64_t(b) * p.D + d);
-  const int64_t zb = int64_t(b) * (p.M + 1) * p.D + d;
-  if (s == 0 && live) P::st(p.zc, zb, c);
-  if (cnt <= 0) return;
-  const float pv = dc_p(p, b, m0 + min(lane, cnt - 1));
-  typename P::T xr[kDcSeg];
-  const int64_t xb = b * p.x_sb + d;
-#pragma unroll
-  for (int i = 0; i < kDcSeg; ++i) xr[i] = P::ld(p.x, xb + int64_t(m0 + min(i, cnt - 1)) * p.x_sr);
-  dc_fold_fwd(p, b, d, s, c);  // c <- A_j c + e_j, j = 0 .. s-1, in order
+  dc_fold(p.grpv + int64_t(b) * p.ngrp * p.D, p.grpd + int64_t(b) * p.ngrp, p.D, d, 0, 1, g, c);
+  __syncthreads();
+  for (int i = 0; i < w; ++i) {
+    const float a = sa[i];
+    c.x = fmaf(a, c.x, se[i][lane].x);
+    c.y = fmaf(a, c.y, se[i][lane].y);
+  }
+  const int64_t ob = b * p.o_sb + d;
+  if (s == 0 && p.init) {
+    const int tf = dc_lo(p, b, 0, n);
+    for (int t = 0; t < tf; ++t)
+      if (live) P::st(p.out, ob + int64_t(t) * p.o_sr, c);
+  }
+  if (sg.cnt <= 0) return;
   float2 z = c;
-  float* wrow = p.w + (int64_t(b) * p.M + m0) * p.D + d;
-  void* zrow = reinterpret_cast<uint8_t*>(p.zc) + (zb + int64_t(m0 + 1) * p.D) * (F32 ? 4 : 2);
+  float* wrow = p.w + (int64_t(b) * p.M + sg.m0) * p.D + d;
 #pragma unroll
   for (int i = 0; i < kDcSeg; ++i) {
-    if (i < cnt) {
-      const float pc = rdl(pv, i), a = 1.f - pc;
-      const float2 x = P::cvt(xr[i]);
+    if (i < sg.cnt) {
+      const float pc = rdl(sg.pv, i), a = 1.f - pc;
+      const float2 x = P::cvt(sg.xr[i]);
       if (live && p.w) stf2(wrow, int64_t(i) * p.D, make_float2(x.x - z.x, x.y - z.y));
       z.x = fmaf(a, z.x, pc * x.x);
       z.y = fmaf(a, z.y, pc * x.y);
-      if (live) P::st(zrow, int64_t(i) * p.D, z);
+      const int t0 = rdl(t0l, i), t1 = rdl(t1l, i);
+      for (int t = t0; t < t1; ++t)
+        if (live) P::st(p.out, ob + int64_t(t) * p.o_sr, z);
     }
-  }
-}
-
-// out[b, t] = zc[b, cum[t]] with the carried value, zc[b, max(cum[t], 1)] without (bytes before the
-// first boundary read chunk 0, dc.py:326): one wave per byte row, 16-byte units when rows allow
-__global__ void __launch_bounds__(256) dechunk_expand_kernel(const DechunkParams p, const int32_t* cum, int es,
-                                                             int vec) {
-  const int lane = threadIdx.x & 63;
-  const int64_t r = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (r >= int64_t(p.B) * p.L) return;
-  const int b = int(r / p.L), t = int(r % p.L);
-  const int c = cum[int64_t(b) * p.L + t];
-  const int idx = p.init ? min(c, p.M) : max(min(c, p.M), 1);
-  const uint8_t* src = reinterpret_cast<const uint8_t*>(p.zc) + ((int64_t(b) * (p.M + 1) + idx) * p.D) * es;
-  uint8_t* dst = reinterpret_cast<uint8_t*>(p.out) + (b * p.o_sb + int64_t(t) * p.o_sr) * es;
-  const int bytes = p.D * es;
-  if (vec) {
-    for (int u = lane; u < bytes / 16; u += 64)
-      reinterpret_cast<uint4*>(dst)[u] = reinterpret_cast<const uint4*>(src)[u];
-  } else {
-    for (int u = lane; u < bytes / 4; u += 64)
-      reinterpret_cast<uint32_t*>(dst)[u] = reinterpret_cast<const uint32_t*>(src)[u];
   }
 }
 
@@ -457,9 +467,15 @@ __global__ void __launch_bounds__(256) dechunk_dsum_kernel(const DechunkParams p
   const int64_t r = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (r >= int64_t(p.B) * p.M) return;
   const int b = int(r / p.M), m = int(r % p.M);
-  const int n = dc_used(p, b);
+  // the count and both positions in one round trip (m < M <= L); dc_used / dc_lo from them
+  const int nraw = p.num[b];
+  const int pa = p.perm[int64_t(b) * p.L + m];
+  const int pb = p.perm[int64_t(b) * p.L + min(m + 1, p.L - 1)];
+  const int n0 = min(nraw, p.M);
+  const int n = (p.init == nullptr && n0 == 0 && p.M > 0) ? 1 : n0;
   if (m >= n) return;
-  const int t0 = dc_lo(p, b, m, n), t1 = dc_lo(p, b, m + 1, n);
+  const int t0 = (m == 0 && p.init == nullptr) ? 0 : pa;
+  const int t1 = m + 1 >= n ? p.L : pb;
   float* dsrow = p.ds + (int64_t(b) * p.M + m) * p.D;
   const int64_t gb = b * p.g_sb;
   for (int d0 = 8 * lane; d0 < p.D; d0 += 512) {
@@ -514,11 +530,18 @@ __global__ void __launch_bounds__(256) dechunk_dsum_kernel(const DechunkParams p
   }
 }
 
-// phase 1 (backward): reverse scan of a segment from zero over its ds rows (loaded up front):
-// h_m = ds_m + (1 - p_{m+1}) h_{m+1}. Keeps the value at the first chunk and the decay
-// prod_{k = m0+1}^{m1} (1 - p_k) that carries the next segment's value into it.
-__global__ void __launch_bounds__(64) dechunk_bwd_seg_kernel(const DechunkParams p) {
-  const int lane = threadIdx.x, strip = blockIdx.x, s = blockIdx.y, b = blockIdx.z;
+// phase 1 (backward): every wave runs the reverse scan of its segment from zero over its ds rows
+// (loaded up front): h_m = ds_m + (1 - p_{m+1}) h_{m+1}; it keeps the value at the first chunk and the
+// decay prod_{k = m0+1}^{m0+cnt} (1 - p_k) that carries the next segment's value into it (segments
+// past the row: value 0, decay 1). The workgroup composes its segments from the last down (LDS)
+// into one aggregate for the earlier workgroups.
+__global__ void __launch_bounds__(64 * kDcGrp) dechunk_bwd_grp_kernel(const DechunkParams p) {
+  __shared__ float2 sh[kDcGrp][64];
+  __shared__ float sa[kDcGrp];
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int strip = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+  const int s = g * kDcGrp + w;
+  const bool live = strip * kDcCh + 2 * lane < p.D;
   const int d = min(strip * kDcCh + 2 * lane, p.D - 2);
   const int n = dc_used(p, b);
   const int m0 = min(s * kDcSeg, n), cnt = min(kDcSeg, n - m0);
@@ -542,18 +565,39 @@ __global__ void __launch_bounds__(64) dechunk_bwd_seg_kernel(const DechunkParams
     }
   }
   const int64_t si = int64_t(b) * p.nseg + s;
-  if (strip * kDcCh + 2 * lane < p.D) stf2(p.segv, si * p.D + d, h);
+  if (live) stf2(p.segv, si * p.D + d, h);
   if (strip == 0 && lane == 0) p.segd[si] = A;
+  sh[w][lane] = h;
+  if (lane == 0) sa[w] = A;
+  __syncthreads();
+  if (w == 0) {
+    float2 e = make_float2(0.f, 0.f);
+    float Ag = 1.f;
+#pragma unroll
+    for (int i = kDcGrp - 1; i >= 0; --i) {
+      const float a = sa[i];
+      e.x = fmaf(a, e.x, sh[i][lane].x);
+      e.y = fmaf(a, e.y, sh[i][lane].y);
+      Ag *= a;
+    }
+    const int64_t gi = int64_t(b) * p.ngrp + g;
+    if (live) stf2(p.grpv, gi * p.D + d, e);
+    if (strip == 0 && lane == 0) p.grpd[gi] = Ag;
+  }
 }
 
-// phase 2 (backward): carry from the later segments, reverse run again over ds; dx = p g and the dp
-// partials sum_d g (x - z_prev) = sum_d g w, reduced over the wave's channels in a fixed order.
-// ds and w rows come in 4 stages of 16 chunks, the next stage loading while the current one runs.
+// phase 2 (backward): the carry into the segment's end from the later workgroups' aggregates (from
+// the row's last down) and the later segments of its own workgroup, then the reverse run again over
+// ds: dx = p g and the dp partials sum_d g (x - z_prev) = sum_d g w, reduced over the wave's channels
+// in a fixed order. ds and w rows come in 4 stages of 16 chunks, the next stage loading while the
+// current one runs.
 template <bool F32>
-__global__ void __launch_bounds__(64) dechunk_bwd_out_kernel(const DechunkParams p) {
+__global__ void __launch_bounds__(64 * kDcGrp) dechunk_bwd_out_kernel(const DechunkParams p) {
   typedef Pair<F32> P;
-  __shared__ float red[kDcSeg][65];
-  const int lane = threadIdx.x, strip = blockIdx.x, s = blockIdx.y, b = blockIdx.z;
+  __shared__ float red[kDcGrp][kDcSeg][65];
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int strip = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+  const int s = g * kDcGrp + w;
   const bool live = strip * kDcCh + 2 * lane < p.D;
   const int d = min(strip * kDcCh + 2 * lane, p.D - 2);
   const int n = dc_used(p, b);
@@ -563,50 +607,522 @@ __global__ void __launch_bounds__(64) dechunk_bwd_out_kernel(const DechunkParams
     for (int m = n; m < p.M; ++m)
       if (live) P::st(p.dx, xb + int64_t(m) * p.dx_sr, make_float2(0.f, 0.f));
   }
-  if (cnt <= 0) return;
-  const int mm = m0 + min(lane, cnt - 1);
-  const float pv = dc_p(p, b, mm);
-  const float pn = mm + 1 < n ? dc_p(p, b, mm + 1) : 0.f;
-  const int64_t db = (int64_t(b) * p.M + m0) * p.D + d;
-  float2 dsa[16], wa[16], dsb[16], wb[16];
-  auto load = [&](float2 (&dsv)[16], float2 (&wv)[16], int q) {
+  if (cnt > 0) {
+    const int mm = m0 + min(lane, cnt - 1);
+    const float pv = dc_p(p, b, mm);
+    const float pn = mm + 1 < n ? dc_p(p, b, mm + 1) : 0.f;
+    const int64_t db = (int64_t(b) * p.M + m0) * p.D + d;
+    float2 dsa[16], wa[16], dsb[16], wb[16];
+    auto load = [&](float2 (&dsv)[16], float2 (&wv)[16], int q) {
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const int i = min(16 * q + k, cnt - 1);
-      dsv[k] = ldf2(p.ds, db + int64_t(i) * p.D);
-      wv[k] = ldf2(p.w, db + int64_t(i) * p.D);
-    }
-  };
-  load(dsa, wa, 3);
-  // G = g at chunk m0 + cnt: fold the row's segments last .. s+1 (G <- f_j + A'_j G)
-  float2 g = make_float2(0.f, 0.f);
-  dc_fold_bwd(p, b, d, s, (n + kDcSeg - 1) / kDcSeg - 1, g);
-  auto run = [&](float2 (&dsv)[16], float2 (&wv)[16], int q) {
-#pragma unroll
-    for (int k = 15; k >= 0; --k) {
-      const int i = 16 * q + k;
-      if (i < cnt) {
-        const float an = 1.f - rdl(pn, i), pc = rdl(pv, i);
-        g.x = fmaf(an, g.x, dsv[k].x);
-        g.y = fmaf(an, g.y, dsv[k].y);
-        if (live) P::st(p.dx, xb + int64_t(m0 + i) * p.dx_sr, make_float2(pc * g.x, pc * g.y));
-        red[i][lane] = live ? g.x * wv[k].x + g.y * wv[k].y : 0.f;
+      for (int k = 0; k < 16; ++k) {
+        const int i = min(16 * q + k, cnt - 1);
+        dsv[k] = ldf2(p.ds, db + int64_t(i) * p.D);
+        wv[k] = ldf2(p.w, db + int64_t(i) * p.D);
       }
+    };
+    load(dsa, wa, 3);
+    // G = g at chunk m0 + cnt: the row's later workgroups (last .. g + 1), then the workgroup's later
+    // segments (kDcGrp - 1 .. w + 1), each G <- f + A' G
+    float2 gg = make_float2(0.f, 0.f);
+    const int lastg = ((n + kDcSeg - 1) / kDcSeg - 1) / kDcGrp;
+    dc_fold(p.grpv + int64_t(b) * p.ngrp * p.D, p.grpd + int64_t(b) * p.ngrp, p.D, d, lastg, -1, lastg - g, gg);
+    for (int i = kDcGrp - 1; i > w; --i) {
+      const int64_t sj = int64_t(b) * p.nseg + g * kDcGrp + i;
+      const float a = p.segd[sj];
+      const float2 f = ldf2(p.segv, sj * p.D + d);
+      gg.x = fmaf(a, gg.x, f.x);
+      gg.y = fmaf(a, gg.y, f.y);
     }
-  };
-  load(dsb, wb, 2);
-  run(dsa, wa, 3);
-  load(dsa, wa, 1);
-  run(dsb, wb, 2);
-  load(dsb, wb, 0);
-  run(dsa, wa, 1);
-  run(dsb, wb, 0);
+    auto run = [&](float2 (&dsv)[16], float2 (&wv)[16], int q) {
+#pragma unroll
+      for (int k = 15; k >= 0; --k) {
+        const int i = 16 * q + k;
+        if (i < cnt) {
+          const float an = 1.f - rdl(pn, i), pc = rdl(pv, i);
+          gg.x = fmaf(an, gg.x, dsv[k].x);
+          gg.y = fmaf(an, gg.y, dsv[k].y);
+          if (live) P::st(p.dx, xb + int64_t(m0 + i) * p.dx_sr, make_float2(pc * gg.x, pc * gg.y));
+          red[w][i][lane] = live ? gg.x * wv[k].x + gg.y * wv[k].y : 0.f;
+        }
+      }
+    };
+    load(dsb, wb, 2);
+    run(dsa, wa, 3);
+    load(dsa, wa, 1);
+    run(dsb, wb, 2);
+    load(dsb, wb, 0);
+    run(dsa, wa, 1);
+    run(dsb, wb, 0);
+  }
   __syncthreads();
   if (lane < cnt) {  // lane k sums chunk m0 + k over the 64 lanes, in lane order
     float a = 0.f;
-    for (int l = 0; l < 64; ++l) a += red[lane][l];
+    for (int l = 0; l < 64; ++l) a += red[w][lane][l];
     p.part[(int64_t(b) * p.nstrips + strip) * p.M + m0 + lane] = a;
   }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Vector path (D % 8 == 0, rows on 16-byte boundaries). A wave still owns one 64-chunk segment of a
+// 128-channel strip, but as four 16-lane groups: group q runs chunks m0 + 16 q .. + 15 (a sub-segment)
+// and lane r of it channels 8 r .. 8 r + 7, with 16-byte loads and stores. Every row access of the
+// wave then moves four rows at once, and the sequential chain of a wave is 16 chunks long; the
+// sub-segments compose in order through LDS like the segments do.
+// A launch here is a chain of dependent memory round trips, so every load that does not need another
+// is issued at the kernel's start: the segment's rows are read clamped to the bucket (M) before the
+// row's chunk count arrives, which then only masks, and the clamped p of every chunk is kept by the
+// first launch (`pc`) so the second reads it in one trip.
+// ------------------------------------------------------------------------------------------------
+constexpr int kDvSub = 16;  // chunks per lane group
+
+template <bool F32> struct V8;
+template <> struct V8<false> {  // 8 bf16
+  struct Raw { uint4 u; };
+  static __device__ __forceinline__ Raw ld(const void* base, int64_t off) {
+    return Raw{*reinterpret_cast<const uint4*>(reinterpret_cast<const bf16_t*>(base) + off)};
+  }
+  static __device__ __forceinline__ void cvt(const Raw& r, float (&v)[8]) {
+    const uint32_t w[4] = {r.u.x, r.u.y, r.u.z, r.u.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      v[2 * k] = bf2f(w[k] & 0xffffu);
+      v[2 * k + 1] = bf2f(w[k] >> 16);
+    }
+  }
+  static __device__ __forceinline__ void st(void* base, int64_t off, const float (&v)[8]) {
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) w[k] = uint32_t(f2bf(v[2 * k])) | (uint32_t(f2bf(v[2 * k + 1])) << 16);
+    *reinterpret_cast<uint4*>(reinterpret_cast<bf16_t*>(base) + off) = uint4{w[0], w[1], w[2], w[3]};
+  }
+};
+template <> struct V8<true> {  // 8 fp32
+  struct Raw { float4 a, b; };
+  static __device__ __forceinline__ Raw ld(const void* base, int64_t off) {
+    const float4* q = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(base) + off);
+    return Raw{q[0], q[1]};
+  }
+  static __device__ __forceinline__ void cvt(const Raw& r, float (&v)[8]) {
+    v[0] = r.a.x; v[1] = r.a.y; v[2] = r.a.z; v[3] = r.a.w; v[4] = r.b.x; v[5] = r.b.y; v[6] = r.b.z; v[7] = r.b.w;
+  }
+  static __device__ __forceinline__ void st(void* base, int64_t off, const float (&v)[8]) {
+    float4* q = reinterpret_cast<float4*>(reinterpret_cast<float*>(base) + off);
+    q[0] = make_float4(v[0], v[1], v[2], v[3]);
+    q[1] = make_float4(v[4], v[5], v[6], v[7]);
+  }
+};
+typedef V8<true> F8;
+
+// c <- A_j c + e_j for j = j0 + step k, k = 0 .. cnt - 1, in that order: each lane group composes a
+// quarter of the sequence (8 maps loaded at a time), then every lane applies the four quarters in
+// order, taking the other groups' from lane shuffles. Every lane of the wave calls it.
+__device__ __forceinline__ void dv_fold(const float* gv, const float* gd, int D, int d, int j0, int step, int cnt,
+                                        float (&c)[8]) {
+  const int lane = threadIdx.x & 63, q = lane >> 4, r = lane & 15;
+  const int per = (max(cnt, 0) + 3) / 4;
+  const int k0 = q * per, k1 = min(cnt, k0 + per);
+  float E[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float A = 1.f;
+  for (int kb = k0; kb < k1; kb += 8) {
+    F8::Raw e[8];
+    float a[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int j = j0 + step * min(kb + k, k1 - 1);
+      e[k] = F8::ld(gv, int64_t(j) * D + d);
+      a[k] = gd[j];
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (kb + k < k1) {
+        float v[8];
+        F8::cvt(e[k], v);
+#pragma unroll
+        for (int ch = 0; ch < 8; ++ch) E[ch] = fmaf(a[k], E[ch], v[ch]);
+        A *= a[k];
+      }
+    }
+  }
+#pragma unroll
+  for (int qq = 0; qq < 4; ++qq) {
+    const int src = 16 * qq + r;
+    const float Aq = __shfl(A, src, 64);
+#pragma unroll
+    for (int ch = 0; ch < 8; ++ch) c[ch] = fmaf(Aq, c[ch], __shfl(E[ch], src, 64));
+  }
+}
+
+// the row's chunk count (dc_used) from the raw count
+__device__ __forceinline__ int dc_used_raw(const DechunkParams& p, int nraw) {
+  const int n = min(nraw, p.M);
+  return (p.init == nullptr && n == 0 && p.M > 0) ? 1 : n;
+}
+__device__ __forceinline__ float dc_clamp(const DechunkParams& p, float v) {
+  return fminf(fmaxf(v, p.eps), 1.0f - p.eps);
+}
+
+// phase 1 (forward, vector path): sub-segments run from zero, composed in order (LDS) into the
+// workgroup's aggregate; the clamped p of the segment's chunks go to pc
+template <bool F32>
+__global__ void __launch_bounds__(64 * kDcGrp) dechunk_grp_v_kernel(const DechunkParams p) {
+  typedef V8<F32> V;
+  __shared__ float se[kDcGrp * 4][16][8];
+  __shared__ float sa[kDcGrp * 4];
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int q = lane >> 4, r = lane & 15;
+  const int strip = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+  const int d = min(strip * kDcCh + 8 * r, p.D - 8);
+  const int ms = (g * kDcGrp + w) * kDcSeg, mq = ms + kDvSub * q, mmax = max(p.M - 1, 0);
+  // independent loads: the count, the lane's chunk position, the sub-segment's rows
+  const int nraw = p.num[b];
+  const int tp = p.perm[int64_t(b) * p.L + min(ms + lane, mmax)];
+  typename V::Raw xr[kDvSub];
+  if (p.M > 0) {
+#pragma unroll
+    for (int i = 0; i < kDvSub; ++i) xr[i] = V::ld(p.x, b * p.x_sb + d + int64_t(min(mq + i, mmax)) * p.x_sr);
+  }
+  const float pv = dc_clamp(p, ld1(p.prob, b * p.p_sb + int64_t(tp) * p.p_sr + 1, p.p_f32));
+  const int n = dc_used_raw(p, nraw);
+  const int cnt = min(kDcSeg, n - ms), cs = min(max(cnt - kDvSub * q, 0), kDvSub);
+  if (strip == 0 && ms + lane < p.M) p.pc[int64_t(b) * p.M + ms + lane] = pv;
+  float e[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float A = 1.f;
+  if (cnt > 0) {
+#pragma unroll
+    for (int i = 0; i < kDvSub; ++i) {
+      const float pc = __shfl(pv, kDvSub * q + i, 64);
+      if (i < cs) {
+        float x[8];
+        V::cvt(xr[i], x);
+        const float a = 1.f - pc;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) e[c] = fmaf(a, e[c], pc * x[c]);
+        A *= a;
+      }
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < 8; ++c) se[4 * w + q][r][c] = e[c];
+  if (r == 0) sa[4 * w + q] = A;
+  __syncthreads();
+  // lane group 0 of each wave: its segment's aggregate (phase 2 reads those of the workgroup's
+  // earlier segments), and wave 0 the workgroup's
+  if (q == 0) {
+    const bool live = strip * kDcCh + 8 * r < p.D;
+    float E[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float Ag = 1.f;
+    for (int k = 0; k < kDcGrp * 4; ++k) {
+      const float a = sa[k];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) E[c] = fmaf(a, E[c], se[k][r][c]);
+      Ag *= a;
+      if (k == 4 * w + 3) {
+        const int64_t si = int64_t(b) * p.nseg + g * kDcGrp + w;
+        float S[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        float As = 1.f;
+        for (int kk = 4 * w; kk < 4 * w + 4; ++kk) {
+#pragma unroll
+          for (int c = 0; c < 8; ++c) S[c] = fmaf(sa[kk], S[c], se[kk][r][c]);
+          As *= sa[kk];
+        }
+        if (live) F8::st(p.segv, si * p.D + d, S);
+        if (strip == 0 && r == 0) p.segd[si] = As;
+        if (w != 0) break;
+      }
+    }
+    if (w == 0) {
+      const int64_t gi = int64_t(b) * p.ngrp + g;
+      if (live) F8::st(p.grpv, gi * p.D + d, E);
+      if (strip == 0 && r == 0) p.grpd[gi] = Ag;
+    }
+  }
+}
+
+// phase 2 (forward, vector path), one wave per workgroup so the stores spread over the chip: the
+// carry into the segment (the row's carried value, the earlier workgroups' aggregates, the earlier
+// segments of its phase-1 workgroup), into each lane group (the earlier sub-segments, by lane
+// shuffles), then the sub-segment again: w_m = x_m - z_{m-1} (fp32) and z_m to every byte of chunk m;
+// bytes before the first boundary hold the carried value with one
+template <bool F32>
+__global__ void __launch_bounds__(64) dechunk_out_v_kernel(const DechunkParams p) {
+  typedef V8<F32> V;
+  const int lane = threadIdx.x & 63;
+  const int q = lane >> 4, r = lane & 15;
+  const int strip = blockIdx.x, s = blockIdx.y, b = blockIdx.z;
+  const int g = s / kDcGrp;
+  const bool live = strip * kDcCh + 8 * r < p.D;
+  const int d = min(strip * kDcCh + 8 * r, p.D - 8);
+  const int ms = s * kDcSeg, mq = ms + kDvSub * q, mmax = max(p.M - 1, 0);
+  const int nraw = p.num[b];
+  const float pv = p.M > 0 ? p.pc[int64_t(b) * p.M + min(ms + lane, mmax)] : 0.f;
+  const int pa = p.perm[int64_t(b) * p.L + min(ms + lane, mmax)];
+  const int pb = p.perm[int64_t(b) * p.L + min(ms + lane + 1, mmax)];
+  typename V::Raw xr[kDvSub];
+  if (p.M > 0) {
+#pragma unroll
+    for (int i = 0; i < kDvSub; ++i) xr[i] = V::ld(p.x, b * p.x_sb + d + int64_t(min(mq + i, mmax)) * p.x_sr);
+  }
+  // the earlier segments of the phase-1 workgroup (at most kDcGrp - 1 maps)
+  F8::Raw sv[kDcGrp - 1];
+  float sd[kDcGrp - 1];
+#pragma unroll
+  for (int k = 0; k < kDcGrp - 1; ++k) {
+    const int64_t si = int64_t(b) * p.nseg + min(g * kDcGrp + k, s);
+    sv[k] = F8::ld(p.segv, si * p.D + d);
+    sd[k] = p.segd[si];
+  }
+  float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (p.init) F8::cvt(F8::ld(p.init, int64_t(b) * p.D + d), z);
+  dv_fold(p.grpv + int64_t(b) * p.ngrp * p.D, p.grpd + int64_t(b) * p.ngrp, p.D, d, 0, 1, g, z);
+#pragma unroll
+  for (int k = 0; k < kDcGrp - 1; ++k) {
+    if (g * kDcGrp + k < s) {
+      float v[8];
+      F8::cvt(sv[k], v);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) z[c] = fmaf(sd[k], z[c], v[c]);
+    }
+  }
+  const int n = dc_used_raw(p, nraw);
+  const int cnt = min(kDcSeg, n - ms), cs = min(max(cnt - kDvSub * q, 0), kDvSub);
+  const int m = ms + lane;
+  const int t0l = m >= n ? p.L : (m == 0 && p.init == nullptr ? 0 : pa);
+  const int t1l = m + 1 >= n ? p.L : pb;
+  const int pa0 = __shfl(pa, 0, 64);  // perm[0] when s == 0
+  float e[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float A = 1.f;
+  if (cnt > 0) {
+#pragma unroll
+    for (int i = 0; i < kDvSub; ++i) {
+      const float pc = __shfl(pv, kDvSub * q + i, 64);
+      if (i < cs) {
+        float x[8];
+        V::cvt(xr[i], x);
+        const float a = 1.f - pc;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) e[c] = fmaf(a, e[c], pc * x[c]);
+        A *= a;
+      }
+    }
+  }
+  // the earlier lane groups' sub-segments, in order
+#pragma unroll
+  for (int qq = 0; qq < 3; ++qq) {
+    const int src = 16 * qq + r;
+    const float Aq = __shfl(A, src, 64);
+    float Eq[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) Eq[c] = __shfl(e[c], src, 64);
+    if (qq < q) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) z[c] = fmaf(Aq, z[c], Eq[c]);
+    }
+  }
+  const int64_t ob = b * p.o_sb + d;
+  if (s == 0 && q == 0 && p.init) {
+    const int tf = n > 0 ? pa0 : p.L;  // dc_lo(0): the first boundary, all bytes without one
+    for (int t = 0; t < tf; ++t)
+      if (live) V::st(p.out, ob + int64_t(t) * p.o_sr, z);
+  }
+  if (cnt <= 0) return;
+  float* wrow = p.w + (int64_t(b) * p.M + mq) * p.D + d;
+#pragma unroll
+  for (int i = 0; i < kDvSub; ++i) {
+    const int src = kDvSub * q + i;
+    const float pc = __shfl(pv, src, 64);
+    const int t0 = __shfl(t0l, src, 64), t1 = __shfl(t1l, src, 64);
+    if (i < cs) {
+      float x[8];
+      V::cvt(xr[i], x);
+      if (live && p.w) {
+        float wv[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) wv[c] = x[c] - z[c];
+        F8::st(wrow, int64_t(i) * p.D, wv);
+      }
+      const float a = 1.f - pc;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) z[c] = fmaf(a, z[c], pc * x[c]);
+      for (int t = t0; t < t1; ++t)
+        if (live) V::st(p.out, ob + int64_t(t) * p.o_sr, z);
+    }
+  }
+}
+
+// The backward sub-segment's reverse run from zero over its ds rows (h = value at its first chunk,
+// A = decay), with pn the clamped p of the chunk after the lane's (0 past the row)
+__device__ __forceinline__ void dv_bwd_run(const F8::Raw (&dsr)[kDvSub], float pn, int q, int cs, float (&h)[8],
+                                           float& A) {
+#pragma unroll
+  for (int i = kDvSub - 1; i >= 0; --i) {
+    const float an = 1.f - __shfl(pn, kDvSub * q + i, 64);
+    if (i < cs) {
+      float v[8];
+      F8::cvt(dsr[i], v);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) h[c] = fmaf(an, h[c], v[c]);
+      A *= an;
+    }
+  }
+}
+
+// phase 1 (backward, vector path): sub-segments' reverse runs from zero, composed from the last down
+// (LDS) into the workgroup's aggregate; the clamped p of the segment's chunks go to pc
+__global__ void __launch_bounds__(64 * kDcGrp) dechunk_bwd_grp_v_kernel(const DechunkParams p) {
+  __shared__ float sh[kDcGrp * 4][16][8];
+  __shared__ float sa[kDcGrp * 4];
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int q = lane >> 4, r = lane & 15;
+  const int strip = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+  const bool live = strip * kDcCh + 8 * r < p.D;
+  const int d = min(strip * kDcCh + 8 * r, p.D - 8);
+  const int ms = (g * kDcGrp + w) * kDcSeg, mq = ms + kDvSub * q, mmax = p.M - 1;  // M >= 1 here
+  const int nraw = p.num[b];
+  const int ta = p.perm[int64_t(b) * p.L + min(ms + lane, mmax)];
+  const int tb = p.perm[int64_t(b) * p.L + min(ms + lane + 1, mmax)];
+  F8::Raw dsr[kDvSub];
+#pragma unroll
+  for (int i = 0; i < kDvSub; ++i) dsr[i] = F8::ld(p.ds, int64_t(b) * p.M * p.D + d + int64_t(min(mq + i, mmax)) * p.D);
+  const float pv = dc_clamp(p, ld1(p.prob, b * p.p_sb + int64_t(ta) * p.p_sr + 1, p.p_f32));
+  const float pnr = dc_clamp(p, ld1(p.prob, b * p.p_sb + int64_t(tb) * p.p_sr + 1, p.p_f32));
+  const int n = dc_used_raw(p, nraw);
+  const int cnt = min(kDcSeg, n - ms), cs = min(max(cnt - kDvSub * q, 0), kDvSub);
+  if (strip == 0 && ms + lane < p.M) p.pc[int64_t(b) * p.M + ms + lane] = pv;
+  const float pn = ms + lane + 1 < n ? pnr : 0.f;  // p of the next chunk
+  float h[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float A = 1.f;
+  if (cnt > 0) dv_bwd_run(dsr, pn, q, cs, h, A);
+#pragma unroll
+  for (int c = 0; c < 8; ++c) sh[4 * w + q][r][c] = h[c];
+  if (r == 0) sa[4 * w + q] = A;
+  __syncthreads();
+  if (q == 0) {  // lane group 0 of each wave: its segment's aggregate; wave 0 the workgroup's
+    float S[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float As = 1.f;
+    for (int kk = 4 * w + 3; kk >= 4 * w; --kk) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) S[c] = fmaf(sa[kk], S[c], sh[kk][r][c]);
+      As *= sa[kk];
+    }
+    const int64_t si = int64_t(b) * p.nseg + g * kDcGrp + w;
+    if (live) F8::st(p.segv, si * p.D + d, S);
+    if (strip == 0 && r == 0) p.segd[si] = As;
+    if (w == 0) {
+      float E[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      float Ag = 1.f;
+      for (int k = kDcGrp * 4 - 1; k >= 0; --k) {
+        const float a = sa[k];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) E[c] = fmaf(a, E[c], sh[k][r][c]);
+        Ag *= a;
+      }
+      const int64_t gi = int64_t(b) * p.ngrp + g;
+      if (live) F8::st(p.grpv, gi * p.D + d, E);
+      if (strip == 0 && r == 0) p.grpd[gi] = Ag;
+    }
+  }
+}
+
+// phase 2 (backward, vector path), one wave per workgroup: the carry into the segment's end from the
+// row's later workgroups (from the last down; past the row they are the identity) and the later
+// segments of its phase-1 workgroup, into each lane group's end from the later sub-segments (lane
+// shuffles), then the reverse run: dx = p g and the dp partial of each chunk, the sum over the
+// strip's channels of g w (8 per lane in order, then a fixed butterfly over the 16 lanes of a group)
+template <bool F32>
+__global__ void __launch_bounds__(64) dechunk_bwd_out_v_kernel(const DechunkParams p) {
+  typedef V8<F32> V;
+  const int lane = threadIdx.x & 63;
+  const int q = lane >> 4, r = lane & 15;
+  const int strip = blockIdx.x, s = blockIdx.y, b = blockIdx.z;
+  const int g = s / kDcGrp;
+  const bool live = strip * kDcCh + 8 * r < p.D;
+  const int d = min(strip * kDcCh + 8 * r, p.D - 8);
+  const int ms = s * kDcSeg, mq = ms + kDvSub * q, mmax = p.M - 1;  // M >= 1 here
+  const int nraw = p.num[b];
+  const float pv = p.pc[int64_t(b) * p.M + min(ms + lane, mmax)];
+  const float pnr = p.pc[int64_t(b) * p.M + min(ms + lane + 1, mmax)];
+  F8::Raw dsr[kDvSub], wr[kDvSub];
+#pragma unroll
+  for (int i = 0; i < kDvSub; ++i) {
+    const int64_t off = int64_t(b) * p.M * p.D + d + int64_t(min(mq + i, mmax)) * p.D;
+    dsr[i] = F8::ld(p.ds, off);
+    wr[i] = F8::ld(p.w, off);
+  }
+  // the later segments of the phase-1 workgroup, last first (at most kDcGrp - 1 maps)
+  F8::Raw sv[kDcGrp - 1];
+  float sd[kDcGrp - 1];
+#pragma unroll
+  for (int k = 0; k < kDcGrp - 1; ++k) {
+    const int64_t si = int64_t(b) * p.nseg + max(g * kDcGrp + kDcGrp - 1 - k, s);
+    sv[k] = F8::ld(p.segv, si * p.D + d);
+    sd[k] = p.segd[si];
+  }
+  float G[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  dv_fold(p.grpv + int64_t(b) * p.ngrp * p.D, p.grpd + int64_t(b) * p.ngrp, p.D, d, p.ngrp - 1, -1, p.ngrp - 1 - g, G);
+#pragma unroll
+  for (int k = 0; k < kDcGrp - 1; ++k) {
+    if (g * kDcGrp + kDcGrp - 1 - k > s) {
+      float v[8];
+      F8::cvt(sv[k], v);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) G[c] = fmaf(sd[k], G[c], v[c]);
+    }
+  }
+  const int n = dc_used_raw(p, nraw);
+  const int cnt = min(kDcSeg, n - ms), cs = min(max(cnt - kDvSub * q, 0), kDvSub);
+  const float pn = ms + lane + 1 < n ? pnr : 0.f;
+  const int64_t xb = b * p.dx_sb + d;
+  if (s == p.nseg - 1) {  // rows no byte reads: zero gradient, the lane groups taking turns
+    const float zero[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int mz = n + q; mz < p.M; mz += 4)
+      if (live) V::st(p.dx, xb + int64_t(mz) * p.dx_sr, zero);
+  }
+  if (cnt <= 0) return;
+  float h[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float A = 1.f;
+  dv_bwd_run(dsr, pn, q, cs, h, A);
+  // the later lane groups' sub-segments, last first
+#pragma unroll
+  for (int qq = 3; qq >= 1; --qq) {
+    const int src = 16 * qq + r;
+    const float Aq = __shfl(A, src, 64);
+    float Hq[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) Hq[c] = __shfl(h[c], src, 64);
+    if (qq > q) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) G[c] = fmaf(Aq, G[c], Hq[c]);
+    }
+  }
+  float mine = 0.f;
+#pragma unroll
+  for (int i = kDvSub - 1; i >= 0; --i) {
+    const int src = kDvSub * q + i;
+    const float an = 1.f - __shfl(pn, src, 64), pc = __shfl(pv, src, 64);
+    float dot = 0.f;
+    if (i < cs) {
+      float v[8], wv[8], dx[8];
+      F8::cvt(dsr[i], v);
+      F8::cvt(wr[i], wv);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        G[c] = fmaf(an, G[c], v[c]);
+        dx[c] = pc * G[c];
+      }
+      if (live) {
+        V::st(p.dx, xb + int64_t(mq + i) * p.dx_sr, dx);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) dot = fmaf(G[c], wv[c], dot);
+      }
+    }
+    dot += __shfl_xor(dot, 8, 64);
+    dot += __shfl_xor(dot, 4, 64);
+    dot += __shfl_xor(dot, 2, 64);
+    dot += __shfl_xor(dot, 1, 64);
+    if (r == i) mine = dot;
+  }
+  if (r < cs) p.part[(int64_t(b) * p.nstrips + strip) * p.M + mq + r] = mine;
 }
 
 // d boundary_prob: [..., 0] = 0, [..., 1] = dp of the chunk the position starts (fixed-order sum over
@@ -690,6 +1206,7 @@ int launch_chunk_route(const mote_chunk_route_args* a, hipStream_t stream) {
   p.mask = a->mask; p.mask_sr = a->mask_sr; p.cum = a->cum; p.perm = a->perm; p.num = a->num; p.L = a->L;
   p.vec = reinterpret_cast<uintptr_t>(a->mask) % 16 == 0 && a->mask_sr % 16 == 0;
   p.vec4 = reinterpret_cast<uintptr_t>(a->cum) % 16 == 0 && a->L % 4 == 0;
+  p.vecp = reinterpret_cast<uintptr_t>(a->perm) % 16 == 0 && a->L % 4 == 0;
   const bool cu_here = a->B == 1 && a->L <= kRouteThreads * kRoutePer;
   p.cu = cu_here ? a->cu_seqlens : nullptr;
   hipLaunchKernelGGL(chunk_route_kernel, dim3(a->B), dim3(kRouteThreads), 0, stream, p);
@@ -758,24 +1275,35 @@ static int dc_check(const char* what, int B, int L, int M, int D) {
   return MOTE_OK;
 }
 
-// forward workspace: zc [B, M + 1, D] in hidden's dtype (256-byte rounded), segment values and decays
-static size_t dc_zc_bytes(const mote_dechunk_args* a) {
-  const size_t zc = size_t(a->B) * (size_t(a->M) + 1) * a->D * es_of(a->dtype);
-  return (zc + 255) / 256 * 256;
-}
+// segments and workgroups of segments per row
+static int dc_ngrp(int M) { return (dc_nseg(M) + kDcGrp - 1) / kDcGrp; }
 
+// floats of a workspace piece, rounded up so the next piece starts on a 256-byte boundary
+static size_t dc_piece(size_t floats) { return (floats + 63) / 64 * 64; }
+
+// forward workspace: the workgroup aggregates (values [B, ngrp, D], decays [B, ngrp]), chunk p [B, M],
+// the segment aggregates (values [B, nseg, D], decays [B, nseg])
 size_t dechunk_workspace_bytes(const mote_dechunk_args* a) {
   if (a->B <= 0 || a->D <= 0) return 0;
-  const size_t nseg = dc_nseg(a->M);
-  return dc_zc_bytes(a) + (size_t(a->B) * nseg * a->D + size_t(a->B) * nseg) * sizeof(float);
+  const size_t ng = size_t(a->B) * dc_ngrp(a->M);
+  const size_t ns = ng * kDcGrp;
+  return (dc_piece(ng * a->D) + dc_piece(ng) + dc_piece(size_t(a->B) * a->M) + dc_piece(ns * a->D) + dc_piece(ns)) *
+         sizeof(float);
 }
 
+// backward workspace: segment and workgroup aggregates, chunk p, dp partials, ds rows
 size_t dechunk_bwd_workspace_bytes(const mote_dechunk_bwd_args* a) {
   if (a->B <= 0 || a->D <= 0) return 0;
-  const size_t nseg = dc_nseg(a->M);
+  const size_t ng = size_t(a->B) * dc_ngrp(a->M), ns = ng * kDcGrp;
   const size_t strips = (a->D + kDcCh - 1) / kDcCh;
-  return (size_t(a->B) * nseg * a->D + size_t(a->B) * nseg + size_t(a->B) * strips * a->M +
-          size_t(a->B) * a->M * a->D + 4) * sizeof(float);
+  return (dc_piece(ns * a->D) + dc_piece(ns) + dc_piece(ng * a->D) + dc_piece(ng) + dc_piece(size_t(a->B) * a->M) +
+          dc_piece(size_t(a->B) * strips * a->M) + dc_piece(size_t(a->B) * a->M * a->D)) *
+         sizeof(float);
+}
+
+// 16-byte rows: the vector path's condition for one tensor (elements of es bytes)
+static bool al16(const void* ptr, int64_t sb, int64_t sr, int es) {
+  return ptr == nullptr || (reinterpret_cast<uintptr_t>(ptr) % 16 == 0 && (sb * es) % 16 == 0 && (sr * es) % 16 == 0);
 }
 
 // 2-element accesses: the pointer aligned to two elements, even strides
@@ -804,31 +1332,33 @@ int launch_dechunk_fwd(const mote_dechunk_args* a, hipStream_t stream) {
   p.perm = a->perm; p.num = a->num; p.init = a->init; p.out = a->out; p.o_sb = a->o_sb; p.o_sr = a->o_sr;
   p.w = a->w; p.B = a->B; p.L = a->L; p.M = a->M; p.D = a->D; p.eps = a->eps;
   p.p_f32 = a->prob_dtype == MOTE_F32;
-  p.nseg = dc_nseg(a->M);
+  p.ngrp = dc_ngrp(a->M);
+  p.nseg = p.ngrp * kDcGrp;
   p.nstrips = (a->D + kDcCh - 1) / kDcCh;
-  p.zc = a->workspace;
-  p.segv = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(a->workspace) + dc_zc_bytes(a));
-  p.segd = p.segv + size_t(a->B) * p.nseg * a->D;
-  const dim3 grid(p.nstrips, p.nseg, a->B);
-  if (a->dtype == MOTE_F32) {
-    hipLaunchKernelGGL(dechunk_seg_kernel<true>, grid, dim3(64), 0, stream, p);
-    rc = check_launch("dechunk_fwd/segments");
-    if (rc) return rc;
-    hipLaunchKernelGGL(dechunk_scan_kernel<true>, grid, dim3(64), 0, stream, p);
-  } else {
-    hipLaunchKernelGGL(dechunk_seg_kernel<false>, grid, dim3(64), 0, stream, p);
-    rc = check_launch("dechunk_fwd/segments");
-    if (rc) return rc;
-    hipLaunchKernelGGL(dechunk_scan_kernel<false>, grid, dim3(64), 0, stream, p);
-  }
-  rc = check_launch("dechunk_fwd/scan");
-  if (rc) return rc;
+  p.grpv = reinterpret_cast<float*>(a->workspace);
+  p.grpd = p.grpv + dc_piece(size_t(a->B) * p.ngrp * a->D);
+  p.pc = p.grpd + dc_piece(size_t(a->B) * p.ngrp);
+  p.segv = p.pc + dc_piece(size_t(a->B) * a->M);
+  p.segd = p.segv + dc_piece(size_t(a->B) * p.nseg * a->D);
+  const dim3 grid(p.nstrips, p.ngrp, a->B), wgrid(p.nstrips, p.nseg, a->B);
+  const dim3 block(64 * kDcGrp);
   const int es = es_of(a->dtype);
-  const int vec = (a->D * es) % 16 == 0 && reinterpret_cast<uintptr_t>(a->out) % 16 == 0 && (a->o_sb * es) % 16 == 0 &&
-                  (a->o_sr * es) % 16 == 0;
-  const int64_t rows = int64_t(a->B) * a->L;
-  hipLaunchKernelGGL(dechunk_expand_kernel, dim3(unsigned((rows + 3) / 4)), dim3(256), 0, stream, p, a->cum, es, vec);
-  return check_launch("dechunk_fwd/expand");
+  const bool vec = a->D % 8 == 0 && al16(a->hidden, a->h_sb, a->h_sr, es) && al16(a->out, a->o_sb, a->o_sr, es) &&
+                   reinterpret_cast<uintptr_t>(a->init) % 16 == 0 && reinterpret_cast<uintptr_t>(a->w) % 16 == 0;
+  if (a->dtype == MOTE_F32) {
+    hipLaunchKernelGGL(vec ? dechunk_grp_v_kernel<true> : dechunk_grp_kernel<true>, grid, block, 0, stream, p);
+    rc = check_launch("dechunk_fwd/segments");
+    if (rc) return rc;
+    if (vec) hipLaunchKernelGGL(dechunk_out_v_kernel<true>, wgrid, dim3(64), 0, stream, p);
+    else hipLaunchKernelGGL(dechunk_out_kernel<true>, grid, block, 0, stream, p);
+  } else {
+    hipLaunchKernelGGL(vec ? dechunk_grp_v_kernel<false> : dechunk_grp_kernel<false>, grid, block, 0, stream, p);
+    rc = check_launch("dechunk_fwd/segments");
+    if (rc) return rc;
+    if (vec) hipLaunchKernelGGL(dechunk_out_v_kernel<false>, wgrid, dim3(64), 0, stream, p);
+    else hipLaunchKernelGGL(dechunk_out_kernel<false>, grid, block, 0, stream, p);
+  }
+  return check_launch("dechunk_fwd/scan");
 }
 
 int launch_dechunk_bwd(const mote_dechunk_bwd_args* a, hipStream_t stream) {
@@ -855,15 +1385,19 @@ int launch_dechunk_bwd(const mote_dechunk_bwd_args* a, hipStream_t stream) {
   p.dout = a->dout; p.g_sb = a->g_sb; p.g_sr = a->g_sr; p.dx = a->dhidden; p.dx_sb = a->dh_sb; p.dx_sr = a->dh_sr;
   p.B = a->B; p.L = a->L; p.M = a->M; p.D = a->D; p.eps = a->eps;
   p.p_f32 = a->prob_dtype == MOTE_F32;
-  p.nseg = dc_nseg(a->M);
+  p.ngrp = dc_ngrp(a->M);
+  p.nseg = p.ngrp * kDcGrp;
   p.nstrips = (a->D + kDcCh - 1) / kDcCh;
+  const size_t ns = size_t(a->B) * p.nseg, ng = size_t(a->B) * p.ngrp;
   p.segv = reinterpret_cast<float*>(a->workspace);
-  p.segd = p.segv + size_t(a->B) * p.nseg * a->D;
-  p.part = p.segd + size_t(a->B) * p.nseg;
-  // ds rows start on 16-byte boundaries (float4 accesses)
-  const uintptr_t ds_at = reinterpret_cast<uintptr_t>(p.part + size_t(a->B) * p.nstrips * a->M);
-  p.ds = reinterpret_cast<float*>((ds_at + 15) & ~uintptr_t(15));
-  const dim3 grid(p.nstrips, p.nseg, a->B);
+  p.segd = p.segv + dc_piece(ns * a->D);
+  p.grpv = p.segd + dc_piece(ns);
+  p.grpd = p.grpv + dc_piece(ng * a->D);
+  p.pc = p.grpd + dc_piece(ng);
+  p.part = p.pc + dc_piece(size_t(a->B) * a->M);
+  p.ds = p.part + dc_piece(size_t(a->B) * p.nstrips * a->M);  // 256-byte aligned (float4 accesses)
+  const dim3 grid(p.nstrips, p.ngrp, a->B);
+  const dim3 block(64 * kDcGrp);
   const int64_t crows = int64_t(a->B) * a->M;
   const int vec = (a->D % 8) == 0 && reinterpret_cast<uintptr_t>(a->dout) % 16 == 0 && (a->g_sb * es) % 16 == 0 &&
                   (a->g_sr * es) % 16 == 0 && reinterpret_cast<uintptr_t>(p.ds) % 16 == 0;
@@ -873,11 +1407,15 @@ int launch_dechunk_bwd(const mote_dechunk_bwd_args* a, hipStream_t stream) {
     hipLaunchKernelGGL(dechunk_dsum_kernel<false>, dim3(unsigned((crows + 3) / 4)), dim3(256), 0, stream, p, vec);
   rc = check_launch("dechunk_bwd/byte sums");
   if (rc) return rc;
-  hipLaunchKernelGGL(dechunk_bwd_seg_kernel, grid, dim3(64), 0, stream, p);
+  const bool vg = a->D % 8 == 0 && al16(a->dhidden, a->dh_sb, a->dh_sr, es) && reinterpret_cast<uintptr_t>(a->w) % 16 == 0;
+  hipLaunchKernelGGL(vg ? dechunk_bwd_grp_v_kernel : dechunk_bwd_grp_kernel, grid, block, 0, stream, p);
   rc = check_launch("dechunk_bwd/segments");
   if (rc) return rc;
-  if (a->dtype == MOTE_F32) hipLaunchKernelGGL(dechunk_bwd_out_kernel<true>, grid, dim3(64), 0, stream, p);
-  else hipLaunchKernelGGL(dechunk_bwd_out_kernel<false>, grid, dim3(64), 0, stream, p);
+  const dim3 wgrid(p.nstrips, p.nseg, a->B);
+  if (vg && a->dtype == MOTE_F32) hipLaunchKernelGGL(dechunk_bwd_out_v_kernel<true>, wgrid, dim3(64), 0, stream, p);
+  else if (vg) hipLaunchKernelGGL(dechunk_bwd_out_v_kernel<false>, wgrid, dim3(64), 0, stream, p);
+  else if (a->dtype == MOTE_F32) hipLaunchKernelGGL(dechunk_bwd_out_kernel<true>, grid, block, 0, stream, p);
+  else hipLaunchKernelGGL(dechunk_bwd_out_kernel<false>, grid, block, 0, stream, p);
   rc = check_launch("dechunk_bwd");
   if (rc) return rc;
   const int64_t n = int64_t(a->B) * a->L;

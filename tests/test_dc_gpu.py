@@ -81,9 +81,9 @@ def test_chunk_pack_layout(cuda):
     assert torch.equal(packed.cpu(), want)
 
 
-def _strided(h, dev):
+def _strided(h, dev, pad=32):
     """h on the device as the first D columns of wider rows (the zc_full[..., :D0] view, hnet.py:239)."""
-    buf = torch.zeros(*h.shape[:-1], h.shape[-1] + 32, device=dev, dtype=h.dtype)
+    buf = torch.zeros(*h.shape[:-1], h.shape[-1] + pad, device=dev, dtype=h.dtype)
     buf[..., : h.shape[-1]] = h.to(dev)
     return buf[..., : h.shape[-1]]
 
@@ -107,15 +107,20 @@ def _dechunk_case(B, L, D, seed, dtype, with_init=False, pad=0):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("with_init", [False, True])
-def test_dechunk_forward_matches_oracle(cuda, dtype, with_init):
+@pytest.mark.parametrize("pad", [32, 34])
+def test_dechunk_forward_matches_oracle(cuda, dtype, with_init, pad):
+    """Rows of D + 32 elements: the 16-byte vector path; D + 34 (rows off 16-byte boundaries): the
+    two-channel path."""
     from mote_amd.dc import DeChunkLayer, DeChunkState
 
-    m, h, prob, init = _dechunk_case(3, 1500, 384, 6, dtype, with_init, pad=40)
+    D = 384
+    print(f"case dechunk fwd {dtype} init={with_init} row pad={pad}", flush=True)
+    m, h, prob, init = _dechunk_case(3, 1500, D, 6, dtype, with_init, pad=40)
     want = O.dechunk_brute(h.double(), m, prob.double(), 1e-4, init.double() if init is not None else None)
-    layer = DeChunkLayer(384)
+    layer = DeChunkLayer(D)
     st = DeChunkState(last_value=init.to(cuda).clone()) if with_init else None
-    out = layer(_strided(h, cuda), m.to(cuda), prob.to(cuda), st)
-    assert out.dtype == dtype and out.shape == (3, 1500, 384)
+    out = layer(_strided(h, cuda, pad), m.to(cuda), prob.to(cuda), st)
+    assert out.dtype == dtype and out.shape == (3, 1500, D)
     tol = 2e-5 if dtype == torch.float32 else 2e-2
     assert _rel(out, want) < tol
     if with_init:
@@ -123,17 +128,20 @@ def test_dechunk_forward_matches_oracle(cuda, dtype, with_init):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_dechunk_backward_matches_autograd(cuda, dtype):
+@pytest.mark.parametrize("D", [256, 202])
+def test_dechunk_backward_matches_autograd(cuda, dtype, D):
+    """D = 256: the 16-byte vector path; D = 202 (not a multiple of 8, heads of 2): the two-channel path."""
     from mote_amd.dc import DeChunkLayer
 
-    m, h, prob, _ = _dechunk_case(3, 1500, 256, 7, dtype, pad=40)
-    dy = torch.randn(3, 1500, 256, generator=torch.Generator().manual_seed(8)).to(dtype)
+    print(f"case dechunk bwd {dtype} D={D}", flush=True)
+    m, h, prob, _ = _dechunk_case(3, 1500, D, 7, dtype, pad=40)
+    dy = torch.randn(3, 1500, D, generator=torch.Generator().manual_seed(8)).to(dtype)
     hr = h.double().requires_grad_(True)
     prr = prob.double().requires_grad_(True)
     (O.dechunk_ref(hr, m, prr, 1e-4) * dy.double()).sum().backward()
     hg = _strided(h, cuda).detach().requires_grad_(True)
     pg = prob.to(cuda).requires_grad_(True)
-    out = DeChunkLayer(256)(hg, m.to(cuda), pg)
+    out = DeChunkLayer(D, headdim=32 if D % 32 == 0 else 2)(hg, m.to(cuda), pg)
     out.backward(dy.to(cuda))
     tol = 5e-5 if dtype == torch.float32 else 2e-2
     assert hg.grad.dtype == dtype and pg.grad.dtype == torch.float32
