@@ -241,7 +241,9 @@ struct DechunkParams {
   float* ds;                                // [B, M, D] fp32: dout summed over each chunk's bytes (backward)
   float* segv; float* segd;                 // [B, nseg, D] segment values, [B, nseg] decays (backward)
   float* grpv; float* grpd;                 // [B, ngrp, D] workgroup aggregates' values, [B, ngrp] decays
-  float* pc;                                // [B, M] clamped p of every chunk (vector path, kept by phase 1)
+  float* pc;                                // [B, M] clamped p of every chunk (vector path, kept by phase 1;
+                                            // the backward's is negative where the clamp was active)
+  void* dprob; int64_t dp_sb, dp_sr; int dp_f32;  // d boundary_prob [B, L, 2] (backward, vector path)
   float* part;                              // [B, nstrips, M] dp partials (backward)
   int B, L, M, D, nseg, ngrp, nstrips, p_f32;
   float eps;
@@ -984,11 +986,14 @@ __global__ void __launch_bounds__(64 * kDcGrp) dechunk_bwd_grp_v_kernel(const De
   F8::Raw dsr[kDvSub];
 #pragma unroll
   for (int i = 0; i < kDvSub; ++i) dsr[i] = F8::ld(p.ds, int64_t(b) * p.M * p.D + d + int64_t(min(mq + i, mmax)) * p.D);
-  const float pv = dc_clamp(p, ld1(p.prob, b * p.p_sb + int64_t(ta) * p.p_sr + 1, p.p_f32));
+  const float praw = ld1(p.prob, b * p.p_sb + int64_t(ta) * p.p_sr + 1, p.p_f32);
+  const float pv = dc_clamp(p, praw);
   const float pnr = dc_clamp(p, ld1(p.prob, b * p.p_sb + int64_t(tb) * p.p_sr + 1, p.p_f32));
   const int n = dc_used_raw(p, nraw);
   const int cnt = min(kDcSeg, n - ms), cs = min(max(cnt - kDvSub * q, 0), kDvSub);
-  if (strip == 0 && ms + lane < p.M) p.pc[int64_t(b) * p.M + ms + lane] = pv;
+  // kept for phase 2 with the clamp's gradient gate in the sign: negative where the raw p was clamped
+  if (strip == 0 && ms + lane < p.M)
+    p.pc[int64_t(b) * p.M + ms + lane] = (praw >= p.eps && praw <= 1.0f - p.eps) ? pv : -pv;
   const float pn = ms + lane + 1 < n ? pnr : 0.f;  // p of the next chunk
   float h[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   float A = 1.f;
@@ -1024,24 +1029,33 @@ __global__ void __launch_bounds__(64 * kDcGrp) dechunk_bwd_grp_v_kernel(const De
   }
 }
 
-// phase 2 (backward, vector path), one wave per workgroup: the carry into the segment's end from the
-// row's later workgroups (from the last down; past the row they are the identity) and the later
-// segments of its phase-1 workgroup, into each lane group's end from the later sub-segments (lane
-// shuffles), then the reverse run: dx = p g and the dp partial of each chunk, the sum over the
-// strip's channels of g w (8 per lane in order, then a fixed butterfly over the 16 lanes of a group)
+// phase 2 (backward, vector path), a workgroup per segment with one wave per channel strip: the carry
+// into the segment's end from the row's later workgroups (from the last down; past the row they are
+// the identity) and the later segments of its phase-1 workgroup, into each lane group's end from the
+// later sub-segments (lane shuffles), then the reverse run: dx = p g and the dp partial of each chunk
+// and strip, the sum over the strip's channels of g w (8 per lane in order, then a fixed butterfly over
+// the 16 lanes of a group). The strips' partials add in strip order through LDS, and the segment's
+// bytes get d boundary_prob: [..., 1] = dp of the chunk at its boundary byte (zero where the clamp was
+// active), zero everywhere else (the dechunk_dprob_kernel of the two-channel path).
+constexpr int kDvMaxStrips = 4;  // D <= 512 (every preset's outer width): one wave per SIMD, 512 VGPRs
+
 template <bool F32>
-__global__ void __launch_bounds__(64) dechunk_bwd_out_v_kernel(const DechunkParams p) {
+__global__ void __launch_bounds__(64 * kDvMaxStrips) dechunk_bwd_out_v_kernel(const DechunkParams p) {
   typedef V8<F32> V;
-  const int lane = threadIdx.x & 63;
+  __shared__ float red[kDvMaxStrips][kDcSeg];
+  const int lane = threadIdx.x & 63, strip = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int q = lane >> 4, r = lane & 15;
-  const int strip = blockIdx.x, s = blockIdx.y, b = blockIdx.z;
+  const int s = blockIdx.x, b = blockIdx.y;
   const int g = s / kDcGrp;
   const bool live = strip * kDcCh + 8 * r < p.D;
   const int d = min(strip * kDcCh + 8 * r, p.D - 8);
   const int ms = s * kDcSeg, mq = ms + kDvSub * q, mmax = p.M - 1;  // M >= 1 here
   const int nraw = p.num[b];
-  const float pv = p.pc[int64_t(b) * p.M + min(ms + lane, mmax)];
-  const float pnr = p.pc[int64_t(b) * p.M + min(ms + lane + 1, mmax)];
+  const float pc_lane = p.pc[int64_t(b) * p.M + min(ms + lane, mmax)];
+  const float pv = fabsf(pc_lane);
+  const float pnr = fabsf(p.pc[int64_t(b) * p.M + min(ms + lane + 1, mmax)]);
+  const int pa = p.perm[int64_t(b) * p.L + min(ms + lane, mmax)];
+  const int pb = p.perm[int64_t(b) * p.L + min(ms + lane + 1, mmax)];
   F8::Raw dsr[kDvSub], wr[kDvSub];
 #pragma unroll
   for (int i = 0; i < kDvSub; ++i) {
@@ -1078,51 +1092,74 @@ __global__ void __launch_bounds__(64) dechunk_bwd_out_v_kernel(const DechunkPara
     for (int mz = n + q; mz < p.M; mz += 4)
       if (live) V::st(p.dx, xb + int64_t(mz) * p.dx_sr, zero);
   }
-  if (cnt <= 0) return;
-  float h[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  float A = 1.f;
-  dv_bwd_run(dsr, pn, q, cs, h, A);
-  // the later lane groups' sub-segments, last first
-#pragma unroll
-  for (int qq = 3; qq >= 1; --qq) {
-    const int src = 16 * qq + r;
-    const float Aq = __shfl(A, src, 64);
-    float Hq[8];
-#pragma unroll
-    for (int c = 0; c < 8; ++c) Hq[c] = __shfl(h[c], src, 64);
-    if (qq > q) {
-#pragma unroll
-      for (int c = 0; c < 8; ++c) G[c] = fmaf(Aq, G[c], Hq[c]);
-    }
-  }
   float mine = 0.f;
+  if (cnt > 0) {
+    float h[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float A = 1.f;
+    dv_bwd_run(dsr, pn, q, cs, h, A);
+    // the later lane groups' sub-segments, last first
 #pragma unroll
-  for (int i = kDvSub - 1; i >= 0; --i) {
-    const int src = kDvSub * q + i;
-    const float an = 1.f - __shfl(pn, src, 64), pc = __shfl(pv, src, 64);
-    float dot = 0.f;
-    if (i < cs) {
-      float v[8], wv[8], dx[8];
-      F8::cvt(dsr[i], v);
-      F8::cvt(wr[i], wv);
+    for (int qq = 3; qq >= 1; --qq) {
+      const int src = 16 * qq + r;
+      const float Aq = __shfl(A, src, 64);
+      float Hq[8];
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        G[c] = fmaf(an, G[c], v[c]);
-        dx[c] = pc * G[c];
-      }
-      if (live) {
-        V::st(p.dx, xb + int64_t(mq + i) * p.dx_sr, dx);
+      for (int c = 0; c < 8; ++c) Hq[c] = __shfl(h[c], src, 64);
+      if (qq > q) {
 #pragma unroll
-        for (int c = 0; c < 8; ++c) dot = fmaf(G[c], wv[c], dot);
+        for (int c = 0; c < 8; ++c) G[c] = fmaf(Aq, G[c], Hq[c]);
       }
     }
-    dot += __shfl_xor(dot, 8, 64);
-    dot += __shfl_xor(dot, 4, 64);
-    dot += __shfl_xor(dot, 2, 64);
-    dot += __shfl_xor(dot, 1, 64);
-    if (r == i) mine = dot;
+#pragma unroll
+    for (int i = kDvSub - 1; i >= 0; --i) {
+      const int src = kDvSub * q + i;
+      const float an = 1.f - __shfl(pn, src, 64), pc = __shfl(pv, src, 64);
+      float dot = 0.f;
+      if (i < cs) {
+        float v[8], wv[8], dx[8];
+        F8::cvt(dsr[i], v);
+        F8::cvt(wr[i], wv);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          G[c] = fmaf(an, G[c], v[c]);
+          dx[c] = pc * G[c];
+        }
+        if (live) {
+          V::st(p.dx, xb + int64_t(mq + i) * p.dx_sr, dx);
+#pragma unroll
+          for (int c = 0; c < 8; ++c) dot = fmaf(G[c], wv[c], dot);
+        }
+      }
+      dot += __shfl_xor(dot, 8, 64);
+      dot += __shfl_xor(dot, 4, 64);
+      dot += __shfl_xor(dot, 2, 64);
+      dot += __shfl_xor(dot, 1, 64);
+      if (r == i) mine = dot;
+    }
   }
-  if (r < cs) p.part[(int64_t(b) * p.nstrips + strip) * p.M + mq + r] = mine;
+  red[strip][kDvSub * q + r] = mine;
+  __syncthreads();
+  if (strip == 0 && lane < cnt) {
+    // chunk m = ms + lane: dp in strip order, gated by the clamp; its bytes [t0, t1) of d prob
+    const int m = ms + lane;
+    float dp = 0.f;
+    for (int k = 0; k < p.nstrips; ++k) dp += red[k][lane];
+    if (pc_lane < 0.f) dp = 0.f;
+    const int t0 = m == 0 ? 0 : pa;                  // no carried value in the backward
+    const int t1 = m + 1 >= n ? p.L : pb;
+    const int tb = nraw > 0 ? pa : 0;                // the boundary byte (byte 0 of a row without one)
+    for (int t = t0; t < t1; ++t) {
+      const float v = t == tb ? dp : 0.f;
+      const int64_t off = b * p.dp_sb + int64_t(t) * p.dp_sr;
+      if (p.dp_f32) {
+        reinterpret_cast<float*>(p.dprob)[off] = 0.f;
+        reinterpret_cast<float*>(p.dprob)[off + 1] = v;
+      } else {
+        reinterpret_cast<bf16_t*>(p.dprob)[off] = 0;
+        reinterpret_cast<bf16_t*>(p.dprob)[off + 1] = f2bf(v);
+      }
+    }
+  }
 }
 
 // d boundary_prob: [..., 0] = 0, [..., 1] = dp of the chunk the position starts (fixed-order sum over
@@ -1407,14 +1444,19 @@ int launch_dechunk_bwd(const mote_dechunk_bwd_args* a, hipStream_t stream) {
     hipLaunchKernelGGL(dechunk_dsum_kernel<false>, dim3(unsigned((crows + 3) / 4)), dim3(256), 0, stream, p, vec);
   rc = check_launch("dechunk_bwd/byte sums");
   if (rc) return rc;
-  const bool vg = a->D % 8 == 0 && al16(a->dhidden, a->dh_sb, a->dh_sr, es) && reinterpret_cast<uintptr_t>(a->w) % 16 == 0;
+  const bool vg = a->D % 8 == 0 && a->D <= kDvMaxStrips * kDcCh && al16(a->dhidden, a->dh_sb, a->dh_sr, es) &&
+                  reinterpret_cast<uintptr_t>(a->w) % 16 == 0;
   hipLaunchKernelGGL(vg ? dechunk_bwd_grp_v_kernel : dechunk_bwd_grp_kernel, grid, block, 0, stream, p);
   rc = check_launch("dechunk_bwd/segments");
   if (rc) return rc;
-  const dim3 wgrid(p.nstrips, p.nseg, a->B);
-  if (vg && a->dtype == MOTE_F32) hipLaunchKernelGGL(dechunk_bwd_out_v_kernel<true>, wgrid, dim3(64), 0, stream, p);
-  else if (vg) hipLaunchKernelGGL(dechunk_bwd_out_v_kernel<false>, wgrid, dim3(64), 0, stream, p);
-  else if (a->dtype == MOTE_F32) hipLaunchKernelGGL(dechunk_bwd_out_kernel<true>, grid, block, 0, stream, p);
+  if (vg) {  // phase 2 with d boundary_prob fused: one workgroup of nstrips waves per segment
+    p.dprob = a->dprob; p.dp_sb = a->dp_sb; p.dp_sr = a->dp_sr; p.dp_f32 = a->dprob_dtype == MOTE_F32;
+    const dim3 sgrid(p.nseg, a->B), sblock(64 * p.nstrips);
+    if (a->dtype == MOTE_F32) hipLaunchKernelGGL(dechunk_bwd_out_v_kernel<true>, sgrid, sblock, 0, stream, p);
+    else hipLaunchKernelGGL(dechunk_bwd_out_v_kernel<false>, sgrid, sblock, 0, stream, p);
+    return check_launch("dechunk_bwd");
+  }
+  if (a->dtype == MOTE_F32) hipLaunchKernelGGL(dechunk_bwd_out_kernel<true>, grid, block, 0, stream, p);
   else hipLaunchKernelGGL(dechunk_bwd_out_kernel<false>, grid, block, 0, stream, p);
   rc = check_launch("dechunk_bwd");
   if (rc) return rc;
