@@ -233,6 +233,7 @@ struct DechunkParams {
   const void* x; int64_t x_sb, x_sr;        // hidden [B, M, D] (elements)
   const void* prob; int64_t p_sb, p_sr;     // boundary_prob [B, L, 2] (elements; p at +1)
   const int32_t* perm; const int32_t* num;
+  const int32_t* cum;                       // [B, L] inclusive boundary count (single-pass kernels)
   const float* init;                        // [B, D] carried value, or null
   void* out; int64_t o_sb, o_sr;            // [B, L, D] (forward)
   float* w;                                 // [B, M, D] fp32: x_m - z_{m-1}, kept for the backward (may be null)
@@ -280,6 +281,7 @@ __device__ __forceinline__ float rdl(float v, int i) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), i));
 }
 __device__ __forceinline__ int rdl(int v, int i) { return __builtin_amdgcn_readlane(v, i); }
+
 __device__ __forceinline__ float2 ldf2(const float* base, int64_t off) {
   return *reinterpret_cast<const float2*>(base + off);
 }
@@ -666,18 +668,11 @@ __global__ void __launch_bounds__(64 * kDcGrp) dechunk_bwd_out_kernel(const Dech
 }
 
 // ------------------------------------------------------------------------------------------------
-// Vector path (D % 8 == 0, rows on 16-byte boundaries). A wave still owns one 64-chunk segment of a
-// 128-channel strip, but as four 16-lane groups: group q runs chunks m0 + 16 q .. + 15 (a sub-segment)
-// and lane r of it channels 8 r .. 8 r + 7, with 16-byte loads and stores. Every row access of the
-// wave then moves four rows at once, and the sequential chain of a wave is 16 chunks long; the
-// sub-segments compose in order through LDS like the segments do.
-// A launch here is a chain of dependent memory round trips, so every load that does not need another
-// is issued at the kernel's start: the segment's rows are read clamped to the bucket (M) before the
-// row's chunk count arrives, which then only masks, and the clamped p of every chunk is kept by the
-// first launch (`pc`) so the second reads it in one trip.
+// Eight consecutive elements of a row (vector path: D % 8 == 0, rows on 16-byte boundaries) as one
+// 16-byte (bf16) or two 16-byte (fp32) accesses. Every launch of the vector path is a chain of
+// dependent memory round trips, so each issues every load that needs no other at its start (rows
+// clamped to the bucket M before the row's chunk count arrives, which then only masks).
 // ------------------------------------------------------------------------------------------------
-constexpr int kDvSub = 16;  // chunks per lane group
-
 template <bool F32> struct V8;
 template <> struct V8<false> {  // 8 bf16
   struct Raw { uint4 u; };
@@ -698,6 +693,15 @@ template <> struct V8<false> {  // 8 bf16
     for (int k = 0; k < 4; ++k) w[k] = uint32_t(f2bf(v[2 * k])) | (uint32_t(f2bf(v[2 * k + 1])) << 16);
     *reinterpret_cast<uint4*>(reinterpret_cast<bf16_t*>(base) + off) = uint4{w[0], w[1], w[2], w[3]};
   }
+  static __device__ __forceinline__ Raw pack(const float (&v)[8]) {
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) w[k] = uint32_t(f2bf(v[2 * k])) | (uint32_t(f2bf(v[2 * k + 1])) << 16);
+    return Raw{uint4{w[0], w[1], w[2], w[3]}};
+  }
+  static __device__ __forceinline__ void st_raw(void* base, int64_t off, const Raw& r) {
+    *reinterpret_cast<uint4*>(reinterpret_cast<bf16_t*>(base) + off) = r.u;
+  }
 };
 template <> struct V8<true> {  // 8 fp32
   struct Raw { float4 a, b; };
@@ -713,47 +717,16 @@ template <> struct V8<true> {  // 8 fp32
     q[0] = make_float4(v[0], v[1], v[2], v[3]);
     q[1] = make_float4(v[4], v[5], v[6], v[7]);
   }
+  static __device__ __forceinline__ Raw pack(const float (&v)[8]) {
+    return Raw{make_float4(v[0], v[1], v[2], v[3]), make_float4(v[4], v[5], v[6], v[7])};
+  }
+  static __device__ __forceinline__ void st_raw(void* base, int64_t off, const Raw& r) {
+    float4* q = reinterpret_cast<float4*>(reinterpret_cast<float*>(base) + off);
+    q[0] = r.a;
+    q[1] = r.b;
+  }
 };
 typedef V8<true> F8;
-
-// c <- A_j c + e_j for j = j0 + step k, k = 0 .. cnt - 1, in that order: each lane group composes a
-// quarter of the sequence (8 maps loaded at a time), then every lane applies the four quarters in
-// order, taking the other groups' from lane shuffles. Every lane of the wave calls it.
-__device__ __forceinline__ void dv_fold(const float* gv, const float* gd, int D, int d, int j0, int step, int cnt,
-                                        float (&c)[8]) {
-  const int lane = threadIdx.x & 63, q = lane >> 4, r = lane & 15;
-  const int per = (max(cnt, 0) + 3) / 4;
-  const int k0 = q * per, k1 = min(cnt, k0 + per);
-  float E[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  float A = 1.f;
-  for (int kb = k0; kb < k1; kb += 8) {
-    F8::Raw e[8];
-    float a[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const int j = j0 + step * min(kb + k, k1 - 1);
-      e[k] = F8::ld(gv, int64_t(j) * D + d);
-      a[k] = gd[j];
-    }
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      if (kb + k < k1) {
-        float v[8];
-        F8::cvt(e[k], v);
-#pragma unroll
-        for (int ch = 0; ch < 8; ++ch) E[ch] = fmaf(a[k], E[ch], v[ch]);
-        A *= a[k];
-      }
-    }
-  }
-#pragma unroll
-  for (int qq = 0; qq < 4; ++qq) {
-    const int src = 16 * qq + r;
-    const float Aq = __shfl(A, src, 64);
-#pragma unroll
-    for (int ch = 0; ch < 8; ++ch) c[ch] = fmaf(Aq, c[ch], __shfl(E[ch], src, 64));
-  }
-}
 
 // the row's chunk count (dc_used) from the raw count
 __device__ __forceinline__ int dc_used_raw(const DechunkParams& p, int nraw) {
@@ -762,404 +735,6 @@ __device__ __forceinline__ int dc_used_raw(const DechunkParams& p, int nraw) {
 }
 __device__ __forceinline__ float dc_clamp(const DechunkParams& p, float v) {
   return fminf(fmaxf(v, p.eps), 1.0f - p.eps);
-}
-
-// phase 1 (forward, vector path): sub-segments run from zero, composed in order (LDS) into the
-// workgroup's aggregate; the clamped p of the segment's chunks go to pc
-template <bool F32>
-__global__ void __launch_bounds__(64 * kDcGrp) dechunk_grp_v_kernel(const DechunkParams p) {
-  typedef V8<F32> V;
-  __shared__ float se[kDcGrp * 4][16][8];
-  __shared__ float sa[kDcGrp * 4];
-  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int q = lane >> 4, r = lane & 15;
-  const int strip = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
-  const int d = min(strip * kDcCh + 8 * r, p.D - 8);
-  const int ms = (g * kDcGrp + w) * kDcSeg, mq = ms + kDvSub * q, mmax = max(p.M - 1, 0);
-  // independent loads: the count, the lane's chunk position, the sub-segment's rows
-  const int nraw = p.num[b];
-  const int tp = p.perm[int64_t(b) * p.L + min(ms + lane, mmax)];
-  typename V::Raw xr[kDvSub];
-  if (p.M > 0) {
-#pragma unroll
-    for (int i = 0; i < kDvSub; ++i) xr[i] = V::ld(p.x, b * p.x_sb + d + int64_t(min(mq + i, mmax)) * p.x_sr);
-  }
-  const float pv = dc_clamp(p, ld1(p.prob, b * p.p_sb + int64_t(tp) * p.p_sr + 1, p.p_f32));
-  const int n = dc_used_raw(p, nraw);
-  const int cnt = min(kDcSeg, n - ms), cs = min(max(cnt - kDvSub * q, 0), kDvSub);
-  if (strip == 0 && ms + lane < p.M) p.pc[int64_t(b) * p.M + ms + lane] = pv;
-  float e[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  float A = 1.f;
-  if (cnt > 0) {
-#pragma unroll
-    for (int i = 0; i < kDvSub; ++i) {
-      const float pc = __shfl(pv, kDvSub * q + i, 64);
-      if (i < cs) {
-        float x[8];
-        V::cvt(xr[i], x);
-        const float a = 1.f - pc;
-#pragma unroll
-        for (int c = 0; c < 8; ++c) e[c] = fmaf(a, e[c], pc * x[c]);
-        A *= a;
-      }
-    }
-  }
-#pragma unroll
-  for (int c = 0; c < 8; ++c) se[4 * w + q][r][c] = e[c];
-  if (r == 0) sa[4 * w + q] = A;
-  __syncthreads();
-  // lane group 0 of each wave: its segment's aggregate (phase 2 reads those of the workgroup's
-  // earlier segments), and wave 0 the workgroup's
-  if (q == 0) {
-    const bool live = strip * kDcCh + 8 * r < p.D;
-    float E[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    float Ag = 1.f;
-    for (int k = 0; k < kDcGrp * 4; ++k) {
-      const float a = sa[k];
-#pragma unroll
-      for (int c = 0; c < 8; ++c) E[c] = fmaf(a, E[c], se[k][r][c]);
-      Ag *= a;
-      if (k == 4 * w + 3) {
-        const int64_t si = int64_t(b) * p.nseg + g * kDcGrp + w;
-        float S[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        float As = 1.f;
-        for (int kk = 4 * w; kk < 4 * w + 4; ++kk) {
-#pragma unroll
-          for (int c = 0; c < 8; ++c) S[c] = fmaf(sa[kk], S[c], se[kk][r][c]);
-          As *= sa[kk];
-        }
-        if (live) F8::st(p.segv, si * p.D + d, S);
-        if (strip == 0 && r == 0) p.segd[si] = As;
-        if (w != 0) break;
-      }
-    }
-    if (w == 0) {
-      const int64_t gi = int64_t(b) * p.ngrp + g;
-      if (live) F8::st(p.grpv, gi * p.D + d, E);
-      if (strip == 0 && r == 0) p.grpd[gi] = Ag;
-    }
-  }
-}
-
-// phase 2 (forward, vector path), one wave per workgroup so the stores spread over the chip: the
-// carry into the segment (the row's carried value, the earlier workgroups' aggregates, the earlier
-// segments of its phase-1 workgroup), into each lane group (the earlier sub-segments, by lane
-// shuffles), then the sub-segment again: w_m = x_m - z_{m-1} (fp32) and z_m to every byte of chunk m;
-// bytes before the first boundary hold the carried value with one
-template <bool F32>
-__global__ void __launch_bounds__(64) dechunk_out_v_kernel(const DechunkParams p) {
-  typedef V8<F32> V;
-  const int lane = threadIdx.x & 63;
-  const int q = lane >> 4, r = lane & 15;
-  const int strip = blockIdx.x, s = blockIdx.y, b = blockIdx.z;
-  const int g = s / kDcGrp;
-  const bool live = strip * kDcCh + 8 * r < p.D;
-  const int d = min(strip * kDcCh + 8 * r, p.D - 8);
-  const int ms = s * kDcSeg, mq = ms + kDvSub * q, mmax = max(p.M - 1, 0);
-  const int nraw = p.num[b];
-  const float pv = p.M > 0 ? p.pc[int64_t(b) * p.M + min(ms + lane, mmax)] : 0.f;
-  const int pa = p.perm[int64_t(b) * p.L + min(ms + lane, mmax)];
-  const int pb = p.perm[int64_t(b) * p.L + min(ms + lane + 1, mmax)];
-  typename V::Raw xr[kDvSub];
-  if (p.M > 0) {
-#pragma unroll
-    for (int i = 0; i < kDvSub; ++i) xr[i] = V::ld(p.x, b * p.x_sb + d + int64_t(min(mq + i, mmax)) * p.x_sr);
-  }
-  // the earlier segments of the phase-1 workgroup (at most kDcGrp - 1 maps)
-  F8::Raw sv[kDcGrp - 1];
-  float sd[kDcGrp - 1];
-#pragma unroll
-  for (int k = 0; k < kDcGrp - 1; ++k) {
-    const int64_t si = int64_t(b) * p.nseg + min(g * kDcGrp + k, s);
-    sv[k] = F8::ld(p.segv, si * p.D + d);
-    sd[k] = p.segd[si];
-  }
-  float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  if (p.init) F8::cvt(F8::ld(p.init, int64_t(b) * p.D + d), z);
-  dv_fold(p.grpv + int64_t(b) * p.ngrp * p.D, p.grpd + int64_t(b) * p.ngrp, p.D, d, 0, 1, g, z);
-#pragma unroll
-  for (int k = 0; k < kDcGrp - 1; ++k) {
-    if (g * kDcGrp + k < s) {
-      float v[8];
-      F8::cvt(sv[k], v);
-#pragma unroll
-      for (int c = 0; c < 8; ++c) z[c] = fmaf(sd[k], z[c], v[c]);
-    }
-  }
-  const int n = dc_used_raw(p, nraw);
-  const int cnt = min(kDcSeg, n - ms), cs = min(max(cnt - kDvSub * q, 0), kDvSub);
-  const int m = ms + lane;
-  const int t0l = m >= n ? p.L : (m == 0 && p.init == nullptr ? 0 : pa);
-  const int t1l = m + 1 >= n ? p.L : pb;
-  const int pa0 = __shfl(pa, 0, 64);  // perm[0] when s == 0
-  float e[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  float A = 1.f;
-  if (cnt > 0) {
-#pragma unroll
-    for (int i = 0; i < kDvSub; ++i) {
-      const float pc = __shfl(pv, kDvSub * q + i, 64);
-      if (i < cs) {
-        float x[8];
-        V::cvt(xr[i], x);
-        const float a = 1.f - pc;
-#pragma unroll
-        for (int c = 0; c < 8; ++c) e[c] = fmaf(a, e[c], pc * x[c]);
-        A *= a;
-      }
-    }
-  }
-  // the earlier lane groups' sub-segments, in order
-#pragma unroll
-  for (int qq = 0; qq < 3; ++qq) {
-    const int src = 16 * qq + r;
-    const float Aq = __shfl(A, src, 64);
-    float Eq[8];
-#pragma unroll
-    for (int c = 0; c < 8; ++c) Eq[c] = __shfl(e[c], src, 64);
-    if (qq < q) {
-#pragma unroll
-      for (int c = 0; c < 8; ++c) z[c] = fmaf(Aq, z[c], Eq[c]);
-    }
-  }
-  const int64_t ob = b * p.o_sb + d;
-  if (s == 0 && q == 0 && p.init) {
-    const int tf = n > 0 ? pa0 : p.L;  // dc_lo(0): the first boundary, all bytes without one
-    for (int t = 0; t < tf; ++t)
-      if (live) V::st(p.out, ob + int64_t(t) * p.o_sr, z);
-  }
-  if (cnt <= 0) return;
-  float* wrow = p.w + (int64_t(b) * p.M + mq) * p.D + d;
-#pragma unroll
-  for (int i = 0; i < kDvSub; ++i) {
-    const int src = kDvSub * q + i;
-    const float pc = __shfl(pv, src, 64);
-    const int t0 = __shfl(t0l, src, 64), t1 = __shfl(t1l, src, 64);
-    if (i < cs) {
-      float x[8];
-      V::cvt(xr[i], x);
-      if (live && p.w) {
-        float wv[8];
-#pragma unroll
-        for (int c = 0; c < 8; ++c) wv[c] = x[c] - z[c];
-        F8::st(wrow, int64_t(i) * p.D, wv);
-      }
-      const float a = 1.f - pc;
-#pragma unroll
-      for (int c = 0; c < 8; ++c) z[c] = fmaf(a, z[c], pc * x[c]);
-      for (int t = t0; t < t1; ++t)
-        if (live) V::st(p.out, ob + int64_t(t) * p.o_sr, z);
-    }
-  }
-}
-
-// The backward sub-segment's reverse run from zero over its ds rows (h = value at its first chunk,
-// A = decay), with pn the clamped p of the chunk after the lane's (0 past the row)
-__device__ __forceinline__ void dv_bwd_run(const F8::Raw (&dsr)[kDvSub], float pn, int q, int cs, float (&h)[8],
-                                           float& A) {
-#pragma unroll
-  for (int i = kDvSub - 1; i >= 0; --i) {
-    const float an = 1.f - __shfl(pn, kDvSub * q + i, 64);
-    if (i < cs) {
-      float v[8];
-      F8::cvt(dsr[i], v);
-#pragma unroll
-      for (int c = 0; c < 8; ++c) h[c] = fmaf(an, h[c], v[c]);
-      A *= an;
-    }
-  }
-}
-
-// phase 1 (backward, vector path): sub-segments' reverse runs from zero, composed from the last down
-// (LDS) into the workgroup's aggregate; the clamped p of the segment's chunks go to pc
-__global__ void __launch_bounds__(64 * kDcGrp) dechunk_bwd_grp_v_kernel(const DechunkParams p) {
-  __shared__ float sh[kDcGrp * 4][16][8];
-  __shared__ float sa[kDcGrp * 4];
-  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int q = lane >> 4, r = lane & 15;
-  const int strip = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
-  const bool live = strip * kDcCh + 8 * r < p.D;
-  const int d = min(strip * kDcCh + 8 * r, p.D - 8);
-  const int ms = (g * kDcGrp + w) * kDcSeg, mq = ms + kDvSub * q, mmax = p.M - 1;  // M >= 1 here
-  const int nraw = p.num[b];
-  const int ta = p.perm[int64_t(b) * p.L + min(ms + lane, mmax)];
-  const int tb = p.perm[int64_t(b) * p.L + min(ms + lane + 1, mmax)];
-  F8::Raw dsr[kDvSub];
-#pragma unroll
-  for (int i = 0; i < kDvSub; ++i) dsr[i] = F8::ld(p.ds, int64_t(b) * p.M * p.D + d + int64_t(min(mq + i, mmax)) * p.D);
-  const float praw = ld1(p.prob, b * p.p_sb + int64_t(ta) * p.p_sr + 1, p.p_f32);
-  const float pv = dc_clamp(p, praw);
-  const float pnr = dc_clamp(p, ld1(p.prob, b * p.p_sb + int64_t(tb) * p.p_sr + 1, p.p_f32));
-  const int n = dc_used_raw(p, nraw);
-  const int cnt = min(kDcSeg, n - ms), cs = min(max(cnt - kDvSub * q, 0), kDvSub);
-  // kept for phase 2 with the clamp's gradient gate in the sign: negative where the raw p was clamped
-  if (strip == 0 && ms + lane < p.M)
-    p.pc[int64_t(b) * p.M + ms + lane] = (praw >= p.eps && praw <= 1.0f - p.eps) ? pv : -pv;
-  const float pn = ms + lane + 1 < n ? pnr : 0.f;  // p of the next chunk
-  float h[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  float A = 1.f;
-  if (cnt > 0) dv_bwd_run(dsr, pn, q, cs, h, A);
-#pragma unroll
-  for (int c = 0; c < 8; ++c) sh[4 * w + q][r][c] = h[c];
-  if (r == 0) sa[4 * w + q] = A;
-  __syncthreads();
-  if (q == 0) {  // lane group 0 of each wave: its segment's aggregate; wave 0 the workgroup's
-    float S[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    float As = 1.f;
-    for (int kk = 4 * w + 3; kk >= 4 * w; --kk) {
-#pragma unroll
-      for (int c = 0; c < 8; ++c) S[c] = fmaf(sa[kk], S[c], sh[kk][r][c]);
-      As *= sa[kk];
-    }
-    const int64_t si = int64_t(b) * p.nseg + g * kDcGrp + w;
-    if (live) F8::st(p.segv, si * p.D + d, S);
-    if (strip == 0 && r == 0) p.segd[si] = As;
-    if (w == 0) {
-      float E[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      float Ag = 1.f;
-      for (int k = kDcGrp * 4 - 1; k >= 0; --k) {
-        const float a = sa[k];
-#pragma unroll
-        for (int c = 0; c < 8; ++c) E[c] = fmaf(a, E[c], sh[k][r][c]);
-        Ag *= a;
-      }
-      const int64_t gi = int64_t(b) * p.ngrp + g;
-      if (live) F8::st(p.grpv, gi * p.D + d, E);
-      if (strip == 0 && r == 0) p.grpd[gi] = Ag;
-    }
-  }
-}
-
-// phase 2 (backward, vector path), a workgroup per segment with one wave per channel strip: the carry
-// into the segment's end from the row's later workgroups (from the last down; past the row they are
-// the identity) and the later segments of its phase-1 workgroup, into each lane group's end from the
-// later sub-segments (lane shuffles), then the reverse run: dx = p g and the dp partial of each chunk
-// and strip, the sum over the strip's channels of g w (8 per lane in order, then a fixed butterfly over
-// the 16 lanes of a group). The strips' partials add in strip order through LDS, and the segment's
-// bytes get d boundary_prob: [..., 1] = dp of the chunk at its boundary byte (zero where the clamp was
-// active), zero everywhere else (the dechunk_dprob_kernel of the two-channel path).
-constexpr int kDvMaxStrips = 4;  // D <= 512 (every preset's outer width): one wave per SIMD, 512 VGPRs
-
-template <bool F32>
-__global__ void __launch_bounds__(64 * kDvMaxStrips) dechunk_bwd_out_v_kernel(const DechunkParams p) {
-  typedef V8<F32> V;
-  __shared__ float red[kDvMaxStrips][kDcSeg];
-  const int lane = threadIdx.x & 63, strip = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int q = lane >> 4, r = lane & 15;
-  const int s = blockIdx.x, b = blockIdx.y;
-  const int g = s / kDcGrp;
-  const bool live = strip * kDcCh + 8 * r < p.D;
-  const int d = min(strip * kDcCh + 8 * r, p.D - 8);
-  const int ms = s * kDcSeg, mq = ms + kDvSub * q, mmax = p.M - 1;  // M >= 1 here
-  const int nraw = p.num[b];
-  const float pc_lane = p.pc[int64_t(b) * p.M + min(ms + lane, mmax)];
-  const float pv = fabsf(pc_lane);
-  const float pnr = fabsf(p.pc[int64_t(b) * p.M + min(ms + lane + 1, mmax)]);
-  const int pa = p.perm[int64_t(b) * p.L + min(ms + lane, mmax)];
-  const int pb = p.perm[int64_t(b) * p.L + min(ms + lane + 1, mmax)];
-  F8::Raw dsr[kDvSub], wr[kDvSub];
-#pragma unroll
-  for (int i = 0; i < kDvSub; ++i) {
-    const int64_t off = int64_t(b) * p.M * p.D + d + int64_t(min(mq + i, mmax)) * p.D;
-    dsr[i] = F8::ld(p.ds, off);
-    wr[i] = F8::ld(p.w, off);
-  }
-  // the later segments of the phase-1 workgroup, last first (at most kDcGrp - 1 maps)
-  F8::Raw sv[kDcGrp - 1];
-  float sd[kDcGrp - 1];
-#pragma unroll
-  for (int k = 0; k < kDcGrp - 1; ++k) {
-    const int64_t si = int64_t(b) * p.nseg + max(g * kDcGrp + kDcGrp - 1 - k, s);
-    sv[k] = F8::ld(p.segv, si * p.D + d);
-    sd[k] = p.segd[si];
-  }
-  float G[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  dv_fold(p.grpv + int64_t(b) * p.ngrp * p.D, p.grpd + int64_t(b) * p.ngrp, p.D, d, p.ngrp - 1, -1, p.ngrp - 1 - g, G);
-#pragma unroll
-  for (int k = 0; k < kDcGrp - 1; ++k) {
-    if (g * kDcGrp + kDcGrp - 1 - k > s) {
-      float v[8];
-      F8::cvt(sv[k], v);
-#pragma unroll
-      for (int c = 0; c < 8; ++c) G[c] = fmaf(sd[k], G[c], v[c]);
-    }
-  }
-  const int n = dc_used_raw(p, nraw);
-  const int cnt = min(kDcSeg, n - ms), cs = min(max(cnt - kDvSub * q, 0), kDvSub);
-  const float pn = ms + lane + 1 < n ? pnr : 0.f;
-  const int64_t xb = b * p.dx_sb + d;
-  if (s == p.nseg - 1) {  // rows no byte reads: zero gradient, the lane groups taking turns
-    const float zero[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int mz = n + q; mz < p.M; mz += 4)
-      if (live) V::st(p.dx, xb + int64_t(mz) * p.dx_sr, zero);
-  }
-  float mine = 0.f;
-  if (cnt > 0) {
-    float h[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    float A = 1.f;
-    dv_bwd_run(dsr, pn, q, cs, h, A);
-    // the later lane groups' sub-segments, last first
-#pragma unroll
-    for (int qq = 3; qq >= 1; --qq) {
-      const int src = 16 * qq + r;
-      const float Aq = __shfl(A, src, 64);
-      float Hq[8];
-#pragma unroll
-      for (int c = 0; c < 8; ++c) Hq[c] = __shfl(h[c], src, 64);
-      if (qq > q) {
-#pragma unroll
-        for (int c = 0; c < 8; ++c) G[c] = fmaf(Aq, G[c], Hq[c]);
-      }
-    }
-#pragma unroll
-    for (int i = kDvSub - 1; i >= 0; --i) {
-      const int src = kDvSub * q + i;
-      const float an = 1.f - __shfl(pn, src, 64), pc = __shfl(pv, src, 64);
-      float dot = 0.f;
-      if (i < cs) {
-        float v[8], wv[8], dx[8];
-        F8::cvt(dsr[i], v);
-        F8::cvt(wr[i], wv);
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          G[c] = fmaf(an, G[c], v[c]);
-          dx[c] = pc * G[c];
-        }
-        if (live) {
-          V::st(p.dx, xb + int64_t(mq + i) * p.dx_sr, dx);
-#pragma unroll
-          for (int c = 0; c < 8; ++c) dot = fmaf(G[c], wv[c], dot);
-        }
-      }
-      dot += __shfl_xor(dot, 8, 64);
-      dot += __shfl_xor(dot, 4, 64);
-      dot += __shfl_xor(dot, 2, 64);
-      dot += __shfl_xor(dot, 1, 64);
-      if (r == i) mine = dot;
-    }
-  }
-  red[strip][kDvSub * q + r] = mine;
-  __syncthreads();
-  if (strip == 0 && lane < cnt) {
-    // chunk m = ms + lane: dp in strip order, gated by the clamp; its bytes [t0, t1) of d prob
-    const int m = ms + lane;
-    float dp = 0.f;
-    for (int k = 0; k < p.nstrips; ++k) dp += red[k][lane];
-    if (pc_lane < 0.f) dp = 0.f;
-    const int t0 = m == 0 ? 0 : pa;                  // no carried value in the backward
-    const int t1 = m + 1 >= n ? p.L : pb;
-    const int tb = nraw > 0 ? pa : 0;                // the boundary byte (byte 0 of a row without one)
-    for (int t = t0; t < t1; ++t) {
-      const float v = t == tb ? dp : 0.f;
-      const int64_t off = b * p.dp_sb + int64_t(t) * p.dp_sr;
-      if (p.dp_f32) {
-        reinterpret_cast<float*>(p.dprob)[off] = 0.f;
-        reinterpret_cast<float*>(p.dprob)[off + 1] = v;
-      } else {
-        reinterpret_cast<bf16_t*>(p.dprob)[off] = 0;
-        reinterpret_cast<bf16_t*>(p.dprob)[off + 1] = f2bf(v);
-      }
-    }
-  }
 }
 
 // d boundary_prob: [..., 0] = 0, [..., 1] = dp of the chunk the position starts (fixed-order sum over
@@ -1187,6 +762,617 @@ __global__ void __launch_bounds__(256) dechunk_dprob_kernel(const DechunkParams 
   } else {
     reinterpret_cast<bf16_t*>(dprob)[off] = 0;
     reinterpret_cast<bf16_t*>(dprob)[off + 1] = f2bf(v);
+  }
+}
+
+// Backward chunk sums, balanced by bytes (vector path): one wave per kDsBytes bytes of a row sums the
+// chunks that start in them, each over all of its bytes (past the range when the last one continues),
+// in byte order from zero, 8 channels per lane over the row in slabs of 512: the sums of
+// dechunk_dsum_kernel bit for bit. A wave's work is its range plus one chunk, wherever the boundaries
+// fall, and the chunk changes are the same for every lane (no divergence).
+constexpr int kDsBytes = 16;
+
+template <bool F32>
+__global__ void __launch_bounds__(64) dechunk_dsum_bal_kernel(const DechunkParams p) {
+  typedef V8<F32> V;
+  const int lane = threadIdx.x & 63;
+  const int R0 = blockIdx.x * kDsBytes, b = blockIdx.y;
+  if (R0 >= p.L) return;
+  const int32_t* cum = p.cum + int64_t(b) * p.L;
+  const int32_t* perm = p.perm + int64_t(b) * p.L;
+  const int n = dc_used_raw(p, p.num[b]);
+  // chunks ka .. kb - 1 start in [R0, R0 + kDsBytes): chunk 0 at byte 0, chunk k >= 1 at perm[k]
+  const int ka = min(R0 == 0 ? 0 : max(cum[R0 - 1], 1), n);
+  const int kb = min(max(cum[min(R0 + kDsBytes, p.L) - 1], R0 == 0 ? 1 : 0), n);
+  if (ka >= kb) return;
+  // lane i: the first byte past chunk ka + i (its end), for the chunks of the range (at most kDsBytes)
+  const int ke = ka + lane;
+  const int endl = ke + 1 >= n ? p.L : perm[min(ke + 1, p.L - 1)];
+  const int t_lo = ka == 0 ? 0 : perm[ka];
+  const int t_hi = __builtin_amdgcn_readlane(endl, kb - 1 - ka);
+  const int64_t gb = b * p.g_sb;
+  for (int d0 = 0; d0 < p.D; d0 += 512) {
+    const int d = min(d0 + 8 * lane, p.D - 8);
+    const bool live = d0 + 8 * lane < p.D;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    int k = ka, kend = __builtin_amdgcn_readlane(endl, 0);
+    constexpr int NR = F32 ? 8 : 16;
+    typename V::Raw ra[NR], rb[NR];
+    auto load = [&](typename V::Raw (&rr)[NR], int t0) {
+#pragma unroll
+      for (int j = 0; j < NR; ++j) rr[j] = V::ld(p.dout, gb + int64_t(min(t0 + j, t_hi - 1)) * p.g_sr + d);
+    };
+    auto add = [&](const typename V::Raw (&rr)[NR], int t0) {
+#pragma unroll
+      for (int j = 0; j < NR; ++j) {
+        const int t = t0 + j;
+        if (t < t_hi) {  // uniform
+          float v[8];
+          V::cvt(rr[j], v);
+#pragma unroll
+          for (int c = 0; c < 8; ++c) acc[c] += v[c];
+          if (t + 1 == kend) {  // chunk k ends here: its row of sums
+            if (live) F8::st(p.ds + (int64_t(b) * p.M + k) * p.D, d, acc);
+#pragma unroll
+            for (int c = 0; c < 8; ++c) acc[c] = 0.f;
+            ++k;
+            kend = __builtin_amdgcn_readlane(endl, min(k - ka, 63));
+          }
+        }
+      }
+    };
+    load(ra, t_lo);
+    for (int t0 = t_lo; t0 < t_hi; t0 += 2 * NR) {
+      if (t0 + NR < t_hi) load(rb, t0 + NR);
+      add(ra, t0);
+      if (t0 + 2 * NR < t_hi) load(ra, t0 + 2 * NR);
+      if (t0 + NR < t_hi) add(rb, t0 + NR);
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Vector path over 64-channel strips (D % 8 == 0, rows on 16-byte boundaries). A wave owns one
+// 64-chunk segment of a 64-channel strip as eight 8-lane groups: group g runs chunks m0 + 8 g .. + 7
+// and lane r of it channels 8 r .. 8 r + 7 (16-byte accesses), so a wave's sequential chain is 8
+// chunks long and a row of 16 384 bytes keeps 640 waves busy at D = 512. Segments compose in groups
+// of four. Two launches per direction: the first writes the segment and group aggregates to the
+// workspace, the second reads them with plain loads. (A single-launch form whose waves exchanged the
+// aggregates through coherent memory, with per-call epochs and bounded polling, measured no faster:
+// two exchange hops of one to two round trips each cost more than the kernel boundary.)
+// ------------------------------------------------------------------------------------------------
+constexpr int kFsCh = 64;                // channels per strip
+constexpr int kFsSub = 8;                // chunks per lane group (8 groups of 8 lanes)
+constexpr int kFsMaxStrips = 8;          // backward: one wave per strip in a workgroup, D <= 512
+
+// lane 8 g + i's value for the lanes of group g (i a constant): lane reads and a select, no LDS trip
+template <typename T>
+__device__ __forceinline__ T grp8(T v, int i, int g) {
+  T a[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) a[k] = rdl(v, 8 * k + i);
+  T o = a[7];
+#pragma unroll
+  for (int k = 6; k >= 0; --k) o = g == k ? a[k] : o;
+  return o;
+}
+
+// the maps (values E, decay A) held by the eight lane groups, composed in order g = 0 .. 7 (forward)
+// or 7 .. 0 (backward) into c, their decays into Ac (every lane holds the result)
+template <bool Rev>
+__device__ __forceinline__ void grp_compose(const float (&E)[8], float A, int r, float (&c)[8], float& Ac) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int gg = Rev ? 7 - k : k;
+    const int src = 8 * gg + r;
+    const float Ag = __shfl(A, src, 64);
+#pragma unroll
+    for (int ch = 0; ch < 8; ++ch) c[ch] = fmaf(Ag, c[ch], __shfl(E[ch], src, 64));
+    Ac *= Ag;
+  }
+}
+
+// c <- A_j c + e_j over workspace aggregates j = j0 + step k (k < cnt) in order: each 8-lane group
+// composes an eighth (8 maps loaded at a time), then every lane applies the eighths in order
+__device__ __forceinline__ void dw_fold(const float* gv, const float* gd, int D, int d, int j0, int step, int cnt,
+                                        int r, int gq, float (&c)[8]) {
+  const int per = (max(cnt, 0) + 7) / 8;
+  const int k0 = gq * per, k1 = min(cnt, k0 + per);
+  float E[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float A = 1.f;
+  for (int kb = k0; kb < k1; kb += 8) {
+    F8::Raw e[8];
+    float a[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int j = j0 + step * min(kb + k, k1 - 1);
+      e[k] = F8::ld(gv, int64_t(j) * D + d);
+      a[k] = gd[j];
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (kb + k < k1) {
+        float v[8];
+        F8::cvt(e[k], v);
+#pragma unroll
+        for (int ch = 0; ch < 8; ++ch) E[ch] = fmaf(a[k], E[ch], v[ch]);
+        A *= a[k];
+      }
+    }
+  }
+  float Ac = 1.f;
+  grp_compose<false>(E, A, r, c, Ac);
+}
+
+// The same fold in two steps, for a kernel with registers to spare: issue() loads the first 8 maps of
+// the group's eighth (all of them while cnt <= 64, i.e. M <= 16 384 chunks) at the kernel's start;
+// fold() composes them with any remaining ones.
+struct DwFold {
+  const float* gv;
+  const float* gd;
+  int D, d, j0, step, k0, k1;
+  F8::Raw e[8];
+  float a[8];
+  __device__ __forceinline__ void issue(const float* gv_, const float* gd_, int D_, int d_, int j0_, int step_,
+                                        int cnt, int gq) {
+    gv = gv_, gd = gd_, D = D_, d = d_, j0 = j0_, step = step_;
+    const int per = (max(cnt, 0) + 7) / 8;
+    k0 = gq * per;
+    k1 = min(cnt, k0 + per);
+    load(k0);
+  }
+  __device__ __forceinline__ void load(int kb) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int j = j0 + step * max(min(kb + k, k1 - 1), 0);
+      e[k] = F8::ld(gv, int64_t(j) * D + d);
+      a[k] = gd[j];
+    }
+  }
+  __device__ __forceinline__ void fold(int r, float (&c)[8]) {
+    float E[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float A = 1.f;
+    for (int kb = k0; kb < k1; kb += 8) {
+      if (kb > k0) load(kb);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        if (kb + k < k1) {
+          float v[8];
+          F8::cvt(e[k], v);
+#pragma unroll
+          for (int ch = 0; ch < 8; ++ch) E[ch] = fmaf(a[k], E[ch], v[ch]);
+          A *= a[k];
+        }
+      }
+    }
+    float Ac = 1.f;
+    grp_compose<false>(E, A, r, c, Ac);
+  }
+};
+
+// phase 1 (forward): a workgroup per (strip, group of four segments, row), a wave per segment: the
+// 8-chunk runs from zero, the segment's map (its lane groups in order) to segv / segd, the group's map
+// (its segments in order, through LDS) to grpv / grpd, and the clamped p of every chunk to pc
+template <bool F32>
+__global__ void __launch_bounds__(64 * kDcGrp) dechunk_grp_w_kernel(const DechunkParams p) {
+  typedef V8<F32> V;
+  __shared__ float se[kDcGrp][8][8];
+  __shared__ float sa[kDcGrp];
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int gq = lane >> 3, r = lane & 7;
+  const int strip = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+  const bool live = strip * kFsCh + 8 * r < p.D;
+  const int d = min(strip * kFsCh + 8 * r, p.D - 8);
+  const int s = g * kDcGrp + w, ms = s * kDcSeg, mq = ms + kFsSub * gq, mmax = max(p.M - 1, 0);
+  const int nraw = p.num[b];
+  const int tp = p.perm[int64_t(b) * p.L + min(ms + lane, mmax)];
+  typename V::Raw xr[kFsSub];
+  if (p.M > 0) {
+#pragma unroll
+    for (int i = 0; i < kFsSub; ++i) xr[i] = V::ld(p.x, b * p.x_sb + d + int64_t(min(mq + i, mmax)) * p.x_sr);
+  }
+  const float pv = dc_clamp(p, ld1(p.prob, b * p.p_sb + int64_t(tp) * p.p_sr + 1, p.p_f32));
+  const int n = dc_used_raw(p, nraw);
+  const int cnt = min(kDcSeg, n - ms), cs = min(max(cnt - kFsSub * gq, 0), kFsSub);
+  if (strip == 0 && ms + lane < p.M) p.pc[int64_t(b) * p.M + ms + lane] = pv;
+  float pcs[kFsSub];
+#pragma unroll
+  for (int i = 0; i < kFsSub; ++i) pcs[i] = grp8(pv, i, gq);
+  float e[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float A = 1.f;
+  if (cnt > 0) {
+#pragma unroll
+    for (int i = 0; i < kFsSub; ++i) {
+      if (i < cs) {
+        float x[8];
+        V::cvt(xr[i], x);
+        const float a = 1.f - pcs[i];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) e[c] = fmaf(a, e[c], pcs[i] * x[c]);
+        A *= a;
+      }
+    }
+  }
+  float S[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float As = 1.f;
+  grp_compose<false>(e, A, r, S, As);
+  const int64_t si = int64_t(b) * p.nseg + s;
+  if (gq == 0) {
+    if (live) F8::st(p.segv, si * p.D + d, S);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) se[w][r][c] = S[c];
+    if (r == 0) {
+      sa[w] = As;
+      if (strip == 0) p.segd[si] = As;
+    }
+  }
+  __syncthreads();
+  if (w == 0 && gq == 0) {
+    float G[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float Ga = 1.f;
+#pragma unroll
+    for (int k = 0; k < kDcGrp; ++k) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) G[c] = fmaf(sa[k], G[c], se[k][r][c]);
+      Ga *= sa[k];
+    }
+    const int64_t gi = int64_t(b) * p.ngrp + g;
+    if (live) F8::st(p.grpv, gi * p.D + d, G);
+    if (strip == 0 && r == 0) p.grpd[gi] = Ga;
+  }
+}
+
+// phase 2 (forward): one wave per (strip, segment, row): the carry (the row's carried value, the
+// earlier groups, the earlier segments of the group), the 8-chunk runs again with w and z (z to LDS in
+// out's dtype), then the segment's bytes [T0, T1): byte t takes the z row of chunk cum[t] - 1, eight
+// bytes per store instruction (group g takes byte T0 + 8 k + g, every store a whole 128-byte row
+// piece), each block's LDS reads issued before its stores; the chunk indices of the first 256 bytes
+// load at the kernel's start
+template <bool F32>
+__global__ void __launch_bounds__(64) dechunk_out_w_kernel(const DechunkParams p) {
+  typedef V8<F32> V;
+  __shared__ typename V::Raw zl[kDcSeg + 1][8];
+  const int lane = threadIdx.x & 63, gq = lane >> 3, r = lane & 7;
+  const int strip = blockIdx.x, s = blockIdx.y, b = blockIdx.z;
+  const int g = s / kDcGrp, nsib = s - g * kDcGrp;
+  const bool live = strip * kFsCh + 8 * r < p.D;
+  const int d = min(strip * kFsCh + 8 * r, p.D - 8);
+  const int ms = s * kDcSeg, mq = ms + kFsSub * gq, mmax = max(p.M - 1, 0);
+  // every load that needs no other first
+  const int nraw = p.num[b];
+  const float pv = p.M > 0 ? p.pc[int64_t(b) * p.M + min(ms + lane, mmax)] : 0.f;
+  const int pa = p.perm[int64_t(b) * p.L + min(ms + lane, mmax)];
+  const int pb = p.perm[int64_t(b) * p.L + min(ms + lane + 1, mmax)];
+  typename V::Raw xr[kFsSub];
+  if (p.M > 0) {
+#pragma unroll
+    for (int i = 0; i < kFsSub; ++i) xr[i] = V::ld(p.x, b * p.x_sb + d + int64_t(min(mq + i, mmax)) * p.x_sr);
+  }
+  float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (p.init) F8::cvt(F8::ld(p.init, int64_t(b) * p.D + d), z);
+  F8::Raw sv[kDcGrp - 1];
+  float sd[kDcGrp - 1];
+#pragma unroll
+  for (int k = 0; k < kDcGrp - 1; ++k) {
+    const int64_t si = int64_t(b) * p.nseg + min(g * kDcGrp + k, s);
+    sv[k] = F8::ld(p.segv, si * p.D + d);
+    sd[k] = p.segd[si];
+  }
+  const int n = dc_used_raw(p, nraw);
+  const int cnt = min(kDcSeg, n - ms), cs = min(max(cnt - kFsSub * gq, 0), kFsSub);
+  const int pa0 = __shfl(pa, 0, 64), pb63 = __shfl(pb, 63, 64);
+  const int T0 = s == 0 ? 0 : (ms < n ? pa0 : p.L);
+  const int T1 = ms + kDcSeg < n ? pb63 : p.L;
+  const int32_t* cum = p.cum + int64_t(b) * p.L;
+  constexpr int kPre = 4;
+  int cv[kPre * 8];
+#pragma unroll
+  for (int i = 0; i < kPre * 8; ++i) cv[i] = cum[max(min(T0 + 8 * i + gq, T1 - 1), 0)];
+  DwFold gf;
+  gf.issue(p.grpv + int64_t(b) * p.ngrp * p.D, p.grpd + int64_t(b) * p.ngrp, p.D, d, 0, 1, g, gq);
+  // the lane group's chunks from zero (for the carry into each group), while the aggregates arrive
+  float pcs[kFsSub];
+#pragma unroll
+  for (int i = 0; i < kFsSub; ++i) pcs[i] = grp8(pv, i, gq);
+  float e[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float A = 1.f;
+  if (cnt > 0) {
+#pragma unroll
+    for (int i = 0; i < kFsSub; ++i) {
+      if (i < cs) {
+        float x[8];
+        V::cvt(xr[i], x);
+        const float a = 1.f - pcs[i];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) e[c] = fmaf(a, e[c], pcs[i] * x[c]);
+        A *= a;
+      }
+    }
+  }
+  // the carry into the segment: the earlier groups, then the earlier segments of the group
+  gf.fold(r, z);
+#pragma unroll
+  for (int k = 0; k < kDcGrp - 1; ++k) {
+    if (k < nsib) {
+      float v[8];
+      F8::cvt(sv[k], v);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) z[c] = fmaf(sd[k], z[c], v[c]);
+    }
+  }
+  if (s == 0 && gq == 0) zl[kDcSeg][r] = V::pack(z);  // bytes before the first boundary (carried value)
+#pragma unroll
+  for (int gg = 0; gg < 7; ++gg) {
+    const int src = 8 * gg + r;
+    const float Ag = __shfl(A, src, 64);
+    float Eg[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) Eg[c] = __shfl(e[c], src, 64);
+    if (gg < gq) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) z[c] = fmaf(Ag, z[c], Eg[c]);
+    }
+  }
+  if (cnt > 0) {
+    float* wrow = p.w ? p.w + (int64_t(b) * p.M + mq) * p.D + d : nullptr;
+#pragma unroll
+    for (int i = 0; i < kFsSub; ++i) {
+      if (i < cs) {
+        float x[8];
+        V::cvt(xr[i], x);
+        if (live && p.w) {
+          float wv[8];
+#pragma unroll
+          for (int c = 0; c < 8; ++c) wv[c] = x[c] - z[c];
+          F8::st(wrow, int64_t(i) * p.D, wv);
+        }
+        const float a = 1.f - pcs[i];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) z[c] = fmaf(a, z[c], pcs[i] * x[c]);
+        zl[kFsSub * gq + i][r] = V::pack(z);
+      }
+    }
+  }
+  __builtin_amdgcn_wave_barrier();  // one wave: LDS in order, no workgroup barrier
+  const int64_t ob = b * p.o_sb + d;
+  auto block = [&](int t0, const int* cb) {
+    typename V::Raw zr[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      int c = cb[i] - 1;
+      if (!p.init) c = max(c, 0);
+      c = min(c, n - 1);
+      zr[i] = zl[c < ms ? kDcSeg : min(c - ms, kDcSeg - 1)][r];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int t = t0 + 8 * i + gq;
+      if (live && t < T1) V::st_raw(p.out, ob + int64_t(t) * p.o_sr, zr[i]);
+    }
+  };
+#pragma unroll
+  for (int k = 0; k < kPre; ++k)
+    if (T0 + 64 * k < T1) block(T0 + 64 * k, cv + 8 * k);
+  for (int t0 = T0 + 64 * kPre; t0 < T1; t0 += 64) {
+    int cn[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) cn[i] = cum[min(t0 + 8 * i + gq, T1 - 1)];
+    block(t0, cn);
+  }
+}
+
+// phase 1 (backward): a workgroup per (strip, group of four segments, row), a wave per segment: the
+// 8-chunk reverse runs from zero over the chunk sums, the segment's map (lane groups from the last) to
+// segv / segd, the group's map (segments from the last, through LDS) to grpv / grpd, and the clamped
+// p of every chunk to pc with the clamp's gradient gate in its sign (negative where it was clamped)
+__global__ void __launch_bounds__(64 * kDcGrp) dechunk_bwd_grp_w_kernel(const DechunkParams p) {
+  __shared__ float se[kDcGrp][8][8];
+  __shared__ float sa[kDcGrp];
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int gq = lane >> 3, r = lane & 7;
+  const int strip = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+  const bool live = strip * kFsCh + 8 * r < p.D;
+  const int d = min(strip * kFsCh + 8 * r, p.D - 8);
+  const int s = g * kDcGrp + w, ms = s * kDcSeg, mq = ms + kFsSub * gq, mmax = p.M - 1;  // M >= 1 here
+  const int nraw = p.num[b];
+  const int ta = p.perm[int64_t(b) * p.L + min(ms + lane, mmax)];
+  const int tb = p.perm[int64_t(b) * p.L + min(ms + lane + 1, mmax)];
+  F8::Raw dsr[kFsSub];
+#pragma unroll
+  for (int i = 0; i < kFsSub; ++i) dsr[i] = F8::ld(p.ds, int64_t(b) * p.M * p.D + d + int64_t(min(mq + i, mmax)) * p.D);
+  const float praw = ld1(p.prob, b * p.p_sb + int64_t(ta) * p.p_sr + 1, p.p_f32);
+  const float pv = dc_clamp(p, praw);
+  const float pnr = dc_clamp(p, ld1(p.prob, b * p.p_sb + int64_t(tb) * p.p_sr + 1, p.p_f32));
+  const int n = dc_used_raw(p, nraw);
+  const int cnt = min(kDcSeg, n - ms), cs = min(max(cnt - kFsSub * gq, 0), kFsSub);
+  if (strip == 0 && ms + lane < p.M)
+    p.pc[int64_t(b) * p.M + ms + lane] = (praw >= p.eps && praw <= 1.0f - p.eps) ? pv : -pv;
+  const float pn = ms + lane + 1 < n ? pnr : 0.f;
+  float h[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float A = 1.f;
+  if (cnt > 0) {
+#pragma unroll
+    for (int i = kFsSub - 1; i >= 0; --i) {
+      const float an = 1.f - grp8(pn, i, gq);
+      if (i < cs) {
+        float v[8];
+        F8::cvt(dsr[i], v);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) h[c] = fmaf(an, h[c], v[c]);
+        A *= an;
+      }
+    }
+  }
+  float S[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float As = 1.f;
+  grp_compose<true>(h, A, r, S, As);
+  const int64_t si = int64_t(b) * p.nseg + s;
+  if (gq == 0) {
+    if (live) F8::st(p.segv, si * p.D + d, S);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) se[w][r][c] = S[c];
+    if (r == 0) {
+      sa[w] = As;
+      if (strip == 0) p.segd[si] = As;
+    }
+  }
+  __syncthreads();
+  if (w == 0 && gq == 0) {
+    float G[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float Ga = 1.f;
+#pragma unroll
+    for (int k = kDcGrp - 1; k >= 0; --k) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) G[c] = fmaf(sa[k], G[c], se[k][r][c]);
+      Ga *= sa[k];
+    }
+    const int64_t gi = int64_t(b) * p.ngrp + g;
+    if (live) F8::st(p.grpv, gi * p.D + d, G);
+    if (strip == 0 && r == 0) p.grpd[gi] = Ga;
+  }
+}
+
+// phase 2 (backward): a workgroup per (segment, row), a wave per strip: the carry into the segment's
+// end (the later groups from the last down, then the later siblings), the lane groups' later chunks,
+// dx = p g, the dp partials (transposed butterfly over each group's 8 lanes), the strips' partials
+// added in order through LDS and d boundary_prob over the segment's bytes
+template <bool F32>
+__global__ void __launch_bounds__(64 * kFsMaxStrips) dechunk_bwd_out_w_kernel(const DechunkParams p) {
+  typedef V8<F32> V;
+  __shared__ float red[kFsMaxStrips][kDcSeg];
+  const int lane = threadIdx.x & 63, strip = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int gq = lane >> 3, r = lane & 7;
+  const int s = blockIdx.x, b = blockIdx.y;
+  const int g = s / kDcGrp, nsib = g * kDcGrp + kDcGrp - 1 - s;
+  const bool live = strip * kFsCh + 8 * r < p.D;
+  const int d = min(strip * kFsCh + 8 * r, p.D - 8);
+  const int ms = s * kDcSeg, mq = ms + kFsSub * gq, mmax = p.M - 1;  // M >= 1 here
+  const int nraw = p.num[b];
+  const float pc_lane = p.pc[int64_t(b) * p.M + min(ms + lane, mmax)];
+  const float pnr = fabsf(p.pc[int64_t(b) * p.M + min(ms + lane + 1, mmax)]);
+  const int pa = p.perm[int64_t(b) * p.L + min(ms + lane, mmax)];
+  const int pb = p.perm[int64_t(b) * p.L + min(ms + lane + 1, mmax)];
+  F8::Raw dsr[kFsSub], wr[kFsSub];
+#pragma unroll
+  for (int i = 0; i < kFsSub; ++i) {
+    const int64_t off = int64_t(b) * p.M * p.D + d + int64_t(min(mq + i, mmax)) * p.D;
+    dsr[i] = F8::ld(p.ds, off);
+    wr[i] = F8::ld(p.w, off);
+  }
+  F8::Raw sv[kDcGrp - 1];
+  float sd[kDcGrp - 1];
+#pragma unroll
+  for (int k = 0; k < kDcGrp - 1; ++k) {
+    const int64_t si = int64_t(b) * p.nseg + max(g * kDcGrp + kDcGrp - 1 - k, s);
+    sv[k] = F8::ld(p.segv, si * p.D + d);
+    sd[k] = p.segd[si];
+  }
+  const int n = dc_used_raw(p, nraw);
+  const int cnt = min(kDcSeg, n - ms), cs = min(max(cnt - kFsSub * gq, 0), kFsSub);
+  const float pn = ms + lane + 1 < n ? pnr : 0.f;
+  const float pv = fabsf(pc_lane);
+  float G[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  dw_fold(p.grpv + int64_t(b) * p.ngrp * p.D, p.grpd + int64_t(b) * p.ngrp, p.D, d, p.ngrp - 1, -1,
+          p.ngrp - 1 - g, r, gq, G);
+#pragma unroll
+  for (int k = 0; k < kDcGrp - 1; ++k) {
+    if (k < nsib) {
+      float v[8];
+      F8::cvt(sv[k], v);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) G[c] = fmaf(sd[k], G[c], v[c]);
+    }
+  }
+  const int64_t xb = b * p.dx_sb + d;
+  if (s == p.nseg - 1) {  // rows no byte reads: zero gradient, the groups taking turns
+    const float zero[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int mz = n + gq; mz < p.M; mz += 8)
+      if (live) V::st(p.dx, xb + int64_t(mz) * p.dx_sr, zero);
+  }
+  float mine = 0.f;
+  if (cnt > 0) {
+    float ans[kFsSub], pcs[kFsSub];
+#pragma unroll
+    for (int i = 0; i < kFsSub; ++i) {
+      ans[i] = 1.f - grp8(pn, i, gq);
+      pcs[i] = grp8(pv, i, gq);
+    }
+    // the lane group's chunks from zero, for the carry into each group from the later ones
+    float h[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float A = 1.f;
+#pragma unroll
+    for (int i = kFsSub - 1; i >= 0; --i) {
+      if (i < cs) {
+        float v[8];
+        F8::cvt(dsr[i], v);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) h[c] = fmaf(ans[i], h[c], v[c]);
+        A *= ans[i];
+      }
+    }
+#pragma unroll
+    for (int gg = 7; gg >= 1; --gg) {
+      const int src = 8 * gg + r;
+      const float Ag = __shfl(A, src, 64);
+      float Hg[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) Hg[c] = __shfl(h[c], src, 64);
+      if (gg > gq) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) G[c] = fmaf(Ag, G[c], Hg[c]);
+      }
+    }
+    float dots[kFsSub];
+#pragma unroll
+    for (int i = kFsSub - 1; i >= 0; --i) {
+      dots[i] = 0.f;
+      if (i < cs) {
+        float v[8], wv[8], dx[8];
+        F8::cvt(dsr[i], v);
+        F8::cvt(wr[i], wv);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          G[c] = fmaf(ans[i], G[c], v[c]);
+          dx[c] = pcs[i] * G[c];
+        }
+        if (live) {
+          V::st(p.dx, xb + int64_t(mq + i) * p.dx_sr, dx);
+          float dt = 0.f;
+#pragma unroll
+          for (int c = 0; c < 8; ++c) dt = fmaf(G[c], wv[c], dt);
+          dots[i] = dt;
+        }
+      }
+    }
+    float t4[4], t2[2];
+    const bool b2 = r & 4, b1 = r & 2, b0 = r & 1;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) t4[j] = (b2 ? dots[j + 4] : dots[j]) + __shfl_xor(b2 ? dots[j] : dots[j + 4], 4, 64);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) t2[j] = (b1 ? t4[j + 2] : t4[j]) + __shfl_xor(b1 ? t4[j] : t4[j + 2], 2, 64);
+    mine = (b0 ? t2[1] : t2[0]) + __shfl_xor(b0 ? t2[0] : t2[1], 1, 64);
+  }
+  red[strip][lane] = mine;
+  __syncthreads();
+  if (strip == 0 && lane < cnt) {
+    // chunk ms + lane: dp in strip order, gated by the clamp; its bytes [t0, t1) of d prob
+    float dp = 0.f;
+    for (int k = 0; k < p.nstrips; ++k) dp += red[k][lane];
+    if (pc_lane < 0.f) dp = 0.f;
+    const int t0 = ms + lane == 0 ? 0 : pa;  // no carried value in the backward
+    const int t1 = ms + lane + 1 >= n ? p.L : pb;
+    const int tb = nraw > 0 ? pa : 0;        // the boundary byte (byte 0 of a row without one)
+    for (int t = t0; t < t1; ++t) {
+      const float v = t == tb ? dp : 0.f;
+      const int64_t off = b * p.dp_sb + int64_t(t) * p.dp_sr;
+      if (p.dp_f32) {
+        reinterpret_cast<float*>(p.dprob)[off] = 0.f;
+        reinterpret_cast<float*>(p.dprob)[off + 1] = v;
+      } else {
+        reinterpret_cast<bf16_t*>(p.dprob)[off] = 0;
+        reinterpret_cast<bf16_t*>(p.dprob)[off + 1] = f2bf(v);
+      }
+    }
   }
 }
 
@@ -1332,7 +1518,7 @@ size_t dechunk_workspace_bytes(const mote_dechunk_args* a) {
 size_t dechunk_bwd_workspace_bytes(const mote_dechunk_bwd_args* a) {
   if (a->B <= 0 || a->D <= 0) return 0;
   const size_t ng = size_t(a->B) * dc_ngrp(a->M), ns = ng * kDcGrp;
-  const size_t strips = (a->D + kDcCh - 1) / kDcCh;
+  const size_t strips = (a->D + kFsCh - 1) / kFsCh;  // the narrower strips of the two paths
   return (dc_piece(ns * a->D) + dc_piece(ns) + dc_piece(ng * a->D) + dc_piece(ng) + dc_piece(size_t(a->B) * a->M) +
           dc_piece(size_t(a->B) * strips * a->M) + dc_piece(size_t(a->B) * a->M * a->D)) *
          sizeof(float);
@@ -1366,7 +1552,7 @@ int launch_dechunk_fwd(const mote_dechunk_args* a, hipStream_t stream) {
     return set_error(MOTE_ERR_WORKSPACE, "dechunk_fwd: workspace too small");
   DechunkParams p = {};
   p.x = a->hidden; p.x_sb = a->h_sb; p.x_sr = a->h_sr; p.prob = a->prob; p.p_sb = a->p_sb; p.p_sr = a->p_sr;
-  p.perm = a->perm; p.num = a->num; p.init = a->init; p.out = a->out; p.o_sb = a->o_sb; p.o_sr = a->o_sr;
+  p.perm = a->perm; p.num = a->num; p.cum = a->cum; p.init = a->init; p.out = a->out; p.o_sb = a->o_sb; p.o_sr = a->o_sr;
   p.w = a->w; p.B = a->B; p.L = a->L; p.M = a->M; p.D = a->D; p.eps = a->eps;
   p.p_f32 = a->prob_dtype == MOTE_F32;
   p.ngrp = dc_ngrp(a->M);
@@ -1377,23 +1563,33 @@ int launch_dechunk_fwd(const mote_dechunk_args* a, hipStream_t stream) {
   p.pc = p.grpd + dc_piece(size_t(a->B) * p.ngrp);
   p.segv = p.pc + dc_piece(size_t(a->B) * a->M);
   p.segd = p.segv + dc_piece(size_t(a->B) * p.nseg * a->D);
-  const dim3 grid(p.nstrips, p.ngrp, a->B), wgrid(p.nstrips, p.nseg, a->B);
+  const dim3 grid(p.nstrips, p.ngrp, a->B);
   const dim3 block(64 * kDcGrp);
   const int es = es_of(a->dtype);
   const bool vec = a->D % 8 == 0 && al16(a->hidden, a->h_sb, a->h_sr, es) && al16(a->out, a->o_sb, a->o_sr, es) &&
                    reinterpret_cast<uintptr_t>(a->init) % 16 == 0 && reinterpret_cast<uintptr_t>(a->w) % 16 == 0;
+  if (vec) {  // 64-channel strips
+    DechunkParams f = p;
+    f.nstrips = (a->D + kFsCh - 1) / kFsCh;
+    const dim3 g1(f.nstrips, f.ngrp, a->B), g2(f.nstrips, f.nseg, a->B);
+    if (a->dtype == MOTE_F32) hipLaunchKernelGGL(dechunk_grp_w_kernel<true>, g1, dim3(64 * kDcGrp), 0, stream, f);
+    else hipLaunchKernelGGL(dechunk_grp_w_kernel<false>, g1, dim3(64 * kDcGrp), 0, stream, f);
+    rc = check_launch("dechunk_fwd/segments");
+    if (rc) return rc;
+    if (a->dtype == MOTE_F32) hipLaunchKernelGGL(dechunk_out_w_kernel<true>, g2, dim3(64), 0, stream, f);
+    else hipLaunchKernelGGL(dechunk_out_w_kernel<false>, g2, dim3(64), 0, stream, f);
+    return check_launch("dechunk_fwd/scan");
+  }
   if (a->dtype == MOTE_F32) {
-    hipLaunchKernelGGL(vec ? dechunk_grp_v_kernel<true> : dechunk_grp_kernel<true>, grid, block, 0, stream, p);
+    hipLaunchKernelGGL(dechunk_grp_kernel<true>, grid, block, 0, stream, p);
     rc = check_launch("dechunk_fwd/segments");
     if (rc) return rc;
-    if (vec) hipLaunchKernelGGL(dechunk_out_v_kernel<true>, wgrid, dim3(64), 0, stream, p);
-    else hipLaunchKernelGGL(dechunk_out_kernel<true>, grid, block, 0, stream, p);
+    hipLaunchKernelGGL(dechunk_out_kernel<true>, grid, block, 0, stream, p);
   } else {
-    hipLaunchKernelGGL(vec ? dechunk_grp_v_kernel<false> : dechunk_grp_kernel<false>, grid, block, 0, stream, p);
+    hipLaunchKernelGGL(dechunk_grp_kernel<false>, grid, block, 0, stream, p);
     rc = check_launch("dechunk_fwd/segments");
     if (rc) return rc;
-    if (vec) hipLaunchKernelGGL(dechunk_out_v_kernel<false>, wgrid, dim3(64), 0, stream, p);
-    else hipLaunchKernelGGL(dechunk_out_kernel<false>, grid, block, 0, stream, p);
+    hipLaunchKernelGGL(dechunk_out_kernel<false>, grid, block, 0, stream, p);
   }
   return check_launch("dechunk_fwd/scan");
 }
@@ -1418,7 +1614,7 @@ int launch_dechunk_bwd(const mote_dechunk_bwd_args* a, hipStream_t stream) {
     return set_error(MOTE_ERR_WORKSPACE, "dechunk_bwd: workspace too small");
   DechunkParams p = {};
   p.x = a->hidden; p.x_sb = a->h_sb; p.x_sr = a->h_sr; p.prob = a->prob; p.p_sb = a->p_sb; p.p_sr = a->p_sr;
-  p.perm = a->perm; p.num = a->num; p.init = nullptr; p.w = const_cast<float*>(a->w);
+  p.perm = a->perm; p.num = a->num; p.cum = a->cum; p.init = nullptr; p.w = const_cast<float*>(a->w);
   p.dout = a->dout; p.g_sb = a->g_sb; p.g_sr = a->g_sr; p.dx = a->dhidden; p.dx_sb = a->dh_sb; p.dx_sr = a->dh_sr;
   p.B = a->B; p.L = a->L; p.M = a->M; p.D = a->D; p.eps = a->eps;
   p.p_f32 = a->prob_dtype == MOTE_F32;
@@ -1432,30 +1628,40 @@ int launch_dechunk_bwd(const mote_dechunk_bwd_args* a, hipStream_t stream) {
   p.grpd = p.grpv + dc_piece(ng * a->D);
   p.pc = p.grpd + dc_piece(ng);
   p.part = p.pc + dc_piece(size_t(a->B) * a->M);
-  p.ds = p.part + dc_piece(size_t(a->B) * p.nstrips * a->M);  // 256-byte aligned (float4 accesses)
+  p.ds = p.part + dc_piece(size_t(a->B) * ((a->D + kFsCh - 1) / kFsCh) * a->M);  // 256-byte aligned
   const dim3 grid(p.nstrips, p.ngrp, a->B);
   const dim3 block(64 * kDcGrp);
   const int64_t crows = int64_t(a->B) * a->M;
   const int vec = (a->D % 8) == 0 && reinterpret_cast<uintptr_t>(a->dout) % 16 == 0 && (a->g_sb * es) % 16 == 0 &&
                   (a->g_sr * es) % 16 == 0 && reinterpret_cast<uintptr_t>(p.ds) % 16 == 0;
+  const bool vg = a->D % 8 == 0 && a->D <= kFsMaxStrips * kFsCh && al16(a->dhidden, a->dh_sb, a->dh_sr, es) &&
+                  reinterpret_cast<uintptr_t>(a->w) % 16 == 0;
+  p.dprob = a->dprob; p.dp_sb = a->dp_sb; p.dp_sr = a->dp_sr; p.dp_f32 = a->dprob_dtype == MOTE_F32;
+  if (vec && vg) {  // balanced chunk sums, then the scan over 64-channel strips
+    const dim3 dgrid(unsigned((a->L + kDsBytes - 1) / kDsBytes), a->B);
+    if (a->dtype == MOTE_F32) hipLaunchKernelGGL(dechunk_dsum_bal_kernel<true>, dgrid, dim3(64), 0, stream, p);
+    else hipLaunchKernelGGL(dechunk_dsum_bal_kernel<false>, dgrid, dim3(64), 0, stream, p);
+    rc = check_launch("dechunk_bwd/chunk sums");
+    if (rc) return rc;
+    DechunkParams f = p;
+    f.nstrips = (a->D + kFsCh - 1) / kFsCh;
+    hipLaunchKernelGGL(dechunk_bwd_grp_w_kernel, dim3(f.nstrips, f.ngrp, a->B), dim3(64 * kDcGrp), 0, stream, f);
+    rc = check_launch("dechunk_bwd/segments");
+    if (rc) return rc;
+    const dim3 sgrid(f.nseg, a->B), sblock(64 * f.nstrips);
+    if (a->dtype == MOTE_F32) hipLaunchKernelGGL(dechunk_bwd_out_w_kernel<true>, sgrid, sblock, 0, stream, f);
+    else hipLaunchKernelGGL(dechunk_bwd_out_w_kernel<false>, sgrid, sblock, 0, stream, f);
+    return check_launch("dechunk_bwd");
+  }
   if (a->dtype == MOTE_F32)
     hipLaunchKernelGGL(dechunk_dsum_kernel<true>, dim3(unsigned((crows + 3) / 4)), dim3(256), 0, stream, p, vec);
   else
     hipLaunchKernelGGL(dechunk_dsum_kernel<false>, dim3(unsigned((crows + 3) / 4)), dim3(256), 0, stream, p, vec);
   rc = check_launch("dechunk_bwd/byte sums");
   if (rc) return rc;
-  const bool vg = a->D % 8 == 0 && a->D <= kDvMaxStrips * kDcCh && al16(a->dhidden, a->dh_sb, a->dh_sr, es) &&
-                  reinterpret_cast<uintptr_t>(a->w) % 16 == 0;
-  hipLaunchKernelGGL(vg ? dechunk_bwd_grp_v_kernel : dechunk_bwd_grp_kernel, grid, block, 0, stream, p);
+  hipLaunchKernelGGL(dechunk_bwd_grp_kernel, grid, block, 0, stream, p);
   rc = check_launch("dechunk_bwd/segments");
   if (rc) return rc;
-  if (vg) {  // phase 2 with d boundary_prob fused: one workgroup of nstrips waves per segment
-    p.dprob = a->dprob; p.dp_sb = a->dp_sb; p.dp_sr = a->dp_sr; p.dp_f32 = a->dprob_dtype == MOTE_F32;
-    const dim3 sgrid(p.nseg, a->B), sblock(64 * p.nstrips);
-    if (a->dtype == MOTE_F32) hipLaunchKernelGGL(dechunk_bwd_out_v_kernel<true>, sgrid, sblock, 0, stream, p);
-    else hipLaunchKernelGGL(dechunk_bwd_out_v_kernel<false>, sgrid, sblock, 0, stream, p);
-    return check_launch("dechunk_bwd");
-  }
   if (a->dtype == MOTE_F32) hipLaunchKernelGGL(dechunk_bwd_out_kernel<true>, grid, block, 0, stream, p);
   else hipLaunchKernelGGL(dechunk_bwd_out_kernel<false>, grid, block, 0, stream, p);
   rc = check_launch("dechunk_bwd");
