@@ -1221,6 +1221,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the C2 / C5 / add+RMSNorm / dechunk lines")
     ap.add_argument("--engine-only", action="store_true",
                     help="only the decode-engine lines (batch 1 and 16, --decode-steps tokens), for profiling")
+    ap.add_argument("--dc-only", action="store_true",
+                    help="only the chunk route / gather / EMA dechunk lines (1 and 8 windows), for profiling")
     ap.add_argument("--kernels-only", choices=("c2", "c3", "c5"), default=None,
                     help="only run one configuration's kernels a few times, for rocprofv3 counter passes")
     ap.add_argument("--summarize-counters", metavar="DIR", default=None,
@@ -1245,6 +1247,9 @@ def main():
     if args.engine_only:
         print(json.dumps({k: bench_decode_engine(b, args.decode_steps, dev) for k, b in (("b1", 1), ("b16", 16))}),
               flush=True)
+        return
+    if args.dc_only:
+        print(json.dumps({"B1": bench_dc(1, dev, copies=8), "B8": bench_dc(8, dev, copies=1)}), flush=True)
         return
     copy_calibration(dev)
     st = bench_stack(args.steps, args.warmup, dev)
