@@ -7,7 +7,7 @@ the largest magnitude in fp32, bf16 outputs within one rounding; the chunk sums 
 bits), and each is deterministic: repeated calls, calls that alternate shapes and replays of a captured
 graph are compared bit for bit. Cases: rows without boundaries, bytes before the first boundary, every
 byte a boundary, a single chunk, one segment, many groups (M above 4096), B > 1, a carried value, fp32
-and bf16, widths 8 to 768 (the backward's vector path stops at 512).
+and bf16, widths 8 to 768 including last strips of 8 channels (the backward's vector path stops at 512).
 """
 
 from __future__ import annotations
@@ -81,6 +81,8 @@ CASES = [
     (1, 16384, 512, 1 / 3.3, True, False),  # the Mote-96M window
     (2, 20000, 512, 0.9, True, False),      # 288 segments, 72 groups: several waits per quarter
     (1, 3000, 768, 1 / 3.3, True, False),   # forward: twelve strips; backward: the two-channel path
+    (2, 2000, 72, 1 / 3.3, True, False),    # a last strip of 8 channels
+    (1, 2500, 200, 1 / 3.3, False, True),   # a last strip of 8 channels, carried value
 ]
 
 
