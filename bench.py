@@ -164,28 +164,34 @@ def run_stage(a, stage: int, stream) -> None:
 
 
 def staged_bwd(p1, p2, info, ibar, lse, g, dy, timers):
-    """The one-pass backward with the key-block kernel bracketed by events (its three launches
-    issued separately through the ABI's `stages` field)."""
+    """The one-pass backward issued stage by stage through the ABI's `stages` field, with events
+    around the key + query work: rows; keys and queries in one call (the fused launch, after the
+    small clear of its control words that a call without the rows stage adds); finish. Then the same
+    backward again in the two-launch form (keys, then queries, each bracketed), for comparison."""
     from mote_amd import _lib as Lb
 
     a, (dp1, dp2, dinfo, dlam, ws) = bwd_stage_args(p1, p2, info, ibar, lse, g, dy)
     st = Lb.stream_of(p1)
-    a.stages = Lb.MOTE_BWD_ROWS
-    Lb.check(Lb.lib().mote_relation_bwd(a, st), "bwd rows")
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
-    ev[0].record()
-    a.stages = Lb.MOTE_BWD_KEYS
-    Lb.check(Lb.lib().mote_relation_bwd(a, st), "bwd keys")
-    ev[1].record()
-    a.stages = Lb.MOTE_BWD_QUERIES
-    Lb.check(Lb.lib().mote_relation_bwd(a, st), "bwd queries")
-    ev[2].record()
-    timers["bwd_keys"][0].append(ev[0])
-    timers["bwd_keys"][1].append(ev[1])
-    timers["bwd_queries"][0].append(ev[1])
-    timers["bwd_queries"][1].append(ev[2])
-    a.stages = Lb.MOTE_BWD_FINISH
-    Lb.check(Lb.lib().mote_relation_bwd(a, st), "bwd finish")
+
+    def stage(bits, what):
+        a.stages = bits
+        Lb.check(Lb.lib().mote_relation_bwd(a, st), what)
+
+    def timed(key, bits, what):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        stage(bits, what)
+        e1.record()
+        timers[key][0].append(e0)
+        timers[key][1].append(e1)
+
+    stage(Lb.MOTE_BWD_ROWS, "bwd rows")
+    timed("bwd_kq", Lb.MOTE_BWD_KEYS | Lb.MOTE_BWD_QUERIES, "bwd keys + queries")
+    stage(Lb.MOTE_BWD_FINISH, "bwd finish")
+    stage(Lb.MOTE_BWD_ROWS, "bwd rows")
+    timed("bwd_keys", Lb.MOTE_BWD_KEYS, "bwd keys")
+    timed("bwd_queries", Lb.MOTE_BWD_QUERIES, "bwd queries")
+    stage(Lb.MOTE_BWD_FINISH, "bwd finish")
     return dp1, dp2, dinfo, dlam
 
 
@@ -207,25 +213,28 @@ def bench_stack(steps: int, warmup: int, dev):
     ms = t0.elapsed_time(t1) / steps
     flops = N_LAYERS * 7.0 * N_HEADS * D_HEAD * T * T
     # kernel-level timing pass (same work, stages bracketed by events)
-    timers = {"fwd": ([], []), "bwd_keys": ([], []), "bwd_queries": ([], [])}
+    timers = {"fwd": ([], []), "bwd_kq": ([], []), "bwd_keys": ([], []), "bwd_queries": ([], [])}
     for _ in range(max(1, min(steps, 3))):
         stack_step(inp, timers)
     torch.cuda.synchronize()
     clock = stack_clock(inp, ms)
     avg = {k: sum(a.elapsed_time(b) for a, b in zip(*v)) / len(v[0]) for k, v in timers.items()}
-    # per-kernel work (units of H*dh*T^2, one per causal product): forward U and P I~ (2); key kernel
-    # U, dW, dV, dK (4); query kernel dQ (1), which reads the key kernel's dU^T tiles and is HBM-bound
+    # per-kernel work (units of H*dh*T^2, one per causal product): forward U and P I~ (2); the fused
+    # key + query launch U, dW, dV, dK and dQ (5); in the two-launch form the key kernel's 4 and the
+    # query kernel's dQ (1), which reads the key kernel's dU^T tiles and is HBM-bound
     unit = N_HEADS * D_HEAD * T * T
     dq_bytes = dq_kernel_bytes(T)
     res = dict(T=T, ms_per_step=ms, wall_s=wall, tflops=flops / (ms * 1e-3) / 1e12, flops_per_step=flops,
+               kq_ms=avg["bwd_kq"], kq_tflops=5.0 * unit / (avg["bwd_kq"] * 1e-3) / 1e12,
                keys_ms=avg["bwd_keys"], queries_ms=avg["bwd_queries"], fwd_ms=avg["fwd"],
                keys_tflops=4.0 * unit / (avg["bwd_keys"] * 1e-3) / 1e12,
                queries_tflops=1.0 * unit / (avg["bwd_queries"] * 1e-3) / 1e12,
                queries_bytes=dq_bytes, queries_gbs=dq_bytes / (avg["bwd_queries"] * 1e-3) / 1e9,
                fwd_tflops=2.0 * unit / (avg["fwd"] * 1e-3) / 1e12, clock=clock, dut=dut_residency(inp))
     log(f"[bench] stack: {ms:.3f} ms/step = {res['tflops']:.1f} TFLOP/s; fwd kernel {avg['fwd']*1e3:.1f} us "
-        f"({res['fwd_tflops']:.1f} TF/s), bwd key kernel {avg['bwd_keys']*1e3:.1f} us ({res['keys_tflops']:.1f} TF/s), "
-        f"bwd dQ kernel {avg['bwd_queries']*1e3:.1f} us ({res['queries_gbs']:.0f} GB/s of dU^T tiles + P2 + dP1); "
+        f"({res['fwd_tflops']:.1f} TF/s), bwd key + query launch {avg['bwd_kq']*1e3:.1f} us ({res['kq_tflops']:.1f} TF/s); "
+        f"two-launch form: key kernel {avg['bwd_keys']*1e3:.1f} us ({res['keys_tflops']:.1f} TF/s), "
+        f"dQ kernel {avg['bwd_queries']*1e3:.1f} us ({res['queries_gbs']:.0f} GB/s of dU^T tiles + P2 + dP1); "
         f"shader clock during a step {clock['sclk_mhz']} MHz {clock['sclk_mhz_runs']}; dQ kernel {res['dut']['dq_us_hot']} us right after the key kernel, "
         f"{res['dut']['dq_us_after_sweep']} us after a {res['dut']['sweep_MiB']} MiB sweep")
     return res
@@ -387,6 +396,7 @@ def copy_calibration(dev, mib: int = 1024):
 # while these files are unchanged since it was measured (their fingerprint is recorded beside it).
 _COMMON = ("common.hpp", "params.hpp")
 KERNEL_SOURCES = {
+    "bwd_kvq_kernel": ("relation_bwd_tiles.hip", "tiles.hpp", "bwd.hpp") + _COMMON,
     "bwd_kv_kernel": ("relation_bwd_tiles.hip", "tiles.hpp", "bwd.hpp") + _COMMON,
     "bwd_dq_kernel": ("relation_bwd_tiles.hip", "tiles.hpp", "bwd.hpp") + _COMMON,
     "relation_fwd_tile_kernel": ("relation_fwd.hip", "tiles.hpp") + _COMMON,
@@ -1283,16 +1293,21 @@ def main():
         "config": {"workload": "Mote-96M Relation stack fwd+bwd (12 layers, B=1, 16384-byte window)",
                    "T_chunks": st["T"], "heads": N_HEADS, "d_head": D_HEAD, "layers": N_LAYERS,
                    "flop_convention": "7*H*dh*T^2 per layer (causal; fwd 2x, bwd 5x)"},
-        "roofline": {"kernel": "bwd_kv_kernel (key-stationary backward: U, dW, dV, dK)", "bound": "mfma",
-                     "achieved": round(st["keys_tflops"], 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(st["keys_tflops"] / PEAK_BF16_TFLOPS, 4), **_traffic("bwd_kv_kernel"),
-                     "counters": measured_counters("bwd_kv_kernel@c3"),
-                     "flop_per_launch": 4.0 * N_HEADS * D_HEAD * st["T"] ** 2, "avg_launch_ms": round(st["keys_ms"], 4)},
-        "roofline_bwd_dq": {"kernel": "bwd_dq_kernel (query-stationary dQ from the stored dU^T tiles)", "bound": "hbm",
-                            "achieved": round(st["queries_gbs"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                            "frac": round(st["queries_gbs"] / PEAK_HBM_GBS, 4),
-                            **_traffic("bwd_dq_kernel"), "counters": measured_counters("bwd_dq_kernel@c3"),
-                            "bytes_per_launch": st["queries_bytes"], "avg_launch_ms": round(st["queries_ms"], 4)},
+        "roofline": {"kernel": "bwd_kvq_kernel (backward key + query work in one launch: U, dW, dV, dK, dQ)",
+                     "bound": "mfma", "achieved": round(st["kq_tflops"], 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(st["kq_tflops"] / PEAK_BF16_TFLOPS, 4), **_traffic("bwd_kvq_kernel"),
+                     "counters": measured_counters("bwd_kvq_kernel@c3"),
+                     "flop_per_launch": 5.0 * N_HEADS * D_HEAD * st["T"] ** 2, "avg_launch_ms": round(st["kq_ms"], 4),
+                     "timed_with": "the clear of the launch's control words (one small kernel) inside the events"},
+        "two_launch_form": {
+            "bwd_kv_kernel": {"bound": "mfma", "achieved": round(st["keys_tflops"], 2), "unit": "TFLOP/s",
+                              "frac": round(st["keys_tflops"] / PEAK_BF16_TFLOPS, 4),
+                              "flop_per_launch": 4.0 * N_HEADS * D_HEAD * st["T"] ** 2,
+                              "avg_launch_ms": round(st["keys_ms"], 4), **_traffic("bwd_kv_kernel")},
+            "bwd_dq_kernel": {"bound": "hbm", "achieved": round(st["queries_gbs"], 1), "unit": "GB/s",
+                              "frac": round(st["queries_gbs"] / PEAK_HBM_GBS, 4), "bytes_per_launch": st["queries_bytes"],
+                              "avg_launch_ms": round(st["queries_ms"], 4), **_traffic("bwd_dq_kernel")},
+            "note": "the same backward as two launches (MOTE_BWD_SPLIT=1 or separate key / query stages)"},
         "roofline_fwd": {"kernel": "relation_fwd_tile_kernel", "bound": "mfma", "achieved": round(st["fwd_tflops"], 2),
                          "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(st["fwd_tflops"] / PEAK_BF16_TFLOPS, 4),

@@ -30,11 +30,22 @@ struct BwdParams {
   float* dlam_part;  // [BH][TQp / 64]
   void* dut;     // [BH][npairs][4 waves][2 query tiles][64 lanes][8] bf16: dU as the key kernel's waves hold it (tile kernels)
   int64_t npairs;    // (query block, key block) pairs per (batch, head), PairTable::total
+  int* kvq;      // control words of the fused key + query launch, or null: the two launches (tile kernels)
+  int kvq_nq;    // its queues: 8, 4, 2 or 1, dividing B H
   int B, H, TQ, TK, D, q_start, TQp;
   float scale, tau_inv;
 };
 
 constexpr int kRowBlock = 64;  // rows per workgroup in the rows stage; also TQp's granularity
+
+// Layout of the fused key + query launch's control words (BwdParams::kvq, cleared by the rows stage
+// with agent-scope stores): up to 8 job counters (one per queue, 128 bytes apart), the overrun flag
+// (a bounded wait gave up) and the per (batch x head, query block) counts of stored dU quadrants, four
+// per (query block, key block) pair.
+constexpr int kKvqJob = 0, kKvqJobStride = 32, kKvqOverrun = 256, kKvqCounts = 288;
+constexpr int kKvqSpinLimit = 1 << 20;  // polls of a count before the wait gives up (seconds)
+
+int device_cu_count();  // compute units of the current device (relation_bwd_tiles.hip)
 
 // The (query block, key block) pairs of 64 x 64 that hold a visible element (key position below the
 // query position): query block qb sees key blocks [0, nkb(qb)). Every block but the last holds 64

@@ -59,6 +59,17 @@ __global__ void __launch_bounds__(256) bwd_rows_kernel(const BwdParams p) {
   const T* yb = reinterpret_cast<const T*>(p.dy) + b * p.y_sb + h * p.y_sh;
   T* wq = LEAN ? nullptr : reinterpret_cast<T*>(p.wq) + (int64_t(bh) * p.TQp + i0) * DP;
   T* wd = reinterpret_cast<T*>(p.wdib) + (int64_t(bh) * p.TQp + i0) * DP;
+  // the fused key + query launch's control words: this block's count, and block (0, 0) the job
+  // counter and the overrun flag (agent-scope stores, as that launch reads and adds them)
+  if (LEAN && p.kvq && tid == 0) {
+    const int nqb = p.TQp / kRowBlock;
+    __hip_atomic_store(p.kvq + kKvqCounts + bh * nqb + blockIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (blockIdx.x == 0 && bh == 0) {
+      for (int q = 0; q < 8; ++q)
+        __hip_atomic_store(p.kvq + kKvqJob + q * kKvqJobStride, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(p.kvq + kKvqOverrun, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
 
   // pass 1: 16-byte chunks; per-chunk partial dot products, dI-bar and the row-major copies
   Chunk kreg[CT];
@@ -714,10 +725,24 @@ __global__ void __launch_bounds__(256) bwd_dlam_kernel(const float* part, int n,
 // host side
 // ------------------------------------------------------------------------------------------------
 struct WsLayout {
-  size_t wq, wdib, wqT, wdibT, lse2, cvec, stat, dut, duii, dp1acc, dlam_part, total;
+  size_t wq, wdib, wqT, wdibT, lse2, cvec, stat, dut, kvq, duii, dp1acc, dlam_part, total;
 };
 
 static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// Whether the tile path's key and query work share one launch (bwd_kvq_kernel). By default when the
+// key work alone fills the GPU's workgroup slots (key blocks x batch x heads >= two per CU): then the
+// query work runs in the slots the key work's tail leaves (C3, 624 key jobs: 162 against 175 us;
+// B H = 16 at 2048 rows: 70 against 77 us); with fewer key jobs the query jobs start early and wait,
+// and the two launches are as fast or faster (2-3 K rows at B H = 8: +1-2 %). The environment
+// variable MOTE_BWD_FUSED overrides: 0 never, 1 wherever the launch applies. It is read on every
+// call (a few hundred ns against tens of microseconds of launches).
+static bool fused_bwd_wanted(const mote_relation_bwd_args* a) {
+  const char* e = getenv("MOTE_BWD_FUSED");
+  if (e && e[0] == '0') return false;
+  if (e && e[0] == '1') return true;
+  return int64_t((a->TK + 63) / 64) * a->B * a->H >= 2 * int64_t(device_cu_count());
+}
 
 // bf16 with a head dim the tile kernels are compiled for: the atomic-free tile path.
 static bool use_tiles(const mote_relation_bwd_args* a) {
@@ -737,6 +762,7 @@ static WsLayout ws_layout(const mote_relation_bwd_args* a) {
     w.stat = o; o = align256(o + BH * (TQp / kRowBlock) * 128 * 4);
     // dU fragments: 8 KB per visible (query block, key block) pair
     w.dut = o; o = align256(o + BH * size_t(PairTable::total(a->TQ, a->q_start)) * 8192);
+    w.kvq = o; o = align256(o + (kKvqCounts + BH * (TQp / kRowBlock)) * 4);
   } else {
     w.wq = o; o = align256(o + BH * TQp * DP * es);
     w.wqT = o; o = align256(o + BH * TQp * DP * es);
@@ -836,6 +862,13 @@ int launch_bwd(const mote_relation_bwd_args* a, hipStream_t stream) {
     p.stat = reinterpret_cast<float*>(ws + w.stat);
     p.dut = ws + w.dut;
     p.npairs = PairTable::total(a->TQ, a->q_start);
+    // the fused key + query launch: head dims with two workgroups per CU, one (batch x head)'s pairs
+    // addressable by a 32-bit buffer offset
+    if (padded_dim(a->D) <= 96 && p.npairs * 8192 < (int64_t(1) << 31) && fused_bwd_wanted(a)) {
+      p.kvq = reinterpret_cast<int*>(ws + w.kvq);
+      const int BH = a->B * a->H;
+      p.kvq_nq = BH % 8 == 0 ? 8 : BH % 4 == 0 ? 4 : BH % 2 == 0 ? 2 : 1;
+    }
   } else {
     p.wq = ws + w.wq; p.wqT = ws + w.wqT; p.wdibT = ws + w.wdibT;
     p.lse2 = reinterpret_cast<float*>(ws + w.lse2);

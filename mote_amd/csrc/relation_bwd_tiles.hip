@@ -26,6 +26,7 @@
 // LDS reads, of the staged P2 tile and of the staged dU fragments; no elementwise work and no
 // recomputed products. The
 // key-half waves add through LDS; the Self part dU_ii P2_i joins before the store.
+#include <atomic>
 #include <type_traits>
 #include <utility>
 
@@ -68,14 +69,39 @@ __device__ __forceinline__ void store_dut_zero(bf16_t* dst, int lane) {
   for (int kt = 0; kt < 2; ++kt) *reinterpret_cast<bf16x8*>(dst + kt * 512 + lane * 8) = bf16x8{};
 }
 
+// The fused launch (bwd_kvq_kernel) stores dU write-through: buffer stores with the SC1 cache-policy
+// bit (agent scope), so once the storing wave's s_waitcnt has seen them complete they are at the
+// device-coherent level, where the query work of any XCD reads them with SC1 loads (no stale line of
+// its own L2). Byte offsets past the buffer's range are dropped by the hardware.
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
+constexpr int kCpolSc1 = 16;          // cache-policy operand of the buffer builtins: SC1
+constexpr int kBufWord3 = 0x00020000; // buffer resource word 3 of the gfx9 family: 32-bit data format
+
+__device__ __forceinline__ void store16_wt(__amdgpu_buffer_rsrc_t rs, uint32_t off, const bf16x8& v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rs, off, 0, kCpolSc1);
+}
+
+// store_dut / store_dut_zero through the write-through stores; `off` = byte offset of the wave's 2 KB
+__device__ __forceinline__ void store_dut_wt(const Elem<bf16_t>::Frag (&au)[2], __amdgpu_buffer_rsrc_t rs, uint32_t off,
+                                             int lane) {
+  const uint32_t o = off + uint32_t(dut_pos(lane)) * 16u;
+  store16_wt(rs, o, au[0].v);
+  store16_wt(rs, o + 1024u, au[1].v);
+}
+
+__device__ __forceinline__ void store_dut_zero_wt(__amdgpu_buffer_rsrc_t rs, uint32_t off, int lane) {
+  store16_wt(rs, off + uint32_t(lane) * 16u, bf16x8{});
+  store16_wt(rs, off + 1024u + uint32_t(lane) * 16u, bf16x8{});
+}
+
 // ------------------------------------------------------------------------------------------------
 // key-stationary kernel: dP2 and dI~
 // ------------------------------------------------------------------------------------------------
-template <int DP, bool MASKED>
+template <int DP, bool MASKED, bool WT>
 __device__ __forceinline__ void kv_block(const bf16_t* Qs, const bf16_t* Ds, const float* Ss, const bf16_t* Ks,
                                          const bf16_t* Vs, f32x4 (&dvacc)[2][DP / 16], f32x4 (&dkacc)[2][DP / 16],
-                                         bf16_t* dut_w, int qh, int kh, int li, int lg, int key0, int qa0,
-                                         float nc2) {
+                                         bf16_t* dut_w, __amdgpu_buffer_rsrc_t rs, uint32_t dut_b, int qh, int kh,
+                                         int li, int lg, int key0, int qa0, float nc2) {
   using E = Elem<bf16_t>;
   using Frag = E::Frag;
   constexpr int KS = DP / 32, DT = DP / 16;
@@ -161,26 +187,36 @@ __device__ __forceinline__ void kv_block(const bf16_t* Qs, const bf16_t* Ds, con
   // both key tiles' dU in two 16-byte stores per lane (two 8-byte stores per key tile, made as each
   // tile finishes, ran the key kernel 20 % slower; the transpose into the dQ product's B layout by
   // identity products here ran the key kernel 2 % slower than the transposed reads in the dQ kernel)
-  if (dut_w) store_dut(au, dut_w, lane_of(li, lg));
+  if (dut_w) {
+    if constexpr (WT)
+      store_dut_wt(au, rs, dut_b, lane_of(li, lg));
+    else
+      store_dut(au, dut_w, lane_of(li, lg));
+  }
 }
 
 template <int DP>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP <= 96 ? 2 : 1)))
-bwd_kv_kernel(const BwdParams p) {
+struct KvShape {
+  static constexpr int TILE = 64 * DP;
+  static constexpr int STAGE = 2 * TILE + 256;     // bf16 slots per stage: Q tile, dI-bar tile, 128 fp32 stats
+  static constexpr int LDS = 2 * STAGE + 2 * TILE;  // two stages, then the job's 64 P2 rows and 64 I~ rows
+};
+
+// The key work of one (batch x head) bh and key block kb: 64 keys, 4 waves. FUSED (the fused launch):
+// the query blocks are walked from the last down, so the pairs of the longest query blocks are stored
+// first, and the dU quadrants of each query block are counted in the kvq counts once stored.
+template <int DP, bool FUSED>
+__device__ __forceinline__ void kv_job(const BwdParams& p, const int bh, const int kb, bf16_t* smem) {
   using E = Elem<bf16_t>;
   using Frag = E::Frag;
-  constexpr int KS = DP / 32, DT = DP / 16, CPR = DP / 8, TILE = 64 * DP;
-  constexpr int STAGE = 2 * TILE + 256;  // bf16 slots per stage: Q tile, dI-bar tile, 128 fp32 stats
-  __shared__ __align__(16) bf16_t smem[2 * STAGE];
-  __shared__ __align__(16) bf16_t kvs[2 * TILE];  // the workgroup's 64 P2 rows, then its 64 I~ rows
+  using S = KvShape<DP>;
+  constexpr int DT = DP / 16, CPR = DP / 8, TILE = S::TILE, STAGE = S::STAGE;
+  bf16_t* kvs = smem + 2 * STAGE;  // the job's 64 P2 rows, then its 64 I~ rows
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: staging in scalar registers
   const int li = lane & 15, lg = lane >> 4;
   const int kh = wave & 1, qh = wave >> 1;
-  const int BH = p.B * p.H;
-  const int bh = blockIdx.x % BH;
-  const int kb = blockIdx.x / BH;  // key block 0 sees the most queries: longest first
   const int b = bh / p.H, h = bh % p.H;
   const int k0 = kb * 64;
   const int nqb = p.TQp / 64;
@@ -213,13 +249,19 @@ bwd_kv_kernel(const BwdParams p) {
   };
 
   const float nc2 = -p.scale * kLog2e;
-  const int qb_lo = max(0, k0 + 1 - p.q_start) / 64;
-  // PairTable::offset(qb) for the block in hand, advanced by qb + A per block (offset(qb + 1) - offset(qb))
+  const int qb_lo = max(0, k0 + 1 - p.q_start) / 64;  // the first query block that sees a key of the block
+  const int qb_first = FUSED ? nqb - 1 : qb_lo;        // the walk's first block
+  // PairTable::offset(qb) for the block in hand, moved by qb + A per block (offset(qb + 1) - offset(qb))
   const int pair_a = (p.q_start + 126) / 64;
-  int64_t pair_off = PairTable::offset(qb_lo, p.q_start);
+  int64_t pair_off = PairTable::offset(qb_first, p.q_start);
   // dU of this key block: pair (qb, kb) at PairTable::offset(qb) + kb, 8 KB per pair; wave (kh, qh)
   // writes its 2 KB at (kh * 4 + 2 qh) * 512 elements (store_dut)
-  bf16_t* dut_bh = reinterpret_cast<bf16_t*>(p.dut) + int64_t(bh) * p.npairs * 4096 + (kh * 4 + 2 * qh) * 512;
+  const int wq_off = (kh * 4 + 2 * qh) * 512;
+  bf16_t* dut_bh = reinterpret_cast<bf16_t*>(p.dut) + int64_t(bh) * p.npairs * 4096 + wq_off;
+  // FUSED: the (batch x head)'s pairs as one buffer (the host keeps it below 2^31 bytes)
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      reinterpret_cast<bf16_t*>(p.dut) + int64_t(bh) * p.npairs * 4096, 0, int(p.npairs * 8192), kBufWord3);
+  int* const cnt = FUSED ? p.kvq + kKvqCounts + bh * nqb : nullptr;
   {
     // the key rows once (rows past the keys: finite copies whose results are never stored)
     const bf16_t* ksrc[2] = {kbase, vbase};
@@ -228,47 +270,91 @@ bwd_kv_kernel(const BwdParams p) {
     kst.init(wave, lane, kstr);
     kst.issue(kvs, ksrc, kstr, k0, p.TK - 1, wave, lane);
   }
-  if (qb_lo < nqb) issue(qb_lo, 0);
+  if (qb_lo < nqb) issue(qb_first, 0);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  // Diagonal query blocks (some key not before some query) first, with the masked block math, then
-  // the rest with the unmasked math: two loops instead of a branch keeps one register assignment
-  // of the accumulators per loop.
+  // FUSED: the count of a block's four dU quadrants is one atomic add by wave 0, issued right after
+  // the transfers two blocks later: the waits of the next two blocks leave it in flight, so it costs
+  // no wait of its own (an add waited for at the end of the next block, against the transfers, ran
+  // the key work 20 % slower). `prev`: the block of the previous step (its stores in flight);
+  // `ready`: the block before (every wave's stores seen complete before the previous barrier).
+  int prev = -1, ready = -1;
+  // Diagonal query blocks (some key not before some query) with the masked block math, the rest
+  // with the unmasked math: two loops instead of a branch keeps one register assignment of the
+  // accumulators per loop.
   auto step = [&](int qb, auto masked) {
-    MOTE_STAMP(0, qb - qb_lo);
-    const int stage = (qb - qb_lo) & 1;
-    if (qb + 1 < nqb) issue(qb + 1, stage ^ 1);
-    MOTE_STAMP(1, qb - qb_lo);
+    const int n = FUSED ? nqb - 1 - qb : qb - qb_lo;  // position in the walk
+    MOTE_STAMP(0, n);
+    const int stage = n & 1;
+    const int qn = FUSED ? qb - 1 : qb + 1;  // the walk's next block
+    if (FUSED ? qn >= qb_lo : qn < nqb) issue(qn, stage ^ 1);
+    bool sig = false;  // wave 0 added a count after the transfers (one more operation in flight)
+    if constexpr (FUSED) {
+      sig = wave == 0 && ready >= 0;
+      asm volatile("" ::: "memory");  // the add after the transfers, in issue order
+      if (sig && lane == 0) __hip_atomic_fetch_add(cnt + ready, 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    MOTE_STAMP(1, n);
     const bf16_t* Qs = smem + stage * STAGE;
     const bf16_t* Ds = Qs + TILE;
     const float* Ss = reinterpret_cast<const float*>(Qs + 2 * TILE);
     const int i0 = qb * 64 + 32 * qh;   // the wave's first query row
     const int qa0 = p.q_start + i0;     // its position
-    bf16_t* dut_w = kb < PairTable::nkb(qb, p.TQ, p.q_start) ? dut_bh + (pair_off + kb) * 4096 : nullptr;
-    pair_off += qb + pair_a;  // PairTable::offset(qb + 1)
+    const bool pair = kb < PairTable::nkb(qb, p.TQ, p.q_start);
+    bf16_t* dut_w = pair ? dut_bh + (pair_off + kb) * 4096 : nullptr;
+    const uint32_t dut_b = uint32_t(pair_off + kb) * 8192u + uint32_t(wq_off) * 2u;
+    pair_off += FUSED ? -int64_t(qb - 1 + pair_a) : int64_t(qb + pair_a);  // PairTable::offset(qn)
     // quadrant visible at all (some key < some query position), and not wholly padding rows
     if (i0 < p.TQ && key0 < qa0 + 31)
-      kv_block<DP, decltype(masked)::value>(Qs, Ds, Ss, kvs, kvs + TILE, dvacc, dkacc, dut_w, qh, kh, li, lg,
-                                            key0, qa0, nc2);
-    else if (dut_w)
-      store_dut_zero(dut_w, lane);
-    MOTE_STAMP(2, qb - qb_lo);
-    // The next block's transfers were issued before this block's two dU^T stores, and vector-memory
-    // operations retire in issue order: waiting until at most the two stores are outstanding means the
-    // transfers have landed, while the stores stay in flight across the barrier.
-    if (dut_w)
-      __builtin_amdgcn_s_waitcnt(kVmWaitStage<2>());
-    else
-      __builtin_amdgcn_s_waitcnt(kVmWaitStage<0>());
-    MOTE_STAMP(3, qb - qb_lo);
+      kv_block<DP, decltype(masked)::value, FUSED>(Qs, Ds, Ss, kvs, kvs + TILE, dvacc, dkacc, dut_w, rs, dut_b, qh,
+                                                   kh, li, lg, key0, qa0, nc2);
+    else if (dut_w) {
+      if constexpr (FUSED)
+        store_dut_zero_wt(rs, dut_b, lane);
+      else
+        store_dut_zero(dut_w, lane);
+    }
+    MOTE_STAMP(2, n);
+    // The next block's transfers were issued before this block's two dU^T stores (and the count's
+    // add), and vector-memory operations retire in issue order: waiting until at most those are
+    // outstanding means the transfers have landed, while the stores stay in flight across the
+    // barrier. Everything issued before the transfers has completed too: the previous block's stores.
+    if (dut_w) {
+      if (sig)
+        __builtin_amdgcn_s_waitcnt(kVmWaitStage<3>());
+      else
+        __builtin_amdgcn_s_waitcnt(kVmWaitStage<2>());
+    } else {
+      if (sig)
+        __builtin_amdgcn_s_waitcnt(kVmWaitStage<1>());
+      else
+        __builtin_amdgcn_s_waitcnt(kVmWaitStage<0>());
+    }
+    MOTE_STAMP(3, n);
     lds_barrier();
-    MOTE_STAMP(4, qb - qb_lo);
+    MOTE_STAMP(4, n);
+    if constexpr (FUSED) {
+      ready = prev;
+      prev = pair ? qb : -1;
+    }
   };
   // unmasked for every wave once the block's first query position exceeds the last key
   const int qb_m = min(nqb, max(qb_lo, k0 + 63 - p.q_start >= 0 ? (k0 + 63 - p.q_start) / 64 + 1 : 0));
-  int qb = qb_lo;
-  for (; qb < qb_m; ++qb) step(qb, std::true_type{});
-  for (; qb < nqb; ++qb) step(qb, std::false_type{});
+  if constexpr (FUSED) {
+    for (int qb = nqb - 1; qb >= qb_m; --qb) step(qb, std::false_type{});
+    for (int qb = qb_m - 1; qb >= qb_lo; --qb) step(qb, std::true_type{});
+    // the last two blocks: every wave's stores complete, then their counts
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (wave == 0 && lane == 0) {
+      if (ready >= 0) __hip_atomic_fetch_add(cnt + ready, 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (prev >= 0) __hip_atomic_fetch_add(cnt + prev, 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  } else {
+    int qb = qb_lo;
+    for (; qb < qb_m; ++qb) step(qb, std::true_type{});
+    for (; qb < nqb; ++qb) step(qb, std::false_type{});
+  }
 
   // add the two query halves through LDS: R[0] = dV, R[1] = dK, [64 keys][DP] fp32
   float* R = reinterpret_cast<float*>(smem);
@@ -335,6 +421,14 @@ bwd_kv_kernel(const BwdParams p) {
   }
 }
 
+template <int DP>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP <= 96 ? 2 : 1)))
+bwd_kv_kernel(const BwdParams p) {
+  __shared__ __align__(16) bf16_t smem[KvShape<DP>::LDS];
+  const int BH = p.B * p.H;
+  kv_job<DP, false>(p, blockIdx.x % BH, blockIdx.x / BH, smem);  // key block 0 sees the most queries: longest first
+}
+
 // ------------------------------------------------------------------------------------------------
 // query-stationary kernel: dP1 = (dU P2 + dU_ii P2_i) / sqrt(D) from the stored dU fragments
 // ------------------------------------------------------------------------------------------------
@@ -348,34 +442,41 @@ bwd_kv_kernel(const BwdParams p) {
 // index is a constant). Query blocks pair from the top (the two longest together, longest pairs
 // first); the earlier block of a pair sees at most one key block fewer, and with an odd count the
 // lowest pair has one block. The key halves add through LDS before the Self term and the stores.
-template <int DP>
-__global__ void __launch_bounds__(512) bwd_dq_kernel(const BwdParams p) {
+// The fused launch runs the same work as a four-wave job of one query block (NW = 4), after a wait
+// for the counts of its pairs' dU quadrants, reading the quadrants with SC1 loads.
+template <int DP, int NW>
+struct DqShape {
+  static constexpr int NQB = NW / 4;                // query blocks per job
+  static constexpr int TILE = 64 * DP;
+  static constexpr int SLOT = TILE + NQB * 4096;    // bf16 per ring slot: the P2 tile, then each query block's 8 fragments
+  static constexpr int NS = NW == 8 ? 4 : 3;        // ring slots: key blocks issued ahead + 1 (five measured slower)
+  static constexpr int LDS = NS * SLOT;
+};
+
+template <int DP, int NW, bool FUSED>
+__device__ __forceinline__ void dq_job(const BwdParams& p, const int bh, const int qtop, bf16_t* ring) {
   using E = Elem<bf16_t>;
   using Frag = E::Frag;
-  constexpr int NW = 8;
-  constexpr int DT = DP / 16, CPR = DP / 8, TILE = 64 * DP;
-  constexpr int SLOT = TILE + 2 * 4096;   // bf16 per ring slot: the P2 tile, then each query block's 8 fragments
-  constexpr int NS = 4;                   // ring slots: key blocks issued ahead + 1 (five measured slower)
+  using Q = DqShape<DP, NW>;
+  static_assert(!FUSED || NW == 4, "the fused launch runs four-wave jobs");
+  constexpr int NQB = Q::NQB, SLOT = Q::SLOT, NS = Q::NS;
+  constexpr int DT = DP / 16, CPR = DP / 8, TILE = Q::TILE;
   using Stager = TileStager<DP, NW, 1>;
   constexpr int PER = Stager::PER;        // P2 transfers per block of the busiest waves
   constexpr int RSF = DP + 4;             // fp32 row stride of the reduction buffer: an odd count of
                                           // 16-byte chunks, so a lane group's rows fall on distinct banks
-  static_assert(128 * RSF * 4 <= NS * SLOT * 2, "the reduction buffer fits the ring");
-  __shared__ __align__(16) bf16_t ring[NS * SLOT];
+  static_assert(64 * NQB * RSF * 4 <= NS * SLOT * 2, "the reduction buffer fits the ring");
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15, lg = lane >> 4;
   const int kh = wave & 1, qq = wave >> 1;
   const int sub = qq >> 1, qh = qq & 1;
-  const int BH = p.B * p.H;
-  const int bh = blockIdx.x % BH;
   const int nqb = p.TQp / 64;
-  const int qtop = nqb - 1 - 2 * (blockIdx.x / BH);  // the pair's later query block
   const bool wq = qtop - sub >= 0;                   // the wave has a query block (wave-uniform)
   const int qbw = wq ? qtop - sub : qtop;            // a wave without one mirrors the other's addresses
   const int b = bh / p.H, h = bh % p.H;
-  const int ibase = (qtop - 1) * 64;                 // query of reduction row 0 (the earlier block)
+  const int ibase = (qtop - (NQB - 1)) * 64;         // query of reduction row 0 (the earlier block)
   const bf16_t* kbase = reinterpret_cast<const bf16_t*>(p.p2) + b * p.k_sb + h * p.k_sh;
   const int nkb = PairTable::nkb(qtop, p.TQ, p.q_start);                   // the workgroup's key blocks
   const int nkb_w = PairTable::nkb(qbw, p.TQ, p.q_start);                  // the wave's (addresses)
@@ -395,8 +496,8 @@ __global__ void __launch_bounds__(512) bwd_dq_kernel(const BwdParams p) {
   // The Self term's inputs, dU_ii and the P2 row of each of the thread's (query, 8-column chunk)
   // items, loaded before the key loop: their latency passes under it instead of after it. Rows
   // outside [0, TQ) load a row inside (not stored).
-  constexpr int NIT = 128 * CPR / (64 * NW);
-  static_assert(128 * CPR % (64 * NW) == 0, "whole (query, chunk) items per thread");
+  constexpr int NIT = 64 * NQB * CPR / (64 * NW);
+  static_assert(64 * NQB * CPR % (64 * NW) == 0, "whole (query, chunk) items per thread");
   float us_pre[NIT];
   Frag k8_pre[NIT];
 #pragma unroll
@@ -422,7 +523,12 @@ __global__ void __launch_bounds__(512) bwd_dq_kernel(const BwdParams p) {
     st.issue(dst, srcs, strides, kb * 64, p.TK - 1, wave, lane);
     const int kc = min(kb, nkb_w - 1);
 #pragma unroll
-    for (int s = 0; s < 2; ++s) Stager::load(fr + int64_t(kc) * 4096 + s * 512, dst + fslot + s * 512);
+    for (int s = 0; s < 2; ++s) {
+      if constexpr (FUSED)
+        lds_dma16_sc1(fr + int64_t(kc) * 4096 + s * 512, dst + fslot + s * 512);
+      else
+        Stager::load(fr + int64_t(kc) * 4096 + s * 512, dst + fslot + s * 512);
+    }
   };
   const bool busy = wave + NW * (PER - 1) < Stager::NINS;  // this wave issues PER staging transfers, else PER - 1
   // wait until at most min(later, NS - 2) blocks of this wave's transfers are outstanding
@@ -457,6 +563,22 @@ __global__ void __launch_bounds__(512) bwd_dq_kernel(const BwdParams p) {
       for (int s = 0; s < 2; ++s) dqacc[dt][s] = E::mma(ak, bf[s], dqacc[dt][s]);
     }
   };
+  if constexpr (FUSED) {
+    // every pair of the query block counted (four quadrants each) before any of its dU is read; the
+    // key work of every pair was taken from the job counter before this job, so each count completes
+    if (tid == 0) {
+      int* c = p.kvq + kKvqCounts + bh * nqb + qtop;
+      for (int spin = 0; __hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < 4 * nkb; ++spin) {
+        if (spin == kKvqSpinLimit) {
+          __hip_atomic_store(p.kvq + kKvqOverrun, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(127);  // about 3.5 us between polls: polls every ~1 us by the waiting
+                                        // jobs held up the key work's count adds (30-60 % slower at 2-3 K rows)
+      }
+    }
+    __syncthreads();
+  }
   if (nkb > 0) {
     static_for<NS - 1>([&](auto u) {
       if (decltype(u)::value < nkb) issue(decltype(u)::value, u);
@@ -464,10 +586,10 @@ __global__ void __launch_bounds__(512) bwd_dq_kernel(const BwdParams p) {
     for (int kb0 = 0; kb0 < nkb; kb0 += NS) static_for<NS>([&](auto u) { step(kb0 + decltype(u)::value, u); });
   }
 
-  // add the two key halves through LDS: [128 queries][RSF] fp32 over the ring, rows 0..63 the
+  // add the two key halves through LDS: [64 NQB queries][RSF] fp32 over the ring, rows 0..63 the
   // earlier block, 64..127 the later one
   float* R = reinterpret_cast<float*>(ring);
-  const int rbase = (1 - sub) * 64 + 32 * qh;
+  const int rbase = (NQB - 1 - sub) * 64 + 32 * qh;
   __syncthreads();  // every wave is done reading the ring (the last step waited for every transfer)
   if (kh == 1) {
 #pragma unroll
@@ -508,20 +630,109 @@ __global__ void __launch_bounds__(512) bwd_dq_kernel(const BwdParams p) {
     const Frag ov = E::from_f32(o);
     *reinterpret_cast<bf16x8*>(dqout + int64_t(i) * p.dq_sr + d0) = ov.v;
   }
+}
+
+template <int DP>
+__global__ void __launch_bounds__(512) bwd_dq_kernel(const BwdParams p) {
+  __shared__ __align__(16) bf16_t ring[DqShape<DP, 8>::LDS];
+  const int BH = p.B * p.H, nqb = p.TQp / 64;
+  dq_job<DP, 8, false>(p, blockIdx.x % BH, nqb - 1 - 2 * (blockIdx.x / BH), ring);  // the pair's later query block
   // the last workgroup (the lowest pair, the shortest) also sums dlam: the rows stage has written
   // every partial before this launch
   if (blockIdx.x == gridDim.x - 1) {
-    __syncthreads();  // the Self-term reads of R are done before dlam_sum reuses the memory
-    dlam_sum<64 * NW>(p.dlam_part, BH * nqb, p.dlam, R);
+    __syncthreads();  // the Self-term reads of the ring are done before dlam_sum reuses the memory
+    dlam_sum<512>(p.dlam_part, BH * nqb, p.dlam, reinterpret_cast<float*>(ring));
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// fused key + query launch
+// ------------------------------------------------------------------------------------------------
+// One launch of four-wave workgroups for both kinds of work: as many workgroups as fit the GPU at
+// once (two per CU), each taking jobs until its queue is empty. The (batch x head)s are dealt over
+// kvq_nq queues (head bh to queue bh % kvq_nq), each with its own job counter, and workgroup i takes
+// its jobs from queue i % kvq_nq: first the queue's key jobs (key blocks, longest first), then its
+// query jobs (query blocks, longest first). Workgroups are dealt round-robin over the 8 XCDs, so a
+// queue's jobs run on the XCDs i % 8 = queue (mod kvq_nq), whose L2s then hold their heads' query
+// tiles, as in the two-launch form. A query job waits until the dU quadrants of all its pairs are
+// counted; the key jobs it waits on are in its own queue and were taken before it by running
+// workgroups, which never wait, so every wait ends. The query work of the long query blocks runs
+// beside the key work's tail (key block 0's walk, the launch's longest chain), in the slots the key
+// work no longer fills. (With one job per workgroup instead, the dispatcher places workgroups in
+// order, round-robin over the XCDs, and one XCD without a free slot holds back every later
+// workgroup: a third of the slots stood empty through the second half of the launch.)
+template <int DP>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) bwd_kvq_kernel(const BwdParams p) {
+  constexpr int LDS = KvShape<DP>::LDS > DqShape<DP, 4>::LDS ? KvShape<DP>::LDS : DqShape<DP, 4>::LDS;
+  static_assert(LDS * 2 <= 80 * 1024, "two workgroups per CU");
+  __shared__ __align__(16) bf16_t lds[LDS];
+  __shared__ int s_job;
+  const int nq = p.kvq_nq, queue = blockIdx.x % nq;
+  const int BH = p.B * p.H, hq = BH / nq, nqb = p.TQp / 64;  // hq heads per queue
+  const int nkey = (p.TK + 63) / 64 * hq, nqj = nqb * hq;
+  for (;;) {
+    if (threadIdx.x == 0)
+      s_job = __hip_atomic_fetch_add(p.kvq + kKvqJob + queue * kKvqJobStride, 1, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    const int job = __builtin_amdgcn_readfirstlane(s_job);
+    if (job >= nkey + nqj) break;
+    if (job < nkey) {
+      kv_job<DP, true>(p, queue + nq * (job % hq), job / hq, lds);
+    } else {
+      const int j = job - nkey;
+      dq_job<DP, 4, true>(p, queue + nq * (j % hq), nqb - 1 - j / hq, lds);
+      if (queue == 0 && j == nqj - 1) {
+        // queue 0's last job (its shortest) also sums dlam: the rows stage has written every partial
+        __syncthreads();
+        dlam_sum<256>(p.dlam_part, BH * nqb, p.dlam, reinterpret_cast<float*>(lds));
+      }
+    }
+    __syncthreads();  // the next job reuses the LDS and s_job
   }
 }
 
 // ------------------------------------------------------------------------------------------------
 // host side
 // ------------------------------------------------------------------------------------------------
+// compute units of the current device (read once per device)
+int device_cu_count() {
+  static std::atomic<int> cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// the fused launch's control words when no rows stage in the same call has cleared them
+__global__ void __launch_bounds__(256) kvq_clear_kernel(int* kvq, int n) {
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256)
+    __hip_atomic_store(kvq + i, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <int DP>
 static void launch_tiles_dp(const BwdParams& p, int stages, hipStream_t stream) {
   const int BH = p.B * p.H;
+  if constexpr (DP <= 96) {
+    if (p.kvq && (stages & MOTE_BWD_KEYS) && (stages & MOTE_BWD_QUERIES)) {
+      const int nqb = p.TQp / 64, nkb = (p.TK + 63) / 64;
+      if (!(stages & MOTE_BWD_ROWS)) {
+        const int n = kKvqCounts + BH * nqb;
+        hipLaunchKernelGGL(kvq_clear_kernel, dim3((n + 255) / 256 < 64 ? (n + 255) / 256 : 64), dim3(256), 0, stream,
+                           p.kvq, n);
+      }
+      // as many workgroups as are resident at once (two per CU), a multiple of the queue count
+      const int resident = 2 * device_cu_count();
+      const int jobs = (nkb + nqb) * BH;
+      const int grid = (jobs < resident ? jobs : resident) / p.kvq_nq * p.kvq_nq;
+      hipLaunchKernelGGL((bwd_kvq_kernel<DP>), dim3(grid > 0 ? grid : p.kvq_nq), dim3(256), 0, stream, p);
+      return;
+    }
+  }
   if (stages & MOTE_BWD_KEYS) {
     const int nkb = (p.TK + 63) / 64;
     hipLaunchKernelGGL((bwd_kv_kernel<DP>), dim3(nkb * BH), dim3(256), 0, stream, p);

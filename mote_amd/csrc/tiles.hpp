@@ -62,6 +62,13 @@ __device__ __forceinline__ void lds_dma16(const void* g, void* l) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(la) : "memory", "m0");
 }
 
+// The same with the SC1 cache-policy bit (agent scope): the data comes from the device-coherent
+// level, not from a line of this XCD's L2 that another XCD's write-through stores left stale.
+__device__ __forceinline__ void lds_dma16_sc1(const void* g, void* l) {
+  const uint32_t la = uint32_t(reinterpret_cast<uintptr_t>((void __attribute__((address_space(3)))*)l));
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off sc1" ::"v"(g), "s"(la) : "memory", "m0");
+}
+
 // The same transfer from a wave-uniform base (SGPR pair) plus a per-lane byte offset. The offset
 // registers can stay constant across a whole loop: a VMEM instruction reads its address registers
 // only when the address unit takes it, so rewriting an address register right after an issue (the
