@@ -32,6 +32,8 @@ struct BwdParams {
   int64_t npairs;    // (query block, key block) pairs per (batch, head), PairTable::total
   int* kvq;      // control words of the fused key + query launch, or null: the two launches (tile kernels)
   int kvq_nq;    // its queues: 8, 4, 2 or 1, dividing B H
+  int kvq_spin;  // polls before a query job's wait gives up (kKvqSpinLimit)
+  int kvq_extra; // added to every wait's target: 0 (a test of the give-up path sets 1: never reached)
   int B, H, TQ, TK, D, q_start, TQp;
   float scale, tau_inv;
 };
@@ -39,11 +41,12 @@ struct BwdParams {
 constexpr int kRowBlock = 64;  // rows per workgroup in the rows stage; also TQp's granularity
 
 // Layout of the fused key + query launch's control words (BwdParams::kvq, cleared by the rows stage
-// with agent-scope stores): up to 8 job counters (one per queue, 128 bytes apart), the overrun flag
-// (a bounded wait gave up) and the per (batch x head, query block) counts of stored dU quadrants, four
-// per (query block, key block) pair.
-constexpr int kKvqJob = 0, kKvqJobStride = 32, kKvqOverrun = 256, kKvqCounts = 288;
-constexpr int kKvqSpinLimit = 1 << 20;  // polls of a count before the wait gives up (seconds)
+// with agent-scope stores): up to 8 job counters (one per queue, 128 bytes apart), then the per
+// (batch x head, query block) counts of stored dU quadrants, four per (query block, key block) pair.
+constexpr int kKvqJob = 0, kKvqJobStride = 32, kKvqCounts = 256;
+// Polls of a count before a query job's wait gives up (seconds; no wait of a correct launch comes
+// near it): the job then writes its dP1 rows as NaN instead of hanging the GPU.
+constexpr int kKvqSpinLimit = 1 << 20;
 
 int device_cu_count();  // compute units of the current device (relation_bwd_tiles.hip)
 

@@ -60,14 +60,13 @@ __global__ void __launch_bounds__(256) bwd_rows_kernel(const BwdParams p) {
   T* wq = LEAN ? nullptr : reinterpret_cast<T*>(p.wq) + (int64_t(bh) * p.TQp + i0) * DP;
   T* wd = reinterpret_cast<T*>(p.wdib) + (int64_t(bh) * p.TQp + i0) * DP;
   // the fused key + query launch's control words: this block's count, and block (0, 0) the job
-  // counter and the overrun flag (agent-scope stores, as that launch reads and adds them)
+  // counters (agent-scope stores, as that launch reads and adds them)
   if (LEAN && p.kvq && tid == 0) {
     const int nqb = p.TQp / kRowBlock;
     __hip_atomic_store(p.kvq + kKvqCounts + bh * nqb + blockIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (blockIdx.x == 0 && bh == 0) {
       for (int q = 0; q < 8; ++q)
         __hip_atomic_store(p.kvq + kKvqJob + q * kKvqJobStride, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(p.kvq + kKvqOverrun, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 
@@ -868,6 +867,13 @@ int launch_bwd(const mote_relation_bwd_args* a, hipStream_t stream) {
       p.kvq = reinterpret_cast<int*>(ws + w.kvq);
       const int BH = a->B * a->H;
       p.kvq_nq = BH % 8 == 0 ? 8 : BH % 4 == 0 ? 4 : BH % 2 == 0 ? 2 : 1;
+      p.kvq_spin = kKvqSpinLimit;
+      // a test of the give-up path: every wait's target out of reach, a few polls
+      const char* u = getenv("MOTE_BWD_UNREACHABLE_WAIT");
+      if (u && u[0] == '1') {
+        p.kvq_extra = 1;
+        p.kvq_spin = 4;
+      }
     }
   } else {
     p.wq = ws + w.wq; p.wqT = ws + w.wqT; p.wdibT = ws + w.wdibT;

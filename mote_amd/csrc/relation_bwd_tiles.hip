@@ -563,23 +563,29 @@ __device__ __forceinline__ void dq_job(const BwdParams& p, const int bh, const i
       for (int s = 0; s < 2; ++s) dqacc[dt][s] = E::mma(ak, bf[s], dqacc[dt][s]);
     }
   };
+  bool overrun = false;  // FUSED: the wait gave up; the job then writes its dP1 rows as NaN
   if constexpr (FUSED) {
     // every pair of the query block counted (four quadrants each) before any of its dU is read; the
     // key work of every pair was taken from the job counter before this job, so each count completes
+    __shared__ int s_over;
     if (tid == 0) {
       int* c = p.kvq + kKvqCounts + bh * nqb + qtop;
-      for (int spin = 0; __hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < 4 * nkb; ++spin) {
-        if (spin == kKvqSpinLimit) {
-          __hip_atomic_store(p.kvq + kKvqOverrun, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      int over = 0;
+      const int target = 4 * nkb + p.kvq_extra;
+      for (int spin = 0; __hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target; ++spin) {
+        if (spin >= p.kvq_spin) {
+          over = 1;
           break;
         }
         __builtin_amdgcn_s_sleep(127);  // about 3.5 us between polls: polls every ~1 us by the waiting
                                         // jobs held up the key work's count adds (30-60 % slower at 2-3 K rows)
       }
+      s_over = over;
     }
     __syncthreads();
+    overrun = s_over != 0;
   }
-  if (nkb > 0) {
+  if (nkb > 0 && !overrun) {
     static_for<NS - 1>([&](auto u) {
       if (decltype(u)::value < nkb) issue(decltype(u)::value, u);
     });
@@ -626,7 +632,7 @@ __device__ __forceinline__ void dq_job(const BwdParams& p, const int bh, const i
       o[e] = a.x; o[e + 1] = a.y; o[e + 2] = a.z; o[e + 3] = a.w;
     }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = fmaf(us, (float)k8.v[e], o[e]) * p.scale;
+    for (int e = 0; e < 8; ++e) o[e] = overrun ? __builtin_nanf("") : fmaf(us, (float)k8.v[e], o[e]) * p.scale;
     const Frag ov = E::from_f32(o);
     *reinterpret_cast<bf16x8*>(dqout + int64_t(i) * p.dq_sr + d0) = ov.v;
   }

@@ -154,3 +154,22 @@ def test_one_launch_graph_replays(cuda):
         torch.cuda.synchronize()
         for a, b in zip(outs, ref):
             assert torch.equal(a, b), f"replay {r}"
+
+
+def test_wait_that_gives_up_writes_nan_rows(cuda):
+    """The query jobs' bounded wait: forced from the host to give up (MOTE_BWD_UNREACHABLE_WAIT=1 puts
+    every count's target out of reach and allows four polls), each query job writes its dP1 rows as
+    NaN and ends, so the launch finishes; the key work's outputs are unaffected."""
+    print("case fused bwd wait gives up", flush=True)
+    p1, p2, info, lam, dy = _inputs(1, 2, 300, 0, 96, seed=5)
+    ref = _bwd(p1, p2, info, lam, dy, 0, split=True)
+    os.environ["MOTE_BWD_UNREACHABLE_WAIT"] = "1"
+    try:
+        got = _bwd(p1, p2, info, lam, dy, 0, split=False)
+    finally:
+        del os.environ["MOTE_BWD_UNREACHABLE_WAIT"]
+    assert torch.isnan(got[0].float()).all(), "dP1"
+    for a, b, n in zip(got[1:3], ref[1:3], ("dP2", "dI~")):
+        assert rel_err(a.float(), b.float()) < 1e-2, n
+    again = _bwd(p1, p2, info, lam, dy, 0, split=False)  # the switch is read per call
+    assert torch.equal(again[0], ref[0])
