@@ -83,7 +83,8 @@ def _bwd(p1, p2, info, lam, dy, S, split: bool):
 
 # (B, H, TQ, S, D): one and several key blocks, ragged last blocks, cached prefixes (q_start > 0,
 # aligned or not), 1, 2, 4 and 8 queues of the launch with one to three heads each, every head dim
-# of the launch, the C3 length at full width (where the library picks the one-launch form itself)
+# of the launch, the C3 length at full width and longer ones (where the library picks the one-launch
+# form itself)
 CASES = [
     (1, 2, 40, 0, 64),
     (2, 3, 333, 0, 64),
@@ -94,6 +95,8 @@ CASES = [
     (2, 3, 2001, 0, 64),
     (2, 2, 2000, 100, 96),
     (1, 8, 4964, 0, 96),
+    (2, 8, 3000, 0, 64),
+    (1, 8, 8192, 0, 96),
 ]
 
 
