@@ -2,11 +2,16 @@
 // x [w1; w2; wi]^T with RoPE on p1 / p2 and the Givens head-pair rotation on I~ in its epilogue,
 // written straight into the [B, T, H, dh] layout the Relation kernels and the arena read.
 //
-// Product. C^T = W X^T on v_mfma_f32_16x16x32_bf16: a workgroup (8 waves) owns 256 tokens and the
-// 2 dh output features of one head pair of one projection (p1, p2: heads 2k, 2k+1; I~: the Givens
-// pair of the layer's parity, (2k, 2k+1) or (2k+1, 2k+2 mod H)). Wave w holds head (w & 1) for tokens
-// 64 (w >> 1) .. +63: dh/16 x 4 accumulator tiles, features in the rows, tokens in the columns, so
-// a lane ends with 4 consecutive features of one token. k advances 64 at a time through two LDS
+// Product. C^T = W X^T on v_mfma_f32_16x16x32_bf16: a workgroup (4 waves at dh 64 / 96, 8 at dh 128)
+// owns 32 tokens per wave and the 2 dh output features of one head pair of one projection (p1, p2:
+// heads 2k, 2k+1; I~: the Givens pair of the layer's parity, (2k, 2k+1) or (2k+1, 2k+2 mod H)). Wave
+// w holds head (w & 1) for tokens 64 (w >> 1) .. +63: dh/16 x 4 accumulator tiles, features in the
+// rows, tokens in the columns, so a lane ends with 4 consecutive features of one token. At dh 64 / 96
+// a workgroup needs 64 / 80 KB of LDS and at most 256 registers a lane, so two share a CU and one's
+// epilogue (rounding, rotations, stores: about 40 % of a workgroup's time) overlaps the other's
+// products; 256 tokens per workgroup (8 waves) left one workgroup per CU and the CU's matrix cores
+// idle through every epilogue (417 against 374 us at 79,424 rows, dh 96). At dh 128 four waves would
+// still leave one workgroup per CU (98 KB of LDS, 272 registers), so it keeps eight. k advances 64 at a time through two LDS
 // slots filled by direct global -> LDS transfers (8 token or weight rows x 128 bytes per wave
 // instruction, chunks XOR-swizzled within a row): after the stage's barrier a wave reads all of its
 // fragments of the stage at once (one LDS latency per stage), issues the next stage's transfers into
@@ -14,7 +19,7 @@
 // at about 110 flop per byte (dh 96).
 //
 // Epilogue. The product, rounded to bf16 (the projection output the reference rotates), goes to a
-// padded LDS tile [256 tokens][2 dh]; then every thread takes pairs of 16-byte chunks of it (RoPE:
+// padded LDS tile [tokens][2 dh]; then every thread takes pairs of 16-byte chunks of it (RoPE:
 // chunk c and c + dh/16 of one head, the two halves that rotate together, relation.py:53-58; Givens:
 // the same chunk of the pair's two heads, :160-174) and stores both rotated chunks,
 // out_a = a C - b S, out_b = b C + a S, with C, S the bf16-rounded factors (cos / sin of
@@ -27,9 +32,10 @@
 
 namespace mote {
 
-constexpr int kQkvTok = 256;     // tokens per workgroup
-constexpr int kQkvWaves = 8;     // waves per workgroup: 64 tokens x dh per wave (4 waves with 128 x dh
-                                 // tiles hold their accumulators in AGPRs at one wave per SIMD: slower)
+// waves per workgroup: a wave pair covers 64 tokens of both heads (64 tokens x dh per wave; 4 waves
+// with 128 x dh per wave hold their accumulators in AGPRs at one wave per SIMD: slower)
+template <int DH>
+constexpr int qkv_waves() { return DH == 128 ? 8 : 4; }
 constexpr int kQkvK = 64;        // k per stage (a 128-byte line of every staged row)
 constexpr int kQkvStg = 2;       // ring depth
 constexpr int kQkvPad = 8;       // bf16 elements of padding per output-tile row
@@ -55,10 +61,11 @@ struct QkvParams {
 
 template <int DH, int NW>
 struct QkvShape {
+  static constexpr int TOK = 32 * NW;                 // tokens per workgroup
   static constexpr int NF = DH / 16;                  // feature tiles per head
-  static constexpr int TPW = kQkvTok / (NW / 2);      // tokens per wave (waves pair up over the two heads)
+  static constexpr int TPW = TOK / (NW / 2);          // tokens per wave (waves pair up over the two heads)
   static constexpr int NT = TPW / 16;                 // token tiles per wave
-  static constexpr int ROWS = 2 * DH + kQkvTok;       // staged rows per stage: W head 0 | W head 1 | X
+  static constexpr int ROWS = 2 * DH + TOK;           // staged rows per stage: W head 0 | W head 1 | X
   static constexpr int CPR = kQkvK / 8;              // 16-byte chunks per staged row
   static constexpr int RPI = 64 / CPR;                // rows per wave instruction
   static constexpr int NINS = ROWS / RPI;             // wave instructions per stage
@@ -67,7 +74,7 @@ struct QkvShape {
   static constexpr int STAGE = ROWS * kQkvK;          // bf16 elements
   static constexpr int OUTW = 2 * DH + kQkvPad;
   static constexpr int NCH = 2 * DH / 8;              // 16-byte chunks per output-tile row
-  static constexpr int LDS = kQkvStg * STAGE > kQkvTok * OUTW ? kQkvStg * STAGE : kQkvTok * OUTW;
+  static constexpr int LDS = kQkvStg * STAGE > TOK * OUTW ? kQkvStg * STAGE : TOK * OUTW;
 };
 
 // rope table: tab[t][k] = bf16(cos a) | bf16(sin a) << 16, a = float(pos0 + t) * inv_freq[k]
@@ -82,7 +89,7 @@ __global__ void __launch_bounds__(256) rope_table_kernel(const float* inv_freq, 
 }
 
 template <int DH, int NW, bool GATE>
-__global__ void __launch_bounds__(64 * NW)
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)))
 qkv_rope_kernel(const QkvParams p) {
   using S = QkvShape<DH, NW>;
   using E = Elem<bf16_t>;
@@ -95,7 +102,7 @@ qkv_rope_kernel(const QkvParams p) {
   const int nwg = p.ntok * p.ncol, per = (nwg + 7) / 8;
   const int seq = (blockIdx.x % 8) * per + blockIdx.x / 8;
   if (seq >= nwg) return;
-  const int r0 = (seq / p.ncol) * kQkvTok;
+  const int r0 = (seq / p.ncol) * S::TOK;
   const int colt = seq % p.ncol;
   const int npair = p.H / 2;
   const int part = GATE ? 0 : colt / npair, hp = GATE ? colt : colt % npair;
@@ -108,10 +115,12 @@ qkv_rope_kernel(const QkvParams p) {
   const bf16_t* wb0 = p.w + int64_t(part * HD + h0 * DH) * p.w_sr;
   const bf16_t* wb1 = p.w + int64_t(part * HD + h1 * DH) * p.w_sr;
   const bf16_t* xb = p.x + int64_t(r0) * p.x_sr;
-  const bool full = r0 + kQkvTok <= p.M;
+  const bool full = r0 + S::TOK <= p.M;
 
   // staging: instruction g covers stage rows RPI g .. RPI g + RPI - 1; lane l takes row RPI g + l / CPR
-  // and physical chunk l % CPR, i.e. logical chunk (l % CPR) ^ tile_swz(row)
+  // and physical chunk l % CPR, i.e. logical chunk (l % CPR) ^ tile_swz(row). The lane offsets hold the
+  // row within the source tile too (strides below 2^23 elements keep them in 32 bits), so a stage
+  // issues from three scalar bases: the two weight heads and the token rows.
   constexpr int GW = DH / S::RPI;  // instructions per weight head
   const int lrow = lane / S::CPR;
   uint32_t voff[S::PER];
@@ -122,28 +131,30 @@ qkv_rope_kernel(const QkvParams p) {
     const int64_t sr = g < 2 * GW ? p.w_sr : p.x_sr;
     const int lch = (lane % S::CPR) ^ tile_swz<kQkvK>(S::RPI * g + lrow);
     lchs[i] = lch;
-    voff[i] = uint32_t(lrow * int(sr) + lch * 8) * 2u;
+    const int trow = g < GW ? S::RPI * g : (g < 2 * GW ? S::RPI * (g - GW) : S::RPI * (g - 2 * GW));
+    voff[i] = uint32_t((trow + lrow) * int(sr) + lch * 8) * 2u;
   }
   const bool more = wave < S::FULL;  // this wave issues PER transfers per stage (else PER - 1)
-  // transfer i of the wave's share of stage kb into ring slot `slot`
-  auto issue_i = [&](int i, int kb, int slot) {
+  // transfer i of the wave's share of stage kb into ring slot `slot` (forced inline: at PER 10 the
+  // compiler otherwise makes the lambdas calls and their scalar operands VGPR arguments)
+  auto issue_i = [&](int i, int kb, int slot) __attribute__((always_inline)) {
     const int g = wave + NW * i;
     if (i == S::PER - 1 && !more) return;
     kb = min(kb, p.nk - 1);  // past the end: the last stage again (keeps every wave's count equal)
     const int k0 = kb * kQkvK;
     bf16_t* d = smem + slot * S::STAGE + g * 512;
     if (g < GW) {
-      lds_dma16_s(wb0 + int64_t(S::RPI * g) * p.w_sr + k0, voff[i], d);
+      lds_dma16_s(wb0 + k0, voff[i], d);
     } else if (g < 2 * GW) {
-      lds_dma16_s(wb1 + int64_t(S::RPI * (g - GW)) * p.w_sr + k0, voff[i], d);
+      lds_dma16_s(wb1 + k0, voff[i], d);
     } else if (full) {
-      lds_dma16_s(xb + int64_t(S::RPI * (g - 2 * GW)) * p.x_sr + k0, voff[i], d);
+      lds_dma16_s(xb + k0, voff[i], d);
     } else {
       const int r = min(r0 + S::RPI * (g - 2 * GW) + lrow, p.M - 1);
       lds_dma16(p.x + int64_t(r) * p.x_sr + k0 + lchs[i] * 8, d);
     }
   };
-  auto issue = [&](int kb, int slot) {
+  auto issue = [&](int kb, int slot) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < S::PER; ++i) issue_i(i, kb, slot);
   };
@@ -210,7 +221,7 @@ qkv_rope_kernel(const QkvParams p) {
     // rounded to bf16 and the product rounded again, as the reference's bf16 ops round them; the
     // sigmoid is also written for the backward. The pair's 2 dh columns are contiguous (h1 = h0 + 1).
     constexpr int CH = 2 * DH / 8;
-    for (int q = threadIdx.x; q < kQkvTok * CH; q += 64 * NW) {
+    for (int q = threadIdx.x; q < S::TOK * CH; q += 64 * NW) {
       const int tok = q / CH, c = q % CH;
       const int r = r0 + tok;
       if (r >= p.M) break;  // tasks go token by token: every later one is past M too
@@ -237,7 +248,7 @@ qkv_rope_kernel(const QkvParams p) {
     // y = x rsqrt(mean(x^2) + eps) times the gain, rounded to bf16 in place in the tile (the
     // reference's HeadRMSNorm returns its input dtype); the pre-norm row is kept for the backward.
     const float* nw = part == 0 ? p.nw1 : p.nw2;
-    for (int q = threadIdx.x; q < 2 * kQkvTok; q += 64 * NW) {
+    for (int q = threadIdx.x; q < 2 * S::TOK; q += 64 * NW) {
       const int tok = q >> 1, hd = q & 1;
       bf16_t* row = smem + tok * S::OUTW + hd * DH;
       float ss = 0.f;
@@ -297,8 +308,8 @@ qkv_rope_kernel(const QkvParams p) {
   const int64_t osh = part == 0 ? p.o1_sh : (part == 1 ? p.o2_sh : p.o3_sh);
   const int64_t osr = part == 0 ? p.o1_sr : (part == 1 ? p.o2_sr : p.o3_sr);
   // every table load of the thread's tasks first (one latency for all of them), then the rotations
-  constexpr int NTASK = kQkvTok * NPAIR / (64 * NW);
-  static_assert(kQkvTok * NPAIR % (64 * NW) == 0, "whole tasks per thread");
+  constexpr int NTASK = S::TOK * NPAIR / (64 * NW);
+  static_assert(S::TOK * NPAIR % (64 * NW) == 0, "whole tasks per thread");
   const int rlast = p.M - 1;
   uint4 tabv[NTASK][2];
   if (rope) {
@@ -380,6 +391,16 @@ size_t qkv_rope_workspace_bytes(const mote_qkv_rope_args* a) {
   return size_t(a->T) * (a->D / 2) * sizeof(uint32_t);
 }
 
+// One launch of the kernel for head dim DH: token tiles of the workgroup size DH takes, whole rounds of
+// the grid over the 8 XCDs (the extra ids return).
+template <int DH, bool GATE>
+static void launch_qkv_kernel(QkvParams p, int64_t M, hipStream_t stream) {
+  constexpr int NW = qkv_waves<DH>();
+  p.ntok = int((M + QkvShape<DH, NW>::TOK - 1) / QkvShape<DH, NW>::TOK);
+  const int nwg = p.ntok * p.ncol;
+  hipLaunchKernelGGL((qkv_rope_kernel<DH, NW, GATE>), dim3(unsigned((nwg + 7) / 8 * 8)), dim3(64 * NW), 0, stream, p);
+}
+
 static bool al16v(const void* ptr, int64_t s0, int64_t s1, int64_t s2) {
   return reinterpret_cast<uintptr_t>(ptr) % 16 == 0 && (s0 * 2) % 16 == 0 && (s1 * 2) % 16 == 0 &&
          (s2 * 2) % 16 == 0;
@@ -400,8 +421,8 @@ int launch_qkv_rope_fwd(const mote_qkv_rope_args* a, hipStream_t stream) {
     return set_error(MOTE_ERR_ARGUMENT, "qkv_rope: null pointer");
   if (a->B > 1 && a->x_sb != int64_t(a->T) * a->x_sr)
     return set_error(MOTE_ERR_ARGUMENT, "qkv_rope: x must hold its batches back to back (x_sb == T * x_sr)");
-  if (a->x_sr >= (int64_t(1) << 24) || a->w_sr >= (int64_t(1) << 24))
-    return set_error(MOTE_ERR_ARGUMENT, "qkv_rope: row strides must stay below 2^24 elements");
+  if (a->x_sr >= (int64_t(1) << 23) || a->w_sr >= (int64_t(1) << 23))
+    return set_error(MOTE_ERR_ARGUMENT, "qkv_rope: row strides must stay below 2^23 elements");
   if (!al16v(a->x, a->x_sr, 0, 0) || !al16v(a->w, a->w_sr, 0, 0) ||
       !al16v(a->p1.data, a->p1.stride_b, a->p1.stride_h, a->p1.stride_r) ||
       !al16v(a->p2.data, a->p2.stride_b, a->p2.stride_h, a->p2.stride_r) ||
@@ -428,7 +449,6 @@ int launch_qkv_rope_fwd(const mote_qkv_rope_args* a, hipStream_t stream) {
   p.qkraw = reinterpret_cast<bf16_t*>(a->qk_raw); p.qr_sb = a->qr_sb; p.qr_sr = a->qr_sr;
   p.gy = nullptr; p.gy_sr = 0; p.gz = p.gs = nullptr; p.gz_sr = 0;
   p.B = a->B; p.T = a->T; p.H = a->H; p.K = K; p.M = int(M); p.parity = a->layer_parity & 1; p.nk = K / kQkvK;
-  p.ntok = int((M + kQkvTok - 1) / kQkvTok);
   p.ncol = 3 * (a->H / 2);
   if (a->inv_freq && !a->table_ready) {
     const int64_t n = int64_t(a->T) * (a->D / 2);
@@ -437,31 +457,31 @@ int launch_qkv_rope_fwd(const mote_qkv_rope_args* a, hipStream_t stream) {
     int rc = check_launch("qkv_rope/table");
     if (rc) return rc;
   }
-  const int nwg = p.ntok * p.ncol;
-  const dim3 grid(unsigned((nwg + 7) / 8 * 8));  // whole rounds over the 8 XCDs; the extra ids return
   switch (a->D) {
-    case 64: hipLaunchKernelGGL((qkv_rope_kernel<64, kQkvWaves, false>), grid, dim3(64 * kQkvWaves), 0, stream, p); break;
-    case 96: hipLaunchKernelGGL((qkv_rope_kernel<96, kQkvWaves, false>), grid, dim3(64 * kQkvWaves), 0, stream, p); break;
-    default: hipLaunchKernelGGL((qkv_rope_kernel<128, kQkvWaves, false>), grid, dim3(64 * kQkvWaves), 0, stream, p); break;
+    case 64: launch_qkv_kernel<64, false>(p, M, stream); break;
+    case 96: launch_qkv_kernel<96, false>(p, M, stream); break;
+    default: launch_qkv_kernel<128, false>(p, M, stream); break;
   }
   return check_launch("qkv_rope");
 }
 
 // The output gate's product on the same kernel: the D columns of x wg^T are tiled as D / (2 dh)
-// "head pairs" of dh in {128, 96, 64}, the first that divides them.
+// "head pairs" of dh in {96, 128, 64}, the first that divides them (dh 96 first: its workgroups are
+// half the size, two to a CU, and at D 768 it measured 25 / 192 us at 4,964 / 79,424 rows where
+// dh 128 took 40 / 197).
 int launch_gate_product(const mote_gate_product_args* a, hipStream_t stream) {
   if (!a) return set_error(MOTE_ERR_ARGUMENT, "gate_product: null args");
   if (a->B < 0 || a->T < 0 || a->D <= 0) return set_error(MOTE_ERR_SHAPE, "gate_product: bad sizes");
   int DH = 0;
-  for (const int c : {128, 96, 64})
+  for (const int c : {96, 128, 64})
     if (a->D % (2 * c) == 0) { DH = c; break; }
   if (!DH || a->D % kQkvK) return set_error(MOTE_ERR_SHAPE, "gate_product: width %d (needs a multiple of 128)", a->D);
   const int64_t M = int64_t(a->B) * a->T;
   if (M == 0) return MOTE_OK;
   if (M > (int64_t(1) << 30)) return set_error(MOTE_ERR_SHAPE, "gate_product: %lld tokens", (long long)M);
   if (!a->x || !a->w || !a->y || !a->z || !a->s) return set_error(MOTE_ERR_ARGUMENT, "gate_product: null pointer");
-  if (a->x_sr >= (int64_t(1) << 24) || a->w_sr >= (int64_t(1) << 24))
-    return set_error(MOTE_ERR_ARGUMENT, "gate_product: row strides must stay below 2^24 elements");
+  if (a->x_sr >= (int64_t(1) << 23) || a->w_sr >= (int64_t(1) << 23))
+    return set_error(MOTE_ERR_ARGUMENT, "gate_product: row strides must stay below 2^23 elements");
   if (!al16v(a->x, a->x_sr, 0, 0) || !al16v(a->w, a->w_sr, 0, 0) || !al16v(a->y, a->y_sr, 0, 0) ||
       !al16v(a->z, a->z_sr, 0, 0) || !al16v(a->s, a->z_sr, 0, 0))
     return set_error(MOTE_ERR_ARGUMENT, "gate_product: rows must start on 16-byte boundaries");
@@ -471,14 +491,11 @@ int launch_gate_product(const mote_gate_product_args* a, hipStream_t stream) {
   p.gy = reinterpret_cast<const bf16_t*>(a->y); p.gy_sr = a->y_sr;
   p.gz = reinterpret_cast<bf16_t*>(a->z); p.gs = reinterpret_cast<bf16_t*>(a->s); p.gz_sr = a->z_sr;
   p.B = 1; p.T = int(M); p.H = a->D / DH; p.K = a->D; p.M = int(M); p.parity = 0; p.nk = a->D / kQkvK;
-  p.ntok = int((M + kQkvTok - 1) / kQkvTok);
   p.ncol = p.H / 2;
-  const int nwg = p.ntok * p.ncol;
-  const dim3 grid(unsigned((nwg + 7) / 8 * 8));
   switch (DH) {
-    case 64: hipLaunchKernelGGL((qkv_rope_kernel<64, kQkvWaves, true>), grid, dim3(64 * kQkvWaves), 0, stream, p); break;
-    case 96: hipLaunchKernelGGL((qkv_rope_kernel<96, kQkvWaves, true>), grid, dim3(64 * kQkvWaves), 0, stream, p); break;
-    default: hipLaunchKernelGGL((qkv_rope_kernel<128, kQkvWaves, true>), grid, dim3(64 * kQkvWaves), 0, stream, p); break;
+    case 64: launch_qkv_kernel<64, true>(p, M, stream); break;
+    case 96: launch_qkv_kernel<96, true>(p, M, stream); break;
+    default: launch_qkv_kernel<128, true>(p, M, stream); break;
   }
   return check_launch("gate_product");
 }

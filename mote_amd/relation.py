@@ -191,13 +191,12 @@ def rope_givens(qkv: torch.Tensor, n_heads: int, inv_freq: Optional[torch.Tensor
 
 
 # ---- mote::qkv_rope (fused projection prologue) ----------------------------------------------------
-USE_FUSED_PROLOGUE = True   # bf16 activations, head dim 64 / 96 / 128, no QK-Norm: one launch for the
-                            # projections and RoPE / Givens; the unfused path serves everything else
-# Without QK-Norm, above this many rows (B T) hipBLASLt's product followed by the RoPE kernel measured
-# faster than the fused launch at Mote-96M widths (39 712 to 79 424 rows: 3 to 10 %; at 4 964 to 29 784
-# rows the fused launch is 0 to 27 % faster). With QK-Norm the fused launch also replaces two norm
-# passes and serves every size.
-FUSED_PROLOGUE_MAX_ROWS = 32768
+USE_FUSED_PROLOGUE = True   # bf16 activations, head dim 64 / 96 / 128 (with or without QK-Norm): one
+                            # launch for the projections, QK-Norm and RoPE / Givens, at every row count;
+                            # the unfused path serves everything else. Against hipBLASLt's product plus
+                            # the RoPE kernel at width 768 it measured 28.6 / 34.8 us at 4,964 rows
+                            # (dh 96) and 365 / 414, 369 / 403, 407 / 406 us at 79,424 rows (dh 96,
+                            # 128, 64).
 
 
 # cos / sin tables of the fused prologue, memoised per (device, stream, inv_freq, T, pos0) the way
@@ -525,8 +524,7 @@ class FullRelation(nn.Module):
         theta = self.theta if self.use_givens else None
         bf16 = x.dtype == torch.bfloat16 or (torch.is_autocast_enabled() and
                                              torch.get_autocast_dtype("cuda") == torch.bfloat16)
-        if (USE_FUSED_PROLOGUE and bf16 and dh in (64, 96, 128) and (H * dh) % 32 == 0
-                and (self.qk_norm or B * T <= FUSED_PROLOGUE_MAX_ROWS)):
+        if USE_FUSED_PROLOGUE and bf16 and dh in (64, 96, 128) and (H * dh) % 32 == 0:
             norm = (self.p1_norm.weight, self.p2_norm.weight, self.p1_norm.eps) if self.qk_norm else None
             return qkv_rope(x.to(torch.bfloat16), w.to(torch.bfloat16), H, inv, theta, self.layer_idx, S, norm)
         qkv = F.linear(x, w)

@@ -217,18 +217,20 @@ def test_head_rms_norm_module_matches_the_oracle():
     assert math.isfinite(float(n(x).float().sum()))
 
 
-@pytest.mark.parametrize("T,qk_norm,fused", [(64, False, True), (40000, False, False), (40000, True, True)])
-def test_fused_prologue_row_threshold(monkeypatch, T, qk_norm, fused):
-    """FullRelation.heads takes the fused prologue up to FUSED_PROLOGUE_MAX_ROWS rows without QK-Norm
-    (beyond it the product + RoPE kernel path measured faster), and at every size with QK-Norm. The
-    launches are replaced by recorders, so this runs on the CPU."""
+@pytest.mark.parametrize("T,qk_norm,dtype,fused", [(64, False, torch.bfloat16, True),
+                                                     (80000, False, torch.bfloat16, True),
+                                                     (80000, True, torch.bfloat16, True),
+                                                     (64, False, torch.float32, False)])
+def test_fused_prologue_dispatch(monkeypatch, T, qk_norm, dtype, fused):
+    """FullRelation.heads takes the fused prologue for bf16 activations at every row count, with and
+    without QK-Norm, and the product + RoPE kernel path for fp32. The launches are replaced by
+    recorders, so this runs on the CPU."""
     from mote_amd import relation as R
 
     calls = []
     monkeypatch.setattr(R, "qkv_rope", lambda *a, **k: calls.append("fused") or ("p1", "p2", "info"))
     monkeypatch.setattr(R, "rope_givens", lambda *a, **k: calls.append("unfused") or ("p1", "p2", "info"))
-    m = R.FullRelation(128, 2, 1, qk_norm=qk_norm, dtype=torch.bfloat16)
-    assert R.FUSED_PROLOGUE_MAX_ROWS < 40000 <= 2 * R.FUSED_PROLOGUE_MAX_ROWS
-    x = torch.zeros(1, T, 128, dtype=torch.bfloat16)
+    m = R.FullRelation(128, 2, 1, qk_norm=qk_norm, dtype=dtype)
+    x = torch.zeros(1, T, 128, dtype=dtype)
     m.heads(x, 0)
     assert calls == ["fused" if fused else "unfused"]

@@ -313,7 +313,7 @@ def test_head_norm_backward_op_passes_opcheck(cuda):
                           test_utils=("test_schema", "test_faketensor"))
 
 
-@pytest.mark.parametrize("B,T,D", [(1, 4964, 768), (2, 333, 512), (1, 1, 256)])
+@pytest.mark.parametrize("B,T,D", [(1, 4964, 768), (2, 333, 512), (1, 1, 256), (1, 77, 640)])
 def test_out_gate_product_matches_oracle(cuda, B, T, D):
     """mote::out_gate: z = y * sigmoid(x wg^T) (relation.py:179-181) with the reference's bf16 rounding
     points; z and the saved sigmoid against float64, gradients of x, wg and y against float64
