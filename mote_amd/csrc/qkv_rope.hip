@@ -11,12 +11,12 @@
 // epilogue (rounding, rotations, stores: about 40 % of a workgroup's time) overlaps the other's
 // products; 256 tokens per workgroup (8 waves) left one workgroup per CU and the CU's matrix cores
 // idle through every epilogue (417 against 374 us at 79,424 rows, dh 96). At dh 128 four waves would
-// still leave one workgroup per CU (98 KB of LDS, 272 registers), so it keeps eight. k advances 64 at a time through two LDS
-// slots filled by direct global -> LDS transfers (8 token or weight rows x 128 bytes per wave
-// instruction, chunks XOR-swizzled within a row): after the stage's barrier a wave reads all of its
-// fragments of the stage at once (one LDS latency per stage), issues the next stage's transfers into
-// the other slot, then runs the products. 256 x 2 dh outputs per stage keep the L2 -> LDS traffic
-// at about 110 flop per byte (dh 96).
+// still leave one workgroup per CU (98 KB of LDS, 272 registers), so it keeps eight.
+// k advances 64 at a time through two LDS slots filled by direct global -> LDS transfers (8 token or
+// weight rows x 128 bytes per wave instruction, chunks XOR-swizzled within a row): after the stage's
+// barrier a wave reads all of its fragments of the stage at once (one LDS latency per stage), issues
+// the next stage's transfers into the other slot, then runs the products. 128 x 2 dh outputs per
+// stage keep the L2 -> LDS traffic at about 77 flop per byte (dh 96).
 //
 // Epilogue. The product, rounded to bf16 (the projection output the reference rotates), goes to a
 // padded LDS tile [tokens][2 dh]; then every thread takes pairs of 16-byte chunks of it (RoPE:
