@@ -414,6 +414,29 @@ typedef struct mote_gate_product_args {
 int mote_gate_product(const mote_gate_product_args* args, void* stream);
 
 /* ------------------------------------------------------------------------------------------------
+ * Weight gradient of a projection (bf16, fp32 accumulation): dW [N, K] = A^T X, A [M, N] (the
+ * output gradient) and X [M, K] (the projection's input) token-major, summed over the M rows and
+ * rounded once to bf16; bitwise reproducible. N and K multiples of 128, rows on 16-byte boundaries,
+ * a_sr, x_sr below 2^24 elements; M == 0 writes zeros. The workspace holds fp32 partials of the
+ * splits of M (mote_wgrad_workspace; 0 bytes when one split serves).
+ * Replaces: the weight half of autograd through the projections of FullRelation.heads
+ * (mote/model/relation.py:204-215: the stacked [w1; w2; wi] product, dW = dqkv^T x), which the
+ * GEMM library runs with its reduction over the token rows.
+ * ------------------------------------------------------------------------------------------------ */
+typedef struct mote_wgrad_args {
+  int dtype;               /* MOTE_BF16 */
+  int M, N, K;
+  const void* a; int64_t a_sr;
+  const void* x; int64_t x_sr;
+  void* dw; int64_t dw_sr;
+  void* workspace;
+  size_t workspace_bytes;
+} mote_wgrad_args;
+
+size_t mote_wgrad_workspace(const mote_wgrad_args* args);
+int mote_wgrad(const mote_wgrad_args* args, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
  * Skinny product for the decode engine's per-token projections (bf16, fp32 accumulation):
  * y [B, N] = x [B, K] W[N, K]^T rounded to bf16, B <= 16 rows (one new chunk per sequence), N a
  * multiple of 16, K a multiple of 128 and at most 1024; x and W rows on 16-byte boundaries, row

@@ -145,6 +145,14 @@ class SkinnyGemmArgs(C.Structure):
     ]
 
 
+class WgradArgs(C.Structure):
+    _fields_ = [
+        ("dtype", C.c_int), ("M", C.c_int), ("N", C.c_int), ("K", C.c_int),
+        ("a", C.c_void_p), ("a_sr", C.c_int64), ("x", C.c_void_p), ("x_sr", C.c_int64),
+        ("dw", C.c_void_p), ("dw_sr", C.c_int64), ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
+    ]
+
+
 class PageCopyArgs(C.Structure):
     _fields_ = [
         ("to_page", C.c_int), ("planes", C.c_int), ("H", C.c_int), ("D", C.c_int), ("elem_bytes", C.c_int),
@@ -240,6 +248,8 @@ EXPORTS = {
     "mote_head_rms_norm_bwd_workspace": ([C.POINTER(HeadNormBwdArgs)], C.c_size_t),
     "mote_head_rms_norm_bwd": ([C.POINTER(HeadNormBwdArgs), C.c_void_p], C.c_int),
     "mote_skinny_gemm": ([C.POINTER(SkinnyGemmArgs), C.c_void_p], C.c_int),
+    "mote_wgrad_workspace": ([C.POINTER(WgradArgs)], C.c_size_t),
+    "mote_wgrad": ([C.POINTER(WgradArgs), C.c_void_p], C.c_int),
     "mote_arena_page_copy": ([C.POINTER(PageCopyArgs), C.c_void_p], C.c_int),
     "mote_chunk_route": ([C.POINTER(ChunkRouteArgs), C.c_void_p], C.c_int),
     "mote_chunk_gather": ([C.POINTER(ChunkGatherArgs), C.c_void_p], C.c_int),
@@ -260,6 +270,7 @@ STRUCTS = {
     "mote_relation_decode_args": DecodeArgs, "mote_add_rms_norm_args": NormArgs,
     "mote_add_rms_norm_bwd_args": NormBwdArgs, "mote_qkv_rope_args": QkvRopeArgs,
     "mote_gate_product_args": GateProductArgs, "mote_head_norm_bwd_args": HeadNormBwdArgs, "mote_skinny_gemm_args": SkinnyGemmArgs,
+    "mote_wgrad_args": WgradArgs,
     "mote_page_copy_args": PageCopyArgs, "mote_chunk_route_args": ChunkRouteArgs,
     "mote_chunk_gather_args": ChunkGatherArgs, "mote_chunk_gather_bwd_args": ChunkGatherBwdArgs,
     "mote_dechunk_args": DechunkArgs, "mote_dechunk_bwd_args": DechunkBwdArgs,

@@ -26,6 +26,10 @@ int check_launch(const char* what) {
   return MOTE_OK;
 }
 
+// wgrad.hip (kept out of params.hpp, whose text every recorded kernel profile is tied to)
+size_t wgrad_workspace_bytes(const mote_wgrad_args* a);
+int launch_wgrad(const mote_wgrad_args* a, hipStream_t stream);
+
 }  // namespace mote
 
 extern "C" {
@@ -116,6 +120,13 @@ int mote_arena_page_copy(const mote_page_copy_args* args, void* stream) {
 int mote_skinny_gemm(const mote_skinny_gemm_args* args, void* stream) {
   mote::g_err[0] = 0;
   return mote::launch_skinny_gemm(args, reinterpret_cast<hipStream_t>(stream));
+}
+
+size_t mote_wgrad_workspace(const mote_wgrad_args* args) { return args ? mote::wgrad_workspace_bytes(args) : 0; }
+
+int mote_wgrad(const mote_wgrad_args* args, void* stream) {
+  mote::g_err[0] = 0;
+  return mote::launch_wgrad(args, reinterpret_cast<hipStream_t>(stream));
 }
 
 int mote_chunk_route(const mote_chunk_route_args* args, void* stream) {

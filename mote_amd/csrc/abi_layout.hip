@@ -121,6 +121,11 @@ const Entry kLayout[] = {
     F(mote_skinny_gemm_args, w), F(mote_skinny_gemm_args, w_sr), F(mote_skinny_gemm_args, y),
     F(mote_skinny_gemm_args, y_sr), F(mote_skinny_gemm_args, run), F(mote_skinny_gemm_args, g),
     F(mote_skinny_gemm_args, xm), F(mote_skinny_gemm_args, heads),
+    MOTE_STRUCT(mote_wgrad_args),
+    F(mote_wgrad_args, dtype), F(mote_wgrad_args, M), F(mote_wgrad_args, N), F(mote_wgrad_args, K),
+    F(mote_wgrad_args, a), F(mote_wgrad_args, a_sr), F(mote_wgrad_args, x), F(mote_wgrad_args, x_sr),
+    F(mote_wgrad_args, dw), F(mote_wgrad_args, dw_sr), F(mote_wgrad_args, workspace),
+    F(mote_wgrad_args, workspace_bytes),
     MOTE_STRUCT(mote_page_copy_args),
     F(mote_page_copy_args, to_page), F(mote_page_copy_args, planes), F(mote_page_copy_args, H),
     F(mote_page_copy_args, D), F(mote_page_copy_args, elem_bytes), F(mote_page_copy_args, rows),

@@ -340,6 +340,50 @@ def _head_norm_bwd_fake(dqkv, qkraw, gain1, gain2, eps, n_heads):
     return dqkv.new_empty(D, dtype=torch.float32), dqkv.new_empty(D, dtype=torch.float32)
 
 
+# ---- mote::wgrad (weight gradient of the projections) -------------------------------------------
+USE_WGRAD = True  # bf16 rows, both widths multiples of 128: mote_wgrad; else the GEMM library
+
+
+@torch.library.custom_op("mote::wgrad", mutates_args=())
+def _wgrad(a: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    """bf16 dW [N, K] = a^T x for a [M, N], x [M, K], fp32 sums (operands whose rows are not unit-stride
+    and 16-byte aligned are copied first)."""
+    if not a.is_cuda:
+        raise RuntimeError("mote::wgrad needs the HIP library and an MI355X")
+    ok = lambda t: t.stride(1) == 1 and (t.stride(0) * 2) % 16 == 0 and t.data_ptr() % 16 == 0
+    a = a if ok(a) else a.contiguous()
+    x = x if ok(x) else x.contiguous()
+    M, N = a.shape
+    K = x.shape[1]
+    dw = torch.empty(N, K, device=a.device, dtype=a.dtype)
+    args = L.WgradArgs()
+    args.dtype, args.M, args.N, args.K = L.dtype_code(a), M, N, K
+    args.a, args.a_sr = a.data_ptr(), a.stride(0)
+    args.x, args.x_sr = x.data_ptr(), x.stride(0)
+    args.dw, args.dw_sr = dw.data_ptr(), dw.stride(0)
+    nbytes = int(L.lib().mote_wgrad_workspace(args))
+    ws = torch.empty(max(nbytes, 16), device=a.device, dtype=torch.uint8)
+    args.workspace, args.workspace_bytes = ws.data_ptr(), ws.numel()
+    L.check(L.lib().mote_wgrad(args, L.stream_of(a)), "mote_wgrad")
+    return dw
+
+
+@_wgrad.register_fake
+def _wgrad_fake(a, x):
+    return a.new_empty((a.shape[1], x.shape[1]))
+
+
+def weight_grad(a: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    """a^T x over the token rows of a [..., N] and x [..., K]: the weight gradient of y = x W^T.
+    mote_wgrad for bf16 on the GPU with N, K multiples of 128; the GEMM library otherwise."""
+    N, K = a.shape[-1], x.shape[-1]
+    a2, x2 = a.reshape(-1, N), x.reshape(-1, K)
+    if (USE_WGRAD and a2.is_cuda and a2.dtype == torch.bfloat16 and x2.dtype == torch.bfloat16
+            and N % 128 == 0 and K % 128 == 0):
+        return _wgrad(a2, x2)
+    return torch.matmul(a2.t(), x2)
+
+
 def _qr_backward(ctx, dp1, dp2, dinfo, _diraw, _dqkraw):
     x, w, inv_freq, theta, iraw, norm_w1, norm_w2, qkraw = ctx.saved_tensors
     if (ctx.has_theta or ctx.norm) and not ctx.keep:
@@ -358,7 +402,7 @@ def _qr_backward(ctx, dp1, dp2, dinfo, _diraw, _dqkraw):
         dn1, dn2 = _head_norm_bwd_(dqkv, qkraw, norm_w1, norm_w2, ctx.eps, H)
         dn1, dn2 = dn1.to(norm_w1.dtype), dn2.to(norm_w2.dtype)
     dx = torch.matmul(dqkv, w)                                        # [B, T, 3K] x [3K, K]
-    dw = torch.matmul(dqkv.reshape(-1, 3 * K).t(), x.reshape(-1, K))  # [3K, K]
+    dw = weight_grad(dqkv, x)                                        # [3K, K]
     return (dx, dw, None, (dtheta[: H // 2] if ctx.has_theta else None), None, None, None, None, dn1, dn2, None)
 
 
@@ -419,7 +463,7 @@ def _og_backward(ctx, dz, _ds):
     dg = (dzf * y.float() * sf * (1.0 - sf)).to(x.dtype)
     D = x.shape[-1]
     dx = torch.matmul(dg, wg)
-    dwg = torch.matmul(dg.reshape(-1, D).t(), x.reshape(-1, D))
+    dwg = weight_grad(dg, x)
     return dx, dwg, dy
 
 

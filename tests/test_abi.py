@@ -91,6 +91,39 @@ def test_skinny_gemm_rejects_unsupported_shapes_without_a_gpu():
     assert _lib.lib().mote_skinny_gemm(a, None) == 0  # nothing to do, nothing launched
 
 
+def test_wgrad_rejects_unsupported_arguments_without_a_gpu():
+    """mote_wgrad checks dtype, the 128-granular widths, strides, alignment and the workspace
+    before any launch; its workspace query sizes the fp32 split partials (none for one split)."""
+    from mote_amd import _lib
+
+    if not _lib.available():
+        pytest.skip("libmote_relation.so not built")
+    a = _lib.WgradArgs()
+    a.dtype, a.M, a.N, a.K = _lib.MOTE_F32, 64, 128, 128
+    a.a = a.x = a.dw = 16
+    a.a_sr = a.x_sr = a.dw_sr = 128
+    assert _lib.lib().mote_wgrad(a, None) == 1
+    assert b"bf16" in _lib.lib().mote_last_error()
+    a.dtype = _lib.MOTE_BF16
+    for M, N, K in ((-1, 128, 128), (64, 100, 128), (64, 128, 96), (64, 0, 128)):
+        a.M, a.N, a.K = M, N, K
+        assert _lib.lib().mote_wgrad(a, None) == 2, (M, N, K)
+    a.M, a.N, a.K, a.a_sr = 64, 256, 128, 128  # a row stride below N
+    assert _lib.lib().mote_wgrad(a, None) == 1
+    a.a_sr, a.a = 256, 24  # a misaligned row start
+    assert _lib.lib().mote_wgrad(a, None) == 1
+    assert b"16-byte" in _lib.lib().mote_last_error()
+    a.a = 16
+    # a long reduction over few tiles splits M; every split holds an N x K fp32 partial
+    a.M, a.N, a.K, a.a_sr, a.x_sr, a.dw_sr = 4964, 2304, 768, 2304, 768, 768
+    ws = int(_lib.lib().mote_wgrad_workspace(a))
+    assert ws > 0 and ws % (2304 * 768 * 4) == 0
+    a.workspace, a.workspace_bytes = 16, ws - 16
+    assert _lib.lib().mote_wgrad(a, None) == 3
+    a.M = 200  # fewer than four stages per split: one split, no workspace
+    assert int(_lib.lib().mote_wgrad_workspace(a)) == 0
+
+
 def test_static_decode_refuses_shapes_beyond_its_array_without_a_gpu():
     """mote_relation_decode_static checks its arguments and the limits of its fixed scratch array
     (256 sequences, 1024 sequence-heads) before it touches a device: a larger call is refused with
