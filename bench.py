@@ -1001,6 +1001,58 @@ def bench_qkv(rows: int, dev, copies: int, launches: int = 20):
                 rel_diff_fused_vs_unfused=diff, **out)
 
 
+def bench_wgrad(rows: int, dev, copies: int, launches: int = 20):
+    """mote::wgrad, the prologue's weight gradient dW = dqkv^T x at the Mote-96M shape (dqkv bf16
+    [rows, 2304], x bf16 [rows, 768]), against the GEMM library's dqkv^T x (torch.matmul of the
+    transposed view, what the unfused backward runs); each a HIP graph of `launches` launches over
+    `copies` input sets. Work: 2 rows 3D D FLOP."""
+    from mote_amd.relation import _wgrad
+
+    D = D_MODEL
+    g = torch.Generator(device="cpu").manual_seed(9)
+    sets = [(torch.randn(rows, 3 * D, generator=g).to(torch.bfloat16).to(dev),
+             torch.randn(rows, D, generator=g).to(torch.bfloat16).to(dev)) for _ in range(copies)]
+    fns = {"mote_wgrad": lambda i: _wgrad(*sets[i % copies]),
+           "library": lambda i: torch.matmul(sets[i % copies][0].t(), sets[i % copies][1])}
+    a, b = fns["mote_wgrad"](0), fns["library"](0)
+    diff = float((a.float() - b.float()).abs().max()) / max(float(b.float().abs().max()), 1e-3)
+    flops = 2.0 * rows * 3 * D * D
+    out = {}
+    side = torch.cuda.Stream()
+    for name, fn in fns.items():
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for i in range(copies):
+                fn(i)
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(gr, stream=side):
+                for i in range(launches):
+                    fn(i)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        for _ in range(2):
+            gr.replay()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 10
+        t0.record()
+        for _ in range(reps):
+            gr.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        us = t0.elapsed_time(t1) * 1e3 / (reps * launches)
+        tf = flops / (us * 1e-6) / 1e12
+        out[name] = dict(us_per_launch=round(us, 2), tflops=round(tf, 1), frac_bf16_peak=round(tf / PEAK_BF16_TFLOPS, 4))
+        del gr
+    log(f"[bench] prologue dW rows {rows}: mote_wgrad {out['mote_wgrad']['us_per_launch']:.1f} us "
+        f"({out['mote_wgrad']['tflops']:.0f} TF/s), library {out['library']['us_per_launch']:.1f} us; rel diff {diff:.2e}")
+    return dict(workload=f"prologue weight gradient dqkv^T x, {rows} rows, [{rows}, {3 * D}]^T [{rows}, {D}] (bf16), "
+                         f"HIP graph of {launches} launches over {copies} inputs", rows=rows, flop_per_launch=flops,
+                rel_diff_vs_library=diff, **out)
+
+
 # ------------------------------------------------------------------------------------------------
 # chunk gather and EMA dechunk (either side of the main network)
 # ------------------------------------------------------------------------------------------------
@@ -1273,6 +1325,7 @@ def main():
         extra["c2_mote32m_stack"] = bench_c2(args.steps, args.warmup, dev)
         extra["c5_mote138m_prefill"] = bench_c5(max(3, args.steps // 4), min(args.warmup, 2), dev)
         extra["qkv_prologue"] = {"T": bench_qkv(st["T"], dev, copies=8), "16T": bench_qkv(16 * st["T"], dev, copies=1)}
+        extra["prologue_wgrad"] = {"T": bench_wgrad(st["T"], dev, copies=8), "16T": bench_wgrad(16 * st["T"], dev, copies=1)}
         extra["add_rms_norm"] = {"T": bench_norm(st["T"], dev, copies=8),
                                  "16T": bench_norm(16 * st["T"], dev, copies=1)}
         extra["chunk_dechunk"] = {"B1": bench_dc(1, dev, copies=8), "B8": bench_dc(8, dev, copies=1)}
