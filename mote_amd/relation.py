@@ -384,6 +384,34 @@ def weight_grad(a: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
     return torch.matmul(a2.t(), x2)
 
 
+class _LinearWgrad(torch.autograd.Function):
+    """y = x W^T on the GEMM library; backward dx = dy W on the library and dW = dy^T x on
+    mote_wgrad (the library runs that product with its reduction over the token rows)."""
+
+    @staticmethod
+    def forward(ctx, x, w):
+        ctx.save_for_backward(x, w)
+        return F.linear(x, w)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w = ctx.saved_tensors
+        dx = torch.matmul(dy, w) if ctx.needs_input_grad[0] else None
+        dw = weight_grad(dy, x) if ctx.needs_input_grad[1] else None
+        return dx, dw
+
+
+def linear_wgrad(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """F.linear(x, w) whose weight gradient runs on mote_wgrad: bf16 x and w on the GPU (or bf16
+    autocast, which casts both as F.linear would) with both widths multiples of 128; F.linear otherwise."""
+    if torch.is_autocast_enabled() and torch.get_autocast_dtype("cuda") == torch.bfloat16 and x.is_cuda:
+        x, w = x.to(torch.bfloat16), w.to(torch.bfloat16)
+    if (USE_WGRAD and x.is_cuda and x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16
+            and w.shape[0] % 128 == 0 and w.shape[1] % 128 == 0):
+        return _LinearWgrad.apply(x, w)
+    return F.linear(x, w)
+
+
 def _qr_backward(ctx, dp1, dp2, dinfo, _diraw, _dqkraw):
     x, w, inv_freq, theta, iraw, norm_w1, norm_w2, qkraw = ctx.saved_tensors
     if (ctx.has_theta or ctx.norm) and not ctx.keep:
@@ -589,7 +617,7 @@ class FullRelation(nn.Module):
                 y = out_gate(x.to(torch.bfloat16), self.wg.weight.to(torch.bfloat16), y)
             else:
                 y = y * torch.sigmoid(self.wg(x))
-        return self.wo(y)
+        return linear_wgrad(y, self.wo.weight)
 
     def forward(self, x: torch.Tensor, cache: Optional[RelationCache] = None, return_cache: bool = False,
                 return_gates: bool = False):

@@ -96,3 +96,35 @@ def test_weight_grad_op_and_dispatch(cuda):
     torch.library.opcheck(_wgrad, (a.reshape(-1, 384), x.reshape(-1, 256).contiguous()))
     odd = weight_grad(a[..., :200], x)  # N = 200: the library product
     assert rel_err(odd, a[..., :200].reshape(-1, 200).double().t() @ x.reshape(-1, 256).double()) < 1e-2
+
+
+@pytest.mark.parametrize("autocast", [False, True])
+def test_module_weight_gradients_on_wgrad(cuda, monkeypatch, autocast):
+    """FullRelation's backward with the weight gradients of the prologue, the gate and wo on
+    mote_wgrad against the same step with them on the GEMM library: bf16 weights, or fp32 weights
+    under bf16 autocast (the weights' bf16 casts carry the gradients back to fp32)."""
+    from mote_amd import relation as R
+
+    print(f"case wgrad module autocast={autocast}", flush=True)
+    torch.manual_seed(12)
+    dtype = torch.float32 if autocast else torch.bfloat16
+    m = R.FullRelation(256, 4, 1, out_gate=True, dtype=dtype).to(cuda)
+    x = (torch.randn(2, 300, 256, device=cuda) * 0.5).to(dtype)
+    dy = torch.randn(2, 300, 256, device=cuda).to(dtype)
+
+    def grads(use):
+        monkeypatch.setattr(R, "USE_WGRAD", use)
+        m.zero_grad(set_to_none=True)
+        xi = x.clone().requires_grad_(True)
+        with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+            out = m(xi)
+        (out.float() * dy.float()).sum().backward()
+        return {n: p.grad.clone() for n, p in m.named_parameters() if p.grad is not None}, xi.grad.clone()
+
+    got, gx = grads(True)
+    ref, rx = grads(False)
+    assert set(got) == set(ref) and {"w1.weight", "wo.weight", "wg.weight"} <= set(got)
+    for n in ref:
+        assert got[n].dtype == ref[n].dtype, n
+        assert rel_err(got[n], ref[n]) < 1e-2, (n, rel_err(got[n], ref[n]))
+    assert rel_err(gx, rx) < 1e-2
