@@ -729,18 +729,17 @@ struct WsLayout {
 
 static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-// Whether the tile path's key and query work share one launch (bwd_kvq_kernel). By default when the
-// key work alone fills the GPU's workgroup slots (key blocks x batch x heads >= two per CU): then the
-// query work runs in the slots the key work's tail leaves (C3, 624 key jobs: 162 against 175 us;
-// B H = 16 at 2048 rows: 70 against 77 us); with fewer key jobs the query jobs start early and wait,
-// and the two launches are as fast or faster (2-3 K rows at B H = 8: +1-2 %). The environment
-// variable MOTE_BWD_FUSED overrides: 0 never, 1 wherever the launch applies. It is read on every
-// call (a few hundred ns against tens of microseconds of launches).
+// Whether the tile path's key and query work share one launch (bwd_kvq_kernel): by default always.
+// Against the two launches (event timing over whole backward calls, rows stage included) it measured
+// as fast or faster at every shape tried from one key block to C3: C3 162-174 against 175-200 us,
+// B 4 x H 8 at 658 rows 32.7 against 36.0 us, H 8 at 2048 rows 68 against 79 us, H 16 at 1024 rows
+// (dh 64) 37 against 42 us; within 0.5 us at 300 rows and at one key block. The environment
+// variable MOTE_BWD_FUSED = 0 selects the two launches (1 the one launch, the default). It is read
+// on every call (a few hundred ns against tens of microseconds of launches).
 static bool fused_bwd_wanted(const mote_relation_bwd_args* a) {
+  (void)a;
   const char* e = getenv("MOTE_BWD_FUSED");
-  if (e && e[0] == '0') return false;
-  if (e && e[0] == '1') return true;
-  return int64_t((a->TK + 63) / 64) * a->B * a->H >= 2 * int64_t(device_cu_count());
+  return !(e && e[0] == '0');
 }
 
 // bf16 with a head dim the tile kernels are compiled for: the atomic-free tile path.

@@ -738,9 +738,13 @@ static void launch_tiles_dp(const BwdParams& p, int stages, hipStream_t stream) 
         hipLaunchKernelGGL(kvq_clear_kernel, dim3((n + 255) / 256 < 64 ? (n + 255) / 256 : 64), dim3(256), 0, stream,
                            p.kvq, n);
       }
-      // as many workgroups as are resident at once (two per CU), a multiple of the queue count
+      // at most as many workgroups as are resident at once (two per CU), a multiple of the queue
+      // count. Workgroups beyond the key jobs take query jobs at once and wait in their slots for the
+      // key work; that pays only while the key walks are short: with 12 or more query blocks the grid
+      // is the key jobs alone (H 8 at 2048 rows: 68 against 81-91 us with one workgroup per job; at
+      // 300-700 rows one per job measured 0.5-1.2 us faster)
       const int resident = 2 * device_cu_count();
-      const int jobs = (nkb + nqb) * BH;
+      const int jobs = nqb >= 12 ? nkb * BH : (nkb + nqb) * BH;
       const int grid = (jobs < resident ? jobs : resident) / p.kvq_nq * p.kvq_nq;
       hipLaunchKernelGGL((bwd_kvq_kernel<DP>), dim3(grid > 0 ? grid : p.kvq_nq), dim3(256), 0, stream, p);
       return;

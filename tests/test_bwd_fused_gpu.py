@@ -1,7 +1,8 @@
 """The bf16 tile backward's key and query work in one launch against the same work in two launches,
-both through the C ABI. The library takes the one-launch form by itself when the key work fills the
-GPU (head dims up to 96); MOTE_BWD_FUSED=1 makes it take that form at every size, which these tests
-set around their one-launch calls, so that short and ragged shapes run it too.
+both through the C ABI. The library takes the one-launch form by default for head dims up to 96
+(MOTE_BWD_FUSED=0 selects the two launches); these tests set MOTE_BWD_FUSED=1 around their one-launch
+calls so that the comparison holds whatever the environment says, and get the two-launch form by
+calling the key and query stages separately.
 
 The one-launch form walks each key block's query blocks from the last down and reads the dU
 quadrants through agent-scope loads once their counts are complete; the two-launch form walks up.
