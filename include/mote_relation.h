@@ -117,6 +117,9 @@ int mote_relation_fwd(const mote_relation_fwd_args* args, void* stream);
  * where the path has one; MOTE_BWD_FINISH: dp1 cast and dlam, which the bf16 tile path computes in
  * its MOTE_BWD_QUERIES launch instead); 0 runs all of them. A caller that
  * splits them (to time or overlap them) issues them in that order on one stream with one workspace.
+ * On the bf16 tile path with D <= 96, MOTE_BWD_KEYS and MOTE_BWD_QUERIES in one call run as one
+ * launch (dp1 bit-identical to the separate launches, dp2 / dinfo the same terms added in another
+ * order); the environment variable MOTE_BWD_FUSED=0, read on every call, keeps them separate.
  * ------------------------------------------------------------------------------------------------ */
 #define MOTE_BWD_ROWS 1
 #define MOTE_BWD_KEYS 2
