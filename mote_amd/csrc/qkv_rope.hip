@@ -466,14 +466,18 @@ int launch_qkv_rope_fwd(const mote_qkv_rope_args* a, hipStream_t stream) {
 }
 
 // The output gate's product on the same kernel: the D columns of x wg^T are tiled as D / (2 dh)
-// "head pairs" of dh in {96, 128, 64}, the first that divides them (dh 96 first: its workgroups are
-// half the size, two to a CU, and at D 768 it measured 25 / 192 us at 4,964 / 79,424 rows where
-// dh 128 took 40 / 197).
+// "head pairs", dh the first of {64, 96, 128} that divides them up to 32,768 rows and of
+// {96, 128, 64} beyond (the narrower tiles give more workgroups where the rows are few). At D 768:
+// 16.3 / 19.8 / 27.0 / 47.7 us at 1,241 / 4,964 / 9,928 / 19,856 rows as dh 64 pairs against
+// 22.2 / 25.9 / 31.8 / 51.5 as dh 96 pairs; 213 against 194 us at 79,424 rows; dh 128 pairs took
+// 40 / 197 us at 4,964 / 79,424. Every output column's sum runs over k in the same order whatever
+// the tiling, so the results do not depend on it.
 int launch_gate_product(const mote_gate_product_args* a, hipStream_t stream) {
   if (!a) return set_error(MOTE_ERR_ARGUMENT, "gate_product: null args");
   if (a->B < 0 || a->T < 0 || a->D <= 0) return set_error(MOTE_ERR_SHAPE, "gate_product: bad sizes");
   int DH = 0;
-  for (const int c : {96, 128, 64})
+  const bool few = int64_t(a->B) * a->T <= 32768;
+  for (const int c : {few ? 64 : 96, few ? 96 : 128, few ? 128 : 64})
     if (a->D % (2 * c) == 0) { DH = c; break; }
   if (!DH || a->D % kQkvK) return set_error(MOTE_ERR_SHAPE, "gate_product: width %d (needs a multiple of 128)", a->D);
   const int64_t M = int64_t(a->B) * a->T;

@@ -340,6 +340,23 @@ def test_out_gate_product_matches_oracle(cuda, B, T, D):
         assert rel_err(a.grad, b.grad) < 2e-2, (name, rel_err(a.grad, b.grad))
 
 
+def test_out_gate_tilings_agree_bitwise(cuda):
+    """The gate product tiles its columns as dh 64 pairs up to 32,768 rows and as dh 96 pairs beyond;
+    each output's sum runs over k in the same order either way, so 33,000 rows in one call (dh 96
+    pairs) equal the same rows in two calls of 16,500 (dh 64 pairs) bit for bit."""
+    from mote_amd.relation import _out_gate
+
+    print("case out_gate tilings", flush=True)
+    g = torch.Generator().manual_seed(81)
+    x = torch.randn(1, 33000, 768, generator=g).bfloat16().to(cuda)
+    wg = (torch.randn(768, 768, generator=g) / 28).bfloat16().to(cuda)
+    y = torch.randn(1, 33000, 768, generator=g).bfloat16().to(cuda)
+    z, s = _out_gate(x, wg, y)
+    z0, s0 = _out_gate(x[:, :16500].contiguous(), wg, y[:, :16500].contiguous())
+    z1, s1 = _out_gate(x[:, 16500:].contiguous(), wg, y[:, 16500:].contiguous())
+    assert torch.equal(z, torch.cat([z0, z1], 1)) and torch.equal(s, torch.cat([s0, s1], 1))
+
+
 def test_out_gate_and_qk_norm_ops_pass_opcheck(cuda):
     from mote_amd.relation import rope_inv_freq
 
