@@ -75,9 +75,12 @@ int mote_clock_probe(int64_t* out, int workgroups, int iters, void* stream);
  * cu_seqlens[B]; stride_b is ignored; ibar is [H, total_rows, D], lse/g are [H, total_rows].
  * Workspace (optional): with at least mote_relation_fwd_workspace() bytes of device memory the
  * longest query blocks are split over two workgroups whose partial softmax states merge in a
- * second launch, which evens out the causal imbalance; with workspace == NULL every query block
- * runs in one workgroup. Results are identical up to float rounding of the merge; contents of the
- * workspace on entry do not matter. Calls that share a workspace must not overlap.
+ * second launch, which evens out the causal imbalance (rows beyond 96 key blocks), or, with many
+ * more query blocks than workgroup slots (B H ceil(TQ / 64) >= 8 per CU), persistent workgroups take
+ * the query blocks from job counters held there (cleared by a small launch first); with workspace ==
+ * NULL every query block runs in one workgroup. Results are identical up to float rounding of the
+ * merge (bit for bit with the persistent workgroups); contents of the workspace on entry do not
+ * matter. Calls that share a workspace must not overlap.
  * ------------------------------------------------------------------------------------------------ */
 typedef struct mote_relation_fwd_args {
   int dtype;          /* MOTE_F32 or MOTE_BF16, for p1, p2, info and y */

@@ -21,6 +21,8 @@ struct FwdParams {
   const int32_t* cu;  // null in dense mode
   float* part;        // split partials [nseq][H][nqb][2][64 * DP + 128] (null: no split)
   int split_c;        // query blocks with more key blocks than this run as two halves
+  int* jobs;          // persistent tile launch: one job counter per queue, 32 ints apart (null: one job per workgroup)
+  int jobs_nq;        // its queue count (heads h go to queue h % jobs_nq)
   int64_t q_sb, q_sh, q_sr;
   int64_t k_sb, k_sh, k_sr;
   int64_t v_sb, v_sh, v_sr;

@@ -20,6 +20,7 @@
 // query blocks are dispatched first (longest-processing-time order) and consecutive workgroups
 // of one query block land on different XCDs, so with 8 heads every XCD's L2 holds one head's
 // P2 / I~ rows.
+#include <stdlib.h>
 #include <type_traits>
 
 #include "common.hpp"
@@ -490,26 +491,33 @@ __device__ __forceinline__ void fwd_softmax_pv(const bf16_t* Vs, const f32x4 (&s
   }
 }
 
+// LDS of the tile kernels: a ring of NSTG stages (P2 tile, I~ tile); a block waits only for its own
+// stage, the next NSTG - 2 stay in flight across its math (three stages: 72 KB at DP = 96, so two
+// workgroups still share a CU).
 template <int DP>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
-relation_fwd_tile_kernel(const FwdParams p) {
+struct FwdTileShape {
+  static constexpr int TILE = 64 * DP;
+  static constexpr int STAGE = 2 * TILE;
+  static constexpr int NSTG = DP <= 96 ? 3 : 2;
+  static constexpr int LDS = NSTG * STAGE;
+};
+
+// One (query block, sequence, head) of the tile forward (or one key-range half of it when split),
+// by its block id (the launch order: head fastest, then (when split) the halves, then query blocks
+// longest first); every wave of the workgroup calls it.
+template <int DP>
+__device__ __forceinline__ void fwd_tile_job(const FwdParams& p, const int bid, bf16_t* smem) {
   using E = Elem<bf16_t>;
   using Frag = E::Frag;
   constexpr int KS = DP / 32, DT = DP / 16, TILE = 64 * DP;
-  constexpr int STAGE = 2 * TILE;  // P2 tile, I~ tile
+  constexpr int STAGE = FwdTileShape<DP>::STAGE;
   constexpr int RLD = DP + 4;      // fp32 row stride of the merge buffer
-  // A ring of NSTG stages: a block waits only for its own stage, the next NSTG - 2 stay in flight
-  // across its math (three stages: 72 KB at DP = 96, so two workgroups still share a CU).
-  constexpr int NSTG = DP <= 96 ? 3 : 2;
-  __shared__ __align__(16) bf16_t smem[NSTG * STAGE];
+  constexpr int NSTG = FwdTileShape<DP>::NSTG;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: staging in scalar registers
   const int li = lane & 15, lg = lane >> 4;
   const int kh = wave & 1, qh = wave >> 1;
-  // block id: head fastest, then (when split) the two halves of a query block, then query blocks
-  // (longest first)
-  const int bid = blockIdx.x;
   const int h = bid % p.H;
   const int half = p.part ? (bid / p.H) & 1 : 0;
   const int rest = p.part ? bid / p.H / 2 : bid / p.H;
@@ -737,6 +745,51 @@ relation_fwd_tile_kernel(const FwdParams p) {
   }
 }
 
+template <int DP>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+relation_fwd_tile_kernel(const FwdParams p) {
+  __shared__ __align__(16) bf16_t smem[FwdTileShape<DP>::LDS];
+  fwd_tile_job<DP>(p, blockIdx.x, smem);
+}
+
+// The same jobs taken by persistent workgroups (two per CU) from per-queue counters: queue q holds the
+// heads h = q (mod jobs_nq) in launch order, and workgroup i takes from queue i % jobs_nq, so a queue's
+// workgroups sit on the XCDs i % 8 = q (mod jobs_nq) (workgroups are dealt round-robin over the XCDs)
+// and their L2s hold those heads' keys. With many more jobs than slots (the varlen prefill: 4,992
+// workgroups of which 3,512 have rows, for 512 slots) one workgroup per job let the dispatcher stall:
+// it places workgroups in order, and an XCD without a free slot holds back every later one, so 260-300
+// of the 512 slots stood busy through the first half of the launch (per-workgroup stamps). The
+// parameters reach each job through an opaque pointer to the kernel argument: the compiler then reads
+// them (scalar loads) inside each job instead of holding every value it derives from them across the
+// loop (61 scalar registers spilled, 6 now).
+template <int DP>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+relation_fwd_tile_persistent_kernel(const FwdParams p) {
+  __shared__ __align__(16) bf16_t smem[FwdTileShape<DP>::LDS];
+  __shared__ int s_job;
+  const int nq = p.jobs_nq, queue = blockIdx.x % nq;
+  const int hq = p.H / nq;                       // heads per queue
+  const int njobs = hq * p.nseq * p.nqb;         // jobs per queue (blocks past a sequence's end included)
+  for (;;) {
+    if (threadIdx.x == 0)
+      s_job = __hip_atomic_fetch_add(p.jobs + 32 * queue, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    const int j = __builtin_amdgcn_readfirstlane(s_job);
+    if (j >= njobs) break;
+    const int h = queue + nq * (j % hq), rest = j / hq;
+    typedef const __attribute__((address_space(4))) FwdParams* ConstFwdParams;
+    ConstFwdParams pp = (ConstFwdParams)__builtin_amdgcn_kernarg_segment_ptr();  // the kernel's one argument
+    asm volatile("" : "+s"(pp));
+    const FwdParams& q = *(const FwdParams*)pp;
+    fwd_tile_job<DP>(q, h + q.H * rest, smem);
+    __syncthreads();  // the next job reuses the LDS and s_job
+  }
+}
+
+__global__ void __launch_bounds__(64) fwd_jobs_clear_kernel(int* jobs) {
+  if (threadIdx.x < 8) jobs[32 * threadIdx.x] = 0;
+}
+
 // Merge of the two halves of a split query block, then the epilogue of relation_fwd_tile_kernel:
 // four threads per row, each owning DP / 4 head-dim elements.
 template <int DP>
@@ -870,8 +923,26 @@ static int fwd_split_c(const mote_relation_fwd_args* a) {
   return n > 96 ? (n + 1) / 2 : 1 << 30;
 }
 
+int device_cu_count();
+
+// Persistent workgroups for the tile forward (one job counter per queue in the workspace) when there
+// are at least four jobs per workgroup slot, as in the varlen prefill (C5: 4,992 jobs on 512 slots,
+// 390 -> 331 us per layer in kernel traces; per-job stamps: 490-512 workgroups busy through the
+// launch against 264-304 for its first half, though each key block then takes 1.42 against 1.25 us);
+// with fewer the one-job-per-workgroup launch measured as fast or faster (C3, 624 jobs: 85.1 against
+// 88.6 us). MOTE_FWD_PERSIST = 0 / 1 overrides.
+static bool fwd_persistent(const mote_relation_fwd_args* a) {
+  const char* e = getenv("MOTE_FWD_PERSIST");
+  if (e && e[0] == '0') return false;
+  if (e && e[0] == '1') return true;
+  const int64_t jobs = int64_t(a->B) * a->H * ((a->TQ + 63) / 64);
+  return jobs >= 4 * 2 * int64_t(device_cu_count());
+}
+constexpr size_t kFwdJobBytes = 8 * 32 * sizeof(int);  // eight queue counters, 128 bytes apart
+
 size_t fwd_workspace_bytes(const mote_relation_fwd_args* a) {
-  if (!a || a->TQ <= 0 || a->D <= 0 || a->D > 128 || !fwd_tiles(a) || fwd_split_c(a) >= (1 << 30)) return 0;
+  if (!a || a->TQ <= 0 || a->D <= 0 || a->D > 128 || !fwd_tiles(a)) return 0;
+  if (fwd_split_c(a) >= (1 << 30)) return fwd_persistent(a) ? kFwdJobBytes : 0;
   const size_t nqb = (size_t(a->TQ) + 63) / 64;
   return size_t(a->B) * a->H * nqb * 2 * (64 * size_t(a->D) + 128) * sizeof(float);
 }
@@ -924,13 +995,25 @@ int launch_fwd(const mote_relation_fwd_args* a, hipStream_t stream) {
   if (fwd_tiles(a)) {
     fp.nqb = (a->TQ + 63) / 64;
     const size_t need = fwd_workspace_bytes(a);
-    const bool split = need > 0 && a->workspace && a->workspace_bytes >= need;
+    const bool have = need > 0 && a->workspace && a->workspace_bytes >= need;
+    const bool split = have && fwd_split_c(a) < (1 << 30);
+    const bool persist = have && !split;  // (the workspace then holds the job counters)
     fp.part = split ? reinterpret_cast<float*>(a->workspace) : nullptr;
     fp.split_c = split ? fwd_split_c(a) : (1 << 30);
+    fp.jobs = persist ? reinterpret_cast<int*>(a->workspace) : nullptr;
+    fp.jobs_nq = a->H % 8 == 0 ? 8 : a->H % 4 == 0 ? 4 : a->H % 2 == 0 ? 2 : 1;
     const int nb = int(units * fp.nqb);
-#define MOTE_FWD_TILE(DPV)                                                                                \
-  hipLaunchKernelGGL((relation_fwd_tile_kernel<DPV>), dim3(split ? 2 * nb : nb), dim3(256), 0, stream, fp); \
-  if (split) hipLaunchKernelGGL((relation_fwd_merge_kernel<DPV>), dim3(nb), dim3(256), 0, stream, fp);
+    const int resident = 2 * device_cu_count();
+    const int pgrid = (resident < nb ? resident : nb) / fp.jobs_nq * fp.jobs_nq;
+    if (persist) hipLaunchKernelGGL(fwd_jobs_clear_kernel, dim3(1), dim3(64), 0, stream, fp.jobs);
+#define MOTE_FWD_TILE(DPV)                                                                                      \
+  if (persist) {                                                                                                \
+    hipLaunchKernelGGL((relation_fwd_tile_persistent_kernel<DPV>), dim3(pgrid > 0 ? pgrid : fp.jobs_nq), dim3(256), 0, \
+                       stream, fp);                                                                             \
+  } else {                                                                                                      \
+    hipLaunchKernelGGL((relation_fwd_tile_kernel<DPV>), dim3(split ? 2 * nb : nb), dim3(256), 0, stream, fp);    \
+    if (split) hipLaunchKernelGGL((relation_fwd_merge_kernel<DPV>), dim3(nb), dim3(256), 0, stream, fp);          \
+  }
     switch (DP) {
       case 32: MOTE_FWD_TILE(32) break;
       case 64: MOTE_FWD_TILE(64) break;

@@ -216,3 +216,36 @@ def test_empty_query_block_and_shapes(cuda):
     assert y.shape == (1, 2, 0, 32) and g.shape == (1, 2, 0)
     with pytest.raises(ValueError):
         flash_relation(p1, p2[:, :, :3], info[:, :, :3], torch.tensor(0.5, device=cuda), 2.0, q_start=5)
+
+
+@pytest.mark.parametrize("B,H,T,S,D,varlen", [
+    (1, 8, 700, 0, 96, True), (4, 8, 1000, 0, 96, False), (2, 4, 333, 50, 64, False), (1, 2, 2000, 0, 128, False),
+    (3, 3, 129, 0, 32, False), (1, 6, 64, 64, 96, False),
+])
+def test_persistent_equals_one_job_per_workgroup(cuda, monkeypatch, B, H, T, S, D, varlen):
+    """The tile forward's persistent form (jobs from per-queue counters, MOTE_FWD_PERSIST=1) runs the
+    same per-job code as one workgroup per job (MOTE_FWD_PERSIST=0): every output bit for bit, with
+    1 / 2 / 4 / 8 queues, cached prefixes, ragged packed sequences and every tile head dim."""
+    from mote_amd.flash_relation import flash_relation  # noqa: F401  (registers the ops)
+
+    print(f"case fwd persistent B={B} H={H} T={T} S={S} D={D} varlen={varlen}", flush=True)
+    lam = torch.tensor(0.45, device=cuda)
+    if varlen:
+        lens = [T, T // 3, T // 2 + 7]
+        cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32)
+        total = int(cu[-1])
+        g = torch.Generator().manual_seed(21)
+        x = [torch.randn(total, H, D, generator=g).to(torch.bfloat16).to(cuda) for _ in range(3)]
+        args = tuple(t.permute(1, 0, 2) for t in x) + (lam, cu.to(cuda), max(lens), 2.0)
+        op = torch.ops.mote.relation_fwd_varlen
+    else:
+        p1, p2, info = _inputs(B, H, T, S, D, torch.bfloat16, seed=22)
+        args = (p1, p2, info, lam, 2.0, S)
+        op = torch.ops.mote.relation_fwd
+    outs = []
+    for flag in ("0", "1"):
+        monkeypatch.setenv("MOTE_FWD_PERSIST", flag)
+        outs.append([t.clone() for t in op(*args)])
+        torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
