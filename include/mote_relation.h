@@ -245,6 +245,9 @@ typedef struct mote_relation_decode_args {
      It stands in for the graph decoder's conditional node around the main step (graph.py:44-57,
      224-226): one captured graph serves both branches. */
   const unsigned char* run;
+  /* Read by mote_relation_decode_static only (ignored by mote_relation_decode): which of its
+     MOTE_DECODE_STATIC_SLOTS scratch copies the call uses, 0 when the block is zero-initialised. */
+  int static_slot;
 } mote_relation_decode_args;
 
 size_t mote_relation_decode_workspace(const mote_relation_decode_args* args);
@@ -255,18 +258,20 @@ int mote_relation_decode(const mote_relation_decode_args* args, void* stream);
  * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc). Arguments and results are those of mote_relation_decode, whose `workspace` /
  * `workspace_bytes` fields are ignored: the per-split partials and completion counters live in a
- * static device array of MOTE_DECODE_STATIC_BYTES bytes per GPU, held until the process ends. A call
- * takes at most 256 sequences and 1024 sequence-heads (B * H); anything beyond is refused with
- * MOTE_ERR_WORKSPACE before any launch. Every call on one GPU shares the array:
- * calls ordered on one stream are fine, calls that overlap on one GPU (unordered streams) race. So
- * a process that decodes on two streams at once (the reference's daemon serves on a stream of its
- * own beside the trainer's, mote/infer/engine.py:150-162) must give this entry point to at most
- * one of them and use mote_relation_decode with a workspace on the other.
- * The first call on a device clears its copy in the caller's stream order and is refused under
- * graph capture (the clear would be captured and rerun on every replay): make it once outside.
+ * static device array of MOTE_DECODE_STATIC_SLOTS slots of MOTE_DECODE_STATIC_BYTES bytes each per
+ * GPU, held until the process ends; `static_slot` picks the slot (anything outside
+ * [0, MOTE_DECODE_STATIC_SLOTS) is refused with MOTE_ERR_ARGUMENT). A call takes at most 256
+ * sequences and 1024 sequence-heads (B * H); anything beyond is refused with MOTE_ERR_WORKSPACE
+ * before any launch. Calls on one GPU that use one slot share it: calls ordered on one stream are
+ * fine, calls on unordered streams race. Calls on different slots are independent, so a process
+ * that decodes on two streams at once (the reference's daemon serves on a stream of its own beside
+ * the trainer's, mote/infer/engine.py:150-162) gives each stream a slot of its own.
+ * The first call on a slot of a device clears that slot in the caller's stream order and is refused
+ * under graph capture (the clear would be captured and rerun on every replay): make it once outside.
  * The stream's device must be the current device. It allocates nothing.
  * ------------------------------------------------------------------------------------------------ */
 #define MOTE_DECODE_STATIC_BYTES (1u << 20)
+#define MOTE_DECODE_STATIC_SLOTS 4
 
 int mote_relation_decode_static(const mote_relation_decode_args* args, void* stream);
 

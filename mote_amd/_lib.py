@@ -22,6 +22,7 @@ MOTE_BF16 = 1
 MOTE_DECODE_ADVANCE = 1
 MOTE_DECODE_ROPE_F32 = 2
 MOTE_DECODE_STATIC_BYTES = 1 << 20
+MOTE_DECODE_STATIC_SLOTS = 4
 MOTE_BWD_ROWS, MOTE_BWD_KEYS, MOTE_BWD_FINISH, MOTE_BWD_QUERIES = 1, 2, 4, 8
 
 _DTYPES = {torch.float32: MOTE_F32, torch.bfloat16: MOTE_BF16}
@@ -83,6 +84,7 @@ class DecodeArgs(C.Structure):
         ("cache_p2", View), ("cache_info", View),
         ("y", C.c_void_p), ("y_sb", C.c_int64), ("g", C.c_void_p),
         ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t), ("xm", C.c_void_p), ("run", C.c_void_p),
+        ("static_slot", C.c_int),
     ]
 
 

@@ -71,6 +71,7 @@ const Entry kLayout[] = {
     F(mote_relation_decode_args, y), F(mote_relation_decode_args, y_sb), F(mote_relation_decode_args, g),
     F(mote_relation_decode_args, workspace), F(mote_relation_decode_args, workspace_bytes),
     F(mote_relation_decode_args, xm), F(mote_relation_decode_args, run),
+    F(mote_relation_decode_args, static_slot),
     MOTE_STRUCT(mote_add_rms_norm_args),
     F(mote_add_rms_norm_args, dtype), F(mote_add_rms_norm_args, res_dtype),
     F(mote_add_rms_norm_args, out_dtype), F(mote_add_rms_norm_args, res_out_dtype),

@@ -527,10 +527,12 @@ int launch_decode(const mote_relation_decode_args* a, hipStream_t stream) {
 
 // ------------------------------------------------------------------------------------------------
 // The no-allocation entry point: the partials and counters live in `scratch`, a static device array
-// (one copy per GPU, alive until the process ends). In host code `scratch` names a host-side stand-in,
-// not device memory: its device address comes from hipGetSymbolAddress, once per device (with that
-// device current), and only that address is ever handed to a kernel. The first call on a device
-// clears its copy with a fill kernel in the caller's stream order. Calls on one GPU share the array.
+// (one copy per GPU, alive until the process ends) of MOTE_DECODE_STATIC_SLOTS slots; a call uses the
+// slot its `static_slot` names, so calls on different slots never touch the same bytes. In host code
+// `scratch` names a host-side stand-in, not device memory: its device address comes from
+// hipGetSymbolAddress, once per device (with that device current), and only that address (plus a
+// slot offset) is ever handed to a kernel. The first call on a slot of a device clears that slot with
+// a fill kernel in the caller's stream order. Calls on one slot of one GPU share it.
 //
 // Layout. The completion counters must be zero when a call starts. A call leaves the counters it
 // used at zero, but the workspace layout (counters after the partials) moves them with the shape, so
@@ -551,17 +553,18 @@ static DecWs decode_ws_static(const mote_relation_decode_args* a) {
   return w;
 }
 
-static __device__ __align__(256) unsigned char scratch[MOTE_DECODE_STATIC_BYTES];
+static __device__ __align__(256) unsigned char scratch[size_t(MOTE_DECODE_STATIC_SLOTS) * MOTE_DECODE_STATIC_BYTES];
 
 constexpr int kMaxScratchDevices = 64;
 static std::mutex g_scratch_mu;
 static void* g_scratch_ptr[kMaxScratchDevices];  // device address of `scratch` per device, once known
+static bool g_slot_clear[kMaxScratchDevices][MOTE_DECODE_STATIC_SLOTS];  // slot cleared on that device
 
 __global__ void __launch_bounds__(256) clear_scratch_kernel(uint4* p, int n16) {
   for (int i = blockIdx.x * 256 + threadIdx.x; i < n16; i += gridDim.x * 256) p[i] = make_uint4(0u, 0u, 0u, 0u);
 }
 
-static int scratch_address(hipStream_t stream, void** out) {
+static int scratch_address(hipStream_t stream, int slot, void** out) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices)
     return set_error(MOTE_ERR_LAUNCH, "relation_decode_static: no usable current device");
@@ -572,22 +575,26 @@ static int scratch_address(hipStream_t stream, void** out) {
                        sdev, dev);
   }
   std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (!g_scratch_ptr[dev]) {
+  if (!g_slot_clear[dev][slot]) {
     // the clear must run once, not on every replay of a graph: refuse a first call under capture
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     if (stream && hipStreamIsCapturing(stream, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone)
-      return set_error(MOTE_ERR_ARGUMENT, "relation_decode_static: the first call on a device clears the static array "
-                                          "and must not be captured; call it once outside the capture first");
-    void* ptr = nullptr;
-    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-    if (e != hipSuccess || !ptr)
-      return set_error(MOTE_ERR_LAUNCH, "relation_decode_static: hipGetSymbolAddress failed: %s", hipGetErrorString(e));
-    hipLaunchKernelGGL(clear_scratch_kernel, dim3(64), dim3(256), 0, stream, reinterpret_cast<uint4*>(ptr),
+      return set_error(MOTE_ERR_ARGUMENT, "relation_decode_static: the first call on slot %d of a device clears that "
+                                          "slot and must not be captured; call it once outside the capture first", slot);
+    if (!g_scratch_ptr[dev]) {
+      void* ptr = nullptr;
+      const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !ptr)
+        return set_error(MOTE_ERR_LAUNCH, "relation_decode_static: hipGetSymbolAddress failed: %s", hipGetErrorString(e));
+      g_scratch_ptr[dev] = ptr;
+    }
+    unsigned char* base = static_cast<unsigned char*>(g_scratch_ptr[dev]) + size_t(slot) * MOTE_DECODE_STATIC_BYTES;
+    hipLaunchKernelGGL(clear_scratch_kernel, dim3(64), dim3(256), 0, stream, reinterpret_cast<uint4*>(base),
                        int(MOTE_DECODE_STATIC_BYTES / 16));
     if (const int rc = check_launch("relation_decode_static (scratch clear)")) return rc;
-    g_scratch_ptr[dev] = ptr;
+    g_slot_clear[dev][slot] = true;
   }
-  *out = g_scratch_ptr[dev];
+  *out = static_cast<unsigned char*>(g_scratch_ptr[dev]) + size_t(slot) * MOTE_DECODE_STATIC_BYTES;
   return MOTE_OK;
 }
 
@@ -597,11 +604,14 @@ int launch_decode_static(const mote_relation_decode_args* a, hipStream_t stream)
   if (a->B > kStaticSeqLines || int64_t(a->B) * a->H > kStaticHeadLines || w.total > MOTE_DECODE_STATIC_BYTES)
     return set_error(MOTE_ERR_WORKSPACE,
                      "relation_decode_static: B = %d sequences x H = %d heads need %zu bytes of scratch with at most "
-                     "%d sequences and %d sequence-heads; the static array holds %u (use mote_relation_decode with a "
+                     "%d sequences and %d sequence-heads; a slot of the static array holds %u (use mote_relation_decode with a "
                      "workspace)", a->B, a->H, w.total, kStaticSeqLines, kStaticHeadLines,
                      unsigned(MOTE_DECODE_STATIC_BYTES));
+  if (a->static_slot < 0 || a->static_slot >= MOTE_DECODE_STATIC_SLOTS)
+    return set_error(MOTE_ERR_ARGUMENT, "relation_decode_static: static_slot = %d, want 0 to %d", a->static_slot,
+                     MOTE_DECODE_STATIC_SLOTS - 1);
   void* ws = nullptr;
-  if (const int rc = scratch_address(stream, &ws)) return rc;
+  if (const int rc = scratch_address(stream, a->static_slot, &ws)) return rc;
   return launch_decode_ws(a, ws, w, stream);
 }
 

@@ -147,6 +147,11 @@ def test_static_decode_refuses_shapes_beyond_its_array_without_a_gpu():
     assert _lib.lib().mote_relation_decode_static(a, None) == 2  # the shape checks come first
     a.D, a.g = 128, None
     assert _lib.lib().mote_relation_decode_static(a, None) == 1
+    a.g = 16
+    for slot in (-1, _lib.MOTE_DECODE_STATIC_SLOTS):  # a slot outside the array
+        a.static_slot = slot
+        assert _lib.lib().mote_relation_decode_static(a, None) == 1, slot
+        assert f"static_slot = {slot}".encode() in _lib.lib().mote_last_error()
 
 
 def test_ctypes_mirrors_match_the_compiled_struct_layout():

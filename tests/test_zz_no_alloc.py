@@ -2,7 +2,9 @@
 mote_relation_decode with a caller workspace: on calls in a row (the second with a smaller
 batch, capacity and fill) the outputs y, g, xm, the appended cache rows and the advanced positions
 are identical bit for bit (same kernel, same split count, deterministic merge order). A third call
-goes back to a larger batch with another head dim: the shared array's counters stay valid."""
+goes back to a larger batch with another head dim: the shared array's counters stay valid. Two
+slots driven from two unordered streams at once give each stream the workspace entry point's
+results."""
 
 from __future__ import annotations
 
@@ -27,8 +29,9 @@ def _inputs(B, H, D, cap, S, seed, dtype):
     )
 
 
-def _call(entry: str, inp, layer_parity: int):
-    """One decode step through the named C entry point on fresh device copies of `inp`."""
+def _call(entry: str, inp, layer_parity: int, slot: int = 0):
+    """One decode step through the named C entry point on fresh device copies of `inp` (the static
+    entry point on scratch slot `slot`)."""
     from mote_amd import _lib as L
 
     dev = torch.device("cuda")
@@ -53,7 +56,7 @@ def _call(entry: str, inp, layer_parity: int):
         ws = torch.zeros(int(L.lib().mote_relation_decode_workspace(a)), device=dev, dtype=torch.uint8)
         a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
     else:
-        a.workspace, a.workspace_bytes = None, 0
+        a.workspace, a.workspace_bytes, a.static_slot = None, 0, slot
     L.check(getattr(L.lib(), entry)(a, L.stream_of(kc)), entry)
     torch.cuda.synchronize()
     return [t.cpu() for t in (y, g, xm, kc, vc, S)]
@@ -75,3 +78,54 @@ def test_static_scratch_entry_point_matches_the_workspace_one(cuda, dtype):
             assert torch.equal(a, b), (i, name)
         assert torch.equal(got[5], inp["S"] + 1)
         assert bool(torch.isfinite(got[0]).all())
+
+
+def test_static_slots_on_two_streams_at_once(cuda):
+    """Slots 1 and 2 driven from two unordered streams, each with a queue of steps launched before
+    either is waited for, so the two streams' decode kernels overlap on the GPU: every step's
+    outputs equal the workspace entry point's bit for bit. Sharing one slot here would race."""
+    from mote_amd import _lib as L
+
+    dev = torch.device("cuda")
+    shapes = [(16, 8, 96, 2048, 1), (8, 16, 128, 2048, 0)]
+    inps = [_inputs(B, H, D, cap, [(37 * i + 5 * s) % (cap - 1) for i in range(B)], seed=90 + s, dtype=torch.bfloat16)
+            for s, (B, H, D, cap, _) in enumerate(shapes)]
+    want = [_call("mote_relation_decode", inp, shp[4]) for inp, shp in zip(inps, shapes)]
+    for slot in (1, 2):  # first calls clear the slots, outside the concurrent part
+        _call("mote_relation_decode_static", inps[0], shapes[0][4], slot=slot)
+    steps = 6
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    state = []
+    for s, (inp, (B, H, D, cap, parity)) in enumerate(zip(inps, shapes)):
+        kc, vc = inp["kc"].to(dev), inp["vc"].to(dev)
+        raw = [t.to(dev) for t in inp["raw"]]
+        outs = []
+        for _ in range(steps):  # one fresh copy of the mutated state per step
+            outs.append(dict(kc=kc.clone(), vc=vc.clone(), S=inp["S"].to(dev),
+                             y=torch.full((B, H, D), float("nan"), device=dev, dtype=kc.dtype),
+                             g=torch.full((B, H), float("nan"), device=dev),
+                             xm=torch.full((B,), float("nan"), device=dev)))
+        state.append((raw, inp["lam"].to(dev), inp["inv"].to(dev), inp["theta"].to(dev), outs))
+    torch.cuda.synchronize()
+    print("case no-alloc decode: slots 1 and 2 on two streams", flush=True)
+    keep = []
+    for k in range(steps):  # interleave the two streams' launches
+        for s, (B, H, D, cap, parity) in enumerate(shapes):
+            raw, lam, inv, theta, outs = state[s]
+            o = outs[k]
+            a = L.DecodeArgs()
+            a.dtype, a.B, a.H, a.D, a.capacity = L.MOTE_BF16, B, H, D, cap
+            a.layer_parity, a.flags, a.tau_s = parity, L.MOTE_DECODE_ADVANCE, 2.0
+            a.lam, a.inv_freq, a.theta, a.S = lam.data_ptr(), inv.data_ptr(), theta.data_ptr(), o["S"].data_ptr()
+            a.p1, a.p2, a.info, a.in_sb = raw[0].data_ptr(), raw[1].data_ptr(), raw[2].data_ptr(), raw[0].stride(0)
+            a.cache_p2, a.cache_info = L.view(o["kc"]), L.view(o["vc"])
+            a.y, a.y_sb, a.g, a.xm = o["y"].data_ptr(), o["y"].stride(0), o["g"].data_ptr(), o["xm"].data_ptr()
+            a.static_slot = 1 + s
+            keep.append(a)
+            L.check(L.lib().mote_relation_decode_static(a, streams[s].cuda_stream), "mote_relation_decode_static")
+    torch.cuda.synchronize()
+    for s in range(2):
+        for k, o in enumerate(state[s][4]):
+            got = [o[n].cpu() for n in ("y", "g", "xm", "kc", "vc", "S")]
+            for name, a, b in zip(("y", "g", "xm", "cache_p2", "cache_info", "S"), got, want[s]):
+                assert torch.equal(a, b), (s, k, name)
