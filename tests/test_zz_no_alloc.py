@@ -129,3 +129,66 @@ def test_static_slots_on_two_streams_at_once(cuda):
             got = [o[n].cpu() for n in ("y", "g", "xm", "kc", "vc", "S")]
             for name, a, b in zip(("y", "g", "xm", "cache_p2", "cache_info", "S"), got, want[s]):
                 assert torch.equal(a, b), (s, k, name)
+
+
+def test_static_entry_point_under_graph_capture(cuda):
+    """The use the entry point exists for: a first call on a fresh slot under capture is refused on
+    the host (its clear would be captured and rerun on every replay); after one eager call on the
+    slot, one captured step replayed on new inputs (copied into the captured buffers, with eager work
+    and synchronisation between the replays) equals the workspace entry point on each."""
+    from mote_amd import _lib as L
+
+    dev = torch.device("cuda")
+    B, H, D, cap, parity = 4, 8, 96, 1024, 1
+    S0 = [1000, 3, 511, 64]
+    inps = [_inputs(B, H, D, cap, S0, seed=70 + i, dtype=torch.bfloat16) for i in range(4)]
+    buf = {k: (v.to(dev) if k != "raw" else [t.to(dev) for t in v]) for k, v in inps[0].items()}
+    y = torch.full((B, H, D), float("nan"), device=dev, dtype=torch.bfloat16)
+    g = torch.full((B, H), float("nan"), device=dev)
+    xm = torch.full((B,), float("nan"), device=dev)
+    a = L.DecodeArgs()
+    a.dtype, a.B, a.H, a.D, a.capacity = L.MOTE_BF16, B, H, D, cap
+    a.layer_parity, a.flags, a.tau_s = parity, L.MOTE_DECODE_ADVANCE, 2.0
+    a.lam, a.inv_freq, a.theta, a.S = (buf[k].data_ptr() for k in ("lam", "inv", "theta", "S"))
+    raw = buf["raw"]
+    a.p1, a.p2, a.info, a.in_sb = raw[0].data_ptr(), raw[1].data_ptr(), raw[2].data_ptr(), raw[0].stride(0)
+    a.cache_p2, a.cache_info = L.view(buf["kc"]), L.view(buf["vc"])
+    a.y, a.y_sb, a.g, a.xm = y.data_ptr(), y.stride(0), g.data_ptr(), xm.data_ptr()
+    a.static_slot = 3  # no other test uses slot 3, so it is fresh here
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    print("case no-alloc decode: first call on a fresh slot under capture", flush=True)
+    refused = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(refused, stream=side):
+            y.zero_()  # keeps the refused capture's graph non-empty; it is never replayed
+            rc = L.lib().mote_relation_decode_static(a, side.cuda_stream)
+    assert rc == 1 and b"must not be captured" in L.lib().mote_last_error()
+    torch.cuda.synchronize()
+    L.check(L.lib().mote_relation_decode_static(a, L.stream_of(y)), "mote_relation_decode_static")  # clears slot 3
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(gr, stream=side):
+            L.check(L.lib().mote_relation_decode_static(a, side.cuda_stream), "mote_relation_decode_static")
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    for i, inp in enumerate(inps):
+        print(f"case no-alloc decode: replay {i}", flush=True)
+        want = _call("mote_relation_decode", inp, parity)
+        for k, v in inp.items():
+            if k == "raw":
+                for dst, src in zip(raw, v):
+                    dst.copy_(src)
+            else:
+                buf[k].copy_(v)
+        for t in (y, g, xm):
+            t.fill_(float("nan"))
+        torch.cuda.synchronize()
+        gr.replay()
+        torch.cuda.synchronize()
+        got = [t.cpu() for t in (y, g, xm, buf["kc"], buf["vc"], buf["S"])]
+        for name, u, w in zip(("y", "g", "xm", "cache_p2", "cache_info", "S"), got, want):
+            assert torch.equal(u, w), (i, name)
